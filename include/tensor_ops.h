@@ -1,0 +1,161 @@
+/*
+ * tensor_ops.h — C ABI of libtensor_ops_hip.so (MI355X / gfx950).
+ *
+ * The first block restates the reference operator library's interface for the
+ * 13 hot-path operators, with identical type layouts (LP64) and identical
+ * symbol names and signatures, so a caller that binds the reference library
+ * through ctypes binds this one unchanged.  Every declaration cites the
+ * reference declaration it replaces (paths relative to the reference tree).
+ *
+ * The second block lists additive extensions: new symbols only, the structs
+ * are unchanged.  They add device-resident tensors (data pointer in HBM),
+ * explicit streams, error reporting and per-axis quantization.
+ *
+ * Semantics common to all operators (tensor_ops/tensor_ops.c:488-588):
+ *   every input element is decoded to double, the operator computes in double
+ *   (or in a narrower type only where that is provably bit-identical), and the
+ *   result is written through the output dtype's encoder.  Outputs are
+ *   pre-created by the caller with their final shape and dtype.
+ *
+ * Residency: a Tensor made by create_tensor() holds host memory (pinned when a
+ * GPU is present); operators on such tensors are synchronous and stage the
+ * data through device memory.  A Tensor made by create_tensor_device() or
+ * tensor_wrap_device() holds device memory; operators whose operands are all
+ * device-resident are enqueued on the library stream and return immediately.
+ */
+#ifndef TENSOR_OPS_HIP_H
+#define TENSOR_OPS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types; values match tensor_ops/tensor_ops.h:10-23 and the Python
+ * DTYPE_MAP of nn/__init__.py:20-34 (int4 is stored one value per byte). */
+typedef enum {
+    DTYPE_FLOAT8_E4M3 = 0,
+    DTYPE_FLOAT8_E5M2 = 1,
+    DTYPE_FLOAT16 = 2,
+    DTYPE_BFLOAT16 = 3,
+    DTYPE_FLOAT32 = 4,
+    DTYPE_FLOAT64 = 5,
+    DTYPE_INT4 = 6,
+    DTYPE_INT8 = 7,
+    DTYPE_UINT8 = 8,
+    DTYPE_INT16 = 9,
+    DTYPE_INT32 = 10,
+    DTYPE_INT64 = 11
+} DataType;
+
+/* tensor_ops/tensor_ops.h:28-34 — sizeof 40: data@0 shape@8 ndim@16 size@24 dtype@32. */
+typedef struct {
+    void* data;
+    int* shape;
+    int ndim;
+    size_t size;
+    DataType dtype;
+} Tensor;
+
+/* tensor_ops/tensor_ops.h:39-44 — pads are [top, left, bottom, right]. */
+typedef struct {
+    int* pads;
+    int* strides;
+    int* dilations;
+    int group;
+} ConvParams;
+
+/* tensor_ops/tensor_ops.h:49-54 */
+typedef struct {
+    int* pads;
+    int* strides;
+    int* dilations;
+    int* kernel_shape;
+} PoolParams;
+
+/* ---------------------------------------------------------------------------
+ * Reference ABI (hot path)
+ * ------------------------------------------------------------------------- */
+
+/* tensor_ops/tensor_ops.h:70 (tensor_ops.c:357-433): zero-filled host tensor,
+ * NULL on allocation failure. */
+Tensor* create_tensor(int* shape, int ndim, DataType dtype);
+/* tensor_ops/tensor_ops.h:77 (tensor_ops.c:440-450): frees any tensor this
+ * library made (host or device); NULL is ignored. */
+void free_tensor(Tensor* tensor);
+/* tensor_ops/tensor_ops.h:85 (tensor_ops.c:708-728) */
+void relu_forward(const Tensor* input, Tensor* output);
+/* tensor_ops/tensor_ops.h:91 (tensor_ops.c:763-807): builds the 4097-entry
+ * cosine table once (thread-safe) and uploads it to the device. */
+void init_cos_lut(void);
+/* tensor_ops/tensor_ops.h:99 (tensor_ops.c:815-854) */
+void cos_forward(const Tensor* input, Tensor* output);
+/* tensor_ops/tensor_ops.h:107 (tensor_ops.c:736-757) */
+void abs_forward(const Tensor* input, Tensor* output);
+/* tensor_ops/tensor_ops.h:116,125,134,143 (tensor_ops.c:864-997).
+ * Equal sizes: flat elementwise, as the reference.  Sizes that differ but
+ * broadcast (numpy rules) to O's shape: broadcast in-kernel (the reference
+ * returns without writing there; its Python caller broadcasts first). */
+void add_forward(const Tensor* A, const Tensor* B, Tensor* O);
+void sub_forward(const Tensor* A, const Tensor* B, Tensor* O);
+void mul_forward(const Tensor* A, const Tensor* B, Tensor* O);
+void div_forward(const Tensor* A, const Tensor* B, Tensor* O);
+/* tensor_ops/tensor_ops.h:149 (tensor_ops.c:999-1016):
+ * y = s != 0 ? rint(x / s) + zp : zp in double, then the output encoder.
+ * Scale / ZeroPoint may be full-size (reference) or broadcastable to Y. */
+void quantize_linear_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint, Tensor* Y);
+/* tensor_ops/tensor_ops.h:155 (tensor_ops.c:1018-1034): y = (x - zp) * s in double. */
+void dequantize_linear_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint, Tensor* Y);
+/* tensor_ops/tensor_ops.h:161 (tensor_ops.c:1036-1114): NCHW, W [M, C/group, KH, KW],
+ * B nullable [M]; output size is taken from Y's shape. */
+void conv2d_forward(const Tensor* X, const Tensor* W, const Tensor* B, Tensor* Y, ConvParams* params);
+/* tensor_ops/tensor_ops.h:166 (tensor_ops.c:1116-1165) */
+void max_pool_forward(const Tensor* X, Tensor* Y, PoolParams* params);
+/* tensor_ops/tensor_ops.h:173-174 (tensor_ops.c:1167-1228): Y = alpha * A' B' + beta * C. */
+void gemm_forward(const Tensor* A, const Tensor* B, const Tensor* C, Tensor* Y,
+                  float alpha, float beta, int transA, int transB);
+/* tensor_ops/tensor_ops.h:179 (tensor_ops.c:1231-1270); negative axis counts from the end. */
+void softmax_forward(const Tensor* input, Tensor* output, int axis);
+
+/* ---------------------------------------------------------------------------
+ * Extensions (no counterpart in the reference)
+ * ------------------------------------------------------------------------- */
+
+/* Zero-filled tensor in device memory (HBM).  NULL on failure. */
+Tensor* create_tensor_device(int* shape, int ndim, DataType dtype);
+/* Tensor header over caller-owned device memory; free_tensor frees only the header. */
+Tensor* tensor_wrap_device(void* device_ptr, int* shape, int ndim, DataType dtype);
+/* 1 if t's data lives in device memory, else 0. */
+int tensor_is_device(const Tensor* t);
+/* Copy between a tensor (host or device) and plain host memory of t->size elements.
+ * Both synchronise the library stream.  Return 0 on success, -1 on error. */
+int tensor_to_host(const Tensor* t, void* host_dst);
+int tensor_from_host(Tensor* t, const void* host_src);
+/* Wait for all work enqueued by this library.  0 on success. */
+int tensor_ops_hip_sync(void);
+/* Use a caller-provided hipStream_t (NULL restores the library's own stream). */
+void tensor_ops_hip_set_stream(void* stream);
+void* tensor_ops_hip_get_stream(void);
+/* Number of usable GPUs (0 on a machine without one). */
+int tensor_ops_hip_device_count(void);
+/* Last error of the calling thread ("" if none); cleared by tensor_ops_hip_clear_error. */
+const char* tensor_ops_hip_last_error(void);
+void tensor_ops_hip_clear_error(void);
+/* Library version string. */
+const char* tensor_ops_hip_version(void);
+/* Gemm/Conv precision mode: 0 = MFMA fp32/fp16 accumulate (default, tolerance class);
+ * 1 = exact replica of the reference (double accumulate, sequential k, bit-identical). */
+void tensor_ops_hip_set_exact(int exact);
+/* Per-axis quantize / dequantize with 1-D Scale / ZeroPoint of length X->shape[axis]. */
+void quantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint,
+                                  Tensor* Y, int axis);
+void dequantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint,
+                                    Tensor* Y, int axis);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TENSOR_OPS_HIP_H */

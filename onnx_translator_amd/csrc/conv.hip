@@ -1,0 +1,252 @@
+// conv.hip — Conv2d (NCHW) for gfx950.
+//
+// tensor_ops/tensor_ops.c:1036-1114: for each output (n, m, oh, ow), a double
+// sum over (ic, kh, kw) of X * W with zero padding (padded taps contribute
+// 0.0 * w), then + bias[m], written through the output encoder.  Output
+// extent comes from Y's shape; pads[0] / pads[1] are top / left.
+//
+//  * k_conv_mfma_f32 — implicit GEMM on v_mfma_f32_32x32x2f32.  Per group:
+//    M = out channels, N = batch * OH * OW pixels, K = Cin/g * KH * KW.  The
+//    block tile is 64 channels x 256 pixels (4 waves side by side, each
+//    64 x 64 = 2x2 MFMA tiles), BK = 16.  Each thread owns one pixel column
+//    of the im2col tile, so the gather along the pixel dimension is
+//    coalesced; the (c, kh, kw) decode of k is uniform across the block.
+//    fp32 accumulate: tolerance class vs the reference.
+//  * k_conv_exact — fp64, reference summation order, bit-identical.
+#include "runtime.h"
+
+namespace tohip {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+struct ConvGeom {
+    int N, C, H, W;      // input
+    int M, KH, KW;       // weights [M, C/g, KH, KW]
+    int OH, OW;          // output (from Y)
+    int pt, pl, sh, sw, dh, dw, group;
+    int Cg, Mg, Kg;      // per-group channels in / out, Cg * KH * KW
+};
+
+__global__ __launch_bounds__(256) void k_conv_exact(const void* __restrict__ X, int dtx, const void* __restrict__ Wt,
+                                                    int dtw, const void* __restrict__ Bv, int dtb, void* __restrict__ Y,
+                                                    int dty, ConvGeom g, int64_t total) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < total; o += stride) {
+        const int ow = (int)(o % g.OW);
+        int64_t t = o / g.OW;
+        const int oh = (int)(t % g.OH);
+        t /= g.OH;
+        const int m = (int)(t % g.M);
+        const int n = (int)(t / g.M);
+        const int grp = m / g.Mg;
+        double acc = 0.0;
+        for (int c = 0; c < g.Cg; c++) {
+            const int ic = grp * g.Cg + c;
+            for (int kh = 0; kh < g.KH; kh++) {
+                const int ih = oh * g.sh + kh * g.dh - g.pt;
+                for (int kw = 0; kw < g.KW; kw++) {
+                    const int iw = ow * g.sw + kw * g.dw - g.pl;
+                    double xv = 0.0;
+                    if (ih >= 0 && ih < g.H && iw >= 0 && iw < g.W)
+                        xv = ld_d_rt(dtx, X, (((int64_t)n * g.C + ic) * g.H + ih) * g.W + iw);
+                    const double wv = ld_d_rt(dtw, Wt, (((int64_t)m * g.Cg + c) * g.KH + kh) * g.KW + kw);
+                    acc += xv * wv;
+                }
+            }
+        }
+        const double bias = Bv ? ld_d_rt(dtb, Bv, m) : 0.0;
+        st_d_rt(dty, Y, o, acc + bias);
+    }
+}
+
+constexpr int kCM = 64, kCN = 256, kCK = 16, kCPad = 4;
+
+// DT >= 0: compile-time dtype; DT < 0: decode with the run-time dtype rdt.
+template <int DT> __device__ __forceinline__ float ldf(const void* p, int64_t i, int rdt) {
+    if constexpr (DT == kF32) return ((const float*)p)[i];
+    else if constexpr (DT >= 0) return (float)ld_d<DT>(p, i);
+    else return (float)ld_d_rt(rdt, p, i);
+}
+
+// Output / bias of uncommon dtypes, kept out of line.
+__device__ __noinline__ void conv_store_rt(void* Y, int dty, int64_t yi, const void* Bv, int dtb, int m, float acc) {
+    const double bias = Bv ? ld_d_rt(dtb, Bv, m) : 0.0;
+    st_d_rt(dty, Y, yi, (double)acc + bias);
+}
+
+template <int DX, int DW, int YDT>
+__global__ __launch_bounds__(256) void k_conv_mfma_f32(const void* __restrict__ X, const void* __restrict__ Wt,
+                                                       const void* __restrict__ Bv, int dtb, void* __restrict__ Y,
+                                                       int dty, ConvGeom g, int dtx, int dtw) {
+    __shared__ float As[2][kCK][kCM + kCPad];
+    __shared__ float Bs[2][kCK][kCN + kCPad];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = blockIdx.z;
+    const int m0 = blockIdx.y * kCM;                 // within the group
+    const int p0 = blockIdx.x * kCN;
+    const int OHW = g.OH * g.OW;
+    const int P = g.N * OHW;
+    const int KHW = g.KH * g.KW;
+
+    // This thread's im2col column.
+    const int p = p0 + threadIdx.x;
+    const bool pv = p < P;
+    const int pn = pv ? p / OHW : 0;
+    const int pr = pv ? p - pn * OHW : 0;
+    const int poh = pr / g.OW, pow_ = pr - poh * g.OW;
+    const int ih0 = poh * g.sh - g.pt, iw0 = pow_ * g.sw - g.pl;
+    const int64_t xbase = ((int64_t)pn * g.C + (int64_t)grp * g.Cg) * g.H * g.W;
+    const int64_t wbase = ((int64_t)grp * g.Mg) * g.Kg;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    auto stage = [&](int buf, int k0) {
+        // Weights: 64 rows (m) x 16 k; thread -> (m = t / 4, 4 consecutive k).
+        {
+            const int mm = threadIdx.x >> 2, kq = (threadIdx.x & 3) * 4;
+            const int gm = m0 + mm;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int gk = k0 + kq + e;
+                As[buf][kq + e][mm] = (gm < g.Mg && gk < g.Kg) ? ldf<DW>(Wt, wbase + (int64_t)gm * g.Kg + gk, dtw) : 0.0f;
+            }
+        }
+        // im2col: 16 k x 256 pixels; thread -> its pixel, all 16 k.
+        int k = k0;
+        int c = k / KHW;
+        int rem = k - c * KHW;
+        int kh = rem / g.KW, kw = rem - kh * g.KW;
+#pragma unroll
+        for (int e = 0; e < kCK; e++) {
+            float v = 0.0f;
+            if (pv && k < g.Kg) {
+                const int ih = ih0 + kh * g.dh, iw = iw0 + kw * g.dw;
+                if (ih >= 0 && ih < g.H && iw >= 0 && iw < g.W)
+                    v = ldf<DX>(X, xbase + ((int64_t)c * g.H + ih) * g.W + iw, dtx);
+            }
+            Bs[buf][e][threadIdx.x] = v;
+            k++;
+            if (++kw == g.KW) { kw = 0; if (++kh == g.KH) { kh = 0; c++; } }
+        }
+    };
+
+    const int nk = (g.Kg + kCK - 1) / kCK;
+    stage(0, 0);
+    __syncthreads();
+    const int lr = lane & 31, lk = lane >> 5;
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) stage(cur ^ 1, (kt + 1) * kCK);
+#pragma unroll
+        for (int ks = 0; ks < kCK; ks += 2) {
+            float a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) a[i] = As[cur][ks + lk][i * 32 + lr];
+#pragma unroll
+            for (int j = 0; j < 2; j++) b[j] = Bs[cur][ks + lk][wave * 64 + j * 32 + lr];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int q = p0 + wave * 64 + j * 32 + lr;
+        if (q >= P) continue;
+        const int qn = q / OHW, qr = q - qn * OHW;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int mloc = m0 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+                if (mloc >= g.Mg) continue;
+                const int m = grp * g.Mg + mloc;
+                const int64_t yi = ((int64_t)qn * g.M + m) * OHW + qr;
+                if constexpr (YDT >= 0) {
+                    if (!Bv || dtb == kF32) {
+                        const double bias = Bv ? (double)((const float*)Bv)[m] : 0.0;
+                        st_d<YDT>(Y, yi, (double)acc[i][j][r] + bias);
+                        continue;
+                    }
+                }
+                conv_store_rt(Y, dty, yi, Bv, dtb, m, acc[i][j][r]);
+            }
+    }
+}
+
+inline bool f32_exact_dtype(int dt) {
+    return dt == kF32 || dt == kF16 || dt == kBF16 || dt == kE4M3 || dt == kE5M2 || dt == kI4 || dt == kI8 ||
+           dt == kU8 || dt == kI16;
+}
+
+template <int DX, int DW>
+void launch_conv_mfma(const void* x, int dtx, const void* w, int dtw, const void* b, int dtb, void* y, int dty,
+                      const ConvGeom& g, hipStream_t s) {
+    const int P = g.N * g.OH * g.OW;
+    const dim3 grid((P + kCN - 1) / kCN, (g.Mg + kCM - 1) / kCM, g.group);
+    if (dty == kF32)
+        hipLaunchKernelGGL((k_conv_mfma_f32<DX, DW, kF32>), grid, dim3(256), 0, s, x, w, b, dtb, y, dty, g, dtx, dtw);
+    else
+        hipLaunchKernelGGL((k_conv_mfma_f32<DX, DW, -1>), grid, dim3(256), 0, s, x, w, b, dtb, y, dty, g, dtx, dtw);
+}
+
+}  // namespace
+}  // namespace tohip
+
+using namespace tohip;
+
+extern "C" void conv2d_forward(const Tensor* X, const Tensor* W, const Tensor* B, Tensor* Y, ConvParams* params) {
+    const char* name = "conv2d_forward";
+    if (!tensor_sane(X, name) || !tensor_sane(W, name) || !tensor_sane(Y, name)) return;
+    if (!params || !params->pads || !params->strides || !params->dilations) { set_error("%s: NULL params", name); return; }
+    if (X->ndim != 4 || W->ndim != 4 || Y->ndim != 4) { set_error("%s: X, W and Y must be 4-D", name); return; }
+    ConvGeom g;
+    g.N = X->shape[0]; g.C = X->shape[1]; g.H = X->shape[2]; g.W = X->shape[3];
+    g.M = W->shape[0]; g.KH = W->shape[2]; g.KW = W->shape[3];
+    g.OH = Y->shape[2]; g.OW = Y->shape[3];
+    g.pt = params->pads[0]; g.pl = params->pads[1];
+    g.sh = params->strides[0]; g.sw = params->strides[1];
+    g.dh = params->dilations[0]; g.dw = params->dilations[1];
+    g.group = params->group;
+    if (g.group < 1 || g.C % g.group || g.M % g.group) { set_error("%s: bad group %d", name, g.group); return; }
+    g.Cg = g.C / g.group; g.Mg = g.M / g.group;
+    if (W->shape[1] != g.Cg) { set_error("%s: W.shape[1]=%d but C/group=%d", name, W->shape[1], g.Cg); return; }
+    if (Y->shape[0] != g.N || Y->shape[1] != g.M) { set_error("%s: Y shape does not match N, M", name); return; }
+    g.Kg = g.Cg * g.KH * g.KW;
+    const bool has_b = B && B->data;
+    if (has_b && (!tensor_sane(B, name) || B->size < (size_t)g.M)) { set_error("%s: bias needs M elements", name); return; }
+    if (!ensure_device()) return;
+    const int64_t total = (int64_t)g.N * g.M * g.OH * g.OW;
+    Staging st;
+    const void* x = st.in(X);
+    const void* w = st.in(W);
+    const void* b = has_b ? st.in(B) : nullptr;
+    void* y = st.out(Y, (size_t)total * dt_bytes((int)Y->dtype));
+    if (!x || !w || !y || (has_b && !b)) { st.finish(); return; }
+    hipStream_t s = stream();
+    const int dtx = (int)X->dtype, dtw = (int)W->dtype, dty = (int)Y->dtype, dtb = has_b ? (int)B->dtype : kF32;
+    if (total > 0) {
+        const bool big = (int64_t)g.N * g.OH * g.OW > 0x7FFFFFFF;
+        bool done = false;
+        if (!exact_mode() && !big && g.Kg > 0 && f32_exact_dtype(dtx) && f32_exact_dtype(dtw)) {
+            if (dtx == kF32 && dtw == kF32) launch_conv_mfma<kF32, kF32>(x, dtx, w, dtw, b, dtb, y, dty, g, s);
+            else launch_conv_mfma<-1, -1>(x, dtx, w, dtw, b, dtb, y, dty, g, s);
+            done = true;
+        }
+        if (!done)
+            hipLaunchKernelGGL(k_conv_exact, dim3(grid_for((size_t)total, 256)), dim3(256), 0, s, x, dtx, w, dtw, b, dtb,
+                               y, dty, g, total);
+        if (!check_launch(name)) { st.finish(); return; }
+    }
+    st.finish();
+}

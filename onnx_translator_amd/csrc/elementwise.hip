@@ -1,0 +1,299 @@
+// elementwise.hip — Relu, Abs, Cos, Add, Sub, Mul, Div for gfx950.
+//
+// Memory-bound kernels: each thread moves 16-byte vectors along the
+// innermost (collapsed) dimension, broadcast operands are indexed through a
+// collapsed stride descriptor (no materialised copies), and launches cover
+// the tensor once with 256-thread blocks.  Numerics follow
+// tensor_ops/tensor_ops.c:708-997 exactly:
+//   * f32 (+-*/) f32 -> f32 runs natively in fp32: double-then-round equals
+//     the correctly rounded fp32 op because 53 >= 2*24 + 2;
+//   * every other float combination computes in fp64 and rounds through the
+//     output encoder; integer outputs use the int64 path with saturation;
+//   * Cos replays the reference's 4097-entry table lookup in fp64 with
+//     contraction off, which reproduces its bits.
+#include "runtime.h"
+
+namespace tohip {
+namespace {
+
+enum { OP_ADD = 0, OP_SUB = 1, OP_MUL = 2, OP_DIV = 3 };
+enum { U_RELU = 0, U_ABS = 1, U_COS = 2 };
+
+constexpr int kBlock = 256;
+
+template <int OP> __device__ __forceinline__ float fop(float a, float b) {
+    if constexpr (OP == OP_ADD) return a + b;
+    else if constexpr (OP == OP_SUB) return a - b;
+    else if constexpr (OP == OP_MUL) return a * b;
+    else return a / b;
+}
+template <int OP> __device__ __forceinline__ double dop(double a, double b) {
+    if constexpr (OP == OP_ADD) return a + b;
+    else if constexpr (OP == OP_SUB) return a - b;
+    else if constexpr (OP == OP_MUL) return a * b;
+    else return a / b;
+}
+// tensor_ops.c:681-684 with two's-complement wrap (the x86 build wraps).
+template <int OP> __device__ __forceinline__ int64_t iop(int64_t a, int64_t b) {
+    const uint64_t ua = (uint64_t)a, ub = (uint64_t)b;
+    if constexpr (OP == OP_ADD) return (int64_t)(ua + ub);
+    else if constexpr (OP == OP_SUB) return (int64_t)(ua - ub);
+    else if constexpr (OP == OP_MUL) return (int64_t)(ua * ub);
+    else {
+        if (b == 0) return a >= 0 ? INT64_MAX : INT64_MIN;
+        if (a == INT64_MIN && b == -1) return INT64_MIN;
+        return a / b;
+    }
+}
+
+// tensor_ops.c:815-833: r = fmod(|x|, 2pi); pos = r * 4096 / 2pi; lerp.
+__device__ __forceinline__ double lut_cos(double x, const double* __restrict__ T) {
+    const double two_pi = 2.0 * 3.141592653589793238462643383279502884197;
+    const double r = fmod(fabs(x), two_pi);
+    if (r != r) return r;                              // NaN / inf input
+    const double pos = r * 4096.0 / two_pi;
+    int k = (int)pos;
+    double w = pos - (double)k;
+    if (k >= 4096) { k = 4095; w = 0.0; }
+    return T[k] * (1.0 - w) + T[k + 1] * w;
+}
+
+__device__ __forceinline__ float abs_f32(float v) {
+    uint32_t u = f2u(v) & 0x7FFFFFFFu;
+    if (u > 0x7F800000u) u |= 0x00400000u;            // fabs through double quiets NaN
+    return u2f(u);
+}
+
+template <int U> __device__ __forceinline__ float unary_f32(float v, const double* T) {
+    if constexpr (U == U_RELU) return v > 0.0f ? v : 0.0f;
+    else if constexpr (U == U_ABS) return abs_f32(v);
+    else return (float)lut_cos((double)v, T);
+}
+
+// ---------------------------------------------------------------- unary ---
+template <int U>
+__global__ __launch_bounds__(kBlock) void k_unary_f32(const float* __restrict__ X, float* __restrict__ Y,
+                                                      size_t n, const double* __restrict__ T) {
+    const size_t nv = n / 4;
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    for (size_t v = (size_t)blockIdx.x * kBlock + threadIdx.x; v < nv; v += stride) {
+        float4 x = reinterpret_cast<const float4*>(X)[v];
+        float4 y;
+        y.x = unary_f32<U>(x.x, T);
+        y.y = unary_f32<U>(x.y, T);
+        y.z = unary_f32<U>(x.z, T);
+        y.w = unary_f32<U>(x.w, T);
+        reinterpret_cast<float4*>(Y)[v] = y;
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+        const size_t i = nv * 4 + threadIdx.x;
+        Y[i] = unary_f32<U>(X[i], T);
+    }
+}
+
+// Any dtypes: tensor_ops.c:708-757 (int input -> int64 path), :840-854 (cos, double path).
+template <int U>
+__global__ __launch_bounds__(kBlock) void k_unary_rt(const void* __restrict__ X, int dtx, void* __restrict__ Y,
+                                                     int dty, size_t n, const double* __restrict__ T) {
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    const bool int_in = (U != U_COS) && dt_is_int(dtx);
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        if (int_in) {
+            const int64_t v = ld_i_rt(dtx, X, (int64_t)i);
+            int64_t r;
+            if constexpr (U == U_RELU) r = v > 0 ? v : 0;
+            else r = v == INT64_MIN ? INT64_MAX : (v < 0 ? -v : v);
+            st_i_rt(dty, Y, (int64_t)i, r);
+        } else {
+            const double v = ld_d_rt(dtx, X, (int64_t)i);
+            double r;
+            if constexpr (U == U_RELU) r = v > 0 ? v : 0.0;
+            else if constexpr (U == U_ABS) r = fabs(v);
+            else r = lut_cos(v, T);
+            st_d_rt(dty, Y, (int64_t)i, r);
+        }
+    }
+}
+
+// --------------------------------------------------------------- binary ---
+template <int ND>
+__device__ __forceinline__ float4 load4(const float* __restrict__ p, int64_t off, int64_t st) {
+    if (st == 1) return *reinterpret_cast<const float4*>(p + off);
+    if (st == 0) { const float v = p[off]; return make_float4(v, v, v, v); }
+    return make_float4(p[off], p[off + st], p[off + 2 * st], p[off + 3 * st]);
+}
+
+// f32 x f32 -> f32, vectorised; requires dim[nd-1] % 4 == 0 and 16-byte aligned bases.
+template <int OP, int ND>
+__global__ __launch_bounds__(kBlock) void k_bin_f32_v4(const float* __restrict__ A, const float* __restrict__ B,
+                                                       float* __restrict__ O, BDesc d, uint32_t nv) {
+    const int64_t sa = d.st[0][d.nd - 1], sb = d.st[1][d.nd - 1];
+    const uint32_t stride = gridDim.x * kBlock;
+    for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nv; v += stride) {
+        int64_t off[2];
+        bd_offsets32<2, ND>(d, v * 4u, off);
+        const float4 a = load4<ND>(A, off[0], sa);
+        const float4 b = load4<ND>(B, off[1], sb);
+        float4 o;
+        o.x = fop<OP>(a.x, b.x);
+        o.y = fop<OP>(a.y, b.y);
+        o.z = fop<OP>(a.z, b.z);
+        o.w = fop<OP>(a.w, b.w);
+        reinterpret_cast<float4*>(O)[v] = o;
+    }
+}
+
+// f32 x f32 -> f32, one element per thread (any broadcast pattern).
+template <int OP, int ND>
+__global__ __launch_bounds__(kBlock) void k_bin_f32_s(const float* __restrict__ A, const float* __restrict__ B,
+                                                      float* __restrict__ O, BDesc d, uint32_t n) {
+    const uint32_t stride = gridDim.x * kBlock;
+    for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        int64_t off[2];
+        bd_offsets32<2, ND>(d, i, off);
+        O[i] = fop<OP>(A[off[0]], B[off[1]]);
+    }
+}
+
+// Typed fp64 path for the hot mixed combinations (e.g. int32 + f32 -> f64 / f32).
+template <int OP, int DA, int DB, int DO, int ND>
+__global__ __launch_bounds__(kBlock) void k_bin_typed(const void* __restrict__ A, const void* __restrict__ B,
+                                                      void* __restrict__ O, BDesc d, uint32_t n) {
+    const uint32_t stride = gridDim.x * kBlock;
+    for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        int64_t off[2];
+        bd_offsets32<2, ND>(d, i, off);
+        st_d<DO>(O, (int64_t)i, dop<OP>(ld_d<DA>(A, off[0]), ld_d<DB>(B, off[1])));
+    }
+}
+
+// Any dtypes (runtime switch); 64-bit indexing.
+template <int OP, bool INTOUT>
+__global__ __launch_bounds__(kBlock) void k_bin_rt(const void* __restrict__ A, int dta, const void* __restrict__ B,
+                                                   int dtb, void* __restrict__ O, int dto, BDesc d, size_t n) {
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        int64_t off[2];
+        if (n <= 0xFFFFFFFFull) bd_offsets32<2, 0>(d, (uint32_t)i, off);
+        else bd_offsets64<2>(d, (int64_t)i, off);
+        if constexpr (INTOUT) {
+            st_i_rt(dto, O, (int64_t)i, iop<OP>(ld_i_rt(dta, A, off[0]), ld_i_rt(dtb, B, off[1])));
+        } else {
+            st_d_rt(dto, O, (int64_t)i, dop<OP>(ld_d_rt(dta, A, off[0]), ld_d_rt(dtb, B, off[1])));
+        }
+    }
+}
+
+#define ND_SWITCH(nd, ...)                              \
+    switch (nd) {                                       \
+    case 1: { constexpr int ND = 1; __VA_ARGS__; } break; \
+    case 2: { constexpr int ND = 2; __VA_ARGS__; } break; \
+    case 3: { constexpr int ND = 3; __VA_ARGS__; } break; \
+    case 4: { constexpr int ND = 4; __VA_ARGS__; } break; \
+    default: { constexpr int ND = 0; __VA_ARGS__; } break; \
+    }
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <int OP>
+bool launch_binary(const void* A, int dta, const void* B, int dtb, void* O, int dto, const BDesc& d, size_t n) {
+    hipStream_t s = stream();
+    if (n == 0) return true;
+    const bool small = n < (size_t(1) << 31);   // 32-bit loop counters cannot wrap
+    if (dt_is_int(dto)) {
+        hipLaunchKernelGGL((k_bin_rt<OP, true>), dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, A, dta, B, dtb, O,
+                           dto, d, n);
+        return check_launch("binary (int)");
+    }
+    if (small && dta == kF32 && dtb == kF32 && dto == kF32) {
+        const float* a = (const float*)A;
+        const float* b = (const float*)B;
+        float* o = (float*)O;
+        const bool v4 = (d.dim[d.nd - 1] % 4u == 0) && aligned16(a) && aligned16(b) && aligned16(o);
+        if (v4) {
+            const uint32_t nv = (uint32_t)(n / 4);
+            ND_SWITCH(d.nd, hipLaunchKernelGGL((k_bin_f32_v4<OP, ND>), dim3(grid_for(nv, kBlock)), dim3(kBlock), 0, s,
+                                               a, b, o, d, nv));
+        } else {
+            ND_SWITCH(d.nd, hipLaunchKernelGGL((k_bin_f32_s<OP, ND>), dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s,
+                                               a, b, o, d, (uint32_t)n));
+        }
+        return check_launch("binary f32");
+    }
+    if (small && dta == kI32 && dtb == kF32 && (dto == kF64 || dto == kF32)) {
+        const uint32_t nn = (uint32_t)n;
+        if (dto == kF64) {
+            ND_SWITCH(d.nd, hipLaunchKernelGGL((k_bin_typed<OP, kI32, kF32, kF64, ND>), dim3(grid_for(n, kBlock)),
+                                               dim3(kBlock), 0, s, A, B, O, d, nn));
+        } else {
+            ND_SWITCH(d.nd, hipLaunchKernelGGL((k_bin_typed<OP, kI32, kF32, kF32, ND>), dim3(grid_for(n, kBlock)),
+                                               dim3(kBlock), 0, s, A, B, O, d, nn));
+        }
+        return check_launch("binary i32/f32");
+    }
+    hipLaunchKernelGGL((k_bin_rt<OP, false>), dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, A, dta, B, dtb, O, dto,
+                       d, n);
+    return check_launch("binary");
+}
+
+template <int OP>
+void binary_entry(const char* name, const Tensor* A, const Tensor* B, Tensor* O) {
+    if (!tensor_sane(A, name) || !tensor_sane(B, name) || !tensor_sane(O, name)) return;
+    if (!ensure_device()) return;
+    BDesc d;
+    const Tensor* ops[2] = {A, B};
+    // Equal sizes index flat (the reference); otherwise numpy broadcasting to
+    // O's shape (the reference returns there; its Python caller broadcasts first).
+    if (!make_bdesc_for(d, O, ops, 2)) return;
+    Staging st;
+    const void* a = st.in(A);
+    const void* b = st.in(B);
+    void* o = st.out(O, tensor_bytes(O));
+    if (!a || !b || !o) { st.finish(); return; }
+    if (!launch_binary<OP>(a, (int)A->dtype, b, (int)B->dtype, o, (int)O->dtype, d, O->size)) {
+        st.finish();
+        return;
+    }
+    st.finish();
+}
+
+template <int U>
+void unary_entry(const char* name, const Tensor* X, Tensor* Y) {
+    if (!tensor_sane(X, name) || !tensor_sane(Y, name)) return;
+    if (X->size != Y->size) { set_error("%s: input and output sizes differ", name); return; }
+    if (!ensure_device()) return;
+    const double* T = nullptr;
+    if (U == U_COS && !(T = device_cos_lut())) return;
+    Staging st;
+    const void* x = st.in(X);
+    void* y = st.out(Y, tensor_bytes(Y));
+    if (!x || !y) { st.finish(); return; }
+    const size_t n = X->size;
+    hipStream_t s = stream();
+    if (n) {
+        if (X->dtype == DTYPE_FLOAT32 && Y->dtype == DTYPE_FLOAT32 && aligned16(x) && aligned16(y)) {
+            hipLaunchKernelGGL((k_unary_f32<U>), dim3(grid_for(n / 4 + 1, kBlock)), dim3(kBlock), 0, s,
+                               (const float*)x, (float*)y, n, T);
+        } else {
+            hipLaunchKernelGGL((k_unary_rt<U>), dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, x, (int)X->dtype, y,
+                               (int)Y->dtype, n, T);
+        }
+        if (!check_launch(name)) { st.finish(); return; }
+    }
+    st.finish();
+}
+
+}  // namespace
+}  // namespace tohip
+
+using namespace tohip;
+
+extern "C" {
+void relu_forward(const Tensor* input, Tensor* output) { unary_entry<U_RELU>("relu_forward", input, output); }
+void abs_forward(const Tensor* input, Tensor* output) { unary_entry<U_ABS>("abs_forward", input, output); }
+void cos_forward(const Tensor* input, Tensor* output) { unary_entry<U_COS>("cos_forward", input, output); }
+void add_forward(const Tensor* A, const Tensor* B, Tensor* O) { binary_entry<OP_ADD>("add_forward", A, B, O); }
+void sub_forward(const Tensor* A, const Tensor* B, Tensor* O) { binary_entry<OP_SUB>("sub_forward", A, B, O); }
+void mul_forward(const Tensor* A, const Tensor* B, Tensor* O) { binary_entry<OP_MUL>("mul_forward", A, B, O); }
+void div_forward(const Tensor* A, const Tensor* B, Tensor* O) { binary_entry<OP_DIV>("div_forward", A, B, O); }
+}

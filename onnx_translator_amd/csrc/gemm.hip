@@ -1,0 +1,463 @@
+// gemm.hip — Gemm (Y = alpha * A' B' + beta * C) for gfx950.
+//
+// tensor_ops/tensor_ops.c:1167-1228 accumulates sum_k A'[m,k] B'[k,n] in
+// double, sequentially in k, then adds beta * C with the reference's bias
+// broadcast rules and writes through the output encoder.  Three kernels:
+//
+//  * k_gemm_mfma_f32 — v_mfma_f32_32x32x2f32 (fp32 operands, fp32 accumulate).
+//    Operands of any dtype exactly representable in fp32 (f32, f16, bf16,
+//    fp8, int4/8/16, uint8) are decoded while staging into LDS.
+//    128x128 block tile, 4 waves (2x2), each wave 64x64 = 2x2 MFMA tiles,
+//    BK = 16, LDS double buffer.  Tolerance class vs the reference.
+//  * k_gemm_mfma_f16 — v_mfma_f32_32x32x16_f16 for f16 x f16 (gfx950 K=16
+//    form), fp32 accumulate; same tiling with BK = 32.
+//  * k_gemm_exact — fp64, sequential k, no contraction: bit-identical to the
+//    reference for every dtype combination.  Used for f64 / int32 / int64
+//    operands and when exact mode is on.
+// The epilogue is shared: alpha * acc + beta * bias in double, then st_d.
+#include "runtime.h"
+
+namespace tohip {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+
+struct Bias {
+    const void* p;
+    int dt;
+    int mode;   // 0 none, 1 scalar, 2 per column (n), 3 per row (m), 4 two-d (H, W broadcast)
+    int H, W;
+};
+
+__device__ __forceinline__ double bias_at(const Bias& c, int m, int n) {
+    switch (c.mode) {
+    case 1: return ld_d_rt(c.dt, c.p, 0);
+    case 2: return ld_d_rt(c.dt, c.p, n);
+    case 3: return ld_d_rt(c.dt, c.p, m);
+    case 4: {
+        const int r = c.H == 1 ? 0 : m, q = c.W == 1 ? 0 : n;
+        return (r < c.H && q < c.W) ? ld_d_rt(c.dt, c.p, (int64_t)r * c.W + q) : 0.0;
+    }
+    default: return 0.0;
+    }
+}
+
+struct GemmArgs {
+    const void* A;
+    const void* B;
+    void* Y;
+    int M, N, K;
+    int lda, ldb;   // row lengths of A and B as stored (A->shape[1], B->shape[1])
+    double alpha, beta;
+    Bias c;
+    int dty;
+};
+
+// Any output dtype / bias dtype: kept out of line so the unrolled MFMA
+// epilogues stay small.
+__device__ __noinline__ void store_rt(const GemmArgs& g, int m, int n, double acc) {
+    double r = g.alpha * acc;
+    if (g.c.mode) r += g.beta * bias_at(g.c, m, n);
+    st_d_rt(g.dty, g.Y, (int64_t)m * g.N + n, r);
+}
+
+// YDT >= 0: output dtype known at compile time; f32 bias (scalar / per
+// column / per row) is handled inline, anything else goes through store_rt.
+template <int YDT>
+__device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, double acc) {
+    if (m >= g.M || n >= g.N) return;
+    if constexpr (YDT >= 0) {
+        if (g.c.mode == 0 || (g.c.dt == kF32 && g.c.mode <= 3)) {
+            double r = g.alpha * acc;
+            if (g.c.mode) {
+                const float* c = (const float*)g.c.p;
+                r += g.beta * (double)c[g.c.mode == 1 ? 0 : (g.c.mode == 2 ? n : m)];
+            }
+            st_d<YDT>(g.Y, (int64_t)m * g.N + n, r);
+            return;
+        }
+    }
+    store_rt(g, m, n, acc);
+}
+
+// ------------------------------------------------------------------- exact ---
+constexpr int kET = 16;
+
+__global__ __launch_bounds__(kET * kET) void k_gemm_exact(GemmArgs g, int dta, int dtb, int ta, int tb) {
+    __shared__ double As[kET][kET + 1];
+    __shared__ double Bs[kET][kET + 1];
+    const int tx = threadIdx.x % kET, ty = threadIdx.x / kET;
+    const int m = blockIdx.y * kET + ty, n = blockIdx.x * kET + tx;
+    double acc = 0.0;
+    for (int k0 = 0; k0 < g.K; k0 += kET) {
+        {
+            const int mm = blockIdx.y * kET + ty, kk = k0 + tx;
+            double v = 0.0;
+            if (mm < g.M && kk < g.K)
+                v = ld_d_rt(dta, g.A, ta ? (int64_t)kk * g.lda + mm : (int64_t)mm * g.lda + kk);
+            As[ty][tx] = v;
+            const int nn = blockIdx.x * kET + tx, kb = k0 + ty;
+            double w = 0.0;
+            if (nn < g.N && kb < g.K)
+                w = ld_d_rt(dtb, g.B, tb ? (int64_t)nn * g.ldb + kb : (int64_t)kb * g.ldb + nn);
+            Bs[ty][tx] = w;
+        }
+        __syncthreads();
+        const int kend = min(kET, g.K - k0);
+        for (int kk = 0; kk < kend; kk++) acc += As[ty][kk] * Bs[kk][tx];
+        __syncthreads();
+    }
+    epilogue_store<-1>(g, m, n, acc);
+}
+
+// ------------------------------------------------------------------- f32 MFMA ---
+constexpr int kBM = 128, kBN = 128, kBK = 16, kThreads = 256;
+constexpr int kPad = 4;
+
+// DT >= 0: compile-time dtype; DT < 0: decode with the run-time dtype rdt.
+template <int DT> __device__ __forceinline__ float ldf(const void* p, int64_t i, int rdt) {
+    if constexpr (DT == kF32) return ((const float*)p)[i];
+    else if constexpr (DT >= 0) return (float)ld_d<DT>(p, i);
+    else return (float)ld_d_rt(rdt, p, i);
+}
+
+// Stage a BK x 128 slice of an operand into LDS laid out [k][row] (row = m or n).
+// KMAJOR: operand stored with k contiguous (A with transA=0, B with transB=1).
+template <int DT, bool KMAJOR>
+__device__ __forceinline__ void stage_f32(float (*dst)[kBM + kPad], const void* src, int ld, int rows, int K,
+                                          int row0, int k0, int rdt) {
+    const int t = threadIdx.x;
+    if constexpr (KMAJOR) {
+        // 128 rows x 16 k: thread handles 8 consecutive k of one row (2 threads per row).
+        const int r = t >> 1, kq = (t & 1) * 8;
+        const int gr = row0 + r;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int gk = k0 + kq + e;
+            dst[kq + e][r] = (gr < rows && gk < K) ? ldf<DT>(src, (int64_t)gr * ld + gk, rdt) : 0.0f;
+        }
+    } else {
+        // 16 k x 128 rows, rows contiguous: thread handles 8 consecutive rows of one k.
+        const int kk = t >> 4, rq = (t & 15) * 8;
+        const int gk = k0 + kk;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int gr = row0 + rq + e;
+            dst[kk][rq + e] = (gr < rows && gk < K) ? ldf<DT>(src, (int64_t)gk * ld + gr, rdt) : 0.0f;
+        }
+    }
+}
+
+// Vectorised staging for f32 operands when the leading dimension allows
+// 16-byte loads (ld % 4 == 0, base 16-byte aligned).
+template <bool KMAJOR>
+__device__ __forceinline__ void stage_f32_vec(float (*dst)[kBM + kPad], const float* src, int ld, int rows, int K,
+                                              int row0, int k0) {
+    const int t = threadIdx.x;
+    if constexpr (KMAJOR) {
+        const int r = t >> 1, kq = (t & 1) * 8;
+        const int gr = row0 + r;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int gk = k0 + kq + 4 * h;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (gr < rows) {
+                if (gk + 3 < K) v = *reinterpret_cast<const float4*>(src + (int64_t)gr * ld + gk);
+                else {
+                    const float* p = src + (int64_t)gr * ld;
+                    v.x = gk < K ? p[gk] : 0.f;
+                    v.y = gk + 1 < K ? p[gk + 1] : 0.f;
+                    v.z = gk + 2 < K ? p[gk + 2] : 0.f;
+                }
+            }
+            dst[kq + 4 * h][r] = v.x;
+            dst[kq + 4 * h + 1][r] = v.y;
+            dst[kq + 4 * h + 2][r] = v.z;
+            dst[kq + 4 * h + 3][r] = v.w;
+        }
+    } else {
+        const int kk = t >> 4, rq = (t & 15) * 8;
+        const int gk = k0 + kk;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int gr = row0 + rq + 4 * h;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (gk < K) {
+                const float* p = src + (int64_t)gk * ld;
+                if (gr + 3 < rows) v = *reinterpret_cast<const float4*>(p + gr);
+                else {
+                    v.x = gr < rows ? p[gr] : 0.f;
+                    v.y = gr + 1 < rows ? p[gr + 1] : 0.f;
+                    v.z = gr + 2 < rows ? p[gr + 2] : 0.f;
+                }
+            }
+            *reinterpret_cast<float4*>(&dst[kk][rq + 4 * h]) = v;
+        }
+    }
+}
+
+// DA / DB: kF32, or -1 for operands decoded with the run-time dtypes dta / dtb.
+template <int DA, int DB, bool TA, bool TB, bool VEC, int YDT>
+__global__ __launch_bounds__(kThreads) void k_gemm_mfma_f32(GemmArgs g, int dta, int dtb) {
+    __shared__ float As[2][kBK][kBM + kPad];
+    __shared__ float Bs[2][kBK][kBN + kPad];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    auto stage = [&](int buf, int k0) {
+        if constexpr (VEC && DA == kF32) stage_f32_vec<!TA>(As[buf], (const float*)g.A, g.lda, g.M, g.K, m0, k0);
+        else stage_f32<DA, !TA>(As[buf], g.A, g.lda, g.M, g.K, m0, k0, dta);
+        if constexpr (VEC && DB == kF32) stage_f32_vec<TB>(Bs[buf], (const float*)g.B, g.ldb, g.N, g.K, n0, k0);
+        else stage_f32<DB, TB>(Bs[buf], g.B, g.ldb, g.N, g.K, n0, k0, dtb);
+    };
+
+    const int nk = (g.K + kBK - 1) / kBK;
+    stage(0, 0);
+    __syncthreads();
+    const int lr = lane & 31, lk = lane >> 5;
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) stage(cur ^ 1, (kt + 1) * kBK);
+#pragma unroll
+        for (int ks = 0; ks < kBK; ks += 2) {
+            float a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) a[i] = As[cur][ks + lk][wm * 64 + i * 32 + lr];
+#pragma unroll
+            for (int j = 0; j < 2; j++) b[j] = Bs[cur][ks + lk][wn * 64 + j * 32 + lr];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    // D[m][n]: n = lane % 32, m = 8 * (r / 4) + 4 * (lane / 32) + r % 4 within the 32x32 tile.
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+                const int n = n0 + wn * 64 + j * 32 + lr;
+                epilogue_store<YDT>(g, m, n, (double)acc[i][j][r]);
+            }
+}
+
+// ------------------------------------------------------------------- f16 MFMA ---
+constexpr int kHBK = 32, kHPad = 8;   // row stride 40 halves = 80 bytes
+
+// Stage a 128-row x 32-k slice of an f16 operand into LDS laid out [row][k].
+template <bool KMAJOR>
+__device__ __forceinline__ void stage_f16(_Float16 (*dst)[kHBK + kHPad], const uint16_t* src, int ld, int rows, int K,
+                                          int row0, int k0, bool vec) {
+    const int t = threadIdx.x;
+    if constexpr (KMAJOR) {
+        // 128 rows x 32 k = 512 chunks of 8 halves; 2 chunks per thread.
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int c = t + h * kThreads;
+            const int r = c >> 2, kq = (c & 3) * 8;
+            const int gr = row0 + r, gk = k0 + kq;
+            halfx8 v;
+            if (vec && gr < rows && gk + 7 < K) {
+                v = *reinterpret_cast<const halfx8*>(src + (int64_t)gr * ld + gk);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    v[e] = (gr < rows && gk + e < K) ? __builtin_bit_cast(_Float16, src[(int64_t)gr * ld + gk + e])
+                                                      : (_Float16)0.0f;
+            }
+            *reinterpret_cast<halfx8*>(&dst[r][kq]) = v;
+        }
+    } else {
+        // stored [k][row]: 32 k x 128 rows, thread reads 8 consecutive rows of 2 k values.
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int c = t + h * kThreads;
+            const int kk = c >> 4, rq = (c & 15) * 8;
+            const int gk = k0 + kk;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int gr = row0 + rq + e;
+                dst[rq + e][kk] = (gr < rows && gk < K) ? __builtin_bit_cast(_Float16, src[(int64_t)gk * ld + gr])
+                                                         : (_Float16)0.0f;
+            }
+        }
+    }
+}
+
+template <bool TA, bool TB, int YDT>
+__global__ __launch_bounds__(kThreads) void k_gemm_mfma_f16(GemmArgs g, int vec) {
+    __shared__ _Float16 As[2][kBM][kHBK + kHPad];
+    __shared__ _Float16 Bs[2][kBN][kHBK + kHPad];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    const uint16_t* A = (const uint16_t*)g.A;
+    const uint16_t* B = (const uint16_t*)g.B;
+    auto stage = [&](int buf, int k0) {
+        stage_f16<!TA>(As[buf], A, g.lda, g.M, g.K, m0, k0, vec != 0);
+        stage_f16<TB>(Bs[buf], B, g.ldb, g.N, g.K, n0, k0, vec != 0);
+    };
+    const int nk = (g.K + kHBK - 1) / kHBK;
+    stage(0, 0);
+    __syncthreads();
+    const int lr = lane & 31, lk = (lane >> 5) * 8;
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) stage(cur ^ 1, (kt + 1) * kHBK);
+#pragma unroll
+        for (int ks = 0; ks < kHBK; ks += 16) {
+            halfx8 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) a[i] = *reinterpret_cast<const halfx8*>(&As[cur][wm * 64 + i * 32 + lr][ks + lk]);
+#pragma unroll
+            for (int j = 0; j < 2; j++) b[j] = *reinterpret_cast<const halfx8*>(&Bs[cur][wn * 64 + j * 32 + lr][ks + lk]);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + (lk >> 1) + (r & 3);
+                const int n = n0 + wn * 64 + j * 32 + lr;
+                epilogue_store<YDT>(g, m, n, (double)acc[i][j][r]);
+            }
+}
+
+// -------------------------------------------------------------------- dispatch ---
+inline bool f32_exact_dtype(int dt) {
+    return dt == kF32 || dt == kF16 || dt == kBF16 || dt == kE4M3 || dt == kE5M2 || dt == kI4 || dt == kI8 ||
+           dt == kU8 || dt == kI16;
+}
+
+template <int DA, int DB, bool TA, bool TB, bool VEC>
+void launch_f32_y(const GemmArgs& g, int dta, int dtb, dim3 grid, hipStream_t s) {
+    if (g.dty == kF32)
+        hipLaunchKernelGGL((k_gemm_mfma_f32<DA, DB, TA, TB, VEC, kF32>), grid, dim3(kThreads), 0, s, g, dta, dtb);
+    else
+        hipLaunchKernelGGL((k_gemm_mfma_f32<DA, DB, TA, TB, VEC, -1>), grid, dim3(kThreads), 0, s, g, dta, dtb);
+}
+
+template <int DA, int DB, bool VEC>
+void launch_f32_t(const GemmArgs& g, int dta, int dtb, int ta, int tb, dim3 grid, hipStream_t s) {
+    if (!ta && tb) launch_f32_y<DA, DB, false, true, VEC>(g, dta, dtb, grid, s);
+    else if (!ta && !tb) launch_f32_y<DA, DB, false, false, VEC>(g, dta, dtb, grid, s);
+    else if (ta && tb) launch_f32_y<DA, DB, true, true, VEC>(g, dta, dtb, grid, s);
+    else launch_f32_y<DA, DB, true, false, VEC>(g, dta, dtb, grid, s);
+}
+
+template <bool TA, bool TB>
+void launch_f16_y(const GemmArgs& g, dim3 grid, int vec, hipStream_t s) {
+    if (g.dty == kF16) hipLaunchKernelGGL((k_gemm_mfma_f16<TA, TB, kF16>), grid, dim3(kThreads), 0, s, g, vec);
+    else if (g.dty == kF32) hipLaunchKernelGGL((k_gemm_mfma_f16<TA, TB, kF32>), grid, dim3(kThreads), 0, s, g, vec);
+    else hipLaunchKernelGGL((k_gemm_mfma_f16<TA, TB, -1>), grid, dim3(kThreads), 0, s, g, vec);
+}
+
+// f32 x f32 uses typed (optionally vectorised) staging; every other pair of
+// fp32-exact dtypes is decoded with a run-time switch while staging.
+bool launch_f32_mfma(const GemmArgs& g, int dta, int dtb, int ta, int tb, hipStream_t s) {
+    const dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
+    if (dta == kF32 && dtb == kF32) {
+        const bool vec = ((g.lda % 4) == 0) && ((g.ldb % 4) == 0) && (((uintptr_t)g.A & 15) == 0) &&
+                         (((uintptr_t)g.B & 15) == 0);
+        if (vec) launch_f32_t<kF32, kF32, true>(g, dta, dtb, ta, tb, grid, s);
+        else launch_f32_t<kF32, kF32, false>(g, dta, dtb, ta, tb, grid, s);
+    } else {
+        launch_f32_t<-1, -1, false>(g, dta, dtb, ta, tb, grid, s);
+    }
+    return true;
+}
+
+}  // namespace
+}  // namespace tohip
+
+using namespace tohip;
+
+extern "C" void gemm_forward(const Tensor* A, const Tensor* B, const Tensor* C, Tensor* Y, float alpha, float beta,
+                             int transA, int transB) {
+    const char* name = "gemm_forward";
+    if (!tensor_sane(A, name) || !tensor_sane(B, name) || !tensor_sane(Y, name)) return;
+    if (A->ndim < 2 || B->ndim < 2) { set_error("%s: A and B must be 2-D", name); return; }
+    const int M = transA ? A->shape[1] : A->shape[0];
+    const int K = transA ? A->shape[0] : A->shape[1];
+    const int N = transB ? B->shape[0] : B->shape[1];
+    const int KB = transB ? B->shape[1] : B->shape[0];
+    if (K != KB) { set_error("%s: inner dimensions differ (%d vs %d)", name, K, KB); return; }
+    if ((size_t)M * (size_t)N > Y->size) { set_error("%s: Y holds %zu elements, needs %d x %d", name, Y->size, M, N); return; }
+    const bool has_c = C && C->data;
+    if (has_c && !tensor_sane(C, name)) return;
+    if (!ensure_device()) return;
+
+    GemmArgs g;
+    g.M = M; g.N = N; g.K = K;
+    g.lda = A->shape[1]; g.ldb = B->shape[1];
+    g.alpha = (double)alpha; g.beta = (double)beta;
+    g.dty = (int)Y->dtype;
+    g.c = Bias{nullptr, has_c ? (int)C->dtype : 0, 0, 0, 0};
+    if (has_c) {
+        // tensor_ops.c:1197-1220
+        if (C->size == 1) g.c.mode = 1;
+        else if (C->ndim == 1) g.c.mode = (C->shape[0] == N) ? 2 : (C->shape[0] == M ? 3 : 0);
+        else if (C->ndim >= 2) { g.c.mode = 4; g.c.H = C->shape[C->ndim - 2]; g.c.W = C->shape[C->ndim - 1]; }
+    }
+    Staging st;
+    g.A = st.in(A);
+    g.B = st.in(B);
+    if (has_c) g.c.p = st.in(C);
+    g.Y = st.out(Y, (size_t)M * N * dt_bytes((int)Y->dtype));
+    if (!g.A || !g.B || !g.Y || (has_c && !g.c.p)) { st.finish(); return; }
+    if (!has_c) g.c.mode = 0;
+    hipStream_t s = stream();
+    const int dta = (int)A->dtype, dtb = (int)B->dtype;
+    if ((size_t)M * N > 0) {
+        bool done = false;
+        if (!exact_mode() && K > 0) {
+            if (dta == kF16 && dtb == kF16) {
+                const dim3 grid((N + kBN - 1) / kBN, (M + kBM - 1) / kBM);
+                const int vec = ((g.lda % 8) == 0 && (g.ldb % 8) == 0 && ((uintptr_t)g.A & 15) == 0 &&
+                                 ((uintptr_t)g.B & 15) == 0) ? 1 : 0;
+                if (!transA && transB) launch_f16_y<false, true>(g, grid, vec, s);
+                else if (!transA && !transB) launch_f16_y<false, false>(g, grid, vec, s);
+                else if (transA && transB) launch_f16_y<true, true>(g, grid, vec, s);
+                else launch_f16_y<true, false>(g, grid, vec, s);
+                done = true;
+            } else if (f32_exact_dtype(dta) && f32_exact_dtype(dtb)) {
+                done = launch_f32_mfma(g, dta, dtb, transA, transB, s);
+            }
+        }
+        if (!done) {
+            const dim3 grid((N + kET - 1) / kET, (M + kET - 1) / kET);
+            hipLaunchKernelGGL(k_gemm_exact, grid, dim3(kET * kET), 0, s, g, dta, dtb, transA, transB);
+        }
+        if (!check_launch(name)) { st.finish(); return; }
+    }
+    st.finish();
+}

@@ -1,0 +1,85 @@
+// runtime.h — host runtime of libtensor_ops_hip.so: device/stream state,
+// memory registry and caching pools, error reporting, and the staging helper
+// that lets one operator entry point serve host tensors (reference
+// semantics: synchronous, host-addressable data) and device tensors
+// (asynchronous, HBM-resident) alike.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+#include "../../include/tensor_ops.h"
+#include "common.h"
+
+namespace tohip {
+
+// ---- errors ---------------------------------------------------------------
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+bool check_hip(hipError_t e, const char* what);   // false (and error set) on failure
+
+// ---- device / stream --------------------------------------------------------
+bool ensure_device();            // lazily initialises; false + error when no GPU
+hipStream_t stream();            // current library stream
+int device_count();
+bool exact_mode();
+const double* device_cos_lut();  // 4097 doubles in device memory (after init_cos_lut)
+int num_cus();
+
+// ---- memory -----------------------------------------------------------------
+enum class Mem { kHostPinned, kHostMalloc, kDevOwned, kDevBorrowed, kHostForeign, kDevForeign };
+Mem classify(const void* p);     // registry first, then hipPointerGetAttributes
+inline bool is_dev(Mem m) { return m == Mem::kDevOwned || m == Mem::kDevBorrowed || m == Mem::kDevForeign; }
+
+void* pool_alloc(size_t bytes);  // device memory from the caching pool
+void pool_free(void* p);
+
+size_t tensor_bytes(const Tensor* t);
+bool tensor_sane(const Tensor* t, const char* what);   // non-null, valid dtype, data present
+
+// ---- launch shape -------------------------------------------------------------
+inline unsigned grid_for(size_t work_items, unsigned block, unsigned max_blocks = 1u << 20) {
+    size_t g = (work_items + block - 1) / block;
+    if (g < 1) g = 1;
+    if (g > max_blocks) g = max_blocks;
+    return (unsigned)g;
+}
+bool check_launch(const char* kernel);   // reports hipGetLastError after a launch
+
+// ---- broadcast descriptor -------------------------------------------------------
+// Build a collapsed descriptor for `nop` operands against output shape `oshape`.
+// Operand k is broadcast numpy-style (right-aligned; size-1 dims repeat).
+// Returns false if a shape does not broadcast to oshape.
+bool make_bdesc(BDesc& d, const int* oshape, int ond, const Tensor* const* ops, int nop);
+// Flat descriptor (every operand indexed 0..n-1, or stride 0 for size-1 operands).
+void make_flat_bdesc(BDesc& d, size_t n, const Tensor* const* ops, int nop);
+// Descriptor against output Y: operands with Y->size elements index flat (as
+// the reference does, whatever their shape), size-1 operands broadcast, and
+// any other operand broadcasts numpy-style by its own shape.
+bool make_bdesc_for(BDesc& d, const Tensor* Y, const Tensor* const* ops, int nop);
+
+// ---- staging ----------------------------------------------------------------------
+// Resolves each operand to a device pointer.  Host inputs are copied to pool
+// buffers (H2D on the library stream); a host output gets a pool buffer that
+// finish() copies back.  finish() synchronises only if staging happened, so
+// calls on device-resident tensors stay asynchronous.
+class Staging {
+  public:
+    Staging() = default;
+    ~Staging();
+    const void* in(const Tensor* t);               // nullptr on error (error set)
+    void* out(Tensor* t, size_t bytes_written);    // bytes_written: prefix copied back
+    bool finish();                                 // D2H + sync when needed
+    bool staged() const { return staged_; }
+
+  private:
+    struct Buf { void* dev; void* host; size_t bytes; bool writeback; };
+    std::vector<Buf> bufs_;
+    bool staged_ = false;
+    bool failed_ = false;
+};
+
+}  // namespace tohip

@@ -1,0 +1,314 @@
+"""The 13 hot-path operator classes over libtensor_ops_hip.so.
+
+Same class names, constructor signatures and ``forward`` / ``forward_``
+results as the reference (``nn/Operators.py:9-704``):
+``forward`` returns ``{"tensor": Tensor, "parameters": None, "graph": None}``
+and stores it in ``self.parameters["values"]``.  Inputs may be host (numpy)
+or device-resident tensors; see :mod:`onnx_translator_amd.nn`.
+
+Additions: ``QuantizeLinear.forward_`` (absent in the reference),
+``DequantizeLinear(axis=...)`` for per-axis scales (the reference ignores the
+axis and lets numpy align a 1-D scale with the last dimension; ``axis=None``
+keeps that behaviour), and ``MaxPool.forward_`` uses the dilation-aware
+output formula of ``MaxPool.forward``.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import DTYPE_TO_NUMPY, DeviceArray, Ops, Tensor, Tensor_, PT
+
+__all__ = ["CConvParams", "CPoolParams", "CReduceParams", "RELU", "COS", "ABS", "ADD", "SUB", "MUL", "DIV",
+           "QuantizeLinear", "DequantizeLinear", "Conv", "MaxPool", "Gemm", "Softmax"]
+
+
+class CConvParams(ctypes.Structure):
+    """``ConvParams`` (tensor_ops.h:39-44; nn/Operators.py:9-15)."""
+    _fields_ = [("pads", ctypes.POINTER(ctypes.c_int)), ("strides", ctypes.POINTER(ctypes.c_int)),
+                ("dilations", ctypes.POINTER(ctypes.c_int)), ("group", ctypes.c_int)]
+
+
+class CPoolParams(ctypes.Structure):
+    """``PoolParams`` (tensor_ops.h:49-54; nn/Operators.py:17-23)."""
+    _fields_ = [("pads", ctypes.POINTER(ctypes.c_int)), ("strides", ctypes.POINTER(ctypes.c_int)),
+                ("dilations", ctypes.POINTER(ctypes.c_int)), ("kernel_shape", ctypes.POINTER(ctypes.c_int))]
+
+
+class CReduceParams(ctypes.Structure):
+    """``ReduceParams`` (tensor_ops.h:56-60; nn/Operators.py:25-30)."""
+    _fields_ = [("axes", ctypes.POINTER(ctypes.c_int)), ("num_axes", ctypes.c_int), ("keepdims", ctypes.c_int)]
+
+
+def _values(op, t):
+    values = {"tensor": t, "parameters": None, "graph": None}
+    op.parameters = {"values": values}
+    return values
+
+
+def _int_arr(vals):
+    return (ctypes.c_int * len(vals))(*[int(v) for v in vals])
+
+
+def _broadcast_dtype(a, b):
+    """Output dtype of a binary op with no declared dtype (nn/Operators.py:216-230)."""
+    import onnx_translator_amd.nn as nn
+    res = np.result_type(np.dtype(DTYPE_TO_NUMPY[a.dtype]), np.dtype(DTYPE_TO_NUMPY[b.dtype]))
+    if res.type in nn.NUMPY_TO_DTYPE:
+        return nn.NUMPY_TO_DTYPE[res.type]
+    if "float" in str(res):
+        return "float64"
+    if "int" in str(res):
+        return "int64"
+    return "float32"
+
+
+class _Unary(Ops):
+    c_name = ""
+
+    def __init__(self, inputs, outputs, dtype, version="17"):
+        super().__init__(inputs, outputs)
+        self.dtype = dtype
+        self.version = version
+
+    def forward(self, input: Tensor):
+        return _values(self, self._execute_unary(input, self.c_name))
+
+    def forward_(self, input: Tensor_):
+        return _values(self, Tensor_(*input.size, dtype=self.dtype))
+
+
+class RELU(_Unary):
+    """ReLU (nn/Operators.py:32-79 -> tensor_ops.c:708-728)."""
+    c_name = "relu_forward"
+
+
+class COS(_Unary):
+    """Cos via the reference's table lookup (nn/Operators.py:81-128 -> tensor_ops.c:840-854)."""
+    c_name = "cos_forward"
+
+
+class ABS(_Unary):
+    """Abs (nn/Operators.py:130-168 -> tensor_ops.c:736-757)."""
+    c_name = "abs_forward"
+
+
+class _Binary(Ops):
+    c_name = ""
+    label = ""
+
+    def __init__(self, inputs, outputs, dtype, version="17"):
+        super().__init__(inputs, outputs)
+        self.dtype = dtype
+        self.version = version
+
+    def forward(self, *inputs):
+        if len(inputs) != 2:
+            raise ValueError(f"{self.label} operator expects 2 inputs, but got {len(inputs)}")
+        return _values(self, self._execute_binary(inputs[0], inputs[1], self.c_name))
+
+    def forward_(self, *inputs):
+        if len(inputs) != 2:
+            raise ValueError(f"{self.label} operator expects 2 inputs (Tensor_), but got {len(inputs)}")
+        a, b = inputs
+        try:
+            shape = np.broadcast_shapes(tuple(a.size), tuple(b.size))
+        except ValueError:
+            print(f"Error during broadcasting shapes {a.size} and {b.size}")
+            raise
+        return _values(self, Tensor_(*shape, dtype=_broadcast_dtype(a, b)))
+
+
+class ADD(_Binary):
+    """A + B with broadcasting and type promotion (nn/Operators.py:170-240 -> tensor_ops.c:864-890)."""
+    c_name, label = "add_forward", "ADD"
+
+
+class SUB(_Binary):
+    """A - B (nn/Operators.py:242-303 -> tensor_ops.c:900-925)."""
+    c_name, label = "sub_forward", "SUB"
+
+
+class MUL(_Binary):
+    """A * B (nn/Operators.py:305-365 -> tensor_ops.c:935-960)."""
+    c_name, label = "mul_forward", "MUL"
+
+
+class DIV(_Binary):
+    """A / B (nn/Operators.py:367-425 -> tensor_ops.c:970-997)."""
+    c_name, label = "div_forward", "DIV"
+
+
+def _is_1d(t):
+    return len(tuple(t.size)) == 1
+
+
+class QuantizeLinear(Ops):
+    """y = saturate(rint(x / s) + zp) (nn/Operators.py:427-450 -> tensor_ops.c:999-1016)."""
+
+    def __init__(self, inputs, outputs, axis=1, dtype=None, version="17"):
+        super().__init__(inputs, outputs)
+        self.dtype = dtype
+        self.axis = axis
+        self.version = version
+
+    def forward(self, x, y_scale, y_zero_point):
+        nd = len(tuple(x.size))
+        if _is_1d(y_scale) and nd > 1:
+            # nn/Operators.py:439-445 reshapes a 1-D scale onto `axis`; the library's
+            # per-axis entry point does the same without touching the data.
+            axis = self.axis if self.axis >= 0 else self.axis + nd
+            out_dtype = self.dtype if self.dtype else "float32"
+            t = self._run("quantize_linear_axis_forward", [x, y_scale, y_zero_point], tuple(x.size),
+                          out_dtype, ctypes.c_int(axis))
+            return _values(self, t)
+        return _values(self, self._execute_ternary(x, y_scale, y_zero_point, "quantize_linear_forward"))
+
+    def forward_(self, x, y_scale, y_zero_point):
+        return _values(self, Tensor_(*x.size, dtype=self.dtype))
+
+
+class DequantizeLinear(Ops):
+    """y = (x - zp) * s (nn/Operators.py:452-473 -> tensor_ops.c:1018-1034)."""
+
+    def __init__(self, inputs, outputs, dtype=None, version="17", axis=None):
+        super().__init__(inputs, outputs)
+        self.dtype = dtype
+        self.version = version
+        self.axis = axis
+
+    def forward(self, x, x_scale, x_zero_point):
+        nd = len(tuple(x.size))
+        if self.axis is not None and _is_1d(x_scale) and nd > 1:
+            axis = self.axis if self.axis >= 0 else self.axis + nd
+            out_dtype = self.dtype if self.dtype else "float32"
+            t = self._run("dequantize_linear_axis_forward", [x, x_scale, x_zero_point], tuple(x.size),
+                          out_dtype, ctypes.c_int(axis))
+            return _values(self, t)
+        return _values(self, self._execute_ternary(x, x_scale, x_zero_point, "dequantize_linear_forward"))
+
+    def forward_(self, x, x_scale, x_zero_point):
+        try:
+            shape = np.broadcast_shapes(tuple(x.size), tuple(x_scale.size), tuple(x_zero_point.size))
+        except ValueError:
+            shape = tuple(x.size)
+        return _values(self, Tensor_(*shape, dtype=self.dtype))
+
+
+def _pool_out(h, w, pads, strides, dilations, kh, kw):
+    """nn/Operators.py:499-501 and :569-570."""
+    oh = (h + pads[0] + pads[2] - dilations[0] * (kh - 1) - 1) // strides[0] + 1
+    ow = (w + pads[1] + pads[3] - dilations[1] * (kw - 1) - 1) // strides[1] + 1
+    return oh, ow
+
+
+class Conv(Ops):
+    """2-D convolution, NCHW (nn/Operators.py:475-548 -> tensor_ops.c:1036-1114)."""
+
+    def __init__(self, inputs, outputs, pads, strides, dilations, group, dtype, version="17"):
+        super().__init__(inputs, outputs)
+        self.pads, self.strides, self.dilations, self.group = pads, strides, dilations, group
+        self.dtype = dtype
+        self.version = version
+        self.lib.conv2d_forward.argtypes = [PT, PT, PT, PT, ctypes.POINTER(CConvParams)]
+        self.lib.conv2d_forward.restype = None
+
+    def _params(self):
+        keep = [_int_arr(self.pads), _int_arr(self.strides), _int_arr(self.dilations)]
+        p = CConvParams()
+        p.pads, p.strides, p.dilations = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep]
+        p.group = int(self.group)
+        return p, keep
+
+    def forward(self, x: Tensor, w: Tensor, b: Tensor = None):
+        N, _, H, W = x.size
+        M, _, KH, KW = w.size
+        OH, OW = _pool_out(H, W, self.pads, self.strides, self.dilations, KH, KW)
+        p, keep = self._params()
+        t = self._run("conv2d_forward", [x, w, b], (N, M, OH, OW), self.dtype, ctypes.byref(p))
+        del keep
+        return _values(self, t)
+
+    def forward_(self, x: Tensor_, w: Tensor_, b: Tensor_ = None):
+        N, _, H, W = x.size
+        M, _, KH, KW = w.size
+        OH, OW = _pool_out(H, W, self.pads, self.strides, self.dilations, KH, KW)
+        return _values(self, Tensor_(N, M, OH, OW, dtype=self.dtype))
+
+
+class MaxPool(Ops):
+    """2-D max pooling (nn/Operators.py:550-611 -> tensor_ops.c:1116-1165)."""
+
+    def __init__(self, inputs, outputs, kernel_shape, pads, strides, dtype, dilations=[1, 1], version="17"):
+        super().__init__(inputs, outputs)
+        self.kernel_shape, self.pads, self.strides, self.dilations = kernel_shape, pads, strides, dilations
+        self.dtype = dtype
+        self.version = version
+        self.lib.max_pool_forward.argtypes = [PT, PT, ctypes.POINTER(CPoolParams)]
+        self.lib.max_pool_forward.restype = None
+
+    def forward(self, x: Tensor):
+        N, C, H, W = x.size
+        KH, KW = self.kernel_shape
+        OH, OW = _pool_out(H, W, self.pads, self.strides, self.dilations, KH, KW)
+        keep = [_int_arr(self.pads), _int_arr(self.strides), _int_arr(self.dilations), _int_arr(self.kernel_shape)]
+        p = CPoolParams()
+        p.pads, p.strides, p.dilations, p.kernel_shape = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep]
+        t = self._run("max_pool_forward", [x], (N, C, OH, OW), self.dtype, ctypes.byref(p))
+        return _values(self, t)
+
+    def forward_(self, x: Tensor_):
+        N, C, H, W = x.size
+        KH, KW = self.kernel_shape
+        OH, OW = _pool_out(H, W, self.pads, self.strides, self.dilations, KH, KW)
+        return _values(self, Tensor_(N, C, OH, OW, dtype=self.dtype))
+
+
+class Gemm(Ops):
+    """Y = alpha * A' B' + beta * C (nn/Operators.py:613-669 -> tensor_ops.c:1167-1228)."""
+
+    def __init__(self, inputs, outputs, alpha, beta, transA, transB, dtype, version="17"):
+        super().__init__(inputs, outputs)
+        self.alpha, self.beta, self.transA, self.transB = alpha, beta, transA, transB
+        self.dtype = dtype
+        self.lib.gemm_forward.argtypes = [PT, PT, PT, PT, ctypes.c_float, ctypes.c_float, ctypes.c_int, ctypes.c_int]
+        self.lib.gemm_forward.restype = None
+
+    def forward(self, A: Tensor, B: Tensor, C: Tensor = None):
+        M = A.size[0] if self.transA == 0 else A.size[1]
+        N = B.size[1] if self.transB == 0 else B.size[0]
+        if C is not None and not isinstance(C.data, DeviceArray) and np.asarray(C.data).ndim == 1:
+            # nn/Operators.py:638-645 (the library reads a 1-D C the same way)
+            c = np.asarray(C.data)
+            if c.shape[0] == N:
+                c = c.reshape(1, -1)
+            elif c.shape[0] == M:
+                c = c.reshape(-1, 1)
+            C = Tensor(*c.shape, dtype=C.dtype, data=np.ascontiguousarray(c))
+        t = self._run("gemm_forward", [A, B, C], (M, N), self.dtype, ctypes.c_float(self.alpha),
+                      ctypes.c_float(self.beta), ctypes.c_int(self.transA), ctypes.c_int(self.transB))
+        return _values(self, t)
+
+    def forward_(self, A: Tensor_, B: Tensor_, C: Tensor_ = None):
+        M = A.size[0] if self.transA == 0 else A.size[1]
+        N = B.size[1] if self.transB == 0 else B.size[0]
+        return _values(self, Tensor_(M, N, dtype=self.dtype))
+
+
+class Softmax(Ops):
+    """Softmax along one axis (nn/Operators.py:671-704 -> tensor_ops.c:1231-1270)."""
+
+    def __init__(self, inputs, outputs, axis, dtype, version="17"):
+        super().__init__(inputs, outputs)
+        self.axis = axis
+        self.dtype = dtype
+        self.lib.softmax_forward.argtypes = [PT, PT, ctypes.c_int]
+        self.lib.softmax_forward.restype = None
+
+    def forward(self, input: Tensor):
+        t = self._run("softmax_forward", [input], tuple(input.size), self.dtype, ctypes.c_int(self.axis))
+        return _values(self, t)
+
+    def forward_(self, input: Tensor_):
+        return _values(self, Tensor_(*input.size, dtype=self.dtype))

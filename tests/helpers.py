@@ -1,0 +1,208 @@
+"""Shared test helpers: golden cases, the C-ABI driver for the HIP library and
+the comparison rules.
+
+Comparison rules (the parity bar):
+* bit-exact: integer / fp8 / f16 / bf16 codes and f32 / f64 bits must match,
+  except that where the reference result is a NaN the result only has to be a
+  NaN of the same format (the reference's own NaN sign/payload depends on
+  which operand x86 SSE propagates, which its C code does not fix);
+* tolerance (MFMA Gemm / Conv, tree-reduced Softmax): |g - r| <= rtol*|r| + atol
+  with rtol 1e-5 for f32 / f64 outputs and atol = rtol * rms(r); for narrow
+  float outputs one unit in the last place of the output format.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+
+import numpy as np
+
+from oracle import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+HIP_SO = os.path.join(ROOT, "onnx_translator_amd", "libtensor_ops_hip.so")
+
+_cases = None
+
+
+def load_cases():
+    global _cases
+    if _cases is None:
+        with open(os.path.join(GOLDEN, "cases.json")) as f:
+            cases = json.load(f)
+        arrays = dict(np.load(os.path.join(GOLDEN, "cases.npz"), allow_pickle=False))
+        _cases = (cases, arrays)
+    return _cases
+
+
+def case_by_name(name):
+    cases, arrays = load_cases()
+    for c in cases:
+        if c["name"] == name:
+            return c, arrays
+    raise KeyError(name)
+
+
+def run_case(lib, case, arrays):
+    ins = [arrays[k] if k is not None else None for k in case["inputs"]]
+    from tests.golden.make_golden import call
+    return call(lib, case["op"], ins, case["dtypes"], case["out_dtype"], case["params"])
+
+
+# ---------------------------------------------------------------- comparisons ---
+def nan_mask(a, dt):
+    dt = O.dtype_code(dt)
+    a = np.asarray(a)
+    if dt == O.F32 or dt == O.F64:
+        return np.isnan(a)
+    if dt == O.F16:
+        b = a.view(np.uint16)
+        return ((b & 0x7C00) == 0x7C00) & ((b & 0x3FF) != 0)
+    if dt == O.BF16:
+        b = a.view(np.uint16)
+        return ((b & 0x7F80) == 0x7F80) & ((b & 0x7F) != 0)
+    if dt == O.E4M3:
+        return (a.view(np.uint8) & 0x7F) == 0x7F
+    if dt == O.E5M2:
+        b = a.view(np.uint8)
+        return ((b & 0x7C) == 0x7C) & ((b & 3) != 0)
+    return np.zeros(a.shape, bool)
+
+
+def bits(a):
+    a = np.asarray(a)
+    return a.view({1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}[a.itemsize])
+
+
+def assert_bitexact(out, ref, dt, what=""):
+    out, ref = np.asarray(out), np.asarray(ref)
+    assert out.shape == ref.shape, f"{what}: shape {out.shape} vs {ref.shape}"
+    rn, on = nan_mask(ref, dt), nan_mask(out, dt)
+    bad = (~rn & (bits(out) != bits(ref))) | (rn & ~on)
+    if bad.any():
+        idx = np.argwhere(bad)[:8]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} differ; first at {idx.tolist()}: "
+                             f"got {[out[tuple(i)] for i in idx]} want {[ref[tuple(i)] for i in idx]}")
+
+
+def decode(a, dt):
+    """Storage -> float64 values (uses the oracle's decoders via a Sub(x, 0) pass)."""
+    dt = O.dtype_code(dt)
+    a = np.asarray(a)
+    if dt in (O.F32, O.F64) or dt >= O.I4:
+        return a.astype(np.float64)
+    if dt == O.F16:
+        return a.view(np.float16).astype(np.float64)
+    z = np.zeros(1, np.float32)
+    return O.oracle().binary("sub", a, dt, z, O.F32, O.F64)
+
+
+MANT_BITS = {O.F16: 10, O.BF16: 7, O.E4M3: 3, O.E5M2: 2}
+
+
+def assert_close(out, ref, dt, rtol=1e-5, what=""):
+    dt = O.dtype_code(dt)
+    g, r = decode(out, dt), decode(ref, dt)
+    assert g.shape == r.shape
+    rn = np.isnan(r)
+    assert not (np.isnan(g) & ~rn).any(), f"{what}: NaN where the reference is finite"
+    if dt in MANT_BITS:
+        tol = np.abs(r) * 2.0 ** -MANT_BITS[dt] + 1e-30
+        # values below the format's normal range are spaced by its subnormal step
+        tol = np.maximum(tol, {O.F16: 2 ** -24, O.BF16: 2 ** -133, O.E4M3: 2 ** -6, O.E5M2: 2 ** -14}[dt])
+    else:
+        finite = r[np.isfinite(r)]
+        rms = float(np.sqrt(np.mean(finite ** 2))) if finite.size else 0.0
+        tol = rtol * np.abs(r) + rtol * rms
+    fin = np.isfinite(r)
+    err = np.abs(g - r)
+    bad = fin & ~(err <= tol)
+    bad |= ~fin & ~rn & (g != r)
+    if bad.any():
+        idx = np.argwhere(bad)[:8]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside tolerance; first "
+                             f"{[(tuple(i), g[tuple(i)], r[tuple(i)]) for i in idx]}")
+
+
+TOL_OPS = {"gemm", "conv2d", "softmax"}
+
+
+def check_case(out, case, arrays, exact):
+    ref = arrays[case["out"]]
+    if case["op"] in TOL_OPS and not exact:
+        assert_close(out, ref, case["out_dtype"], what=case["name"])
+    else:
+        assert_bitexact(out, ref, case["out_dtype"], what=case["name"])
+
+
+# ---------------------------------------------------------------- HIP driver ---
+class HipLib(O.CpuLib):
+    """libtensor_ops_hip.so driven through its C ABI (host tensors: reference semantics)."""
+
+    def __init__(self, path=HIP_SO):
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} missing: run `python -m onnx_translator_amd.build` first")
+        super().__init__(path)
+        lib = self.lib
+        lib.tensor_ops_hip_last_error.restype = ctypes.c_char_p
+        lib.tensor_ops_hip_last_error.argtypes = []
+        lib.tensor_ops_hip_clear_error.argtypes = []
+        lib.tensor_ops_hip_device_count.restype = ctypes.c_int
+        lib.tensor_ops_hip_set_exact.argtypes = [ctypes.c_int]
+        lib.tensor_ops_hip_set_stream.argtypes = [ctypes.c_void_p]
+        lib.tensor_ops_hip_sync.restype = ctypes.c_int
+        lib.create_tensor_device.restype = O.PT
+        lib.create_tensor_device.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int]
+        lib.tensor_wrap_device.restype = O.PT
+        lib.tensor_wrap_device.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int), ctypes.c_int,
+                                           ctypes.c_int]
+        lib.tensor_to_host.argtypes = [O.PT, ctypes.c_void_p]
+        lib.tensor_to_host.restype = ctypes.c_int
+        lib.tensor_from_host.argtypes = [O.PT, ctypes.c_void_p]
+        lib.tensor_from_host.restype = ctypes.c_int
+        lib.tensor_is_device.argtypes = [O.PT]
+        lib.tensor_is_device.restype = ctypes.c_int
+        for n in ("quantize_linear_axis_forward", "dequantize_linear_axis_forward"):
+            getattr(lib, n).argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int]
+
+    def device_count(self):
+        return int(self.lib.tensor_ops_hip_device_count())
+
+    def last_error(self):
+        e = self.lib.tensor_ops_hip_last_error()
+        return e.decode() if e else ""
+
+    def set_exact(self, on):
+        self.lib.tensor_ops_hip_set_exact(1 if on else 0)
+
+    def _run(self, fn, ins, out_shape, out_dt, *extra):
+        self.lib.tensor_ops_hip_clear_error()
+        out = super()._run(fn, ins, out_shape, out_dt, *extra)
+        err = self.last_error()
+        if err:
+            raise RuntimeError(err)
+        return out
+
+    # device tensors --------------------------------------------------------
+    def dev_from(self, arr, dt):
+        a = O.as_storage(arr, dt)
+        shape = a.shape if a.ndim else (1,)
+        t = self.lib.create_tensor_device((ctypes.c_int * len(shape))(*shape), len(shape), O.dtype_code(dt))
+        assert t, self.last_error()
+        assert self.lib.tensor_from_host(t, a.ctypes.data) == 0, self.last_error()
+        return t
+
+    def dev_empty(self, shape, dt):
+        shape = tuple(shape) or (1,)
+        t = self.lib.create_tensor_device((ctypes.c_int * len(shape))(*shape), len(shape), O.dtype_code(dt))
+        assert t, self.last_error()
+        return t
+
+    def dev_read(self, t, dt):
+        c = t.contents
+        shape = [c.shape[i] for i in range(c.ndim)]
+        out = np.empty(shape, dtype=O.STORAGE[O.dtype_code(dt)])
+        assert self.lib.tensor_to_host(t, out.ctypes.data) == 0, self.last_error()
+        return out

@@ -1,0 +1,182 @@
+"""GPU parity at the BASELINE configuration sizes.
+
+Elementwise, Q/DQ, MaxPool: bit-exact against the oracle at full size.
+Gemm / Conv: MFMA results within tolerance of a float64 reference on sampled
+rows / images (the oracle itself on the images it finishes in seconds), and
+bit-exact in exact mode on the same samples.  Softmax: tolerance plus
+rows summing to one.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import assert_bitexact, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def config1_inputs():
+    rng = np.random.default_rng(0)
+    A = rng.uniform(-4, 4, (8, 64, 56, 56)).astype(np.float32)
+    B = rng.uniform(-4, 4, (64, 1, 1)).astype(np.float32)
+    Bd = (np.sign(B) * np.maximum(np.abs(B), 0.1)).astype(np.float32)
+    return A, B, Bd
+
+
+def test_config1_chain_full_size(hip, oracle_lib):
+    A, B, Bd = config1_inputs()
+    o, h = oracle_lib, hip
+    t_o, t_h = A, A
+    for op, b in (("add", B), ("mul", B), ("sub", B), ("div", Bd)):
+        t_o = o.binary(op, t_o, O.F32, b, O.F32, O.F32)
+        t_h = h.binary(op, t_h, O.F32, b, O.F32, O.F32)
+        assert_bitexact(t_h, t_o, O.F32, what=op)
+        t_h = t_o
+    for op in ("relu", "abs", "cos"):
+        t_o2 = o.unary(op, t_o, O.F32, O.F32)
+        assert_bitexact(h.unary(op, t_o, O.F32, O.F32), t_o2, O.F32, what=op)
+        t_o = t_o2
+
+
+@pytest.mark.parametrize("wide", [True, False])
+def test_config1_int32_promotion(hip, oracle_lib, wide):
+    rng = np.random.default_rng(0)
+    _, B, _ = config1_inputs()
+    lo, hi = (-(2 ** 31), 2 ** 31 - 1) if wide else (-(2 ** 20), 2 ** 20)
+    I = rng.integers(lo, hi, (8, 64, 56, 56), dtype=np.int64).astype(np.int32)
+    for dt in (O.F64, O.F32):
+        assert_bitexact(hip.binary("add", I, O.I32, B, O.F32, dt), oracle_lib.binary("add", I, O.I32, B, O.F32, dt),
+                        dt, what=f"int32+f32 -> {dt}")
+
+
+def config2_input():
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 1.5, (32, 512, 1024))
+    x[rng.random(x.shape) < 0.001] *= 20
+    return x.astype(np.float32)
+
+
+def config2_variants(x):
+    mn, mx = float(x.min()), float(x.max())
+    s_u8 = np.float32((mx - mn) / 255)
+    z_u8 = np.uint8(np.clip(np.round(-mn / float(s_u8)), 0, 255))
+    amax = float(np.abs(x).max())
+    return [
+        ("u8", np.array([s_u8]), np.array([z_u8]), O.U8, None),
+        ("i8axis", (np.abs(x).max(axis=(0, 2)) / 127).astype(np.float32), np.zeros(512, np.int8), O.I8, 1),
+        ("e4m3", np.array([amax / 448], np.float32), np.zeros(1, np.uint8), O.E4M3, None),
+        ("e5m2", np.array([amax / 57344], np.float32), np.zeros(1, np.uint8), O.E5M2, None),
+        ("e4m3_stress", np.array([amax / 448 / 16], np.float32), np.zeros(1, np.uint8), O.E4M3, None),
+        ("e5m2_stress", np.array([amax / 57344 / 16], np.float32), np.zeros(1, np.uint8), O.E5M2, None),
+    ]
+
+
+@pytest.fixture(scope="module")
+def x2():
+    return config2_input()
+
+
+@pytest.mark.parametrize("idx", range(6), ids=["u8", "i8axis", "e4m3", "e5m2", "e4m3_stress", "e5m2_stress"])
+def test_config2_qdq_full_size(hip, oracle_lib, x2, idx):
+    tag, s, z, ydt, axis = config2_variants(x2)[idx]
+    sv, zv = (s.reshape(1, -1, 1), z.reshape(1, -1, 1)) if axis is not None else (s, z)
+    y_ref = oracle_lib.qdq("quantize", x2, O.F32, sv, O.F32, zv, ydt, ydt)
+    y = hip.qdq("quantize", x2, O.F32, sv, O.F32, zv, ydt, ydt)
+    assert_bitexact(y, y_ref, ydt, what=f"Q {tag}")
+    xr_ref = oracle_lib.qdq("dequantize", y_ref, ydt, sv, O.F32, zv, ydt, O.F32)
+    xr = hip.qdq("dequantize", y_ref, ydt, sv, O.F32, zv, ydt, O.F32)
+    assert_bitexact(xr, xr_ref, O.F32, what=f"DQ {tag}")
+    if ydt in (O.U8, O.I8):
+        # round-trip property: unsaturated codes reproduce x within half a step
+        lo, hi = (0, 255) if ydt == O.U8 else (-128, 127)
+        ok = (y > lo) & (y < hi)
+        step = np.broadcast_to(sv, x2.shape)[ok].astype(np.float64)
+        assert np.all(np.abs(xr[ok].astype(np.float64) - x2[ok]) <= step * 0.5 * (1 + 1e-6))
+
+
+def test_config2_per_axis_entry_point(hip, oracle_lib, x2):
+    import ctypes
+    tag, s, z, ydt, axis = config2_variants(x2)[1]
+    y = hip._run(hip.lib.quantize_linear_axis_forward, [(x2, O.F32), (s, O.F32), (z, O.I8)], x2.shape, O.I8,
+                 ctypes.c_int(1))
+    ref = oracle_lib.qdq("quantize", x2, O.F32, s.reshape(1, -1, 1), O.F32, z.reshape(1, -1, 1), O.I8, O.I8)
+    assert_bitexact(y, ref, O.I8, what="axis entry point")
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_config3_gemm_4096(hip, dt):
+    rng = np.random.default_rng(2)
+    K = 4096
+    a = rng.normal(0, 1 / np.sqrt(K), (4096, K)).astype(np.float32)
+    b = rng.normal(0, 1 / np.sqrt(K), (4096, K)).astype(np.float32)
+    c = rng.normal(0, 1 / 64, (4096,)).astype(np.float32)
+    if dt == "float16":
+        a, b = a.astype(np.float16), b.astype(np.float16)
+    y = hip.gemm(a, dt, b, dt, c, "float32", dt, 1.0, 1.0, 0, 1)
+    rows = rng.choice(4096, 48, replace=False)
+    ref = a[rows].astype(np.float64) @ b.astype(np.float64).T + c.astype(np.float64)
+    if dt == "float16":
+        ref_codes = O.oracle().encode_f32(ref.astype(np.float32), O.F16)
+        assert_close(y[rows], ref_codes, O.F16, what="gemm f16 4096")
+    else:
+        assert_close(y[rows], ref.astype(np.float32), O.F32, what="gemm f32 4096")
+
+
+def test_config3_woq(hip, oracle_lib):
+    rng = np.random.default_rng(2)
+    bw = rng.normal(0, 1 / 64, (4096, 4096))
+    sw = (np.abs(bw).max(axis=1) / 127).astype(np.float32)
+    bq = np.clip(np.rint(bw / sw[:, None]), -127, 127).astype(np.int8)
+    z = np.zeros(4096, np.int8)
+    deq = hip.qdq("dequantize", bq, O.I8, sw.reshape(-1, 1), O.F32, z.reshape(-1, 1), O.I8, O.F32)
+    ref = oracle_lib.qdq("dequantize", bq, O.I8, sw.reshape(-1, 1), O.F32, z.reshape(-1, 1), O.I8, O.F32)
+    assert_bitexact(deq, ref, O.F32, what="WOQ DQ")
+    a = rng.normal(0, 1 / 64, (256, 4096)).astype(np.float32)
+    cb = rng.normal(0, 1 / 64, (4096,)).astype(np.float32)
+    y = hip.gemm(a, O.F32, deq, O.F32, cb, O.F32, O.F32, 1.0, 1.0, 0, 1)
+    r = a.astype(np.float64) @ deq.astype(np.float64).T + cb
+    assert_close(y, r.astype(np.float32), O.F32, what="WOQ gemm")
+
+
+CONVS = [("stem", (32, 3, 224, 224), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2]),
+         ("3x3", (32, 64, 56, 56), (64, 64, 3, 3), [1, 1, 1, 1], [1, 1]),
+         ("1x1", (32, 64, 56, 56), (256, 64, 1, 1), [0, 0, 0, 0], [1, 1])]
+
+
+@pytest.mark.parametrize("layer", CONVS, ids=[c[0] for c in CONVS])
+def test_config4_conv_full_size(hip, oracle_lib, layer):
+    tag, xs, ws, pads, strides = layer
+    rng = np.random.default_rng(3)
+    x = rng.normal(0, 1, xs).astype(np.float32)
+    w = rng.normal(0, np.sqrt(2 / (ws[1] * ws[2] * ws[3])), ws).astype(np.float32)
+    b = rng.normal(0, 1 / 64, (ws[0],)).astype(np.float32)
+    y = hip.conv(x, O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], 1)
+    imgs = [0, xs[0] - 1]
+    ref = oracle_lib.conv(x[imgs], O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], 1)
+    assert_close(y[imgs], ref, O.F32, what=f"conv {tag}")
+    hip.set_exact(True)
+    try:
+        ye = hip.conv(x[imgs], O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], 1)
+    finally:
+        hip.set_exact(False)
+    assert_bitexact(ye, ref, O.F32, what=f"conv {tag} exact")
+
+
+def test_config4_maxpool_full_size(hip, oracle_lib):
+    rng = np.random.default_rng(3)
+    x = rng.normal(0, 1, (32, 64, 112, 112)).astype(np.float32)
+    y = hip.maxpool(x, O.F32, O.F32, [3, 3], [1, 1, 1, 1], [2, 2])
+    assert_bitexact(y, oracle_lib.maxpool(x, O.F32, O.F32, [3, 3], [1, 1, 1, 1], [2, 2]), O.F32, what="maxpool")
+
+
+def test_config5_softmax(hip, oracle_lib):
+    rng = np.random.default_rng(4)
+    x = rng.normal(0, 3, (64, 32000)).astype(np.float32)
+    y = hip.softmax(x, O.F32, O.F32, 1)
+    ref = oracle_lib.softmax(x, O.F32, O.F32, 1)
+    assert_close(y, ref, O.F32, what="softmax")
+    frac_exact = float(np.mean(y == ref))
+    assert frac_exact > 0.99, frac_exact
+    np.testing.assert_allclose(y.astype(np.float64).sum(axis=1), 1.0, rtol=1e-5)
+    x2 = rng.normal(0, 3, (64, 1000)).astype(np.float32)
+    assert_close(hip.softmax(x2, O.F32, O.F32, -1), oracle_lib.softmax(x2, O.F32, O.F32, -1), O.F32)

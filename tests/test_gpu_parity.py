@@ -1,0 +1,153 @@
+"""GPU parity: every golden case through libtensor_ops_hip.so's C ABI.
+
+* host tensors (reference semantics: synchronous, staged through HBM);
+* Gemm / Conv in both precision modes: MFMA (tolerance class) and exact
+  (fp64, reference summation order: bit-exact);
+* device-resident tensors through the Python operator layer, which must give
+  the same bits as the host path;
+* error paths forced from the host (bad shapes) return an error, never fault.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import HipLib, assert_bitexact, check_case, load_cases, run_case
+
+pytestmark = pytest.mark.gpu
+
+CASES, ARRAYS = load_cases()
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c["name"] for c in CASES])
+def test_golden_default_mode(hip, case):
+    hip.set_exact(False)
+    out = run_case(hip, case, ARRAYS)
+    check_case(out, case, ARRAYS, exact=False)
+
+
+EXACT_CASES = [c for c in CASES if c["op"] in ("gemm", "conv2d")]
+
+
+@pytest.mark.parametrize("case", EXACT_CASES, ids=[c["name"] for c in EXACT_CASES])
+def test_golden_exact_mode(hip, case):
+    hip.set_exact(True)
+    try:
+        out = run_case(hip, case, ARRAYS)
+    finally:
+        hip.set_exact(False)
+    assert_bitexact(out, ARRAYS[case["out"]], case["out_dtype"], what=case["name"])
+
+
+def test_mfma_f32_layout_single_tile(hip):
+    """A 32x2 @ 2x32 product (one MFMA) checks the operand / result lane layout."""
+    rng = np.random.default_rng(0)
+    a = rng.integers(-8, 8, (32, 2)).astype(np.float32)
+    b = rng.integers(-8, 8, (2, 32)).astype(np.float32)
+    out = hip.gemm(a, O.F32, b, O.F32, None, O.F32, O.F32, 1.0, 0.0, 0, 0)
+    assert np.array_equal(out, a @ b)
+    a16 = rng.integers(-8, 8, (32, 16)).astype(np.float16)
+    b16 = rng.integers(-8, 8, (32, 16)).astype(np.float16)
+    out = hip.gemm(a16, O.F16, b16, O.F16, None, O.F32, O.F32, 1.0, 0.0, 0, 1)
+    assert np.array_equal(out, a16.astype(np.float32) @ b16.astype(np.float32).T)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (127, 129, 67), (200, 64, 300), (64, 250, 17)])
+@pytest.mark.parametrize("trans", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_ragged_shapes(hip, oracle_lib, shape, trans):
+    M, N, K = shape
+    ta, tb = trans
+    rng = np.random.default_rng(M * 7 + N)
+    a = rng.normal(0, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    b = rng.normal(0, 1, (N, K) if tb else (K, N)).astype(np.float32)
+    c = rng.normal(0, 1, (N,)).astype(np.float32)
+    for dt in ("float32", "float16"):
+        aa = a if dt == "float32" else a.astype(np.float16).view(np.uint16)
+        bb = b if dt == "float32" else b.astype(np.float16).view(np.uint16)
+        ref = oracle_lib.gemm(aa, dt, bb, dt, c, "float32", "float32", 1.25, 0.5, ta, tb)
+        got = hip.gemm(aa, dt, bb, dt, c, "float32", "float32", 1.25, 0.5, ta, tb)
+        from tests.helpers import assert_close
+        assert_close(got, ref, O.F32, what=f"gemm {dt} {shape} {trans}")
+
+
+def test_device_path_matches_host_path(hip):
+    """Config-1 chain with device-resident tensors (no host round trips between ops)."""
+    from onnx_translator_amd.nn import Tensor
+    from onnx_translator_amd.nn.Operators import ABS, ADD, COS, DIV, MUL, RELU, SUB
+    rng = np.random.default_rng(0)
+    A = rng.uniform(-4, 4, (2, 64, 14, 14)).astype(np.float32)
+    B = rng.uniform(-4, 4, (64, 1, 1)).astype(np.float32)
+    Bd = (np.sign(B) * np.maximum(np.abs(B), 0.1)).astype(np.float32)
+    ta, tb, tbd = [Tensor(*x.shape, dtype="float32", data=x) for x in (A, B, Bd)]
+
+    def chain(a, b, bd):
+        t = ADD([], [], "float32").forward(a, b)["tensor"]
+        t = MUL([], [], "float32").forward(t, b)["tensor"]
+        t = SUB([], [], "float32").forward(t, b)["tensor"]
+        t = DIV([], [], "float32").forward(t, bd)["tensor"]
+        t = RELU([], [], "float32").forward(t)["tensor"]
+        t = ABS([], [], "float32").forward(t)["tensor"]
+        return COS([], [], "float32").forward(t)["tensor"]
+
+    host = chain(ta, tb, tbd)
+    dev = chain(ta.to_device(), tb.to_device(), tbd.to_device())
+    assert dev.on_device and not host.on_device
+    assert_bitexact(dev.numpy(), host.numpy(), O.F32, what="device chain")
+    # and against the oracle, op by op on the host
+    o = O.oracle()
+    t = o.binary("add", A, O.F32, B, O.F32, O.F32)
+    t = o.binary("mul", t, O.F32, B, O.F32, O.F32)
+    t = o.binary("sub", t, O.F32, B, O.F32, O.F32)
+    t = o.binary("div", t, O.F32, Bd, O.F32, O.F32)
+    t = o.unary("cos", o.unary("abs", o.unary("relu", t, O.F32, O.F32), O.F32, O.F32), O.F32, O.F32)
+    assert_bitexact(host.numpy(), t, O.F32, what="host chain vs oracle")
+
+
+def test_operator_layer_qdq_axis_and_gemm(hip):
+    from onnx_translator_amd.nn import Tensor
+    from onnx_translator_amd.nn.Operators import DequantizeLinear, Gemm, QuantizeLinear, Softmax
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 1.5, (4, 16, 64)).astype(np.float32)
+    s = (np.abs(x).max(axis=(0, 2)) / 127).astype(np.float32)
+    z = np.zeros(16, np.int8)
+    X = Tensor(*x.shape, dtype="float32", data=x)
+    S = Tensor(16, dtype="float32", data=s)
+    Z = Tensor(16, dtype="int8", data=z)
+    for dev in (False, True):
+        xs, ss, zs = (X.to_device(), S.to_device(), Z.to_device()) if dev else (X, S, Z)
+        y = QuantizeLinear([], [], axis=1, dtype="int8").forward(xs, ss, zs)["tensor"]
+        xr = DequantizeLinear([], [], dtype="float32", axis=1).forward(y, ss, zs)["tensor"]
+        ref_y = O.oracle().qdq("quantize", x, O.F32, s.reshape(1, 16, 1), O.F32, z.reshape(1, 16, 1), O.I8, O.I8)
+        assert_bitexact(y.numpy(), ref_y, O.I8, what="q axis")
+        ref_x = O.oracle().qdq("dequantize", ref_y, O.I8, s.reshape(1, 16, 1), O.F32, z.reshape(1, 16, 1), O.I8,
+                               O.F32)
+        assert_bitexact(xr.numpy(), ref_x, O.F32, what="dq axis")
+    a = rng.normal(0, 1, (33, 70)).astype(np.float32)
+    b = rng.normal(0, 1, (17, 70)).astype(np.float32)
+    c = rng.normal(0, 1, (17,)).astype(np.float32)
+    g = Gemm([], [], 1.0, 1.0, 0, 1, "float32").forward(
+        Tensor(*a.shape, data=a), Tensor(*b.shape, data=b), Tensor(17, data=c))["tensor"]
+    np.testing.assert_allclose(g.numpy(), a.astype(np.float64) @ b.T.astype(np.float64) + c, rtol=1e-5,
+                               atol=1e-5)
+    sm = Softmax([], [], axis=1, dtype="float32").forward(Tensor(*a.shape, data=a))["tensor"].numpy()
+    np.testing.assert_allclose(sm.sum(axis=1), 1.0, rtol=1e-5)
+
+
+def test_errors_are_reported_not_faulted(hip):
+    with pytest.raises(RuntimeError, match="broadcast"):
+        hip._run(hip.lib.add_forward, [(np.ones((3, 4), np.float32), O.F32), (np.ones((5,), np.float32), O.F32)],
+                 (3, 4), O.F32)
+    with pytest.raises(RuntimeError, match="inner dimensions"):
+        hip._run(hip.lib.gemm_forward, [(np.ones((4, 5), np.float32), O.F32), (np.ones((6, 7), np.float32), O.F32),
+                                        (None, O.F32)], (4, 7), O.F32, ctypes.c_float(1), ctypes.c_float(0), 0, 0)
+    with pytest.raises(RuntimeError, match="sizes differ"):
+        hip._run(hip.lib.relu_forward, [(np.ones(5, np.float32), O.F32)], (6,), O.F32)
+    # the library still works afterwards
+    out = hip.unary("relu", np.array([-1.0, 2.0], np.float32), O.F32, O.F32)
+    assert out.tolist() == [0.0, 2.0]
+
+
+def test_zero_size_tensors(hip):
+    out = hip.binary("add", np.zeros((0, 3), np.float32), O.F32, np.zeros((0, 3), np.float32), O.F32, O.F32)
+    assert out.shape == (0, 3)
