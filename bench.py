@@ -153,26 +153,20 @@ def run_headline(lib, torch, steps, warmup):
     R = 8
     X = [lib.dev(x, F32) for _ in range(R)]
     shp = list(x.shape)
-    Y = [lib.empty(shp, variants[r % 4][3]) for r in range(R)]
+    Y = [[lib.empty(shp, v[3]) for _ in range(R)] for v in variants]   # per-variant code sets
     XR = [lib.empty(shp, F32) for _ in range(R)]
     S = [lib.dev(v[1], F32) for v in variants]
     Z = [lib.dev(v[2], v[3]) for v in variants]
     L = lib.lib
     bytes_per_launch = 5 * n
-    launches = []        # (kind, variant, fn) in one step's order
 
-    def step(k, events=None):
+    def step(k):
+        # launch q reads input set q % R; the dequantize of variant v reads the
+        # codes its quantize wrote one step earlier (4 launches, > 600 MB ago)
         for v in range(4):
             q = 4 * k + v
-            if events is not None:
-                events[2 * v][0].record()
-            L.quantize_linear_forward(X[q % R], S[v], Z[v], Y[q % R])
-            if events is not None:
-                events[2 * v][1].record()
-                events[2 * v + 1][0].record()
-            L.dequantize_linear_forward(Y[(q - 4) % R], S[v], Z[v], XR[q % R])
-            if events is not None:
-                events[2 * v + 1][1].record()
+            L.quantize_linear_forward(X[q % R], S[v], Z[v], Y[v][k % R])
+            L.dequantize_linear_forward(Y[v][(k - 1) % R], S[v], Z[v], XR[q % R])
 
     for k in range(warmup):
         step(k)
@@ -189,21 +183,21 @@ def run_headline(lib, torch, steps, warmup):
     lib.check("timed steps")
     ms = t0.elapsed_time(t1) / steps
 
-    # Per-kernel durations: same steps again with events around every launch.
-    names = []
-    for v in variants:
-        names += [f"quantize_f32_to_{v[0]}", f"dequantize_{v[0]}_to_f32"]
-    durs = {nm: [] for nm in names}
-    for k in range(steps):
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(8)]
-        step(warmup + steps + k, ev)
-        torch.cuda.synchronize()
-        for i, (a, b) in enumerate(ev):
-            durs[names[i]].append(a.elapsed_time(b))
+    # Per-kernel average launch duration: `steps` back-to-back launches of one
+    # kernel (rotating over the R sets) between one pair of HIP events on the
+    # launch stream.
+    kern = {}
+    for v, var in enumerate(variants):
+        def q_fn(i, v=v):
+            L.quantize_linear_forward(X[i % R], S[v], Z[v], Y[v][i % R])
+
+        def dq_fn(i, v=v):
+            L.dequantize_linear_forward(Y[v][i % R], S[v], Z[v], XR[i % R])
+        kern[f"quantize_f32_to_{var[0]}"] = bench_loop(torch, q_fn, steps, warm=4)
+        kern[f"dequantize_{var[0]}_to_f32"] = bench_loop(torch, dq_fn, steps, warm=4)
     lib.check("per-kernel pass")
-    kern = {nm: float(np.mean(d)) for nm, d in durs.items()}
     dom = max(kern, key=kern.get)
-    for t in X + Y + XR + S + Z:
+    for t in X + [t for ys in Y for t in ys] + XR + S + Z:
         L.free_tensor(t)
     per_step_bytes = 8 * bytes_per_launch
     return {"ms_per_step": ms, "wall_s": wall, "bytes_per_step": per_step_bytes, "kernel_ms": kern,
@@ -376,7 +370,20 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--calib", action="store_true",
+                    help="only run a plain copy kernel (torch.neg, 512 MiB in + 512 MiB out, 5 launches) to "
+                         "calibrate the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.calib:
+        import torch
+        src = torch.ones(1 << 27, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib": "torch.neg f32", "bytes_in": src.numel() * 4, "bytes_out": dst.numel() * 4,
+                          "launches": 5}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
               "(every hot op shards without exchange; see DESIGN.md)", file=sys.stderr)

@@ -220,6 +220,22 @@ TO_HD void st_d_rt(int dt, void* p, int64_t i, double v) { TOHIP_DT_SWITCH(dt, s
 TO_HD void st_i_rt(int dt, void* p, int64_t i, int64_t v) { TOHIP_DT_SWITCH(dt, st_i<D>(p, i, v)); }
 
 // ----------------------------------------------------------------------------
+// Streaming access: nontemporal loads / stores for operands touched once.
+// ----------------------------------------------------------------------------
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 ld_stream(const float4* p) {
+    const f32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
+    return make_float4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ void st_stream(float4* p, float4 v) {
+    const f32x4_t t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<f32x4_t*>(p));
+}
+__device__ __forceinline__ uint32_t ld_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st_stream(uint32_t* p, uint32_t v) { __builtin_nontemporal_store(v, p); }
+
+// ----------------------------------------------------------------------------
 // Broadcast indexing.  Output shape is collapsed to at most kMaxDims dims
 // (adjacent dims merge when every operand is contiguous across them); each
 // operand has one element stride per dim (0 where it broadcasts).

@@ -77,13 +77,13 @@ __global__ __launch_bounds__(kBlock) void k_unary_f32(const float* __restrict__ 
     const size_t nv = n / 4;
     const size_t stride = (size_t)gridDim.x * kBlock;
     for (size_t v = (size_t)blockIdx.x * kBlock + threadIdx.x; v < nv; v += stride) {
-        float4 x = reinterpret_cast<const float4*>(X)[v];
+        const float4 x = ld_stream(reinterpret_cast<const float4*>(X) + v);
         float4 y;
         y.x = unary_f32<U>(x.x, T);
         y.y = unary_f32<U>(x.y, T);
         y.z = unary_f32<U>(x.z, T);
         y.w = unary_f32<U>(x.w, T);
-        reinterpret_cast<float4*>(Y)[v] = y;
+        st_stream(reinterpret_cast<float4*>(Y) + v, y);
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         const size_t i = nv * 4 + threadIdx.x;
@@ -116,9 +116,10 @@ __global__ __launch_bounds__(kBlock) void k_unary_rt(const void* __restrict__ X,
 }
 
 // --------------------------------------------------------------- binary ---
-template <int ND>
-__device__ __forceinline__ float4 load4(const float* __restrict__ p, int64_t off, int64_t st) {
-    if (st == 1) return *reinterpret_cast<const float4*>(p + off);
+// stream: the operand is read once (full size), so use nontemporal loads.
+__device__ __forceinline__ float4 load4(const float* __restrict__ p, int64_t off, int64_t st, bool stream) {
+    if (st == 1) return stream ? ld_stream(reinterpret_cast<const float4*>(p + off))
+                               : *reinterpret_cast<const float4*>(p + off);
     if (st == 0) { const float v = p[off]; return make_float4(v, v, v, v); }
     return make_float4(p[off], p[off + st], p[off + 2 * st], p[off + 3 * st]);
 }
@@ -126,20 +127,21 @@ __device__ __forceinline__ float4 load4(const float* __restrict__ p, int64_t off
 // f32 x f32 -> f32, vectorised; requires dim[nd-1] % 4 == 0 and 16-byte aligned bases.
 template <int OP, int ND>
 __global__ __launch_bounds__(kBlock) void k_bin_f32_v4(const float* __restrict__ A, const float* __restrict__ B,
-                                                       float* __restrict__ O, BDesc d, uint32_t nv) {
+                                                       float* __restrict__ O, BDesc d, uint32_t nv,
+                                                       int stream_a, int stream_b) {
     const int64_t sa = d.st[0][d.nd - 1], sb = d.st[1][d.nd - 1];
     const uint32_t stride = gridDim.x * kBlock;
     for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nv; v += stride) {
         int64_t off[2];
         bd_offsets32<2, ND>(d, v * 4u, off);
-        const float4 a = load4<ND>(A, off[0], sa);
-        const float4 b = load4<ND>(B, off[1], sb);
+        const float4 a = load4(A, off[0], sa, stream_a != 0);
+        const float4 b = load4(B, off[1], sb, stream_b != 0);
         float4 o;
         o.x = fop<OP>(a.x, b.x);
         o.y = fop<OP>(a.y, b.y);
         o.z = fop<OP>(a.z, b.z);
         o.w = fop<OP>(a.w, b.w);
-        reinterpret_cast<float4*>(O)[v] = o;
+        st_stream(reinterpret_cast<float4*>(O) + v, o);
     }
 }
 
@@ -196,7 +198,8 @@ __global__ __launch_bounds__(kBlock) void k_bin_rt(const void* __restrict__ A, i
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 template <int OP>
-bool launch_binary(const void* A, int dta, const void* B, int dtb, void* O, int dto, const BDesc& d, size_t n) {
+bool launch_binary(const void* A, int dta, const void* B, int dtb, void* O, int dto, const BDesc& d, size_t n,
+                   size_t sz_a, size_t sz_b) {
     hipStream_t s = stream();
     if (n == 0) return true;
     const bool small = n < (size_t(1) << 31);   // 32-bit loop counters cannot wrap
@@ -213,7 +216,7 @@ bool launch_binary(const void* A, int dta, const void* B, int dtb, void* O, int 
         if (v4) {
             const uint32_t nv = (uint32_t)(n / 4);
             ND_SWITCH(d.nd, hipLaunchKernelGGL((k_bin_f32_v4<OP, ND>), dim3(grid_for(nv, kBlock)), dim3(kBlock), 0, s,
-                                               a, b, o, d, nv));
+                                               a, b, o, d, nv, sz_a == n, sz_b == n));
         } else {
             ND_SWITCH(d.nd, hipLaunchKernelGGL((k_bin_f32_s<OP, ND>), dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s,
                                                a, b, o, d, (uint32_t)n));
@@ -250,7 +253,7 @@ void binary_entry(const char* name, const Tensor* A, const Tensor* B, Tensor* O)
     const void* b = st.in(B);
     void* o = st.out(O, tensor_bytes(O));
     if (!a || !b || !o) { st.finish(); return; }
-    if (!launch_binary<OP>(a, (int)A->dtype, b, (int)B->dtype, o, (int)O->dtype, d, O->size)) {
+    if (!launch_binary<OP>(a, (int)A->dtype, b, (int)B->dtype, o, (int)O->dtype, d, O->size, A->size, B->size)) {
         st.finish();
         return;
     }

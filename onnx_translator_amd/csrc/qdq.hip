@@ -3,22 +3,33 @@
 // tensor_ops/tensor_ops.c:999-1034:
 //   quantize:   y = s != 0 ? rint(x / s) + zp : zp   (double), then the output encoder
 //   dequantize: y = (x - zp) * s                     (double), then the output encoder
-// The quotient is an fp64 division (an fp32 quotient can round onto or across
-// a .5 tie, so it is not equivalent); rint is round-half-to-even.  Scale and
-// zero point are indexed through a broadcast descriptor against Y (scalar,
-// per-axis or full-size), so nothing is materialised.
+// Scale and zero point are indexed through a broadcast descriptor against Y
+// (scalar, per-axis or full-size), so nothing is materialised.
 //
-// Fast kernels: f32 X (quantize) / 1-byte X (dequantize) with f32 scale,
-// V = 16 elements per thread: four 16-byte f32 vectors and one 16-byte code
-// vector per thread, all coalesced.  Other dtype combinations use a generic
-// one-element-per-thread kernel with a run-time dtype switch.
+// Quantize fast path (exact).  The reference rounds the fp64 quotient
+// q64 = RN64(x / s).  We form q32 = RN32(x * RN32(1 / s)), which is within
+// 2^-23 |x/s| of the exact quotient, and q64 is within 2^-53 of it.  When q32
+// lies more than 2^-22 |q32| away from the nearest half-integer (and
+// |q32| < 2^22) all three values fall strictly inside the same rounding
+// interval, so rint(q32) == rint(q64); the remaining lanes (about 2^-21 of
+// them: near-ties, huge quotients, NaN / inf, s == 0) take the fp64 division.
+// For integer outputs the fast path also needs an integral zero point, so
+// that rint(q) + zp stays an exactly representable integer in fp32; fp8
+// outputs are rounded once to fp32 exactly as the reference's (float)res.
+//
+// Launch shapes (measured on MI355X): quantize — one 16-byte f32 load per
+// thread per iteration, 512-thread blocks, grid-stride over 2048 blocks;
+// dequantize — four 4-byte code loads per thread, 256-thread blocks.  Both
+// read and write with nontemporal (streaming) accesses.
 #include "runtime.h"
 
 namespace tohip {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kV = 16;
+constexpr int kQBlock = 512;
+constexpr int kQGrid = 2048;
+constexpr int kU = 4;        // dequantize: 4-element groups per thread, group u of a block is one contiguous span
 
 template <int YDT> __device__ __forceinline__ uint8_t code8(double r) {
     if constexpr (YDT == kU8) return (uint8_t)sat(cvt_i64(__builtin_rint(r)), 0, 255);
@@ -30,79 +41,115 @@ template <int YDT> __device__ __forceinline__ uint8_t code8(double r) {
 
 __device__ __forceinline__ double qval(double x, double s, double z) { return s != 0.0 ? __builtin_rint(x / s) + z : z; }
 
-// Quantize f32 -> 1-byte code, V elements per thread along the innermost dim.
-// Operand order in d: 0 = X, 1 = Scale, 2 = ZeroPoint.
+// Integral zero point small enough that rint(q) + zp (|rint(q)| < 2^22) stays
+// an exact fp32 integer below 2^23, far from the int64 conversion limits.
+__device__ __forceinline__ bool zint_ok(float zf, double z) {
+    return __builtin_fabsf(zf) < 0x1p22f && __builtin_rintf(zf) == zf && (double)zf == z;
+}
+
+// Code of one element: fp32 fast path with the fp64 fallback described above.
+// rs = RN32(1 / s); zint: the zero point is an integer (needed for int outputs).
+template <int YDT>
+__device__ __forceinline__ uint32_t qcode(float x, float s, float rs, float zf, double zd, bool zint) {
+    const float q = x * rs;
+    const float aq = __builtin_fabsf(q);
+    const float d = __builtin_fabsf(__builtin_amdgcn_fractf(aq) - 0.5f);
+    const bool ok = (aq < 0x1p22f) && (d > aq * 0x1p-22f) && (s != 0.0f) && (YDT == kE4M3 || YDT == kE5M2 || zint);
+    if (__builtin_expect(ok, 1)) {
+        const float r = __builtin_rintf(q) + zf;
+        if constexpr (YDT == kU8) return (uint32_t)(int)__builtin_amdgcn_fmed3f(r, 0.0f, 255.0f);
+        else if constexpr (YDT == kI8) return (uint32_t)(uint8_t)(int8_t)(int)__builtin_amdgcn_fmed3f(r, -128.0f, 127.0f);
+        else if constexpr (YDT == kE4M3) return enc_e4m3(r);
+        else return enc_e5m2(r);
+    }
+    return code8<YDT>(qval((double)x, (double)s, zd));
+}
+
+// Quantize f32 -> 1-byte code.  X and Y are flat (X has Y's size); Scale and
+// ZeroPoint go through the descriptor (operands 1 and 2).  A thread handles
+// 4 consecutive elements per iteration (one 16-byte load, one 4-byte store),
+// so each load / store instruction is contiguous across the wave.
+// Requires n % 4 == 0 and dim[nd-1] % 4 == 0.
 template <int YDT, int ZDT, int ND>
-__global__ __launch_bounds__(kBlock) void k_quant_v(const float* __restrict__ X, const float* __restrict__ S,
-                                                    const void* __restrict__ Z, uint8_t* __restrict__ Y, BDesc d,
-                                                    uint32_t nv) {
+__global__ __launch_bounds__(kQBlock) void k_quant_v(const float* __restrict__ X, const float* __restrict__ S,
+                                                     const void* __restrict__ Z, uint8_t* __restrict__ Y, BDesc d,
+                                                     uint32_t nv) {
     const int inner = d.nd - 1;
     const int64_t ss = d.st[1][inner], sz = d.st[2][inner];
-    const uint32_t stride = gridDim.x * kBlock;
-    for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nv; v += stride) {
-        int64_t off[3];
-        bd_offsets32<3, ND>(d, v * (uint32_t)kV, off);
-        float x[kV];
+    const bool uniform = (ND == 1) && ss == 0 && sz == 0;      // per-tensor scale / zero point
+    const float su = S[0];
+    const double zu = ld_d<ZDT>(Z, 0);
+    const float rsu = 1.0f / su, zfu = (float)zu;
+    const bool zintu = zint_ok(zfu, zu);
+    const float4* X4 = reinterpret_cast<const float4*>(X);
+    uint32_t* Y4 = reinterpret_cast<uint32_t*>(Y);
+    for (uint32_t v = blockIdx.x * kQBlock + threadIdx.x; v < nv; v += gridDim.x * kQBlock) {
+        const float4 xv = ld_stream(X4 + v);
+        const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+        uint32_t w = 0;
+        if (uniform) {
 #pragma unroll
-        for (int q = 0; q < kV / 4; q++) {
-            const float4 t = *reinterpret_cast<const float4*>(X + off[0] + 4 * q);
-            x[4 * q] = t.x; x[4 * q + 1] = t.y; x[4 * q + 2] = t.z; x[4 * q + 3] = t.w;
-        }
-        uint32_t w[kV / 4];
-        if (ss == 0 && sz == 0) {
-            const double s = (double)S[off[1]], z = ld_d<ZDT>(Z, off[2]);
-#pragma unroll
-            for (int q = 0; q < kV / 4; q++) {
-                uint32_t acc = 0;
-#pragma unroll
-                for (int b = 0; b < 4; b++) acc |= (uint32_t)code8<YDT>(qval((double)x[4 * q + b], s, z)) << (8 * b);
-                w[q] = acc;
-            }
+            for (int b = 0; b < 4; b++) w |= qcode<YDT>(xs[b], su, rsu, zfu, zu, zintu) << (8 * b);
         } else {
+            int64_t off[3];
+            bd_offsets32<3, ND>(d, v * 4u, off);
+            if (ss == 0 && sz == 0) {                           // per-axis: one channel per group
+                const float s = S[off[1]];
+                const double z = ld_d<ZDT>(Z, off[2]);
+                const float rs = 1.0f / s, zf = (float)z;
+                const bool zi = zint_ok(zf, z);
 #pragma unroll
-            for (int q = 0; q < kV / 4; q++) {
-                uint32_t acc = 0;
+                for (int b = 0; b < 4; b++) w |= qcode<YDT>(xs[b], s, rs, zf, z, zi) << (8 * b);
+            } else {
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
-                    const int t = 4 * q + b;
-                    const double s = (double)S[off[1] + t * ss], z = ld_d<ZDT>(Z, off[2] + t * sz);
-                    acc |= (uint32_t)code8<YDT>(qval((double)x[t], s, z)) << (8 * b);
+                    const float s = S[off[1] + b * ss];
+                    const double z = ld_d<ZDT>(Z, off[2] + b * sz);
+                    const float zf = (float)z;
+                    w |= qcode<YDT>(xs[b], s, 1.0f / s, zf, z, zint_ok(zf, z)) << (8 * b);
                 }
-                w[q] = acc;
             }
         }
-        *reinterpret_cast<uint4*>(Y + (size_t)v * kV) = make_uint4(w[0], w[1], w[2], w[3]);
+        st_stream(Y4 + v, w);
     }
 }
 
-// Dequantize 1-byte code -> f32, V elements per thread.
+// Dequantize 1-byte code -> f32: kU 4-byte code loads per thread, float4
+// streaming stores.  (x - zp) * s is evaluated in fp64 and rounded once.
 template <int XDT, int ZDT, int ND>
 __global__ __launch_bounds__(kBlock) void k_dequant_v(const uint8_t* __restrict__ X, const float* __restrict__ S,
                                                       const void* __restrict__ Z, float* __restrict__ Y, BDesc d,
                                                       uint32_t nv) {
     const int inner = d.nd - 1;
     const int64_t ss = d.st[1][inner], sz = d.st[2][inner];
-    const uint32_t stride = gridDim.x * kBlock;
-    for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nv; v += stride) {
-        int64_t off[3];
-        bd_offsets32<3, ND>(d, v * (uint32_t)kV, off);
-        const uint4 raw = *reinterpret_cast<const uint4*>(X + off[0]);
-        const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-        float y[kV];
-        const bool uni = (ss == 0 && sz == 0);
-        const double s0 = (double)S[off[1]], z0 = ld_d<ZDT>(Z, off[2]);
+    const bool uniform = (ND == 1) && ss == 0 && sz == 0;
+    const double su = (double)S[0], zu = ld_d<ZDT>(Z, 0);
+    const uint32_t* X4 = reinterpret_cast<const uint32_t*>(X);
+    float4* Y4 = reinterpret_cast<float4*>(Y);
+    for (uint32_t base = blockIdx.x * (kBlock * kU); base < nv; base += gridDim.x * (kBlock * kU)) {
+        uint32_t xv[kU];
 #pragma unroll
-        for (int t = 0; t < kV; t++) {
-            const uint8_t c = (uint8_t)(wv[t >> 2] >> (8 * (t & 3)));
-            const double xv = ld_d<XDT>(&c, 0);
-            const double s = uni ? s0 : (double)S[off[1] + t * ss];
-            const double z = uni ? z0 : ld_d<ZDT>(Z, off[2] + t * sz);
-            y[t] = (float)((xv - z) * s);
+        for (int u = 0; u < kU; u++) {
+            const uint32_t v = base + u * kBlock + threadIdx.x;
+            if (v < nv) xv[u] = X4[v];
         }
-        float* out = Y + (size_t)v * kV;
 #pragma unroll
-        for (int q = 0; q < kV / 4; q++)
-            reinterpret_cast<float4*>(out)[q] = make_float4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]);
+        for (int u = 0; u < kU; u++) {
+            const uint32_t v = base + u * kBlock + threadIdx.x;
+            if (v >= nv) continue;
+            float y[4];
+            int64_t off[3] = {0, 0, 0};
+            if (!uniform) bd_offsets32<3, ND>(d, v * 4u, off);
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const uint8_t c = (uint8_t)(xv[u] >> (8 * b));
+                const double x = ld_d<XDT>(&c, 0);
+                const double s = uniform ? su : (double)S[off[1] + b * ss];
+                const double z = uniform ? zu : ld_d<ZDT>(Z, off[2] + b * sz);
+                y[b] = (float)((x - z) * s);
+            }
+            st_stream(Y4 + v, make_float4(y[0], y[1], y[2], y[3]));
+        }
     }
 }
 
@@ -138,9 +185,10 @@ __global__ __launch_bounds__(kBlock) void k_qdq_rt(const void* __restrict__ X, i
 inline bool is_code8(int dt) { return dt == kU8 || dt == kI8 || dt == kE4M3 || dt == kE5M2; }
 inline bool zdt_fast(int dt) { return is_code8(dt) || dt == kF32; }
 
-bool fast_ok(const BDesc& d, size_t n, const void* x, const void* y, size_t xalign) {
-    return n < (size_t(1) << 31) && n % kV == 0 && d.dim[d.nd - 1] % kV == 0 && d.st[0][d.nd - 1] == 1 &&
-           ((uintptr_t)x % xalign) == 0 && ((uintptr_t)y % 16) == 0;
+// Fast kernels: X flat with Y's size, 4-element groups sharing outer coordinates.
+bool fast_ok(const BDesc& d, const Tensor* X, size_t n, const void* x, const void* y) {
+    return X->size == n && n < (size_t(1) << 31) && n % 4 == 0 && d.dim[d.nd - 1] % 4 == 0 &&
+           ((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0;
 }
 
 template <bool QUANT>
@@ -161,9 +209,9 @@ void qdq_entry(const char* name, const Tensor* X, const Tensor* S, const Tensor*
     hipStream_t sm = stream();
     if (n) {
         bool launched = false;
-        if (QUANT && dtx == kF32 && dts == kF32 && zdt_fast(dtz) && is_code8(dty) && fast_ok(d, n, x, y, 16)) {
-            const uint32_t nv = (uint32_t)(n / kV);
-            const dim3 g(grid_for(nv, kBlock)), b(kBlock);
+        if (QUANT && dtx == kF32 && dts == kF32 && zdt_fast(dtz) && is_code8(dty) && fast_ok(d, X, n, x, y)) {
+            const uint32_t nv = (uint32_t)(n / 4);
+            const dim3 g(grid_for(nv, kQBlock, kQGrid)), b(kQBlock);
 #define QLAUNCH(YD)                                                                                           \
     ZDT_SWITCH(dtz, QND_SWITCH(d.nd, hipLaunchKernelGGL((k_quant_v<YD, ZD, ND>), g, b, 0, sm, (const float*)x,  \
                                                         (const float*)s, z, (uint8_t*)y, d, nv)))
@@ -175,9 +223,9 @@ void qdq_entry(const char* name, const Tensor* X, const Tensor* S, const Tensor*
             }
 #undef QLAUNCH
             launched = true;
-        } else if (!QUANT && is_code8(dtx) && dts == kF32 && zdt_fast(dtz) && dty == kF32 && fast_ok(d, n, x, y, 16)) {
-            const uint32_t nv = (uint32_t)(n / kV);
-            const dim3 g(grid_for(nv, kBlock)), b(kBlock);
+        } else if (!QUANT && is_code8(dtx) && dts == kF32 && zdt_fast(dtz) && dty == kF32 && fast_ok(d, X, n, x, y)) {
+            const uint32_t nv = (uint32_t)(n / 4);
+            const dim3 g(grid_for(nv, kBlock * kU)), b(kBlock);
 #define DQLAUNCH(XD)                                                                                            \
     ZDT_SWITCH(dtz, QND_SWITCH(d.nd, hipLaunchKernelGGL((k_dequant_v<XD, ZD, ND>), g, b, 0, sm, (const uint8_t*)x, \
                                                         (const float*)s, z, (float*)y, d, nv)))

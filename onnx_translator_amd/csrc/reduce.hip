@@ -34,15 +34,15 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-// Block-wide reduction across the 16 waves of a 1024-thread block.
-template <bool MAX> __device__ __forceinline__ double block_reduce(double v, double* lds) {
+// Block-wide reduction across the NW waves of a block (NW * 64 threads).
+template <bool MAX, int NW = kWaves> __device__ __forceinline__ double block_reduce(double v, double* lds) {
     v = MAX ? wave_max(v) : wave_sum(v);
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
     if (l == 0) lds[w] = v;
     __syncthreads();
     double r = lds[0];
 #pragma unroll
-    for (int i = 1; i < kWaves; i++) {
+    for (int i = 1; i < NW; i++) {
         const double t = lds[i];
         r = MAX ? (t > r ? t : r) : r + t;
     }
@@ -95,6 +95,72 @@ __global__ __launch_bounds__(kRowThreads) void k_softmax_row_rt(const void* __re
     sum = block_reduce<false>(sum, lds);
     for (int64_t j = threadIdx.x; j < L; j += kRowThreads)
         st_d_rt(dty, Y, base + j, exp(ld_d_rt(dtx, X, base + j) - mx) / sum);
+}
+
+// Long rows, few of them (inner == 1, e.g. [64, 32000]): each row is split
+// over G blocks of 256 threads so the fp64 exp / divide work spreads over the
+// whole chip.  Three passes keep the reference's arithmetic: (1) block maxima,
+// (2) every block folds the G maxima into the row max M and sums exp(v - M)
+// over its chunk, (3) every block folds the G partial sums in a fixed order
+// and writes exp(v - M) / sum.  part holds 2 * rows * G doubles.
+constexpr int kSplitThreads = 256;
+
+template <int DIN>
+__global__ __launch_bounds__(kSplitThreads) void k_sm_split_max(const void* __restrict__ X, int dtx, int64_t L,
+                                                                int G, double* __restrict__ part) {
+    __shared__ double lds[kSplitThreads / 64];
+    const int64_t row = blockIdx.y, chunk = (L + G - 1) / G;
+    const int64_t j0 = blockIdx.x * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
+    const int64_t base = row * L;
+    double mx = -DBL_MAX;
+    for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) {
+        const double v = DIN >= 0 ? ld_d<(DIN >= 0 ? DIN : 0)>(X, base + j) : ld_d_rt(dtx, X, base + j);
+        mx = v > mx ? v : mx;
+    }
+    mx = block_reduce<true, kSplitThreads / 64>(mx, lds);
+    if (threadIdx.x == 0) part[row * G + blockIdx.x] = mx;
+}
+
+__device__ __forceinline__ double fold_max(const double* p, int G) {
+    double m = -DBL_MAX;
+    for (int g = 0; g < G; g++) m = p[g] > m ? p[g] : m;
+    return m;
+}
+
+template <int DIN>
+__global__ __launch_bounds__(kSplitThreads) void k_sm_split_sum(const void* __restrict__ X, int dtx, int64_t L,
+                                                                int G, double* __restrict__ part) {
+    __shared__ double lds[kSplitThreads / 64];
+    const int64_t row = blockIdx.y, chunk = (L + G - 1) / G, rows = gridDim.y;
+    const int64_t j0 = blockIdx.x * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
+    const int64_t base = row * L;
+    const double M = fold_max(part + row * G, G);
+    double sum = 0.0;
+    for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) {
+        const double v = DIN >= 0 ? ld_d<(DIN >= 0 ? DIN : 0)>(X, base + j) : ld_d_rt(dtx, X, base + j);
+        sum += exp(v - M);
+    }
+    sum = block_reduce<false, kSplitThreads / 64>(sum, lds);
+    if (threadIdx.x == 0) part[rows * G + row * G + blockIdx.x] = sum;
+}
+
+template <int DIN, int DOUT>
+__global__ __launch_bounds__(kSplitThreads) void k_sm_split_out(const void* __restrict__ X, int dtx,
+                                                                void* __restrict__ Y, int dty, int64_t L, int G,
+                                                                const double* __restrict__ part) {
+    const int64_t row = blockIdx.y, chunk = (L + G - 1) / G, rows = gridDim.y;
+    const int64_t j0 = blockIdx.x * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
+    const int64_t base = row * L;
+    const double M = fold_max(part + row * G, G);
+    const double* ps = part + rows * G + row * G;
+    double S = 0.0;
+    for (int g = 0; g < G; g++) S += ps[g];
+    for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) {
+        const double v = DIN >= 0 ? ld_d<(DIN >= 0 ? DIN : 0)>(X, base + j) : ld_d_rt(dtx, X, base + j);
+        const double r = exp(v - M) / S;
+        if constexpr (DOUT >= 0) st_d<DOUT>(Y, base + j, r);
+        else st_d_rt(dty, Y, base + j, r);
+    }
 }
 
 // inner > 1: one thread per (outer, r) column; rows of the axis are coalesced across threads.
@@ -161,6 +227,47 @@ __global__ __launch_bounds__(256) void k_maxpool(const void* __restrict__ X, voi
     }
 }
 
+// f32, LDS-tiled: block (tile, plane) stages the input rows that kTOH output
+// rows need (rows outside the image hold -inf, which never wins a strict >
+// against the -inf start, exactly like skipping them), then every thread
+// reduces its windows from LDS.  Loads are coalesced along W; outputs are
+// written along OW.
+constexpr int kTOH = 8;
+constexpr int kPoolLdsFloats = 8192;   // 32 KB
+
+__global__ __launch_bounds__(256) void k_maxpool_lds(const float* __restrict__ X, float* __restrict__ Y, PoolGeom g,
+                                                     int IR) {
+    __shared__ float tile[kPoolLdsFloats];
+    const int64_t plane = blockIdx.y;
+    const int oh0 = blockIdx.x * kTOH;
+    const int ih0 = oh0 * g.sh - g.pt;
+    const float* xp = X + plane * (int64_t)g.H * g.W;
+    const int total = IR * g.W;
+    for (int i = threadIdx.x; i < total; i += 256) {
+        const int r = i / g.W, c = i - r * g.W;
+        const int ih = ih0 + r;
+        tile[i] = (ih >= 0 && ih < g.H) ? xp[(int64_t)ih * g.W + c] : -__builtin_inff();
+    }
+    __syncthreads();
+    const int nrow = (g.OH - oh0) < kTOH ? (g.OH - oh0) : kTOH;
+    const int nout = nrow * g.OW;
+    float* yp = Y + plane * (int64_t)g.OH * g.OW + (int64_t)oh0 * g.OW;
+    for (int o = threadIdx.x; o < nout; o += 256) {
+        const int r = o / g.OW, ow = o - r * g.OW;
+        float best = -__builtin_inff();
+        for (int kh = 0; kh < g.KH; kh++) {
+            const float* trow = tile + (r * g.sh + kh * g.dh) * g.W;
+            for (int kw = 0; kw < g.KW; kw++) {
+                const int iw = ow * g.sw + kw * g.dw - g.pl;
+                if (iw < 0 || iw >= g.W) continue;
+                const float v = trow[iw];
+                if (v > best) best = v;
+            }
+        }
+        yp[o] = best;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_maxpool_rt(const void* __restrict__ X, int dtx, void* __restrict__ Y, int dty,
                                                     PoolGeom g, int64_t total) {
     const int64_t stride = (int64_t)gridDim.x * 256;
@@ -210,7 +317,34 @@ void softmax_forward(const Tensor* input, Tensor* output, int axis) {
     hipStream_t s = stream();
     const int dtx = (int)input->dtype, dty = (int)output->dtype;
     if (input->size) {
-        if (inner == 1) {
+        // Split rows over G blocks when there are too few rows to fill the chip.
+        int G = 1;
+        if (inner == 1 && outer < 2 * num_cus() && outer <= 65535) {
+            G = (int)((2 * num_cus() + outer - 1) / outer);
+            const int64_t gmax = (L + 2047) / 2048;            // at least ~2K elements per block
+            if (G > gmax) G = (int)gmax;
+            if (G > 64) G = 64;
+        }
+        if (inner == 1 && G > 1) {
+            double* part = (double*)pool_alloc(sizeof(double) * 2 * (size_t)outer * G);
+            if (!part) { st.finish(); return; }
+            const dim3 g((unsigned)G, (unsigned)outer), b(kSplitThreads);
+            if (dtx == kF32) {
+                hipLaunchKernelGGL((k_sm_split_max<kF32>), g, b, 0, s, x, dtx, L, G, part);
+                hipLaunchKernelGGL((k_sm_split_sum<kF32>), g, b, 0, s, x, dtx, L, G, part);
+                if (dty == kF32) hipLaunchKernelGGL((k_sm_split_out<kF32, kF32>), g, b, 0, s, x, dtx, y, dty, L, G, part);
+                else hipLaunchKernelGGL((k_sm_split_out<kF32, -1>), g, b, 0, s, x, dtx, y, dty, L, G, part);
+            } else {
+                hipLaunchKernelGGL((k_sm_split_max<-1>), g, b, 0, s, x, dtx, L, G, part);
+                hipLaunchKernelGGL((k_sm_split_sum<-1>), g, b, 0, s, x, dtx, L, G, part);
+                hipLaunchKernelGGL((k_sm_split_out<-1, -1>), g, b, 0, s, x, dtx, y, dty, L, G, part);
+            }
+            const bool ok = check_launch(name);
+            // The partials buffer returns to the pool once the stream has drained
+            // past its last use (pool buffers are reused in stream order).
+            pool_free(part);
+            if (!ok) { st.finish(); return; }
+        } else if (inner == 1) {
             bool done = false;
             if (outer <= 0x7FFFFFFF && L <= 0x7FFFFFFF) {
                 if (dtx == kF32 && dty == kF32) done = launch_row<kF32, kF32>(x, y, outer, L, s);
@@ -249,7 +383,13 @@ void max_pool_forward(const Tensor* X, Tensor* Y, PoolParams* p) {
     hipStream_t s = stream();
     if (total > 0) {
         const dim3 grid(grid_for((size_t)total, 256)), blk(256);
-        if (X->dtype == DTYPE_FLOAT32 && Y->dtype == DTYPE_FLOAT32)
+        const int IR = (kTOH - 1) * g.sh + (g.KH - 1) * g.dh + 1;
+        const bool lds_fits = g.KH > 0 && g.KW > 0 && g.sh > 0 && g.dh > 0 && (int64_t)IR * g.W <= kPoolLdsFloats &&
+                              (int64_t)g.N * g.C <= 65535;
+        if (X->dtype == DTYPE_FLOAT32 && Y->dtype == DTYPE_FLOAT32 && lds_fits) {
+            const dim3 tg((unsigned)((g.OH + kTOH - 1) / kTOH), (unsigned)(g.N * g.C));
+            hipLaunchKernelGGL(k_maxpool_lds, tg, blk, 0, s, (const float*)x, (float*)y, g, IR);
+        } else if (X->dtype == DTYPE_FLOAT32 && Y->dtype == DTYPE_FLOAT32)
             hipLaunchKernelGGL((k_maxpool<kF32, kF32>), grid, blk, 0, s, x, y, g, total);
         else
             hipLaunchKernelGGL(k_maxpool_rt, grid, blk, 0, s, x, (int)X->dtype, y, (int)Y->dtype, g, total);

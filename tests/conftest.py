@@ -22,6 +22,15 @@ def oracle_lib():
 @pytest.fixture(scope="session")
 def hip():
     """The HIP library driven through its C ABI; GPU tests fail loudly without it."""
+    # torch bundles its own libamdhip64.so.7.  Whichever copy is loaded first
+    # serves the whole process, and torch cannot initialise on a runtime that
+    # another library loaded before it.  Initialise torch first (as bench.py
+    # does) so the tests that use torch for device plumbing share its runtime.
+    try:
+        import torch
+        torch.cuda.init()
+    except Exception:
+        pass
     from tests.helpers import HipLib
     lib = HipLib()
     if lib.device_count() == 0:

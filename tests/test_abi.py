@@ -89,9 +89,11 @@ def test_host_roundtrip_through_memmove(lib):
     lib.lib.free_tensor(t)
 
 
-@pytest.mark.skipif(HipLib().device_count() > 0, reason="checks the no-GPU behaviour")
 def test_no_gpu_fails_loudly(lib):
-    assert lib.device_count() == 0
+    # Decided at run time, not at collection: loading the library while pytest
+    # collects would bind the process to its HIP runtime before torch loads.
+    if lib.device_count() > 0:
+        pytest.skip("checks the no-GPU behaviour")
     with pytest.raises(RuntimeError, match="no HIP device"):
         lib.binary("add", np.ones(4, np.float32), O.F32, np.ones(4, np.float32), O.F32, O.F32)
     # output untouched (zeros), as the reference's silent no-op leaves it

@@ -180,3 +180,36 @@ def test_config5_softmax(hip, oracle_lib):
     np.testing.assert_allclose(y.astype(np.float64).sum(axis=1), 1.0, rtol=1e-5)
     x2 = rng.normal(0, 3, (64, 1000)).astype(np.float32)
     assert_close(hip.softmax(x2, O.F32, O.F32, -1), oracle_lib.softmax(x2, O.F32, O.F32, -1), O.F32)
+
+
+@pytest.mark.parametrize("ydt,zdt", [(O.U8, O.U8), (O.I8, O.I8), (O.E4M3, O.E4M3), (O.E5M2, O.E5M2),
+                                     (O.I8, O.F32), (O.U8, O.F32)])
+def test_quantize_fast_path_boundaries(hip, oracle_lib, ydt, zdt):
+    """Inputs placed on and next to rounding ties of x / s, huge quotients and
+    special scales: the fp32 fast path must hand every doubtful lane to fp64."""
+    rng = np.random.default_rng(int(ydt) * 13 + int(zdt))
+    n = 1 << 16
+    s = np.float32(rng.uniform(0.003, 3.0))
+    k = rng.integers(-200, 200, n).astype(np.float64)
+    rel = rng.choice([0.0, 1e-7, -1e-7, 3e-7, -3e-7, 1e-6, -1e-6, 6e-8, -6e-8], n)
+    x = ((k + 0.5) * float(s) * (1.0 + rel)).astype(np.float32)
+    ulp = np.spacing(x).astype(np.float32)
+    x = np.where(rng.random(n) < 0.3, x + ulp * rng.integers(-2, 3, n).astype(np.float32), x).astype(np.float32)
+    x[:64] = np.array([2 ** 22, 2 ** 22 + 1, 2 ** 23 + 0.5, -2 ** 24, 1e30, -1e30, np.inf, -np.inf, np.nan, 0.0, -0.0,
+                       1e-40, -1e-45, 0.5, -0.5, 1.5] * 4, np.float32) * np.float32(s)
+    zvals = {O.U8: [0, 3, 128, 255], O.I8: [0, -5, 127, -128], O.E4M3: [0x00, 0x38, 0xB8, 0x01],
+             O.E5M2: [0x00, 0x3C, 0xBC, 0x01], O.F32: [0.0, 3.0, -2.5, 1e30]}[zdt]
+    for zv in zvals:
+        z = np.array([zv], O.STORAGE[zdt])
+        for sv in (s, np.float32(-s), np.float32(0.0), np.float32(-0.0), np.float32(1e-42), np.float32(np.inf),
+                   np.float32(np.nan)):
+            sa = np.array([sv], np.float32)
+            got = hip.qdq("quantize", x, O.F32, sa, O.F32, z, zdt, ydt)
+            ref = oracle_lib.qdq("quantize", x, O.F32, sa, O.F32, z, zdt, ydt)
+            assert_bitexact(got, ref, ydt, what=f"Q y={ydt} z={zv} s={sv}")
+    # per-axis scales with mixed magnitudes
+    x3 = x[: 64 * 1024].reshape(4, 64, 256)
+    sax = rng.uniform(0.001, 5.0, 64).astype(np.float32).reshape(1, 64, 1)
+    zax = np.array(zvals * 16, O.STORAGE[zdt])[:64].reshape(1, 64, 1)
+    assert_bitexact(hip.qdq("quantize", x3, O.F32, sax, O.F32, zax, zdt, ydt),
+                    oracle_lib.qdq("quantize", x3, O.F32, sax, O.F32, zax, zdt, ydt), ydt, what="Q per-axis")
