@@ -1,15 +1,26 @@
 // reduce.hip — Softmax and MaxPool for gfx950.
 //
 // Softmax (tensor_ops/tensor_ops.c:1231-1270): the tensor is viewed as
-// [outer, L, inner] around the axis.  max over the axis (from -DBL_MAX),
-// sum of exp(v - max) in double, output exp(v - max) / sum.  For inner == 1
-// one 1024-thread block owns a row: the row is read once into registers,
-// reduced with wave64 shuffles and an LDS exchange between the 16 waves, and
-// written once.  The double sum is a tree instead of the reference's
-// sequential loop (relative difference ~1e-16 before the final rounding).
+// [outer, L, inner] around the axis; per (outer, inner) column the reference
+// takes the max over the axis (from -DBL_MAX), sums exp(v - max) in double and
+// writes exp(v - max) / sum.  Kernels here:
+//   * many rows (inner == 1): one 1024-thread block per row, the row held in
+//     registers, wave64 shuffle + LDS reductions, read once / written once;
+//   * few long rows (inner == 1, e.g. [64, 32000]): each row is split over G
+//     blocks so the fp64 exp / divide work covers the chip: pass 1 writes each
+//     block's (max m_b, sum_b exp(v - m_b)); pass 2 folds them into the row's
+//     max M and sum S = sum_b s_b * exp(m_b - M) (fixed order) and writes
+//     exp(v - M) / S;
+//   * inner > 1: one thread per column, coalesced along the inner dimension.
+// All sums are in double; they are trees instead of the reference's sequential
+// loop, so results agree to ~1e-16 relative before the final rounding.
 //
 // MaxPool (tensor_ops.c:1116-1165): -inf start, in-bounds taps only, strict >
-// (NaN never wins, an all-padding window gives -inf, the first of +-0 wins).
+// in the reference's (kh, kw) order — NaN never wins, an all-padding window
+// gives -inf, the first of +-0 wins.  One wave per output row, one lane per
+// output column (no per-element integer division); a dedicated f32 kernel for
+// the ResNet 3x3 / stride 2 / pad 1 window reads each input row once with
+// 8-byte loads and takes the left tap from the neighbouring lane.
 #include <cfloat>
 
 #include "runtime.h"
@@ -35,7 +46,7 @@ __device__ __forceinline__ double wave_sum(double v) {
 }
 
 // Block-wide reduction across the NW waves of a block (NW * 64 threads).
-template <bool MAX, int NW = kWaves> __device__ __forceinline__ double block_reduce(double v, double* lds) {
+template <bool MAX, int NW> __device__ __forceinline__ double block_reduce(double v, double* lds) {
     v = MAX ? wave_max(v) : wave_sum(v);
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
     if (l == 0) lds[w] = v;
@@ -48,6 +59,15 @@ template <bool MAX, int NW = kWaves> __device__ __forceinline__ double block_red
     }
     __syncthreads();
     return r;
+}
+
+template <int DT> __device__ __forceinline__ double ldx(const void* p, int64_t i, int rdt) {
+    if constexpr (DT >= 0) return ld_d<DT>(p, i);
+    else return ld_d_rt(rdt, p, i);
+}
+template <int DT> __device__ __forceinline__ void stx(void* p, int64_t i, double v, int rdt) {
+    if constexpr (DT >= 0) st_d<DT>(p, i, v);
+    else st_d_rt(rdt, p, i, v);
 }
 
 // One block per row (inner == 1), the row kept in registers (IPT per thread).
@@ -63,7 +83,7 @@ __global__ __launch_bounds__(kRowThreads) void k_softmax_row(const void* __restr
         v[t] = j < L ? ld_d<DIN>(X, (int64_t)(base + j)) : -DBL_MAX;
         mx = v[t] > mx ? v[t] : mx;
     }
-    mx = block_reduce<true>(mx, lds);
+    mx = block_reduce<true, kWaves>(mx, lds);
     double sum = 0.0;
 #pragma unroll
     for (int t = 0; t < IPT; t++) {
@@ -71,7 +91,7 @@ __global__ __launch_bounds__(kRowThreads) void k_softmax_row(const void* __restr
         v[t] = j < L ? exp(v[t] - mx) : 0.0;
         sum += v[t];
     }
-    sum = block_reduce<false>(sum, lds);
+    sum = block_reduce<false, kWaves>(sum, lds);
 #pragma unroll
     for (int t = 0; t < IPT; t++) {
         const int j = threadIdx.x + t * kRowThreads;
@@ -89,78 +109,57 @@ __global__ __launch_bounds__(kRowThreads) void k_softmax_row_rt(const void* __re
         const double v = ld_d_rt(dtx, X, base + j);
         mx = v > mx ? v : mx;
     }
-    mx = block_reduce<true>(mx, lds);
+    mx = block_reduce<true, kWaves>(mx, lds);
     double sum = 0.0;
     for (int64_t j = threadIdx.x; j < L; j += kRowThreads) sum += exp(ld_d_rt(dtx, X, base + j) - mx);
-    sum = block_reduce<false>(sum, lds);
+    sum = block_reduce<false, kWaves>(sum, lds);
     for (int64_t j = threadIdx.x; j < L; j += kRowThreads)
         st_d_rt(dty, Y, base + j, exp(ld_d_rt(dtx, X, base + j) - mx) / sum);
 }
 
-// Long rows, few of them (inner == 1, e.g. [64, 32000]): each row is split
-// over G blocks of 256 threads so the fp64 exp / divide work spreads over the
-// whole chip.  Three passes keep the reference's arithmetic: (1) block maxima,
-// (2) every block folds the G maxima into the row max M and sums exp(v - M)
-// over its chunk, (3) every block folds the G partial sums in a fixed order
-// and writes exp(v - M) / sum.  part holds 2 * rows * G doubles.
+// Split rows: pass 1.  part[row * G + g] = m_b, part[rows * G + row * G + g] = s_b.
 constexpr int kSplitThreads = 256;
+constexpr int kSplitWaves = kSplitThreads / 64;
 
 template <int DIN>
-__global__ __launch_bounds__(kSplitThreads) void k_sm_split_max(const void* __restrict__ X, int dtx, int64_t L,
-                                                                int G, double* __restrict__ part) {
-    __shared__ double lds[kSplitThreads / 64];
-    const int64_t row = blockIdx.y, chunk = (L + G - 1) / G;
+__global__ __launch_bounds__(kSplitThreads) void k_sm_part(const void* __restrict__ X, int dtx, int64_t L, int G,
+                                                           double* __restrict__ part) {
+    __shared__ double lds[kSplitWaves];
+    const int64_t row = blockIdx.y, rows = gridDim.y, chunk = (L + G - 1) / G;
     const int64_t j0 = blockIdx.x * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
     const int64_t base = row * L;
     double mx = -DBL_MAX;
     for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) {
-        const double v = DIN >= 0 ? ld_d<(DIN >= 0 ? DIN : 0)>(X, base + j) : ld_d_rt(dtx, X, base + j);
+        const double v = ldx<DIN>(X, base + j, dtx);
         mx = v > mx ? v : mx;
     }
-    mx = block_reduce<true, kSplitThreads / 64>(mx, lds);
-    if (threadIdx.x == 0) part[row * G + blockIdx.x] = mx;
-}
-
-__device__ __forceinline__ double fold_max(const double* p, int G) {
-    double m = -DBL_MAX;
-    for (int g = 0; g < G; g++) m = p[g] > m ? p[g] : m;
-    return m;
-}
-
-template <int DIN>
-__global__ __launch_bounds__(kSplitThreads) void k_sm_split_sum(const void* __restrict__ X, int dtx, int64_t L,
-                                                                int G, double* __restrict__ part) {
-    __shared__ double lds[kSplitThreads / 64];
-    const int64_t row = blockIdx.y, chunk = (L + G - 1) / G, rows = gridDim.y;
-    const int64_t j0 = blockIdx.x * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
-    const int64_t base = row * L;
-    const double M = fold_max(part + row * G, G);
+    mx = block_reduce<true, kSplitWaves>(mx, lds);
     double sum = 0.0;
-    for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) {
-        const double v = DIN >= 0 ? ld_d<(DIN >= 0 ? DIN : 0)>(X, base + j) : ld_d_rt(dtx, X, base + j);
-        sum += exp(v - M);
+    for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) sum += exp(ldx<DIN>(X, base + j, dtx) - mx);
+    sum = block_reduce<false, kSplitWaves>(sum, lds);
+    if (threadIdx.x == 0) {
+        part[row * G + blockIdx.x] = mx;
+        part[rows * G + row * G + blockIdx.x] = sum;
     }
-    sum = block_reduce<false, kSplitThreads / 64>(sum, lds);
-    if (threadIdx.x == 0) part[rows * G + row * G + blockIdx.x] = sum;
 }
 
+// Split rows: pass 2.
 template <int DIN, int DOUT>
-__global__ __launch_bounds__(kSplitThreads) void k_sm_split_out(const void* __restrict__ X, int dtx,
-                                                                void* __restrict__ Y, int dty, int64_t L, int G,
-                                                                const double* __restrict__ part) {
-    const int64_t row = blockIdx.y, chunk = (L + G - 1) / G, rows = gridDim.y;
+__global__ __launch_bounds__(kSplitThreads) void k_sm_out(const void* __restrict__ X, int dtx, void* __restrict__ Y,
+                                                          int dty, int64_t L, int G, const double* __restrict__ part) {
+    const int64_t row = blockIdx.y, rows = gridDim.y, chunk = (L + G - 1) / G;
     const int64_t j0 = blockIdx.x * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
     const int64_t base = row * L;
-    const double M = fold_max(part + row * G, G);
+    const double* pm = part + row * G;
     const double* ps = part + rows * G + row * G;
-    double S = 0.0;
-    for (int g = 0; g < G; g++) S += ps[g];
-    for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) {
-        const double v = DIN >= 0 ? ld_d<(DIN >= 0 ? DIN : 0)>(X, base + j) : ld_d_rt(dtx, X, base + j);
-        const double r = exp(v - M) / S;
-        if constexpr (DOUT >= 0) st_d<DOUT>(Y, base + j, r);
-        else st_d_rt(dty, Y, base + j, r);
-    }
+    // Lane g folds partial g (G <= 64); every wave of every block of the row
+    // runs the same butterfly on the same values, so all agree on M and S.
+    const int lane = threadIdx.x & 63;
+    const double m_l = lane < G ? pm[lane] : -DBL_MAX;
+    const double M = wave_max(m_l);
+    const double S = wave_sum(lane < G ? ps[lane] * exp(m_l - M) : 0.0);
+    for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads)
+        stx<DOUT>(Y, base + j, exp(ldx<DIN>(X, base + j, dtx) - M) / S, dty);
 }
 
 // inner > 1: one thread per (outer, r) column; rows of the axis are coalesced across threads.
@@ -202,93 +201,60 @@ struct PoolGeom {
     int N, C, H, W, OH, OW, KH, KW, pt, pl, sh, sw, dh, dw;
 };
 
+constexpr int kPoolRows = 4;   // output rows per 256-thread block (one per wave)
+
+// Any window: wave per output row, lane per output column.
 template <int DIN, int DOUT>
-__global__ __launch_bounds__(256) void k_maxpool(const void* __restrict__ X, void* __restrict__ Y, PoolGeom g,
-                                                 int64_t total) {
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < total; o += stride) {
-        const int ow = (int)(o % g.OW);
-        const int64_t t1 = o / g.OW;
-        const int oh = (int)(t1 % g.OH);
-        const int64_t plane = t1 / g.OH;              // n * C + c
+__global__ __launch_bounds__(256) void k_maxpool_rows(const void* __restrict__ X, int dtx, void* __restrict__ Y,
+                                                      int dty, PoolGeom g, int64_t planes) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int oh = blockIdx.x * kPoolRows + wave;
+    if (oh >= g.OH) return;
+    for (int64_t plane = blockIdx.y; plane < planes; plane += gridDim.y) {
         const int64_t xb = plane * (int64_t)g.H * g.W;
-        double best = -__builtin_inf();
-        for (int kh = 0; kh < g.KH; kh++) {
-            const int ih = oh * g.sh + kh * g.dh - g.pt;
-            if (ih < 0 || ih >= g.H) continue;
-            for (int kw = 0; kw < g.KW; kw++) {
-                const int iw = ow * g.sw + kw * g.dw - g.pl;
-                if (iw < 0 || iw >= g.W) continue;
-                const double v = ld_d<DIN>(X, xb + (int64_t)ih * g.W + iw);
-                if (v > best) best = v;
+        const int64_t yb = (plane * g.OH + oh) * (int64_t)g.OW;
+        for (int ow = lane; ow < g.OW; ow += 64) {
+            double best = -__builtin_inf();
+            for (int kh = 0; kh < g.KH; kh++) {
+                const int ih = oh * g.sh + kh * g.dh - g.pt;
+                if (ih < 0 || ih >= g.H) continue;
+                const int64_t rb = xb + (int64_t)ih * g.W;
+                for (int kw = 0; kw < g.KW; kw++) {
+                    const int iw = ow * g.sw + kw * g.dw - g.pl;
+                    if (iw < 0 || iw >= g.W) continue;
+                    const double v = ldx<DIN>(X, rb + iw, dtx);
+                    if (v > best) best = v;
+                }
             }
+            stx<DOUT>(Y, yb + ow, best, dty);
         }
-        st_d<DOUT>(Y, o, best);
     }
 }
 
-// f32, LDS-tiled: block (tile, plane) stages the input rows that kTOH output
-// rows need (rows outside the image hold -inf, which never wins a strict >
-// against the -inf start, exactly like skipping them), then every thread
-// reduces its windows from LDS.  Loads are coalesced along W; outputs are
-// written along OW.
-constexpr int kTOH = 8;
-constexpr int kPoolLdsFloats = 8192;   // 32 KB
-
-__global__ __launch_bounds__(256) void k_maxpool_lds(const float* __restrict__ X, float* __restrict__ Y, PoolGeom g,
-                                                     int IR) {
-    __shared__ float tile[kPoolLdsFloats];
-    const int64_t plane = blockIdx.y;
-    const int oh0 = blockIdx.x * kTOH;
-    const int ih0 = oh0 * g.sh - g.pt;
-    const float* xp = X + plane * (int64_t)g.H * g.W;
-    const int total = IR * g.W;
-    for (int i = threadIdx.x; i < total; i += 256) {
-        const int r = i / g.W, c = i - r * g.W;
-        const int ih = ih0 + r;
-        tile[i] = (ih >= 0 && ih < g.H) ? xp[(int64_t)ih * g.W + c] : -__builtin_inff();
-    }
-    __syncthreads();
-    const int nrow = (g.OH - oh0) < kTOH ? (g.OH - oh0) : kTOH;
-    const int nout = nrow * g.OW;
-    float* yp = Y + plane * (int64_t)g.OH * g.OW + (int64_t)oh0 * g.OW;
-    for (int o = threadIdx.x; o < nout; o += 256) {
-        const int r = o / g.OW, ow = o - r * g.OW;
+// f32, 3x3 window, stride 2, top/left pad 1, W == 2 * OW, OW <= 64: lane l
+// loads columns (2l, 2l+1) of each input row with one 8-byte load and takes
+// column 2l-1 from lane l-1 (lane 0: the left padding, skipped).
+__global__ __launch_bounds__(256) void k_maxpool_3s2(const float* __restrict__ X, float* __restrict__ Y, PoolGeom g,
+                                                     int64_t planes) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int oh = blockIdx.x * kPoolRows + wave;
+    if (oh >= g.OH) return;
+    const bool live = lane < g.OW;
+    for (int64_t plane = blockIdx.y; plane < planes; plane += gridDim.y) {
+        const float* xp = X + plane * (int64_t)g.H * g.W;
         float best = -__builtin_inff();
-        for (int kh = 0; kh < g.KH; kh++) {
-            const float* trow = tile + (r * g.sh + kh * g.dh) * g.W;
-            for (int kw = 0; kw < g.KW; kw++) {
-                const int iw = ow * g.sw + kw * g.dw - g.pl;
-                if (iw < 0 || iw >= g.W) continue;
-                const float v = trow[iw];
-                if (v > best) best = v;
-            }
-        }
-        yp[o] = best;
-    }
-}
-
-__global__ __launch_bounds__(256) void k_maxpool_rt(const void* __restrict__ X, int dtx, void* __restrict__ Y, int dty,
-                                                    PoolGeom g, int64_t total) {
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < total; o += stride) {
-        const int ow = (int)(o % g.OW);
-        const int64_t t1 = o / g.OW;
-        const int oh = (int)(t1 % g.OH);
-        const int64_t plane = t1 / g.OH;
-        const int64_t xb = plane * (int64_t)g.H * g.W;
-        double best = -__builtin_inf();
-        for (int kh = 0; kh < g.KH; kh++) {
-            const int ih = oh * g.sh + kh * g.dh - g.pt;
+#pragma unroll
+        for (int kh = 0; kh < 3; kh++) {
+            const int ih = 2 * oh - 1 + kh;                     // uniform across the wave
             if (ih < 0 || ih >= g.H) continue;
-            for (int kw = 0; kw < g.KW; kw++) {
-                const int iw = ow * g.sw + kw * g.dw - g.pl;
-                if (iw < 0 || iw >= g.W) continue;
-                const double v = ld_d_rt(dtx, X, xb + (int64_t)ih * g.W + iw);
-                if (v > best) best = v;
-            }
+            float2 v = make_float2(-__builtin_inff(), -__builtin_inff());
+            if (live) v = *reinterpret_cast<const float2*>(xp + (int64_t)ih * g.W + 2 * lane);
+            const float left = __shfl_up(v.y, 1, 64);
+            if (lane > 0 && left > best) best = left;           // kw = 0: column 2l - 1
+            if (v.x > best) best = v.x;                          // kw = 1: column 2l
+            if (v.y > best) best = v.y;                          // kw = 2: column 2l + 1
         }
-        st_d_rt(dty, Y, o, best);
+        if (live) Y[(plane * g.OH + oh) * (int64_t)g.OW + lane] = best;
     }
 }
 
@@ -320,8 +286,8 @@ void softmax_forward(const Tensor* input, Tensor* output, int axis) {
         // Split rows over G blocks when there are too few rows to fill the chip.
         int G = 1;
         if (inner == 1 && outer < 2 * num_cus() && outer <= 65535) {
-            G = (int)((2 * num_cus() + outer - 1) / outer);
-            const int64_t gmax = (L + 2047) / 2048;            // at least ~2K elements per block
+            G = (int)((4 * num_cus() + outer - 1) / outer);
+            const int64_t gmax = (L + 1023) / 1024;            // at least ~1K elements per block
             if (G > gmax) G = (int)gmax;
             if (G > 64) G = 64;
         }
@@ -330,18 +296,15 @@ void softmax_forward(const Tensor* input, Tensor* output, int axis) {
             if (!part) { st.finish(); return; }
             const dim3 g((unsigned)G, (unsigned)outer), b(kSplitThreads);
             if (dtx == kF32) {
-                hipLaunchKernelGGL((k_sm_split_max<kF32>), g, b, 0, s, x, dtx, L, G, part);
-                hipLaunchKernelGGL((k_sm_split_sum<kF32>), g, b, 0, s, x, dtx, L, G, part);
-                if (dty == kF32) hipLaunchKernelGGL((k_sm_split_out<kF32, kF32>), g, b, 0, s, x, dtx, y, dty, L, G, part);
-                else hipLaunchKernelGGL((k_sm_split_out<kF32, -1>), g, b, 0, s, x, dtx, y, dty, L, G, part);
+                hipLaunchKernelGGL((k_sm_part<kF32>), g, b, 0, s, x, dtx, L, G, part);
+                if (dty == kF32) hipLaunchKernelGGL((k_sm_out<kF32, kF32>), g, b, 0, s, x, dtx, y, dty, L, G, part);
+                else hipLaunchKernelGGL((k_sm_out<kF32, -1>), g, b, 0, s, x, dtx, y, dty, L, G, part);
             } else {
-                hipLaunchKernelGGL((k_sm_split_max<-1>), g, b, 0, s, x, dtx, L, G, part);
-                hipLaunchKernelGGL((k_sm_split_sum<-1>), g, b, 0, s, x, dtx, L, G, part);
-                hipLaunchKernelGGL((k_sm_split_out<-1, -1>), g, b, 0, s, x, dtx, y, dty, L, G, part);
+                hipLaunchKernelGGL((k_sm_part<-1>), g, b, 0, s, x, dtx, L, G, part);
+                hipLaunchKernelGGL((k_sm_out<-1, -1>), g, b, 0, s, x, dtx, y, dty, L, G, part);
             }
             const bool ok = check_launch(name);
-            // The partials buffer returns to the pool once the stream has drained
-            // past its last use (pool buffers are reused in stream order).
+            // Pool buffers are reused in stream order, so the partials can go back now.
             pool_free(part);
             if (!ok) { st.finish(); return; }
         } else if (inner == 1) {
@@ -375,24 +338,27 @@ void max_pool_forward(const Tensor* X, Tensor* Y, PoolParams* p) {
     g.dh = p->dilations[0]; g.dw = p->dilations[1];
     if (Y->shape[0] != g.N || Y->shape[1] != g.C) { set_error("%s: Y batch/channels differ from X", name); return; }
     if (!ensure_device()) return;
-    const int64_t total = (int64_t)g.N * g.C * g.OH * g.OW;
+    const int64_t planes = (int64_t)g.N * g.C;
+    const int64_t total = planes * g.OH * g.OW;
     Staging st;
     const void* x = st.in(X);
     void* y = st.out(Y, (size_t)total * dt_bytes((int)Y->dtype));
     if (!x || !y) { st.finish(); return; }
     hipStream_t s = stream();
     if (total > 0) {
-        const dim3 grid(grid_for((size_t)total, 256)), blk(256);
-        const int IR = (kTOH - 1) * g.sh + (g.KH - 1) * g.dh + 1;
-        const bool lds_fits = g.KH > 0 && g.KW > 0 && g.sh > 0 && g.dh > 0 && (int64_t)IR * g.W <= kPoolLdsFloats &&
-                              (int64_t)g.N * g.C <= 65535;
-        if (X->dtype == DTYPE_FLOAT32 && Y->dtype == DTYPE_FLOAT32 && lds_fits) {
-            const dim3 tg((unsigned)((g.OH + kTOH - 1) / kTOH), (unsigned)(g.N * g.C));
-            hipLaunchKernelGGL(k_maxpool_lds, tg, blk, 0, s, (const float*)x, (float*)y, g, IR);
-        } else if (X->dtype == DTYPE_FLOAT32 && Y->dtype == DTYPE_FLOAT32)
-            hipLaunchKernelGGL((k_maxpool<kF32, kF32>), grid, blk, 0, s, x, y, g, total);
+        const dim3 grid((unsigned)((g.OH + kPoolRows - 1) / kPoolRows), (unsigned)(planes < 65535 ? planes : 65535));
+        const dim3 blk(256);
+        const int dtx = (int)X->dtype, dty = (int)Y->dtype;
+        const bool f32 = dtx == kF32 && dty == kF32;
+        const bool res3s2 = f32 && g.KH == 3 && g.KW == 3 && g.sh == 2 && g.sw == 2 && g.dh == 1 && g.dw == 1 &&
+                            g.pt == 1 && g.pl == 1 && g.W == 2 * g.OW && g.OW <= 64 && 2 * g.OH <= g.H + 2 &&
+                            ((uintptr_t)x & 7) == 0;
+        if (res3s2)
+            hipLaunchKernelGGL(k_maxpool_3s2, grid, blk, 0, s, (const float*)x, (float*)y, g, planes);
+        else if (f32)
+            hipLaunchKernelGGL((k_maxpool_rows<kF32, kF32>), grid, blk, 0, s, x, dtx, y, dty, g, planes);
         else
-            hipLaunchKernelGGL(k_maxpool_rt, grid, blk, 0, s, x, (int)X->dtype, y, (int)Y->dtype, g, total);
+            hipLaunchKernelGGL((k_maxpool_rows<-1, -1>), grid, blk, 0, s, x, dtx, y, dty, g, planes);
         if (!check_launch(name)) { st.finish(); return; }
     }
     st.finish();
