@@ -233,6 +233,20 @@ __device__ __forceinline__ void st_stream(float4* p, float4 v) {
     __builtin_nontemporal_store(t, reinterpret_cast<f32x4_t*>(p));
 }
 __device__ __forceinline__ uint32_t ld_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+
+// Buffer resources: loads at byte offsets >= `bytes` return zero without a
+// memory access, so a tile beyond the end of a tensor can be loaded without a
+// branch (which would force the compiler to wait for every outstanding load).
+// Word 3 is the gfx9 raw-buffer format (32-bit data, no swizzle).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// 16-byte nontemporal load through a buffer resource.
+__device__ __forceinline__ float4 ld_buf_stream(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    typedef unsigned int u32x4_t __attribute__((__vector_size__(16)));
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 2 /* nt */);
+    return make_float4(u2f(v[0]), u2f(v[1]), u2f(v[2]), u2f(v[3]));
+}
 __device__ __forceinline__ void st_stream(uint32_t* p, uint32_t v) { __builtin_nontemporal_store(v, p); }
 
 // ----------------------------------------------------------------------------

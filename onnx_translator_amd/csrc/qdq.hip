@@ -6,30 +6,48 @@
 // Scale and zero point are indexed through a broadcast descriptor against Y
 // (scalar, per-axis or full-size), so nothing is materialised.
 //
-// Quantize fast path (exact).  The reference rounds the fp64 quotient
-// q64 = RN64(x / s).  We form q32 = RN32(x * RN32(1 / s)), which is within
-// 2^-23 |x/s| of the exact quotient, and q64 is within 2^-53 of it.  When q32
-// lies more than 2^-22 |q32| away from the nearest half-integer (and
-// |q32| < 2^22) all three values fall strictly inside the same rounding
-// interval, so rint(q32) == rint(q64); the remaining lanes (about 2^-21 of
-// them: near-ties, huge quotients, NaN / inf, s == 0) take the fp64 division.
-// For integer outputs the fast path also needs an integral zero point, so
-// that rint(q) + zp stays an exactly representable integer in fp32; fp8
-// outputs are rounded once to fp32 exactly as the reference's (float)res.
+// Quantize fast path (exact, branch-free).  The reference rounds the fp64
+// quotient: rint(RN64(x / s)).  For fp32 x and s that equals the
+// round-half-even of the exact rational x / s whenever |x / s| < 2^27: for a
+// quotient that is not a half-integer, x / s - (k + 1/2) = (2x - (2k+1)s) / 2s,
+// whose numerator is a nonzero multiple of 2^(min(ex,es)-23), so the distance
+// to the nearest half-integer is at least 2^-25 once ex >= es (and larger
+// otherwise), while RN64's error is at most 2^(ex-es-52) < 2^-25 below 2^27:
+// RN64 neither creates nor crosses a tie.  Per element the kernel forms
+//     r = rint(x * rcp(s))            (any approximation of 1/s will do)
+//     rho = fma(-r, s, x)             (= RN32(x - r s), one rounding)
+// and accepts r when |rho| < |s| / 2.  RN32 is monotone and |s| / 2 is exact, so
+// |rho| < |s|/2 implies |x - r s| < |s|/2, i.e. r is the unique nearest integer
+// to x / s.  Every other lane (ties, a poor r, s == 0, s or x NaN / inf, huge
+// quotients) takes the fp64 division, under one wave-level branch.
+// The zero point must be integral with |zp| < 2^22 for the fast path, so that
+// v = r + zp is an exact fp32 integer below 2^24 whenever |r| < 2^23; beyond
+// that every output format saturates (or, e5m2, overflows to inf) for both v
+// and the reference's value, so the result is the same code.  Codes are formed
+// by hardware conversions, each checked against the reference encoders over
+// all 2^32 fp32 inputs on gfx950:
+//   u8 / i8  v_cvt_pk_u8_f32 rounds half-even and clamps to [0, 255]; on an
+//            exact integer v it is the reference's saturate((int64_t)rint(v))
+//            (i8 adds 128 first and flips bit 7 after);
+//   e4m3     v_cvt_pk_fp8_f32 equals the reference encoder for every input of
+//            magnitude >= 2^-6 up to 464 and for +-0; integers are clamped to
+//            +-448 first (the reference saturates to 0x7E);
+//   e5m2     v_cvt_pk_bf8_f32 equals the reference encoder for every non-NaN
+//            input of magnitude >= 2^-14 (including overflow to inf) and +-0.
+// Integral v never falls in the flush-to-zero band, so the hardware's
+// subnormal outputs never arise.
 //
-// Launch shapes (measured on MI355X): quantize — one 16-byte f32 load per
-// thread per iteration, 512-thread blocks, grid-stride over 2048 blocks;
-// dequantize — four 4-byte code loads per thread, 256-thread blocks.  Both
-// read and write with nontemporal (streaming) accesses.
+// Launch shapes (swept on MI355X; 64 MiB f32 <-> 16 MiB codes, not cache-resident):
+// quantize — software-pipelined grid-stride loop, kQU 16-byte nontemporal
+// loads per thread, plain 4-byte stores (nontemporal 4-byte stores cost ~1 us),
+// 256-thread blocks, 8 blocks per CU; dequantize — one 4-byte code load and
+// one 16-byte nontemporal store per thread, 256-thread blocks, full grid.
 #include "runtime.h"
 
 namespace tohip {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kQBlock = 512;
-constexpr int kQGrid = 2048;
-constexpr int kU = 4;        // dequantize: 4-element groups per thread, group u of a block is one contiguous span
 
 template <int YDT> __device__ __forceinline__ uint8_t code8(double r) {
     if constexpr (YDT == kU8) return (uint8_t)sat(cvt_i64(__builtin_rint(r)), 0, 255);
@@ -41,115 +59,291 @@ template <int YDT> __device__ __forceinline__ uint8_t code8(double r) {
 
 __device__ __forceinline__ double qval(double x, double s, double z) { return s != 0.0 ? __builtin_rint(x / s) + z : z; }
 
-// Integral zero point small enough that rint(q) + zp (|rint(q)| < 2^22) stays
-// an exact fp32 integer below 2^23, far from the int64 conversion limits.
-__device__ __forceinline__ bool zint_ok(float zf, double z) {
-    return __builtin_fabsf(zf) < 0x1p22f && __builtin_rintf(zf) == zf && (double)zf == z;
+// Quantization parameters of one scale / zero-point pair.
+struct QParm {
+    float s, rs, hs, zf;   // scale, ~1/s, |s|/2, zero point (+128 for i8 outputs)
+    double zd;             // zero point as the reference reads it
+    bool fast;             // zero point integral with |zp| < 2^22
+};
+
+template <int YDT>
+__device__ __forceinline__ QParm qparm(float s, double zd) {
+    QParm p;
+    p.s = s;
+    p.rs = __builtin_amdgcn_rcpf(s);
+    p.hs = __builtin_fabsf(s) * 0.5f;
+    p.zd = zd;
+    const float zf = (float)p.zd;
+    p.fast = (double)zf == p.zd && __builtin_rintf(zf) == zf && __builtin_fabsf(zf) < 0x1p22f;
+    p.zf = (YDT == kI8) ? zf + 128.0f : zf;
+    return p;
 }
 
-// Code of one element: fp32 fast path with the fp64 fallback described above.
-// rs = RN32(1 / s); zint: the zero point is an integer (needed for int outputs).
+// r + zp of one element through the fast path; good becomes false when the
+// lane must be recomputed exactly.
+__device__ __forceinline__ float qfast(float x, const QParm& p, bool& good) {
+    const float r = __builtin_rintf(x * p.rs);
+    const float rho = __builtin_fmaf(-r, p.s, x);
+    good = good && p.fast && (__builtin_fabsf(rho) < p.hs);
+    return r + p.zf;
+}
+
+// Codes of four fast-path values, little-endian in one word.
 template <int YDT>
-__device__ __forceinline__ uint32_t qcode(float x, float s, float rs, float zf, double zd, bool zint) {
-    const float q = x * rs;
-    const float aq = __builtin_fabsf(q);
-    const float d = __builtin_fabsf(__builtin_amdgcn_fractf(aq) - 0.5f);
-    const bool ok = (aq < 0x1p22f) && (d > aq * 0x1p-22f) && (s != 0.0f) && (YDT == kE4M3 || YDT == kE5M2 || zint);
-    if (__builtin_expect(ok, 1)) {
-        const float r = __builtin_rintf(q) + zf;
-        if constexpr (YDT == kU8) return (uint32_t)(int)__builtin_amdgcn_fmed3f(r, 0.0f, 255.0f);
-        else if constexpr (YDT == kI8) return (uint32_t)(uint8_t)(int8_t)(int)__builtin_amdgcn_fmed3f(r, -128.0f, 127.0f);
-        else if constexpr (YDT == kE4M3) return enc_e4m3(r);
-        else return enc_e5m2(r);
+__device__ __forceinline__ uint32_t qpack4(float v0, float v1, float v2, float v3) {
+    uint32_t w;
+    if constexpr (YDT == kU8 || YDT == kI8) {
+        w = __builtin_amdgcn_cvt_pk_u8_f32(v0, 0, 0u);
+        w = __builtin_amdgcn_cvt_pk_u8_f32(v1, 1, w);
+        w = __builtin_amdgcn_cvt_pk_u8_f32(v2, 2, w);
+        w = __builtin_amdgcn_cvt_pk_u8_f32(v3, 3, w);
+        if constexpr (YDT == kI8) w ^= 0x80808080u;
+    } else if constexpr (YDT == kE4M3) {
+        v0 = __builtin_amdgcn_fmed3f(v0, -448.0f, 448.0f);
+        v1 = __builtin_amdgcn_fmed3f(v1, -448.0f, 448.0f);
+        v2 = __builtin_amdgcn_fmed3f(v2, -448.0f, 448.0f);
+        v3 = __builtin_amdgcn_fmed3f(v3, -448.0f, 448.0f);
+        w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+        w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, (int)w, true);
+    } else {
+        w = (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(v0, v1, 0, false);
+        w = (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(v2, v3, (int)w, true);
     }
+    return w;
+}
+
+// The reference's arithmetic for four elements: fp64 quotient, rint, + zp.
+template <int YDT>
+__device__ __forceinline__ uint32_t qslow4(float x0, float x1, float x2, float x3, float s, double zd) {
+    const double sd = (double)s;
+    return (uint32_t)code8<YDT>(qval((double)x0, sd, zd)) | ((uint32_t)code8<YDT>(qval((double)x1, sd, zd)) << 8) |
+           ((uint32_t)code8<YDT>(qval((double)x2, sd, zd)) << 16) |
+           ((uint32_t)code8<YDT>(qval((double)x3, sd, zd)) << 24);
+}
+
+template <int YDT>
+__device__ __forceinline__ uint8_t qslow1(float x, float s, double zd) {
     return code8<YDT>(qval((double)x, (double)s, zd));
 }
 
-// Quantize f32 -> 1-byte code.  X and Y are flat (X has Y's size); Scale and
-// ZeroPoint go through the descriptor (operands 1 and 2).  A thread handles
-// 4 consecutive elements per iteration (one 16-byte load, one 4-byte store),
-// so each load / store instruction is contiguous across the wave.
-// Requires n % 4 == 0 and dim[nd-1] % 4 == 0.
-template <int YDT, int ZDT, int ND>
-__global__ __launch_bounds__(kQBlock) void k_quant_v(const float* __restrict__ X, const float* __restrict__ S,
-                                                     const void* __restrict__ Z, uint8_t* __restrict__ Y, BDesc d,
-                                                     uint32_t nv) {
-    const int inner = d.nd - 1;
-    const int64_t ss = d.st[1][inner], sz = d.st[2][inner];
-    const bool uniform = (ND == 1) && ss == 0 && sz == 0;      // per-tensor scale / zero point
-    const float su = S[0];
-    const double zu = ld_d<ZDT>(Z, 0);
-    const float rsu = 1.0f / su, zfu = (float)zu;
-    const bool zintu = zint_ok(zfu, zu);
-    const float4* X4 = reinterpret_cast<const float4*>(X);
-    uint32_t* Y4 = reinterpret_cast<uint32_t*>(Y);
-    for (uint32_t v = blockIdx.x * kQBlock + threadIdx.x; v < nv; v += gridDim.x * kQBlock) {
-        const float4 xv = ld_stream(X4 + v);
-        const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
-        uint32_t w = 0;
-        if (uniform) {
-#pragma unroll
-            for (int b = 0; b < 4; b++) w |= qcode<YDT>(xs[b], su, rsu, zfu, zu, zintu) << (8 * b);
+// One unit of work: 4 consecutive elements (one 16-byte X load or one 4-byte
+// code word) with the scale / zero-point values they need, loaded together so
+// that the parameter loads overlap the data loads.  MODE 0: one pair for the
+// tensor (not stored per unit); 1: one pair per unit; 2: one pair per element;
+// 3: one pair per wave — the 64 units of a wave are 256 consecutive elements
+// starting at a multiple of 256 and the parameters change only every `inner`
+// elements, a multiple of 256, so the wave shares one pair, located from its
+// first unit's index (uniform: its address math and loads go to the scalar unit).
+template <int ZDT> using zraw_t = typename std::conditional<ZDT == kF32, float, uint8_t>::type;
+
+template <int ZDT, int MODE>
+struct Params {
+    static constexpr int kN = MODE == 2 ? 4 : 1;
+    float s[kN];
+    zraw_t<ZDT> z[kN];
+};
+
+// Per-axis parameters (MODE 1 and 3): element e uses Scale[(e / inner) % C]
+// and ZeroPoint[zs * ((e / inner) % C)], zs = 0 for a single zero point.
+struct AxisDesc {
+    FastDiv inner, c;
+    uint32_t zs;
+};
+
+template <int ZDT, int MODE, int ND>
+__device__ __forceinline__ void load_params(Params<ZDT, MODE>& p, const float* S, const void* Z, const BDesc& d,
+                                            const AxisDesc& ax, uint32_t v) {
+    if constexpr (MODE == 1 || MODE == 3) {
+        const uint32_t q = ax.inner.div(v * 4u);
+        const uint32_t ch = q - ax.c.div(q) * ax.c.d;
+        const uint32_t zi = ch * ax.zs;
+        p.s[0] = S[ch];
+        if constexpr (MODE == 3 && ZDT != kF32) {
+            // v is the wave's first unit (uniform), so both loads are scalar.  A
+            // 1-byte zero point is read as the aligned 32-bit word that holds it
+            // (the host selects this mode only when ZeroPoint's byte size and
+            // address are multiples of 4, so that word lies inside the tensor).
+            const uint32_t w = reinterpret_cast<const uint32_t*>(Z)[zi >> 2];
+            p.z[0] = (uint8_t)(w >> (8 * (zi & 3)));
         } else {
-            int64_t off[3];
-            bd_offsets32<3, ND>(d, v * 4u, off);
-            if (ss == 0 && sz == 0) {                           // per-axis: one channel per group
-                const float s = S[off[1]];
-                const double z = ld_d<ZDT>(Z, off[2]);
-                const float rs = 1.0f / s, zf = (float)z;
-                const bool zi = zint_ok(zf, z);
-#pragma unroll
-                for (int b = 0; b < 4; b++) w |= qcode<YDT>(xs[b], s, rs, zf, z, zi) << (8 * b);
-            } else {
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const float s = S[off[1] + b * ss];
-                    const double z = ld_d<ZDT>(Z, off[2] + b * sz);
-                    const float zf = (float)z;
-                    w |= qcode<YDT>(xs[b], s, 1.0f / s, zf, z, zint_ok(zf, z)) << (8 * b);
-                }
-            }
+            p.z[0] = reinterpret_cast<const zraw_t<ZDT>*>(Z)[zi];
         }
-        st_stream(Y4 + v, w);
+    } else if constexpr (MODE == 2) {
+        int64_t off[3];
+        bd_offsets32<3, ND>(d, v * 4u, off);
+        const zraw_t<ZDT>* Zt = reinterpret_cast<const zraw_t<ZDT>*>(Z);
+        const int inner = d.nd - 1;
+        const int64_t ss = d.st[1][inner], sz = d.st[2][inner];
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            p.s[b] = S[off[1] + b * ss];
+            p.z[b] = Zt[off[2] + b * sz];
+        }
     }
 }
 
-// Dequantize 1-byte code -> f32: kU 4-byte code loads per thread, float4
-// streaming stores.  (x - zp) * s is evaluated in fp64 and rounded once.
-template <int XDT, int ZDT, int ND>
+constexpr int kQU = 4;         // quantize: float4 units per thread and iteration
+constexpr int kQBlocksPerCU = 8;
+constexpr uint32_t kMaxUnitsPerLaunch = 1u << 27;   // 2 GiB of f32 per launch: buffer offsets stay below 2^32
+
+// Codes of the 4 elements of one float4 of X.
+template <int YDT, int ZDT, int MODE>
+__device__ __forceinline__ uint32_t quant_unit(const float4 xv, const Params<ZDT, MODE>& pp, const QParm& pu) {
+    const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+    uint32_t w;
+    if constexpr (MODE == 2) {
+        float q[4];
+        double zd[4];
+        bool good = true;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            zd[b] = ld_d<ZDT>(&pp.z[b], 0);
+            q[b] = qfast(xs[b], qparm<YDT>(pp.s[b], zd[b]), good);
+        }
+        w = qpack4<YDT>(q[0], q[1], q[2], q[3]);
+        if (!good) {
+            w = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) w |= (uint32_t)qslow1<YDT>(xs[b], pp.s[b], zd[b]) << (8 * b);
+        }
+    } else {
+        const QParm p = (MODE == 0) ? pu : qparm<YDT>(pp.s[0], ld_d<ZDT>(&pp.z[0], 0));
+        bool good = true;
+        const float q0 = qfast(xs[0], p, good), q1 = qfast(xs[1], p, good);
+        const float q2 = qfast(xs[2], p, good), q3 = qfast(xs[3], p, good);
+        w = qpack4<YDT>(q0, q1, q2, q3);
+        if (!good) w = qslow4<YDT>(xs[0], xs[1], xs[2], xs[3], p.s, p.zd);
+    }
+    return w;
+}
+
+// One tile: kQU float4 units per thread, unit u of a block is one contiguous span.
+template <int ZDT, int MODE>
+struct QTile {
+    float4 x[kQU];
+    Params<ZDT, MODE> p[kQU];
+};
+
+// Loads tile t.  X goes through the buffer resource (units at or beyond nv
+// read as zero without touching memory); parameter indices are clamped to the
+// last unit, so every parameter load stays inside Scale / ZeroPoint.
+template <int ZDT, int MODE, int ND>
+__device__ __forceinline__ void qload(QTile<ZDT, MODE>& q, __amdgpu_buffer_rsrc_t xr, const float* S, const void* Z,
+                                      const BDesc& d, const AxisDesc& ax, uint32_t vbase, uint32_t nv, uint32_t t) {
+    // first thread of this wave, as a uniform value (MODE 3 indexes parameters per wave)
+    const uint32_t wbase = __builtin_amdgcn_readfirstlane(threadIdx.x) & ~63u;
+#pragma unroll
+    for (int u = 0; u < kQU; u++) {
+        const uint32_t v = t * (kBlock * kQU) + u * kBlock + threadIdx.x;
+        q.x[u] = ld_buf_stream(xr, v * 16u);
+        const uint32_t vp = MODE == 3 ? t * (kBlock * kQU) + u * kBlock + wbase : v;
+        load_params<ZDT, MODE, ND>(q.p[u], S, Z, d, ax, vbase + min(vp, nv - 1));
+    }
+}
+
+template <int YDT, int ZDT, int MODE>
+__device__ __forceinline__ void qstore(const QTile<ZDT, MODE>& q, uint32_t* Y4, const QParm& pu, uint32_t nv,
+                                       uint32_t t) {
+#pragma unroll
+    for (int u = 0; u < kQU; u++) {
+        const uint32_t v = t * (kBlock * kQU) + u * kBlock + threadIdx.x;
+        const uint32_t w = quant_unit<YDT, ZDT, MODE>(q.x[u], q.p[u], pu);
+        if (v < nv) Y4[v] = w;
+    }
+}
+
+// Quantize f32 -> 1-byte code.  X and Y are flat (X has Y's size) and hold
+// the nv units starting at unit vbase of the tensor; Scale and ZeroPoint go
+// through the descriptor (operands 1 and 2).  MODE 0: one scale / zero point
+// for the tensor; 1: constant across each 4-element group (per-axis on a
+// non-innermost axis); 2: anything else (per-element parameters).
+// Requires n % 4 == 0, dim[nd-1] % 4 == 0 and nv * 16 < 2^32.
+// Block b handles tiles b, b + G, b + 2G, ... (G = gridDim.x) with two tiles
+// of registers in ping-pong: the loads of the next tile are issued before
+// the current tile is converted, and since those loads are unconditional the
+// compiler waits only for the current tile's data.
+template <int YDT, int ZDT, int MODE, int ND>
+__global__ __launch_bounds__(kBlock) void k_quant_v(const float* __restrict__ X, const float* __restrict__ S,
+                                                    const void* __restrict__ Z, uint8_t* __restrict__ Y, BDesc d,
+                                                    AxisDesc ax, uint32_t vbase, uint32_t nv) {
+    uint32_t* Y4 = reinterpret_cast<uint32_t*>(Y);
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, nv * 16u);
+    QParm pu{};
+    if constexpr (MODE == 0) pu = qparm<YDT>(S[0], ld_d<ZDT>(Z, 0));
+    const uint32_t ntiles = (nv + kBlock * kQU - 1) / (kBlock * kQU);
+    uint32_t t = blockIdx.x;
+    QTile<ZDT, MODE> A, B;
+    qload<ZDT, MODE, ND>(A, xr, S, Z, d, ax, vbase, nv, t);
+    while (t < ntiles) {
+        const uint32_t t1 = t + gridDim.x;
+        qload<ZDT, MODE, ND>(B, xr, S, Z, d, ax, vbase, nv, t1);
+        qstore<YDT, ZDT, MODE>(A, Y4, pu, nv, t);
+        if (t1 >= ntiles) break;
+        const uint32_t t2 = t1 + gridDim.x;
+        qload<ZDT, MODE, ND>(A, xr, S, Z, d, ax, vbase, nv, t2);
+        qstore<YDT, ZDT, MODE>(B, Y4, pu, nv, t1);
+        t = t2;
+    }
+}
+
+// Four codes of one word -> fp32 values (exact).  fp8 codes use the gfx950
+// conversions v_cvt_pk_f32_fp8 / _bf8, which equal the reference decoders
+// (tensor_ops.c:236-256, 295-316) on all 256 codes; NaN codes give a NaN.
+template <int XDT>
+__device__ __forceinline__ void decode4(uint32_t w, float (&x)[4]) {
+    if constexpr (XDT == kE4M3 || XDT == kE5M2) {
+        typedef float f32x2_t __attribute__((ext_vector_type(2)));
+        f32x2_t lo, hi;
+        if constexpr (XDT == kE4M3) {
+            lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+            hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+        } else {
+            lo = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, false);
+            hi = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, true);
+        }
+        x[0] = lo.x; x[1] = lo.y; x[2] = hi.x; x[3] = hi.y;
+    } else {
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const uint8_t c = (uint8_t)(w >> (8 * b));
+            x[b] = (float)ld_d<XDT>(&c, 0);
+        }
+    }
+}
+
+// Dequantize 1-byte code -> f32: one 4-byte code word per thread and one
+// float4 nontemporal store, full grid (grid-stride beyond 2^20 blocks).
+// (x - zp) * s is evaluated in fp64 and rounded once.
+template <int XDT, int ZDT, int MODE, int ND>
 __global__ __launch_bounds__(kBlock) void k_dequant_v(const uint8_t* __restrict__ X, const float* __restrict__ S,
                                                       const void* __restrict__ Z, float* __restrict__ Y, BDesc d,
-                                                      uint32_t nv) {
-    const int inner = d.nd - 1;
-    const int64_t ss = d.st[1][inner], sz = d.st[2][inner];
-    const bool uniform = (ND == 1) && ss == 0 && sz == 0;
-    const double su = (double)S[0], zu = ld_d<ZDT>(Z, 0);
+                                                      AxisDesc ax, uint32_t vbase, uint32_t nv) {
     const uint32_t* X4 = reinterpret_cast<const uint32_t*>(X);
     float4* Y4 = reinterpret_cast<float4*>(Y);
-    for (uint32_t base = blockIdx.x * (kBlock * kU); base < nv; base += gridDim.x * (kBlock * kU)) {
-        uint32_t xv[kU];
+    double su = 0.0, zu = 0.0;
+    if constexpr (MODE == 0) {
+        su = (double)S[0];
+        zu = ld_d<ZDT>(Z, 0);
+    }
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wbase = __builtin_amdgcn_readfirstlane(threadIdx.x) & ~63u;
+    // vw: the wave's first unit (uniform); lanes past nv only skip their store
+    for (uint32_t vw = blockIdx.x * kBlock + wbase; vw < nv; vw += gridDim.x * kBlock) {
+        const uint32_t v = vw + lane;
+        if (v >= nv) continue;
+        const uint32_t w = X4[v];
+        Params<ZDT, MODE> p;
+        load_params<ZDT, MODE, ND>(p, S, Z, d, ax, vbase + (MODE == 3 ? vw : v));
+        float x[4], y[4];
+        decode4<XDT>(w, x);
 #pragma unroll
-        for (int u = 0; u < kU; u++) {
-            const uint32_t v = base + u * kBlock + threadIdx.x;
-            if (v < nv) xv[u] = X4[v];
+        for (int b = 0; b < 4; b++) {
+            const int k = MODE == 2 ? b : 0;
+            const double s = MODE == 0 ? su : (double)p.s[k];
+            const double z = MODE == 0 ? zu : ld_d<ZDT>(&p.z[k], 0);
+            y[b] = (float)(((double)x[b] - z) * s);
         }
-#pragma unroll
-        for (int u = 0; u < kU; u++) {
-            const uint32_t v = base + u * kBlock + threadIdx.x;
-            if (v >= nv) continue;
-            float y[4];
-            int64_t off[3] = {0, 0, 0};
-            if (!uniform) bd_offsets32<3, ND>(d, v * 4u, off);
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const uint8_t c = (uint8_t)(xv[u] >> (8 * b));
-                const double x = ld_d<XDT>(&c, 0);
-                const double s = uniform ? su : (double)S[off[1] + b * ss];
-                const double z = uniform ? zu : ld_d<ZDT>(Z, off[2] + b * sz);
-                y[b] = (float)((x - z) * s);
-            }
-            st_stream(Y4 + v, make_float4(y[0], y[1], y[2], y[3]));
-        }
+        st_stream(Y4 + v, make_float4(y[0], y[1], y[2], y[3]));
     }
 }
 
@@ -167,11 +361,6 @@ __global__ __launch_bounds__(kBlock) void k_qdq_rt(const void* __restrict__ X, i
         st_d_rt(dty, Y, (int64_t)i, QUANT ? qval(x, s, z) : (x - z) * s);
     }
 }
-
-#define QND_SWITCH(nd, ...)                               \
-    if (nd == 1) { constexpr int ND = 1; __VA_ARGS__; }   \
-    else if (nd == 3) { constexpr int ND = 3; __VA_ARGS__; } \
-    else { constexpr int ND = 0; __VA_ARGS__; }
 
 #define ZDT_SWITCH(zdt, ...)                                          \
     switch (zdt) {                                                    \
@@ -209,33 +398,79 @@ void qdq_entry(const char* name, const Tensor* X, const Tensor* S, const Tensor*
     hipStream_t sm = stream();
     if (n) {
         bool launched = false;
-        if (QUANT && dtx == kF32 && dts == kF32 && zdt_fast(dtz) && is_code8(dty) && fast_ok(d, X, n, x, y)) {
-            const uint32_t nv = (uint32_t)(n / 4);
-            const dim3 g(grid_for(nv, kQBlock, kQGrid)), b(kQBlock);
-#define QLAUNCH(YD)                                                                                           \
-    ZDT_SWITCH(dtz, QND_SWITCH(d.nd, hipLaunchKernelGGL((k_quant_v<YD, ZD, ND>), g, b, 0, sm, (const float*)x,  \
-                                                        (const float*)s, z, (uint8_t*)y, d, nv)))
-            switch (dty) {
-            case kU8: QLAUNCH(kU8); break;
-            case kI8: QLAUNCH(kI8); break;
-            case kE4M3: QLAUNCH(kE4M3); break;
-            default: QLAUNCH(kE5M2); break;
+        const bool qfast_ok = QUANT && dtx == kF32 && dts == kF32 && zdt_fast(dtz) && is_code8(dty);
+        const bool dqfast_ok = !QUANT && is_code8(dtx) && dts == kF32 && zdt_fast(dtz) && dty == kF32;
+        if ((qfast_ok || dqfast_ok) && fast_ok(d, X, n, x, y)) {
+            // Per-axis parameters: Scale varies along exactly one collapsed dimension
+            // (not the innermost) with unit stride; ZeroPoint along the same one or not at all.
+            int axis = -1;
+            bool axis_ok = true;
+            for (int a = 0; a < d.nd; a++) {
+                if (d.st[1][a] == 0) continue;
+                if (axis >= 0 || d.st[1][a] != 1) axis_ok = false;
+                axis = a;
             }
-#undef QLAUNCH
-            launched = true;
-        } else if (!QUANT && is_code8(dtx) && dts == kF32 && zdt_fast(dtz) && dty == kF32 && fast_ok(d, X, n, x, y)) {
-            const uint32_t nv = (uint32_t)(n / 4);
-            const dim3 g(grid_for(nv, kBlock * kU)), b(kBlock);
-#define DQLAUNCH(XD)                                                                                            \
-    ZDT_SWITCH(dtz, QND_SWITCH(d.nd, hipLaunchKernelGGL((k_dequant_v<XD, ZD, ND>), g, b, 0, sm, (const uint8_t*)x, \
-                                                        (const float*)s, z, (float*)y, d, nv)))
-            switch (dtx) {
-            case kU8: DQLAUNCH(kU8); break;
-            case kI8: DQLAUNCH(kI8); break;
-            case kE4M3: DQLAUNCH(kE4M3); break;
-            default: DQLAUNCH(kE5M2); break;
+            uint32_t zs = 0;
+            for (int a = 0; a < d.nd; a++) {
+                if (d.st[2][a] == 0) continue;
+                if (a != axis || d.st[2][a] != 1) axis_ok = false;
+                zs = 1;
             }
-#undef DQLAUNCH
+            bool uniform = true;
+            for (int a = 0; a < d.nd; a++) uniform = uniform && d.st[1][a] == 0 && d.st[2][a] == 0;
+            AxisDesc ax{};
+            int mode = 2;
+            if (uniform && d.nd == 1) {
+                mode = 0;
+            } else if (axis_ok && axis >= 0 && axis < d.nd - 1) {
+                uint64_t inner = 1;
+                for (int a = axis + 1; a < d.nd; a++) inner *= d.dim[a];
+                ax.inner = make_fastdiv((uint32_t)inner);
+                ax.c = make_fastdiv(d.dim[axis]);
+                ax.zs = zs;
+                // kBlock is a multiple of 64 and each wave's 64 units start at a multiple of
+                // 64 units, so inner % 256 == 0 keeps a wave inside one channel.
+                const bool zword = dtz == kF32 || (tensor_bytes(Z) % 4 == 0 && ((uintptr_t)z % 4) == 0);
+                mode = (inner % 256 == 0 && zword && ((uintptr_t)s % 4) == 0) ? 3 : 1;
+            }
+#define QDQ_MODES(LAUNCH_K)                                          \
+    if (mode == 0) { LAUNCH_K(0, 1); }                               \
+    else if (mode == 3) { LAUNCH_K(3, 0); }                          \
+    else if (mode == 1) { LAUNCH_K(1, 0); }                          \
+    else { LAUNCH_K(2, 0); }
+#define CODE_SWITCH(dt, ...)                                         \
+    switch (dt) {                                                    \
+    case kU8: { constexpr int CD = kU8; __VA_ARGS__; } break;        \
+    case kI8: { constexpr int CD = kI8; __VA_ARGS__; } break;        \
+    case kE4M3: { constexpr int CD = kE4M3; __VA_ARGS__; } break;    \
+    default: { constexpr int CD = kE5M2; __VA_ARGS__; } break;       \
+    }
+            const uint32_t nv_all = (uint32_t)(n / 4);
+            // Launch in chunks of at most kMaxUnitsPerLaunch units so that buffer
+            // byte offsets stay below 2^32; vbase keeps the descriptor indexing global.
+            for (uint32_t vbase = 0; vbase < nv_all; vbase += kMaxUnitsPerLaunch) {
+                const uint32_t nv = nv_all - vbase < kMaxUnitsPerLaunch ? nv_all - vbase : kMaxUnitsPerLaunch;
+                const dim3 b(kBlock);
+                if (QUANT) {
+                    const dim3 g(grid_for(nv, kBlock * kQU, kQBlocksPerCU * num_cus()));
+                    const float* xc = (const float*)x + (size_t)vbase * 4;
+                    uint8_t* yc = (uint8_t*)y + (size_t)vbase * 4;
+#define QK(M, NDV) \
+    hipLaunchKernelGGL((k_quant_v<CD, ZD, M, NDV>), g, b, 0, sm, xc, (const float*)s, z, yc, d, ax, vbase, nv)
+                    CODE_SWITCH(dty, ZDT_SWITCH(dtz, QDQ_MODES(QK)))
+#undef QK
+                } else {
+                    const dim3 g(grid_for(nv, kBlock));
+                    const uint8_t* xc = (const uint8_t*)x + (size_t)vbase * 4;
+                    float* yc = (float*)y + (size_t)vbase * 4;
+#define DQK(M, NDV) \
+    hipLaunchKernelGGL((k_dequant_v<CD, ZD, M, NDV>), g, b, 0, sm, xc, (const float*)s, z, yc, d, ax, vbase, nv)
+                    CODE_SWITCH(dtx, ZDT_SWITCH(dtz, QDQ_MODES(DQK)))
+#undef DQK
+                }
+            }
+#undef CODE_SWITCH
+#undef QDQ_MODES
             launched = true;
         }
         if (!launched)

@@ -183,7 +183,7 @@ def test_config5_softmax(hip, oracle_lib):
 
 
 @pytest.mark.parametrize("ydt,zdt", [(O.U8, O.U8), (O.I8, O.I8), (O.E4M3, O.E4M3), (O.E5M2, O.E5M2),
-                                     (O.I8, O.F32), (O.U8, O.F32)])
+                                     (O.I8, O.F32), (O.U8, O.F32), (O.E4M3, O.F32), (O.E5M2, O.F32)])
 def test_quantize_fast_path_boundaries(hip, oracle_lib, ydt, zdt):
     """Inputs placed on and next to rounding ties of x / s, huge quotients and
     special scales: the fp32 fast path must hand every doubtful lane to fp64."""
@@ -197,19 +197,76 @@ def test_quantize_fast_path_boundaries(hip, oracle_lib, ydt, zdt):
     x = np.where(rng.random(n) < 0.3, x + ulp * rng.integers(-2, 3, n).astype(np.float32), x).astype(np.float32)
     x[:64] = np.array([2 ** 22, 2 ** 22 + 1, 2 ** 23 + 0.5, -2 ** 24, 1e30, -1e30, np.inf, -np.inf, np.nan, 0.0, -0.0,
                        1e-40, -1e-45, 0.5, -0.5, 1.5] * 4, np.float32) * np.float32(s)
-    zvals = {O.U8: [0, 3, 128, 255], O.I8: [0, -5, 127, -128], O.E4M3: [0x00, 0x38, 0xB8, 0x01],
-             O.E5M2: [0x00, 0x3C, 0xBC, 0x01], O.F32: [0.0, 3.0, -2.5, 1e30]}[zdt]
+    # quotients between 2^17 and 2^28 (fp32 spacing of x / s above 1), and around the fp8 saturation points
+    big = np.float64(s) * np.concatenate([rng.uniform(2 ** 17, 2 ** 28, 96) * rng.choice([-1, 1], 96),
+                                          np.array([447.5, 448.5, 463.5, 464.5, 57343.5, 61439.5, 61440.5, 65535.5])])
+    x[64:168] = big.astype(np.float32)
+    # zero points: integral, fractional (0x01 codes, -2.5, 0.001: fp8 flush-to-zero band of r + zp),
+    # beyond the fast path's |zp| < 2^22 and huge
+    zvals = {O.U8: [0, 3, 128, 255], O.I8: [0, -5, 127, -128], O.E4M3: [0x00, 0x38, 0xB8, 0x01, 0x80],
+             O.E5M2: [0x00, 0x3C, 0xBC, 0x01, 0x80],
+             O.F32: [0.0, 3.0, -2.5, 1e30, 0.001, 2.0 ** 22, 2.0 ** 22 + 2, -(2.0 ** 22 - 1)]}[zdt]
     for zv in zvals:
         z = np.array([zv], O.STORAGE[zdt])
+        # special scales, including ones whose reciprocal is subnormal (|s| > 2^126) or overflows
         for sv in (s, np.float32(-s), np.float32(0.0), np.float32(-0.0), np.float32(1e-42), np.float32(np.inf),
-                   np.float32(np.nan)):
+                   np.float32(np.nan), np.float32(1e38), np.float32(-3e38), np.float32(1.2e-38)):
             sa = np.array([sv], np.float32)
             got = hip.qdq("quantize", x, O.F32, sa, O.F32, z, zdt, ydt)
             ref = oracle_lib.qdq("quantize", x, O.F32, sa, O.F32, z, zdt, ydt)
             assert_bitexact(got, ref, ydt, what=f"Q y={ydt} z={zv} s={sv}")
     # per-axis scales with mixed magnitudes
     x3 = x[: 64 * 1024].reshape(4, 64, 256)
-    sax = rng.uniform(0.001, 5.0, 64).astype(np.float32).reshape(1, 64, 1)
+    sax = rng.uniform(0.001, 5.0, 64).astype(np.float32)
+    sax[:6] = [0.0, -1.5, np.inf, np.nan, 1e38, 1e-42]
+    sax = sax.reshape(1, 64, 1)
     zax = np.array(zvals * 16, O.STORAGE[zdt])[:64].reshape(1, 64, 1)
     assert_bitexact(hip.qdq("quantize", x3, O.F32, sax, O.F32, zax, zdt, ydt),
                     oracle_lib.qdq("quantize", x3, O.F32, sax, O.F32, zax, zdt, ydt), ydt, what="Q per-axis")
+    # inner dimension not a multiple of 256 (parameters per 4-element group rather than per wave)
+    x4 = x[: 64 * 1000].reshape(50, 64, 20)
+    assert_bitexact(hip.qdq("quantize", x4, O.F32, sax, O.F32, zax, zdt, ydt),
+                    oracle_lib.qdq("quantize", x4, O.F32, sax, O.F32, zax, zdt, ydt), ydt, what="Q per-axis inner 20")
+    # full-size scale and zero point (the reference's Python pre-broadcasts them): per-element parameters
+    sfull = np.broadcast_to(sax, x3.shape).copy()
+    sfull[:, :, ::7] = s
+    zfull = np.broadcast_to(zax, x3.shape).copy()
+    assert_bitexact(hip.qdq("quantize", x3, O.F32, sfull, O.F32, zfull, zdt, ydt),
+                    oracle_lib.qdq("quantize", x3, O.F32, sfull, O.F32, zfull, zdt, ydt), ydt, what="Q full-size")
+
+
+@pytest.mark.parametrize("xdt", [O.U8, O.I8, O.E4M3, O.E5M2])
+def test_dequantize_all_codes(hip, oracle_lib, xdt):
+    """Every code of every 1-byte format through the dequantize kernels (per-tensor,
+    per-axis and full-size parameters): pins the hardware fp8 decode and the fp64
+    (x - zp) * s against the reference, bit for bit."""
+    rng = np.random.default_rng(int(xdt))
+    codes = np.tile(np.arange(256, dtype=np.uint8), 64).reshape(4, 16, 256)
+    zdts = [xdt, O.F32]
+    for zdt in zdts:
+        zv = {O.U8: [0, 7, 255], O.I8: [0, -9, 127], O.E4M3: [0x00, 0x39, 0xC4, 0x7F], O.E5M2: [0x00, 0x3D, 0xBA, 0x7D],
+              O.F32: [0.0, 0.3, -1e30, 5.0]}[zdt]
+        for z0 in zv:
+            for s0 in (np.float32(0.0123), np.float32(-3.5), np.float32(1e38), np.float32(0.0), np.float32(np.inf),
+                       np.float32(np.nan), np.float32(1e-45)):
+                sa, za = np.array([s0], np.float32), np.array([z0], O.STORAGE[zdt])
+                assert_bitexact(hip.qdq("dequantize", codes, xdt, sa, O.F32, za, zdt, O.F32),
+                                oracle_lib.qdq("dequantize", codes, xdt, sa, O.F32, za, zdt, O.F32), O.F32,
+                                what=f"DQ x={xdt} z={z0} s={s0}")
+        sax = rng.uniform(-2, 2, 16).astype(np.float32)
+        sax[:3] = [0.0, np.inf, 1e30]
+        zax = np.array((zv * 16)[:16], O.STORAGE[zdt])
+        c2 = codes.reshape(64, 16, 16)
+        assert_bitexact(hip.qdq("dequantize", c2, xdt, sax.reshape(1, 16, 1), O.F32, zax.reshape(1, 16, 1), zdt, O.F32),
+                        oracle_lib.qdq("dequantize", c2, xdt, sax.reshape(1, 16, 1), O.F32, zax.reshape(1, 16, 1), zdt,
+                                       O.F32), O.F32, what="DQ per-axis inner 16")
+        assert_bitexact(hip.qdq("dequantize", codes, xdt, sax.reshape(1, 16, 1), O.F32, zax.reshape(1, 16, 1), zdt,
+                                O.F32),
+                        oracle_lib.qdq("dequantize", codes, xdt, sax.reshape(1, 16, 1), O.F32, zax.reshape(1, 16, 1),
+                                       zdt, O.F32), O.F32, what="DQ per-axis")
+        sfull = np.broadcast_to(sax.reshape(1, 16, 1), codes.shape).copy()
+        sfull[..., ::5] = np.float32(0.75)
+        zfull = np.broadcast_to(zax.reshape(1, 16, 1), codes.shape).copy()
+        assert_bitexact(hip.qdq("dequantize", codes, xdt, sfull, O.F32, zfull, zdt, O.F32),
+                        oracle_lib.qdq("dequantize", codes, xdt, sfull, O.F32, zfull, zdt, O.F32), O.F32,
+                        what="DQ full-size")
