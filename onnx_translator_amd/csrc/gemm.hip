@@ -9,8 +9,11 @@
 //    fp8, int4/8/16, uint8) are decoded while staging into LDS.
 //    128x128 block tile, 4 waves (2x2), each wave 64x64 = 2x2 MFMA tiles,
 //    BK = 16, LDS double buffer.  Tolerance class vs the reference.
-//  * k_gemm_mfma_f16 — v_mfma_f32_32x32x16_f16 for f16 x f16 (gfx950 K=16
-//    form), fp32 accumulate; same tiling with BK = 32.
+//  * k_gemm_f16_nt — f16 x f16 with A [M, K] and B [N, K] (transB = 1):
+//    v_mfma_f32_32x32x16_f16, 256x256x64 block tiles over 8 waves (128x64
+//    each), operands through raw buffer loads into registers one k-tile
+//    ahead, LDS double buffer, XCD-aware tile order.  fp32 accumulate.
+//  * k_gemm_mfma_f16 — the other f16 transposes: 128x128x32 tiles.
 //  * k_gemm_exact — fp64, sequential k, no contraction: bit-identical to the
 //    reference for every dtype combination.  Used for f64 / int32 / int64
 //    operands and when exact mode is on.
@@ -22,11 +25,28 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((__vector_size__(16)));
+typedef __attribute__((address_space(1))) float gfloat;
+typedef __attribute__((address_space(1))) uint16_t gu16;
+
+__device__ __forceinline__ u32x4 ld_buf_b128(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+}
+// Zero the halves of an 8-half chunk starting at k whose index is >= K.
+__device__ __forceinline__ u32x4 mask_k8(u32x4 v, int k, int K) {
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint32_t lo = (k + 2 * w < K) ? 0x0000FFFFu : 0u, hi = (k + 2 * w + 1 < K) ? 0xFFFF0000u : 0u;
+        v[w] &= lo | hi;
+    }
+    return v;
+}
 
 struct Bias {
     const void* p;
     int dt;
-    int mode;   // 0 none, 1 scalar, 2 per column (n), 3 per row (m), 4 two-d (H, W broadcast)
+    int mode;   // 0 none, 1 scalar, 2 per column (n), 3 per row (m), 4 two-d (H, W broadcast),
+                // 5 present but matching neither N nor M: beta * 0.0 is still added
     int H, W;
 };
 
@@ -55,11 +75,17 @@ struct GemmArgs {
 };
 
 // Any output dtype / bias dtype: kept out of line so the unrolled MFMA
-// epilogues stay small.
-__device__ __noinline__ void store_rt(const GemmArgs& g, int m, int n, double acc) {
-    double r = g.alpha * acc;
-    if (g.c.mode) r += g.beta * bias_at(g.c, m, n);
-    st_d_rt(g.dty, g.Y, (int64_t)m * g.N + n, r);
+// epilogues stay small.  It takes scalars, not the argument struct: a
+// reference to the kernel's by-value argument would move it to scratch memory
+// and make every field a per-lane (divergent) load in the main loop.
+__device__ __noinline__ void store_rt_s(void* Y, int dty, int N, double alpha, double beta, const void* cp, int cdt,
+                                        int cmode, int cH, int cW, int m, int n, double acc) {
+    double r = alpha * acc;
+    if (cmode) r += beta * bias_at(Bias{cp, cdt, cmode, cH, cW}, m, n);
+    st_d_rt(dty, Y, (int64_t)m * N + n, r);
+}
+__device__ __forceinline__ void store_rt(const GemmArgs& g, int m, int n, double acc) {
+    store_rt_s(g.Y, g.dty, g.N, g.alpha, g.beta, g.c.p, g.c.dt, g.c.mode, g.c.H, g.c.W, m, n, acc);
 }
 
 // YDT >= 0: output dtype known at compile time; f32 bias (scalar / per
@@ -352,6 +378,169 @@ __global__ __launch_bounds__(kThreads) void k_gemm_mfma_f16(GemmArgs g, int vec)
             }
 }
 
+// ------------------------------------------------ f16 MFMA, both operands K-major ---
+// A [M, K] and B [N, K] row-major (transA = 0, transB = 1: the layout of the
+// ONNX Gemm with transB = 1).  Block tile BM x BN x BK over NT = 64 * WGM * WGN
+// threads; wave tile (BM / WGM) x (BN / WGN) of 32x32 MFMA tiles.
+// Pipeline per k-tile: issue the global loads of tile k + 1 into registers,
+// run the MFMAs of tile k from LDS, write the registers to the other LDS
+// buffer, one barrier.  LDS rows are BK + 8 halves (16 bytes of padding), so
+// the 16-byte fragment reads of 8 consecutive rows cover all banks once.
+// Tile order: consecutive workgroups are spread over the 8 XCDs by the
+// dispatcher, so the block index is remapped to give each XCD a contiguous
+// run of tiles, and tiles are walked in groups of kGroupM tile rows, so one
+// XCD's L2 serves a few A panels and B panels.
+constexpr int kGroupM = 4;
+
+__device__ __forceinline__ void tile_of_block(int nbm, int nbn, int& tm, int& tn) {
+    const int nb = nbm * nbn;
+    int bid = blockIdx.x;
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    const int per_group = kGroupM * nbn;
+    const int first_m = (bid / per_group) * kGroupM;
+    const int gsz = min(nbm - first_m, kGroupM);
+    const int r = bid % per_group;
+    tm = first_m + r % gsz;
+    tn = r / gsz;
+}
+
+// Epilogue of the tiled kernels.  YDT = kF16 / kF32 with no bias or an f32
+// bias (scalar, per column, per row) is fully inline and call-free: a call
+// would force the accumulators, live across it, into scratch memory.  Every
+// other case (YDT = -1) goes through the out-of-line store_rt.  Output goes
+// through a global-address-space pointer (a generic pointer compiles to flat
+// stores, which also count against the LDS wait counter).
+template <int YDT>
+__device__ __forceinline__ void epilogue_fast(const GemmArgs& g, int m, int n, double acc) {
+    if constexpr (YDT == kF16 || YDT == kF32) {
+        double r = g.alpha * acc;
+        if (g.c.mode) {
+            const gfloat* c = (const gfloat*)g.c.p;
+            r += g.beta * (double)c[g.c.mode == 1 ? 0 : (g.c.mode == 2 ? n : m)];
+        }
+        const int64_t i = (int64_t)m * g.N + n;
+        if constexpr (YDT == kF16) ((gu16*)g.Y)[i] = enc_f16((float)r);
+        else ((gfloat*)g.Y)[i] = (float)r;
+    } else {
+        store_rt(g, m, n, acc);
+    }
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, int YDT, int NBUF = 2, int IGLP = -1>
+__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_f16_nt(GemmArgs g) {
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int LDK = BK + 8;
+    constexpr int WTM = BM / WGM, WTN = BN / WGN;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    constexpr int CPR = BK / 8;                   // 16-byte chunks per tile row
+    constexpr int CA = BM * CPR / NT, CB = BN * CPR / NT;
+    static_assert(CA * NT == BM * CPR && CB * NT == BN * CPR, "tile / thread mismatch");
+    __shared__ _Float16 lds[NBUF][(BM + BN) * LDK];
+
+    const int nbm = (g.M + BM - 1) / BM, nbn = (g.N + BN - 1) / BN;
+    int tm, tn;
+    tile_of_block(nbm, nbn, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+    // Buffer resources over the operands: rows past M / N read as zero.  The
+    // host guarantees (rows + tile) * ld * 2 < 2^31 and ld % 8 == 0.
+    const __amdgpu_buffer_rsrc_t ar = buffer_rsrc(g.A, (uint32_t)((int64_t)g.M * g.lda * 2));
+    const __amdgpu_buffer_rsrc_t br = buffer_rsrc(g.B, (uint32_t)((int64_t)g.N * g.ldb * 2));
+
+    u32x4 ra[CA], rb[CB];
+    auto load_tile = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < CA; i++) {
+            const int c = t + i * NT;
+            ra[i] = ld_buf_b128(ar, (uint32_t)(((m0 + c / CPR) * g.lda + k0 + (c % CPR) * 8) * 2));
+        }
+#pragma unroll
+        for (int i = 0; i < CB; i++) {
+            const int c = t + i * NT;
+            rb[i] = ld_buf_b128(br, (uint32_t)(((n0 + c / CPR) * g.ldb + k0 + (c % CPR) * 8) * 2));
+        }
+    };
+    // Chunks that straddle K are zeroed here, after the wait for the loads.
+    auto mask_tile = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < CA; i++) ra[i] = mask_k8(ra[i], k0 + ((t + i * NT) % CPR) * 8, g.K);
+#pragma unroll
+        for (int i = 0; i < CB; i++) rb[i] = mask_k8(rb[i], k0 + ((t + i * NT) % CPR) * 8, g.K);
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < CA; i++) {
+            const int c = t + i * NT;
+            *reinterpret_cast<u32x4*>(&lds[buf][(c / CPR) * LDK + (c % CPR) * 8]) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < CB; i++) {
+            const int c = t + i * NT;
+            *reinterpret_cast<u32x4*>(&lds[buf][(BM + c / CPR) * LDK + (c % CPR) * 8]) = rb[i];
+        }
+    };
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    const int lr = lane & 31, lk = (lane >> 5) * 8;
+    auto compute = [&](int buf) {
+        const _Float16* As = &lds[buf][(wm * WTM + lr) * LDK + lk];
+        const _Float16* Bs = &lds[buf][(BM + wn * WTN + lr) * LDK + lk];
+#pragma unroll
+        for (int ks = 0; ks < BK; ks += 16) {
+            halfx8 a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) a[i] = *reinterpret_cast<const halfx8*>(As + i * 32 * LDK + ks);
+#pragma unroll
+            for (int j = 0; j < TN; j++) b[j] = *reinterpret_cast<const halfx8*>(Bs + j * 32 * LDK + ks);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    const int nk = (g.K + BK - 1) / BK;
+    load_tile(0);
+    if (BK > g.K) mask_tile(0);
+    store_tile(0);
+    __syncthreads();
+    // All k-tiles but the last: one basic block per iteration (loads of the
+    // next tile, MFMAs of this one, LDS writes of the next), so the scheduler
+    // can interleave the three streams.
+    int kt = 0;
+    for (; kt + 1 < nk; kt++) {
+        const int cur = NBUF == 2 ? (kt & 1) : 0;
+        const int k1 = (kt + 1) * BK;
+        load_tile(k1);
+        compute(cur);
+        if constexpr (IGLP >= 0) __builtin_amdgcn_iglp_opt(IGLP);
+        if (k1 + BK > g.K) mask_tile(k1);
+        if constexpr (NBUF == 1) __syncthreads();
+        store_tile(NBUF == 2 ? (cur ^ 1) : 0);
+        __syncthreads();
+    }
+    compute(NBUF == 2 ? (kt & 1) : 0);
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + (lk >> 1) + (r & 3);
+                const int n = n0 + wn * WTN + j * 32 + lr;
+                if (m < g.M && n < g.N) epilogue_fast<YDT>(g, m, n, (double)acc[i][j][r]);
+            }
+}
+
 // -------------------------------------------------------------------- dispatch ---
 inline bool f32_exact_dtype(int dt) {
     return dt == kF32 || dt == kF16 || dt == kBF16 || dt == kE4M3 || dt == kE5M2 || dt == kI4 || dt == kI8 ||
@@ -379,6 +568,32 @@ void launch_f16_y(const GemmArgs& g, dim3 grid, int vec, hipStream_t s) {
     if (g.dty == kF16) hipLaunchKernelGGL((k_gemm_mfma_f16<TA, TB, kF16>), grid, dim3(kThreads), 0, s, g, vec);
     else if (g.dty == kF32) hipLaunchKernelGGL((k_gemm_mfma_f16<TA, TB, kF32>), grid, dim3(kThreads), 0, s, g, vec);
     else hipLaunchKernelGGL((k_gemm_mfma_f16<TA, TB, -1>), grid, dim3(kThreads), 0, s, g, vec);
+}
+
+// f16 x f16 with both operands K-major (A [M, K], B [N, K]) and 16-byte
+// aligned rows: the tiled kernel.  256x256 tiles (8 waves of 128x64) when the
+// grid still covers the 256 CUs, else 128x128 tiles (4 waves of 64x64).
+// Returns false when the operands exceed the 2 GB reach of a buffer resource.
+template <int BM, int BN, int BK, int WGM, int WGN, int NBUF, int IGLP>
+void launch_f16_nt_cfg(const GemmArgs& g, hipStream_t s) {
+    const int nb = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+    const bool fast_bias = g.c.mode == 0 || (g.c.dt == kF32 && g.c.mode <= 3);
+    const dim3 grid(nb), block(64 * WGM * WGN);
+    if (fast_bias && g.dty == kF16)
+        hipLaunchKernelGGL((k_gemm_f16_nt<BM, BN, BK, WGM, WGN, kF16, NBUF, IGLP>), grid, block, 0, s, g);
+    else if (fast_bias && g.dty == kF32)
+        hipLaunchKernelGGL((k_gemm_f16_nt<BM, BN, BK, WGM, WGN, kF32, NBUF, IGLP>), grid, block, 0, s, g);
+    else
+        hipLaunchKernelGGL((k_gemm_f16_nt<BM, BN, BK, WGM, WGN, -1, NBUF, IGLP>), grid, block, 0, s, g);
+}
+
+bool launch_f16_nt(const GemmArgs& g, hipStream_t s) {
+    const int64_t reach = (int64_t)1 << 31;
+    if ((int64_t)(g.M + 256) * g.lda * 2 >= reach || (int64_t)(g.N + 256) * g.ldb * 2 >= reach) return false;
+    const int64_t big_tiles = (int64_t)((g.M + 255) / 256) * ((g.N + 255) / 256);
+    if (big_tiles >= 192) launch_f16_nt_cfg<256, 256, 64, 2, 4, 2, 1>(g, s);
+    else launch_f16_nt_cfg<128, 128, 64, 2, 2, 2, 0>(g, s);
+    return true;
 }
 
 // f32 x f32 uses typed (optionally vectorised) staging; every other pair of
@@ -425,8 +640,15 @@ extern "C" void gemm_forward(const Tensor* A, const Tensor* B, const Tensor* C, 
     if (has_c) {
         // tensor_ops.c:1197-1220
         if (C->size == 1) g.c.mode = 1;
-        else if (C->ndim == 1) g.c.mode = (C->shape[0] == N) ? 2 : (C->shape[0] == M ? 3 : 0);
+        else if (C->ndim == 1) g.c.mode = (C->shape[0] == N) ? 2 : (C->shape[0] == M ? 3 : 5);
         else if (C->ndim >= 2) { g.c.mode = 4; g.c.H = C->shape[C->ndim - 2]; g.c.W = C->shape[C->ndim - 1]; }
+        // The reference's Python passes a 1-D bias reshaped to (1, N) or (M, 1)
+        // (nn/Operators.py:638-645); those index exactly like the per-column /
+        // per-row modes, which the MFMA epilogues handle inline.
+        if (g.c.mode == 4 && C->size == (size_t)g.c.H * g.c.W) {
+            if (g.c.H == 1 && g.c.W == N) g.c.mode = 2;
+            else if (g.c.H == M && g.c.W == 1) g.c.mode = 3;
+        }
     }
     Staging st;
     g.A = st.in(A);
@@ -444,7 +666,8 @@ extern "C" void gemm_forward(const Tensor* A, const Tensor* B, const Tensor* C, 
                 const dim3 grid((N + kBN - 1) / kBN, (M + kBM - 1) / kBM);
                 const int vec = ((g.lda % 8) == 0 && (g.ldb % 8) == 0 && ((uintptr_t)g.A & 15) == 0 &&
                                  ((uintptr_t)g.B & 15) == 0) ? 1 : 0;
-                if (!transA && transB) launch_f16_y<false, true>(g, grid, vec, s);
+                if (!transA && transB && vec && launch_f16_nt(g, s)) {
+                } else if (!transA && transB) launch_f16_y<false, true>(g, grid, vec, s);
                 else if (!transA && !transB) launch_f16_y<false, false>(g, grid, vec, s);
                 else if (transA && transB) launch_f16_y<true, true>(g, grid, vec, s);
                 else launch_f16_y<true, false>(g, grid, vec, s);

@@ -8,7 +8,8 @@ Comparison rules (the parity bar):
   which operand x86 SSE propagates, which its C code does not fix);
 * tolerance (MFMA Gemm / Conv, tree-reduced Softmax): |g - r| <= rtol*|r| + atol
   with rtol 1e-5 for f32 / f64 outputs and atol = rtol * rms(r); for narrow
-  float outputs one unit in the last place of the output format.
+  float outputs one unit in the last place of the output format plus the same
+  atol.
 """
 from __future__ import annotations
 
@@ -108,13 +109,16 @@ def assert_close(out, ref, dt, rtol=1e-5, what=""):
     assert g.shape == r.shape
     rn = np.isnan(r)
     assert not (np.isnan(g) & ~rn).any(), f"{what}: NaN where the reference is finite"
+    finite = r[np.isfinite(r)]
+    rms = float(np.sqrt(np.mean(finite ** 2))) if finite.size else 0.0
     if dt in MANT_BITS:
         tol = np.abs(r) * 2.0 ** -MANT_BITS[dt] + 1e-30
         # values below the format's normal range are spaced by its subnormal step
         tol = np.maximum(tol, {O.F16: 2 ** -24, O.BF16: 2 ** -133, O.E4M3: 2 ** -6, O.E5M2: 2 ** -14}[dt])
+        # the same absolute floor as f32: results that cancel to near zero carry
+        # the fp32 accumulation error of their terms, not of the result
+        tol = tol + rtol * rms
     else:
-        finite = r[np.isfinite(r)]
-        rms = float(np.sqrt(np.mean(finite ** 2))) if finite.size else 0.0
         tol = rtol * np.abs(r) + rtol * rms
     fin = np.isfinite(r)
     err = np.abs(g - r)

@@ -71,6 +71,40 @@ def test_gemm_ragged_shapes(hip, oracle_lib, shape, trans):
         assert_close(got, ref, O.F32, what=f"gemm {dt} {shape} {trans}")
 
 
+# f16 x f16 with transB = 1 and K % 8 == 0 runs the tiled kernel (buffer loads,
+# K tail masked in registers): 128x128 tiles for small grids, 256x256 tiles when
+# the grid has >= 192 of them.  Ragged M / N and K % 64 != 0 exercise the edges;
+# the bias modes cover the inline epilogue (none / scalar / per row / per
+# column) and the out-of-line one (2-D bias).
+F16_NT = [(300, 200, 136, "col"), (130, 1000, 8, "none"), (257, 129, 64, "scalar"), (96, 72, 520, "row"),
+          (3600, 3500, 72, "col"), (3584, 3584, 200, "2d")]
+
+
+@pytest.mark.parametrize("M,N,K,bias", F16_NT, ids=[f"{m}x{n}x{k}-{b}" for m, n, k, b in F16_NT])
+@pytest.mark.parametrize("ydt", ["float16", "float32"])
+def test_gemm_f16_tiled_kernel(hip, M, N, K, bias, ydt):
+    from tests.helpers import assert_close
+    rng = np.random.default_rng(M + 3 * N + 7 * K)
+    a = rng.normal(0, 1, (M, K)).astype(np.float16)
+    b = rng.normal(0, 1, (N, K)).astype(np.float16)
+    c = {"none": None, "scalar": rng.normal(0, 1, (1,)), "row": rng.normal(0, 1, (M,)),
+         "col": rng.normal(0, 1, (N,)), "2d": rng.normal(0, 1, (M, N))}[bias]
+    if c is not None:
+        c = c.astype(np.float32)
+    alpha, beta = 0.75, 1.5
+    y = hip.gemm(a, O.F16, b, O.F16, c, O.F32, ydt, alpha, beta, 0, 1)
+    rows = np.arange(M) if M * N <= 1 << 20 else np.unique(np.r_[rng.choice(M, 40, replace=False), 0, M - 1])
+    ref = alpha * (a[rows].astype(np.float64) @ b.astype(np.float64).T)
+    if c is not None:
+        cc = {"row": lambda: c[rows].reshape(-1, 1), "2d": lambda: c[rows]}.get(bias, lambda: c.reshape(1, -1))()
+        ref = ref + beta * cc.astype(np.float64)
+    if ydt == "float16":
+        assert_close(y[rows], O.oracle().encode_f32(ref.astype(np.float32), O.F16), O.F16,
+                     what=f"f16 nt {M}x{N}x{K} {bias}")
+    else:
+        assert_close(y[rows], ref.astype(np.float32), O.F32, rtol=2e-5, what=f"f16 nt {M}x{N}x{K} {bias}")
+
+
 def test_device_path_matches_host_path(hip):
     """Config-1 chain with device-resident tensors (no host round trips between ops)."""
     from onnx_translator_amd.nn import Tensor
