@@ -5,7 +5,10 @@
 // 0.0 * w), then + bias[m], written through the output encoder.  Output
 // extent comes from Y's shape; pads[0] / pads[1] are top / left.
 //
-//  * k_conv_mfma_f32 — implicit GEMM on v_mfma_f32_32x32x2f32.  Per group:
+//  * k_conv_tiled — f32 x f32: implicit GEMM with register prefetch, buffer
+//    loads and an LDS double buffer (described at the kernel).
+//  * k_conv_mfma_f32 — other fp32-exact dtypes (decoded while staging):
+//    implicit GEMM on v_mfma_f32_32x32x2f32.  Per group:
 //    M = out channels, N = batch * OH * OW pixels, K = Cin/g * KH * KW.  The
 //    block tile is 64 channels x 256 pixels (4 waves side by side, each
 //    64 x 64 = 2x2 MFMA tiles), BK = 16.  Each thread owns one pixel column
@@ -184,6 +187,226 @@ __global__ __launch_bounds__(256) void k_conv_mfma_f32(const void* __restrict__ 
     }
 }
 
+// ---------------------------------------------------------------- tiled f32 ---
+// f32 input and weights.  Implicit GEMM per group: A = weights [Mg, Kg]
+// (k = (c, kh, kw), contiguous), B = im2col [Kg, P] gathered on the fly,
+// P = N * OH * OW.  Block tile BM channels x BP pixels x BK, NT = 64 * WGM * WGN
+// threads, wave tile (BM / WGM) x (BP / WGN) of 32x32 v_mfma_f32_32x32x2f32.
+// The next k-tile is loaded into registers (raw buffer loads; a padding tap or
+// a k past Kg gets an out-of-range offset and reads zero, so the gather has no
+// branches) while the MFMAs run on the current LDS buffer; one barrier per
+// k-tile.  MODE 1 is the 1x1 / stride 1 / no padding case with HW % 4 == 0:
+// im2col is the input itself, read as float4 along the pixels.
+// Epilogue (f32 output, f32 or no bias): acc + bias in fp32, which equals the
+// reference's double sum rounded to float (two floats: 53 >= 2 * 24 + 2).
+struct ConvTiled {
+    int C, H, W, M, KH, KW, OH, OW;
+    int pt, pl, sh, sw, dh, dw;
+    int Cg, Mg, Kg, HW, OHW, P;
+    FastDiv fd_ohw, fd_ow, fd_khw, fd_kw;
+};
+
+typedef __attribute__((address_space(1))) float gfloat;
+constexpr uint32_t kOOB = 0x80000000u;    // beyond every buffer resource here (< 2 GB)
+
+template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int YDT>
+__global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __restrict__ X, const float* __restrict__ Wt,
+                                                               const float* __restrict__ Bv, void* __restrict__ Y,
+                                                               int dty, int dtb, ConvTiled g, uint32_t xbytes,
+                                                               uint32_t wbytes) {
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int WTM = BM / WGM, WTP = BP / WGN, TM = WTM / 32, TP = WTP / 32;
+    constexpr int EA = BM * BK / NT;              // weights per thread per k-tile (consecutive k)
+    constexpr int EB = BK * BP / NT;              // im2col values per thread per k-tile
+    static_assert(EA >= 1 && BK % EA == 0 && EB >= 1, "tile / thread mismatch");
+    __shared__ float As[2][BK][BM + 4];
+    __shared__ float Bs[2][BK][BP + 4];
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int grp = blockIdx.z;
+    const int m0 = blockIdx.y * BM, p0 = blockIdx.x * BP;
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, xbytes);
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(Wt, wbytes);
+
+    // weights: thread -> row am, EA consecutive k from ak
+    const int am = t / (BK / EA), ak = (t % (BK / EA)) * EA;
+    const int wrow = grp * g.Mg + m0 + am;
+    const bool am_ok = m0 + am < g.Mg;
+
+    // im2col: MODE 0 -> one pixel, EB consecutive k; MODE 1 -> 4 pixels, EB / 4 k
+    constexpr int PPT = MODE == 1 ? 4 : 1;
+    constexpr int KPT = EB / PPT;
+    constexpr int PCOLS = BP / PPT;
+    const int pc = (t % PCOLS) * PPT, kg = (t / PCOLS) * KPT;
+    const int p = p0 + pc;
+    int ih0 = -(1 << 29), iw0 = 0, xb = 0;
+    if (p < g.P) {
+        const int n = (int)g.fd_ohw.div((uint32_t)p), r = p - n * g.OHW;
+        const int oh = (int)g.fd_ow.div((uint32_t)r), ow = r - oh * g.OW;
+        ih0 = oh * g.sh - g.pt;
+        iw0 = ow * g.sw - g.pl;
+        xb = (n * g.C + grp * g.Cg) * g.HW + (MODE == 1 ? r : 0);
+    }
+
+    float ra[EA];
+    float rb[EB];
+    auto load_tile = [&](int k0) {
+#pragma unroll
+        for (int e = 0; e < EA; e++) {
+            const int k = k0 + ak + e;
+            const uint32_t off = (am_ok && k < g.Kg) ? (uint32_t)(wrow * g.Kg + k) * 4u : kOOB;
+            ra[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0));
+        }
+        if constexpr (MODE == 1) {
+#pragma unroll
+            for (int e = 0; e < KPT; e++) {
+                const int k = k0 + kg + e;
+                const uint32_t off = (ih0 >= 0 && k < g.Kg) ? (uint32_t)(xb + k * g.HW) * 4u : kOOB;
+                typedef unsigned int u32x4 __attribute__((__vector_size__(16)));
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    // element copied to a scalar first: hipcc 7.2 folds
+                    // __builtin_bit_cast of a vector subscript to element 0
+                    const uint32_t u = v[q];
+                    rb[e * 4 + q] = __builtin_bit_cast(float, u);
+                }
+            }
+        } else {
+            int k = k0 + kg;
+            int c = (int)g.fd_khw.div((uint32_t)k);
+            const int rem = k - c * (g.KH * g.KW);
+            int kh = (int)g.fd_kw.div((uint32_t)rem);
+            int kw = rem - kh * g.KW;
+#pragma unroll
+            for (int e = 0; e < KPT; e++) {
+                const int ih = ih0 + kh * g.dh, iw = iw0 + kw * g.dw;
+                const bool ok = k < g.Kg && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+                const uint32_t off = ok ? (uint32_t)(xb + c * g.HW + ih * g.W + iw) * 4u : kOOB;
+                rb[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
+                k++;
+                if (++kw == g.KW) { kw = 0; if (++kh == g.KH) { kh = 0; c++; } }
+            }
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int e = 0; e < EA; e++) As[buf][ak + e][am] = ra[e];
+        if constexpr (MODE == 1) {
+#pragma unroll
+            for (int e = 0; e < KPT; e++)
+                *reinterpret_cast<float4*>(&Bs[buf][kg + e][pc]) = make_float4(rb[4 * e], rb[4 * e + 1], rb[4 * e + 2],
+                                                                                rb[4 * e + 3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < KPT; e++) Bs[buf][kg + e][pc] = rb[e];
+        }
+    };
+
+    floatx16 acc[TM][TP];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TP; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    const int lr = lane & 31, lk = lane >> 5;
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int ks = 0; ks < BK; ks += 2) {
+            float a[TM], b[TP];
+#pragma unroll
+            for (int i = 0; i < TM; i++) a[i] = As[buf][ks + lk][wm * WTM + i * 32 + lr];
+#pragma unroll
+            for (int j = 0; j < TP; j++) b[j] = Bs[buf][ks + lk][wn * WTP + j * 32 + lr];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TP; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    const int nk = (g.Kg + BK - 1) / BK;
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 1 < nk; kt++) {
+        load_tile((kt + 1) * BK);
+        compute(kt & 1);
+        store_tile((kt & 1) ^ 1);
+        __syncthreads();
+    }
+    compute(kt & 1);
+
+#pragma unroll
+    for (int j = 0; j < TP; j++) {
+        const int q = p0 + wn * WTP + j * 32 + lr;
+        if (q >= g.P) continue;
+        const int qn = (int)g.fd_ohw.div((uint32_t)q), qr = q - qn * g.OHW;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int mloc = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+                if (mloc >= g.Mg) continue;
+                const int m = grp * g.Mg + mloc;
+                const int64_t yi = ((int64_t)qn * g.M + m) * g.OHW + qr;
+                if constexpr (YDT == kF32) {
+                    // + 0.0f without a bias, as the reference adds bias_val = 0.0 (-0 -> +0)
+                    ((gfloat*)Y)[yi] = acc[i][j][r] + (Bv ? ((const gfloat*)Bv)[m] : 0.0f);
+                } else {
+                    conv_store_rt(Y, dty, yi, Bv, dtb, m, acc[i][j][r]);
+                }
+            }
+    }
+}
+
+template <int BM, int BP, int BK, int WGM, int WGN, int MODE>
+void launch_conv_tiled_cfg(const float* x, const float* w, const void* b, int dtb, void* y, int dty, const ConvTiled& g,
+                           int group, uint32_t xbytes, uint32_t wbytes, hipStream_t s) {
+    const dim3 grid((g.P + BP - 1) / BP, (g.Mg + BM - 1) / BM, group), block(64 * WGM * WGN);
+    if (dty == kF32 && (!b || dtb == kF32))
+        hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32>), grid, block, 0, s, x, w, (const float*)b,
+                           y, dty, dtb, g, xbytes, wbytes);
+    else
+        hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, -1>), grid, block, 0, s, x, w, (const float*)b, y,
+                           dty, dtb, g, xbytes, wbytes);
+}
+
+// Returns false (caller falls back) when a tensor is beyond the 2 GB reach of
+// 32-bit buffer offsets.
+bool launch_conv_tiled(const void* x, const void* w, const void* b, int dtb, void* y, int dty, const ConvGeom& cg,
+                       hipStream_t s) {
+    const int64_t xb = (int64_t)cg.N * cg.C * cg.H * cg.W * 4, wb = (int64_t)cg.M * cg.Kg * 4;
+    const int64_t P = (int64_t)cg.N * cg.OH * cg.OW;
+    if (xb >= ((int64_t)1 << 31) || wb >= ((int64_t)1 << 31) || P >= ((int64_t)1 << 31)) return false;
+    ConvTiled g;
+    g.C = cg.C; g.H = cg.H; g.W = cg.W; g.M = cg.M; g.KH = cg.KH; g.KW = cg.KW; g.OH = cg.OH; g.OW = cg.OW;
+    g.pt = cg.pt; g.pl = cg.pl; g.sh = cg.sh; g.sw = cg.sw; g.dh = cg.dh; g.dw = cg.dw;
+    g.Cg = cg.Cg; g.Mg = cg.Mg; g.Kg = cg.Kg; g.HW = cg.H * cg.W; g.OHW = cg.OH * cg.OW; g.P = (int)P;
+    g.fd_ohw = make_fastdiv((uint32_t)g.OHW);
+    g.fd_ow = make_fastdiv((uint32_t)g.OW);
+    g.fd_khw = make_fastdiv((uint32_t)(g.KH * g.KW));
+    g.fd_kw = make_fastdiv((uint32_t)g.KW);
+    const bool direct = g.KH == 1 && g.KW == 1 && g.sh == 1 && g.sw == 1 && g.pt == 0 && g.pl == 0 &&
+                        g.OH == g.H && g.OW == g.W && g.HW % 4 == 0;
+    const float* xf = (const float*)x;
+    const float* wf = (const float*)w;
+    if (direct && g.Mg >= 128)
+        launch_conv_tiled_cfg<128, 128, 16, 2, 2, 1>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, s);
+    else if (direct)
+        launch_conv_tiled_cfg<64, 256, 16, 1, 4, 1>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, s);
+    else if (g.Mg >= 128)
+        launch_conv_tiled_cfg<128, 128, 16, 2, 2, 0>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, s);
+    else
+        launch_conv_tiled_cfg<64, 256, 16, 1, 4, 0>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, s);
+    return true;
+}
+
 inline bool f32_exact_dtype(int dt) {
     return dt == kF32 || dt == kF16 || dt == kBF16 || dt == kE4M3 || dt == kE5M2 || dt == kI4 || dt == kI8 ||
            dt == kU8 || dt == kI16;
@@ -239,8 +462,12 @@ extern "C" void conv2d_forward(const Tensor* X, const Tensor* W, const Tensor* B
         const bool big = (int64_t)g.N * g.OH * g.OW > 0x7FFFFFFF;
         bool done = false;
         if (!exact_mode() && !big && g.Kg > 0 && f32_exact_dtype(dtx) && f32_exact_dtype(dtw)) {
-            if (dtx == kF32 && dtw == kF32) launch_conv_mfma<kF32, kF32>(x, dtx, w, dtw, b, dtb, y, dty, g, s);
-            else launch_conv_mfma<-1, -1>(x, dtx, w, dtw, b, dtb, y, dty, g, s);
+            if (dtx == kF32 && dtw == kF32) {
+                if (!launch_conv_tiled(x, w, b, dtb, y, dty, g, s))
+                    launch_conv_mfma<kF32, kF32>(x, dtx, w, dtw, b, dtb, y, dty, g, s);
+            } else {
+                launch_conv_mfma<-1, -1>(x, dtx, w, dtw, b, dtb, y, dty, g, s);
+            }
             done = true;
         }
         if (!done)

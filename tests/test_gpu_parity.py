@@ -105,6 +105,38 @@ def test_gemm_f16_tiled_kernel(hip, M, N, K, bias, ydt):
         assert_close(y[rows], ref.astype(np.float32), O.F32, rtol=2e-5, what=f"f16 nt {M}x{N}x{K} {bias}")
 
 
+# f32 x f32 Conv runs the tiled implicit GEMM: MODE 0 (gathered im2col) and
+# MODE 1 (1x1 / stride 1 / no padding with HW % 4 == 0), 64-channel and
+# 128-channel block tiles, groups, dilation, asymmetric padding, ragged channel
+# and pixel counts, no bias, and a narrow output through the generic epilogue.
+CONV_TILED = [
+    ("gather_dil_pads", (2, 5, 13, 11), (7, 5, 3, 2), [1, 0, 2, 1], [2, 1], [1, 2], 1, True, "float32"),
+    ("depthwise", (1, 8, 9, 9), (8, 1, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 8, True, "float32"),
+    ("grouped", (2, 12, 10, 9), (18, 4, 3, 3), [0, 1, 1, 0], [1, 2], [1, 1], 3, True, "float32"),
+    ("direct_m160", (2, 64, 12, 12), (160, 64, 1, 1), [0, 0, 0, 0], [1, 1], [1, 1], 1, True, "float32"),
+    ("direct_m32_nobias", (3, 16, 10, 10), (32, 16, 1, 1), [0, 0, 0, 0], [1, 1], [1, 1], 1, False, "float32"),
+    ("1x1_hw49", (2, 16, 7, 7), (32, 16, 1, 1), [0, 0, 0, 0], [1, 1], [1, 1], 1, True, "float32"),
+    ("1x1_stride2", (2, 32, 14, 14), (64, 32, 1, 1), [0, 0, 0, 0], [2, 2], [1, 1], 1, True, "float32"),
+    ("3x3_m200_k1170", (1, 130, 20, 20), (200, 130, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 1, True, "float32"),
+    ("stem_like", (2, 3, 37, 41), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2], [1, 1], 1, True, "float32"),
+    ("f16_out", (2, 5, 13, 11), (7, 5, 3, 2), [1, 0, 2, 1], [2, 1], [1, 2], 1, True, "float16"),
+    ("direct_f16_out", (2, 64, 12, 12), (160, 64, 1, 1), [0, 0, 0, 0], [1, 1], [1, 1], 1, False, "float16"),
+]
+
+
+@pytest.mark.parametrize("case", CONV_TILED, ids=[c[0] for c in CONV_TILED])
+def test_conv_tiled_kernel(hip, oracle_lib, case):
+    from tests.helpers import assert_close
+    tag, xs, ws, pads, strides, dil, group, has_b, ydt = case
+    rng = np.random.default_rng(len(tag) * 131 + xs[1])
+    x = rng.normal(0, 1, xs).astype(np.float32)
+    w = rng.normal(0, np.sqrt(2 / (ws[1] * ws[2] * ws[3])), ws).astype(np.float32)
+    b = rng.normal(0, 1, (ws[0],)).astype(np.float32) if has_b else None
+    got = hip.conv(x, O.F32, w, O.F32, b, O.F32, ydt, pads, strides, dil, group)
+    ref = oracle_lib.conv(x, O.F32, w, O.F32, b, O.F32, ydt, pads, strides, dil, group)
+    assert_close(got, ref, ydt, what=f"conv {tag}")
+
+
 def test_device_path_matches_host_path(hip):
     """Config-1 chain with device-resident tensors (no host round trips between ops)."""
     from onnx_translator_amd.nn import Tensor
