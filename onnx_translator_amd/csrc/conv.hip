@@ -213,7 +213,7 @@ template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int YDT>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __restrict__ X, const float* __restrict__ Wt,
                                                                const float* __restrict__ Bv, void* __restrict__ Y,
                                                                int dty, int dtb, ConvTiled g, uint32_t xbytes,
-                                                               uint32_t wbytes) {
+                                                               uint32_t wbytes, uint32_t ybytes) {
     constexpr int NT = 64 * WGM * WGN;
     constexpr int WTM = BM / WGM, WTP = BP / WGN, TM = WTM / 32, TP = WTP / 32;
     constexpr int EA = BM * BK / NT;              // weights per thread per k-tile (consecutive k)
@@ -234,19 +234,25 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
     const int wrow = grp * g.Mg + m0 + am;
     const bool am_ok = m0 + am < g.Mg;
 
-    // im2col: MODE 0 -> one pixel, EB consecutive k; MODE 1 -> 4 pixels, EB / 4 k
+    // im2col: MODE 0 -> one pixel, KPT consecutive k; MODE 1 -> 4 pixels, KPT k.
+    // In MODE 0 a thread's k range (kg) is the same across its wave (PCOLS is
+    // a multiple of 64), so the (c, kh, kw) decode runs on scalar registers and
+    // a gathered element costs two adds, two compares and a select.
     constexpr int PPT = MODE == 1 ? 4 : 1;
     constexpr int KPT = EB / PPT;
     constexpr int PCOLS = BP / PPT;
-    const int pc = (t % PCOLS) * PPT, kg = (t / PCOLS) * KPT;
+    static_assert(MODE == 1 || PCOLS % 64 == 0, "a wave must share its k range");
+    const int pc = (t % PCOLS) * PPT;
+    const int kg = MODE == 0 ? __builtin_amdgcn_readfirstlane((t / PCOLS) * KPT) : (t / PCOLS) * KPT;
     const int p = p0 + pc;
-    int ih0 = -(1 << 29), iw0 = 0, xb = 0;
+    int ih0 = -(1 << 29), iw0 = 0, pix = 0;
     if (p < g.P) {
         const int n = (int)g.fd_ohw.div((uint32_t)p), r = p - n * g.OHW;
         const int oh = (int)g.fd_ow.div((uint32_t)r), ow = r - oh * g.OW;
         ih0 = oh * g.sh - g.pt;
         iw0 = ow * g.sw - g.pl;
-        xb = (n * g.C + grp * g.Cg) * g.HW + (MODE == 1 ? r : 0);
+        // element offset of tap (c = 0, kh = 0, kw = 0); in bounds only for valid taps
+        pix = (n * g.C + grp * g.Cg) * g.HW + (MODE == 1 ? r : ih0 * g.W + iw0);
     }
 
     float ra[EA];
@@ -262,7 +268,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
 #pragma unroll
             for (int e = 0; e < KPT; e++) {
                 const int k = k0 + kg + e;
-                const uint32_t off = (ih0 >= 0 && k < g.Kg) ? (uint32_t)(xb + k * g.HW) * 4u : kOOB;
+                const uint32_t off = (ih0 >= 0 && k < g.Kg) ? (uint32_t)(pix + k * g.HW) * 4u : kOOB;
                 typedef unsigned int u32x4 __attribute__((__vector_size__(16)));
                 const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
 #pragma unroll
@@ -281,9 +287,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
             int kw = rem - kh * g.KW;
 #pragma unroll
             for (int e = 0; e < KPT; e++) {
-                const int ih = ih0 + kh * g.dh, iw = iw0 + kw * g.dw;
-                const bool ok = k < g.Kg && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
-                const uint32_t off = ok ? (uint32_t)(xb + c * g.HW + ih * g.W + iw) * 4u : kOOB;
+                const int sdh = kh * g.dh, sdw = kw * g.dw;
+                const int koff = c * g.HW + sdh * g.W + sdw;
+                const bool ok = k < g.Kg && (unsigned)(ih0 + sdh) < (unsigned)g.H && (unsigned)(iw0 + sdw) < (unsigned)g.W;
+                const uint32_t off = ok ? (uint32_t)(pix + koff) * 4u : kOOB;
                 rb[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
                 k++;
                 if (++kw == g.KW) { kw = 0; if (++kh == g.KH) { kh = 0; c++; } }
@@ -329,19 +336,108 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
         }
     };
 
+    // MODE 0: the next tile's gather is interleaved with this tile's MFMA
+    // steps (KPT / (BK / 2) elements after each k-pair), so the wave issues its
+    // address arithmetic while the matrix core works.
+    struct Gather { int k, c, kh, kw; };
+    auto gather_start = [&](int k0) {
+        Gather q;
+        q.k = k0 + kg;
+        q.c = (int)g.fd_khw.div((uint32_t)q.k);
+        const int rem = q.k - q.c * (g.KH * g.KW);
+        q.kh = (int)g.fd_kw.div((uint32_t)rem);
+        q.kw = rem - q.kh * g.KW;
+        return q;
+    };
+    auto gather_one = [&](Gather& q, int e) {
+        const int sdh = q.kh * g.dh, sdw = q.kw * g.dw;
+        const int koff = q.c * g.HW + sdh * g.W + sdw;
+        const bool ok = q.k < g.Kg && (unsigned)(ih0 + sdh) < (unsigned)g.H && (unsigned)(iw0 + sdw) < (unsigned)g.W;
+        const uint32_t off = ok ? (uint32_t)(pix + koff) * 4u : kOOB;
+        rb[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
+        q.k++;
+        if (++q.kw == g.KW) { q.kw = 0; if (++q.kh == g.KH) { q.kh = 0; q.c++; } }
+    };
+    auto load_weights = [&](int k0) {
+#pragma unroll
+        for (int e = 0; e < EA; e++) {
+            const int k = k0 + ak + e;
+            const uint32_t off = (am_ok && k < g.Kg) ? (uint32_t)(wrow * g.Kg + k) * 4u : kOOB;
+            ra[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0));
+        }
+    };
+    auto compute_and_gather = [&](int buf, int k1) {
+        constexpr int PER = (KPT + BK / 2 - 1) / (BK / 2);
+        Gather q = gather_start(k1);
+        load_weights(k1);
+#pragma unroll
+        for (int ks = 0; ks < BK; ks += 2) {
+            float a[TM], b[TP];
+#pragma unroll
+            for (int i = 0; i < TM; i++) a[i] = As[buf][ks + lk][wm * WTM + i * 32 + lr];
+#pragma unroll
+            for (int j = 0; j < TP; j++) b[j] = Bs[buf][ks + lk][wn * WTP + j * 32 + lr];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TP; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int e = (ks / 2) * PER; e < (ks / 2 + 1) * PER; e++)
+                if (e < KPT) gather_one(q, e);
+        }
+    };
+
     const int nk = (g.Kg + BK - 1) / BK;
     load_tile(0);
     store_tile(0);
     __syncthreads();
     int kt = 0;
     for (; kt + 1 < nk; kt++) {
-        load_tile((kt + 1) * BK);
-        compute(kt & 1);
+        if constexpr (MODE == 0) {
+            compute_and_gather(kt & 1, (kt + 1) * BK);
+        } else {
+            load_tile((kt + 1) * BK);
+            compute(kt & 1);
+        }
         store_tile((kt & 1) ^ 1);
         __syncthreads();
     }
     compute(kt & 1);
 
+    // Output row m of the 32x32 tile (i, j), register r: m = mw + i*32 + 8*(r/4) + (r%4) + 4*lk,
+    // pixel q = qw + j*32 + lr.
+    const int mw = m0 + wm * WTM;
+    if (YDT == kF32 && mw + WTM <= g.Mg) {
+        // Raw buffer stores: per-lane byte offset of (m = mw + 4*lk, pixel q) plus
+        // a uniform offset for the tile row, so the 16 x TM x TP stores need no
+        // address arithmetic.
+        const __amdgpu_buffer_rsrc_t yr = buffer_rsrc(Y, ybytes);
+        float bv[TM][16];
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                bv[i][r] = Bv ? ((const gfloat*)Bv)[grp * g.Mg + mw + i * 32 + 8 * (r >> 2) + (r & 3) + 4 * lk] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < TP; j++) {
+            const int q = p0 + wn * WTP + j * 32 + lr;
+            if (q < g.P) {
+                const int qn = (int)g.fd_ohw.div((uint32_t)q), qr = q - qn * g.OHW;
+                const uint32_t vo = (uint32_t)((qn * g.M + grp * g.Mg + mw + 4 * lk) * g.OHW + qr) * 4u;
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const uint32_t so = (uint32_t)((i * 32 + 8 * (r >> 2) + (r & 3)) * g.OHW) * 4u;
+                        // + 0.0f without a bias, as the reference adds bias_val = 0.0 (-0 -> +0)
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc[i][j][r] + bv[i][r]),
+                                                              yr, vo, so, 0);
+                    }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < TP; j++) {
         const int q = p0 + wn * WTP + j * 32 + lr;
@@ -351,12 +447,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int mloc = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+                const int mloc = mw + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
                 if (mloc >= g.Mg) continue;
                 const int m = grp * g.Mg + mloc;
                 const int64_t yi = ((int64_t)qn * g.M + m) * g.OHW + qr;
                 if constexpr (YDT == kF32) {
-                    // + 0.0f without a bias, as the reference adds bias_val = 0.0 (-0 -> +0)
                     ((gfloat*)Y)[yi] = acc[i][j][r] + (Bv ? ((const gfloat*)Bv)[m] : 0.0f);
                 } else {
                     conv_store_rt(Y, dty, yi, Bv, dtb, m, acc[i][j][r]);
@@ -367,14 +462,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
 
 template <int BM, int BP, int BK, int WGM, int WGN, int MODE>
 void launch_conv_tiled_cfg(const float* x, const float* w, const void* b, int dtb, void* y, int dty, const ConvTiled& g,
-                           int group, uint32_t xbytes, uint32_t wbytes, hipStream_t s) {
+                           int group, uint32_t xbytes, uint32_t wbytes, uint32_t ybytes, hipStream_t s) {
     const dim3 grid((g.P + BP - 1) / BP, (g.Mg + BM - 1) / BM, group), block(64 * WGM * WGN);
     if (dty == kF32 && (!b || dtb == kF32))
         hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32>), grid, block, 0, s, x, w, (const float*)b,
-                           y, dty, dtb, g, xbytes, wbytes);
+                           y, dty, dtb, g, xbytes, wbytes, ybytes);
     else
         hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, -1>), grid, block, 0, s, x, w, (const float*)b, y,
-                           dty, dtb, g, xbytes, wbytes);
+                           dty, dtb, g, xbytes, wbytes, ybytes);
 }
 
 // Returns false (caller falls back) when a tensor is beyond the 2 GB reach of
@@ -383,7 +478,8 @@ bool launch_conv_tiled(const void* x, const void* w, const void* b, int dtb, voi
                        hipStream_t s) {
     const int64_t xb = (int64_t)cg.N * cg.C * cg.H * cg.W * 4, wb = (int64_t)cg.M * cg.Kg * 4;
     const int64_t P = (int64_t)cg.N * cg.OH * cg.OW;
-    if (xb >= ((int64_t)1 << 31) || wb >= ((int64_t)1 << 31) || P >= ((int64_t)1 << 31)) return false;
+    const int64_t yb = P * cg.M * 4;
+    if (xb >= ((int64_t)1 << 31) || wb >= ((int64_t)1 << 31) || yb >= ((int64_t)1 << 31)) return false;
     ConvTiled g;
     g.C = cg.C; g.H = cg.H; g.W = cg.W; g.M = cg.M; g.KH = cg.KH; g.KW = cg.KW; g.OH = cg.OH; g.OW = cg.OW;
     g.pt = cg.pt; g.pl = cg.pl; g.sh = cg.sh; g.sw = cg.sw; g.dh = cg.dh; g.dw = cg.dw;
@@ -397,13 +493,13 @@ bool launch_conv_tiled(const void* x, const void* w, const void* b, int dtb, voi
     const float* xf = (const float*)x;
     const float* wf = (const float*)w;
     if (direct && g.Mg >= 128)
-        launch_conv_tiled_cfg<128, 128, 16, 2, 2, 1>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, s);
+        launch_conv_tiled_cfg<128, 128, 16, 2, 2, 1>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, (uint32_t)yb, s);
     else if (direct)
-        launch_conv_tiled_cfg<64, 256, 16, 1, 4, 1>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, s);
+        launch_conv_tiled_cfg<64, 256, 16, 1, 4, 1>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, (uint32_t)yb, s);
     else if (g.Mg >= 128)
-        launch_conv_tiled_cfg<128, 128, 16, 2, 2, 0>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, s);
+        launch_conv_tiled_cfg<128, 128, 16, 2, 2, 0>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, (uint32_t)yb, s);
     else
-        launch_conv_tiled_cfg<64, 256, 16, 1, 4, 0>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, s);
+        launch_conv_tiled_cfg<64, 256, 16, 1, 4, 0>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, (uint32_t)yb, s);
     return true;
 }
 
