@@ -12,21 +12,36 @@
 //     max M and sum S = sum_b s_b * exp(m_b - M) (fixed order) and writes
 //     exp(v - M) / S;
 //   * inner > 1: one thread per column, coalesced along the inner dimension.
-// All sums are in double; they are trees instead of the reference's sequential
-// loop, so results agree to ~1e-16 relative before the final rounding.
+// Max, sums and the final scaling are in double (the sums are trees instead of the
+// reference's sequential loop); exp is sm_exp below (fp64 range reduction,
+// fp32 core) and the divide is a multiply by 1 / sum, so outputs agree with
+// the reference to ~1e-7 relative: a tolerance class (rtol 1e-5).
 //
 // MaxPool (tensor_ops.c:1116-1165): -inf start, in-bounds taps only, strict >
 // in the reference's (kh, kw) order — NaN never wins, an all-padding window
-// gives -inf, the first of +-0 wins.  One wave per output row, one lane per
-// output column (no per-element integer division); a dedicated f32 kernel for
-// the ResNet 3x3 / stride 2 / pad 1 window reads each input row once with
-// 8-byte loads and takes the left tap from the neighbouring lane.
+// gives -inf, the first of +-0 wins.  General windows: one wave per output
+// row, one lane per output column.  The ResNet 3x3 / stride 2 / pad 1 f32
+// window has a block-per-plane strip kernel that loads each input row once.
 #include <cfloat>
 
 #include "runtime.h"
 
 namespace tohip {
 namespace {
+
+// exp(x) for x <= 0 (x = v - max), NaN propagated.  Range reduction in fp64
+// (t = x * log2 e, n = rint(t), f = t - n exactly, |f| <= 1/2), the core 2^f
+// on the fp32 exp2 unit, scaled back with ldexp in fp64: ~1e-7 relative to
+// the reference's libm exp in double, at a fraction of the cost of a full
+// fp64 exp (which made this operator ALU-bound).  Below 2^-1080 the double
+// result underflows to 0, as exp() does.
+__device__ __forceinline__ double sm_exp(double x) {
+    const double t = x * 1.4426950408889634;
+    if (!(t > -1080.0)) return t != t ? t : 0.0;
+    const double n = __builtin_rint(t);
+    const float r = exp2f((float)(t - n));
+    return __builtin_ldexp((double)r, (int)n);
+}
 
 constexpr int kRowThreads = 1024;
 constexpr int kWaves = kRowThreads / 64;
@@ -88,14 +103,15 @@ __global__ __launch_bounds__(kRowThreads) void k_softmax_row(const void* __restr
 #pragma unroll
     for (int t = 0; t < IPT; t++) {
         const int j = threadIdx.x + t * kRowThreads;
-        v[t] = j < L ? exp(v[t] - mx) : 0.0;
+        v[t] = j < L ? sm_exp(v[t] - mx) : 0.0;
         sum += v[t];
     }
     sum = block_reduce<false, kWaves>(sum, lds);
+    const double rs = 1.0 / sum;     // tolerance class: reciprocal instead of a divide per element
 #pragma unroll
     for (int t = 0; t < IPT; t++) {
         const int j = threadIdx.x + t * kRowThreads;
-        if (j < L) st_d<DOUT>(Y, (int64_t)(base + j), v[t] / sum);
+        if (j < L) st_d<DOUT>(Y, (int64_t)(base + j), v[t] * rs);
     }
 }
 
@@ -111,31 +127,49 @@ __global__ __launch_bounds__(kRowThreads) void k_softmax_row_rt(const void* __re
     }
     mx = block_reduce<true, kWaves>(mx, lds);
     double sum = 0.0;
-    for (int64_t j = threadIdx.x; j < L; j += kRowThreads) sum += exp(ld_d_rt(dtx, X, base + j) - mx);
+    for (int64_t j = threadIdx.x; j < L; j += kRowThreads) sum += sm_exp(ld_d_rt(dtx, X, base + j) - mx);
     sum = block_reduce<false, kWaves>(sum, lds);
     for (int64_t j = threadIdx.x; j < L; j += kRowThreads)
-        st_d_rt(dty, Y, base + j, exp(ld_d_rt(dtx, X, base + j) - mx) / sum);
+        st_d_rt(dty, Y, base + j, sm_exp(ld_d_rt(dtx, X, base + j) - mx) / sum);
 }
 
-// Split rows: pass 1.  part[row * G + g] = m_b, part[rows * G + row * G + g] = s_b.
+// Split rows: pass 1.  Block b of a row holds its chunk (up to IPT * 256
+// elements) in registers, reduces its max m_b and then s_b = sum exp(v - m_b)
+// (no second read of X), and writes part[row * G + b] = m_b and
+// part[rows * G + row * G + b] = s_b.  IPT = 0: loop over the chunk instead.
 constexpr int kSplitThreads = 256;
 constexpr int kSplitWaves = kSplitThreads / 64;
 
-template <int DIN>
+template <int DIN, int IPT>
 __global__ __launch_bounds__(kSplitThreads) void k_sm_part(const void* __restrict__ X, int dtx, int64_t L, int G,
                                                            double* __restrict__ part) {
     __shared__ double lds[kSplitWaves];
     const int64_t row = blockIdx.y, rows = gridDim.y, chunk = (L + G - 1) / G;
     const int64_t j0 = blockIdx.x * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
     const int64_t base = row * L;
-    double mx = -DBL_MAX;
-    for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) {
-        const double v = ldx<DIN>(X, base + j, dtx);
-        mx = v > mx ? v : mx;
+    double mx = -DBL_MAX, sum = 0.0;
+    if constexpr (IPT > 0) {
+        double v[IPT];
+#pragma unroll
+        for (int t = 0; t < IPT; t++) {
+            const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
+            v[t] = j < j1 ? ldx<DIN>(X, base + j, dtx) : -DBL_MAX;
+            mx = v[t] > mx ? v[t] : mx;
+        }
+        mx = block_reduce<true, kSplitWaves>(mx, lds);
+#pragma unroll
+        for (int t = 0; t < IPT; t++) {
+            const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
+            if (j < j1) sum += sm_exp(v[t] - mx);
+        }
+    } else {
+        for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) {
+            const double v = ldx<DIN>(X, base + j, dtx);
+            mx = v > mx ? v : mx;
+        }
+        mx = block_reduce<true, kSplitWaves>(mx, lds);
+        for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) sum += sm_exp(ldx<DIN>(X, base + j, dtx) - mx);
     }
-    mx = block_reduce<true, kSplitWaves>(mx, lds);
-    double sum = 0.0;
-    for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) sum += exp(ldx<DIN>(X, base + j, dtx) - mx);
     sum = block_reduce<false, kSplitWaves>(sum, lds);
     if (threadIdx.x == 0) {
         part[row * G + blockIdx.x] = mx;
@@ -143,8 +177,10 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_part(const void* __restric
     }
 }
 
-// Split rows: pass 2.
-template <int DIN, int DOUT>
+// Split rows: pass 2.  Output exp(v - M) * (1 / S): a tolerance-class
+// operator, so the reciprocal (one division per thread, within one double ulp
+// of a division per element) replaces the fp64 divide per element.
+template <int DIN, int DOUT, int IPT>
 __global__ __launch_bounds__(kSplitThreads) void k_sm_out(const void* __restrict__ X, int dtx, void* __restrict__ Y,
                                                           int dty, int64_t L, int G, const double* __restrict__ part) {
     const int64_t row = blockIdx.y, rows = gridDim.y, chunk = (L + G - 1) / G;
@@ -157,9 +193,39 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_out(const void* __restrict
     const int lane = threadIdx.x & 63;
     const double m_l = lane < G ? pm[lane] : -DBL_MAX;
     const double M = wave_max(m_l);
-    const double S = wave_sum(lane < G ? ps[lane] * exp(m_l - M) : 0.0);
-    for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads)
-        stx<DOUT>(Y, base + j, exp(ldx<DIN>(X, base + j, dtx) - M) / S, dty);
+    const double S = wave_sum(lane < G ? ps[lane] * sm_exp(m_l - M) : 0.0);
+    const double rs = 1.0 / S;
+    if constexpr (IPT > 0) {
+        double v[IPT];
+#pragma unroll
+        for (int t = 0; t < IPT; t++) {
+            const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
+            v[t] = j < j1 ? ldx<DIN>(X, base + j, dtx) : 0.0;
+        }
+#pragma unroll
+        for (int t = 0; t < IPT; t++) {
+            const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
+            if (j < j1) stx<DOUT>(Y, base + j, sm_exp(v[t] - M) * rs, dty);
+        }
+    } else {
+        for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads)
+            stx<DOUT>(Y, base + j, sm_exp(ldx<DIN>(X, base + j, dtx) - M) * rs, dty);
+    }
+}
+
+template <int DIN, int DOUT, int IPT>
+void launch_split_ipt(const void* x, int dtx, void* y, int dty, int64_t L, int G, double* part, dim3 g, hipStream_t s) {
+    hipLaunchKernelGGL((k_sm_part<DIN, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, L, G, part);
+    hipLaunchKernelGGL((k_sm_out<DIN, DOUT, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, y, dty, L, G, part);
+}
+
+template <int DIN, int DOUT>
+void launch_split(const void* x, int dtx, void* y, int dty, int64_t L, int G, double* part, dim3 g, hipStream_t s) {
+    const int64_t ipt = ((L + G - 1) / G + kSplitThreads - 1) / kSplitThreads;
+    if (ipt <= 4) launch_split_ipt<DIN, DOUT, 4>(x, dtx, y, dty, L, G, part, g, s);
+    else if (ipt <= 8) launch_split_ipt<DIN, DOUT, 8>(x, dtx, y, dty, L, G, part, g, s);
+    else if (ipt <= 16) launch_split_ipt<DIN, DOUT, 16>(x, dtx, y, dty, L, G, part, g, s);
+    else launch_split_ipt<DIN, DOUT, 0>(x, dtx, y, dty, L, G, part, g, s);
 }
 
 // inner > 1: one thread per (outer, r) column; rows of the axis are coalesced across threads.
@@ -174,10 +240,10 @@ __global__ __launch_bounds__(256) void k_softmax_cols(const void* __restrict__ X
         mx = v > mx ? v : mx;
     }
     double sum = 0.0;
-    for (int64_t j = 0; j < L; j++) sum += exp(ld_d_rt(dtx, X, base + j * inner) - mx);
+    for (int64_t j = 0; j < L; j++) sum += sm_exp(ld_d_rt(dtx, X, base + j * inner) - mx);
     for (int64_t j = 0; j < L; j++) {
         const int64_t i = base + j * inner;
-        st_d_rt(dty, Y, i, exp(ld_d_rt(dtx, X, i) - mx) / sum);
+        st_d_rt(dty, Y, i, sm_exp(ld_d_rt(dtx, X, i) - mx) / sum);
     }
 }
 
@@ -258,6 +324,48 @@ __global__ __launch_bounds__(256) void k_maxpool_3s2(const float* __restrict__ X
     }
 }
 
+// f32, 3x3 window, stride 2, top/left pad 1, W == 2 * OW, OW <= 64: one
+// block per plane, wave w walks a strip of output rows.  Output row oh reads
+// input rows 2oh-1, 2oh, 2oh+1; the last is carried to the next iteration as
+// its first, so every input row is loaded once, as one 8-byte load per lane
+// (columns 2l, 2l+1; column 2l-1 comes from lane l-1).
+__global__ __launch_bounds__(256) void k_maxpool_3s2_strip(const float* __restrict__ X, float* __restrict__ Y,
+                                                           PoolGeom g, int rows_per_wave) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t plane = blockIdx.x;
+    const float* xp = X + plane * (int64_t)g.H * g.W;
+    float* yp = Y + plane * (int64_t)g.OH * g.OW;
+    const bool live = lane < g.OW;
+    const int oh0 = wave * rows_per_wave, oh1 = min(g.OH, oh0 + rows_per_wave);
+    const float ninf = -__builtin_inff();
+    auto ldrow = [&](int ih) {
+        float2 v = make_float2(ninf, ninf);
+        if ((unsigned)ih < (unsigned)g.H && live) v = *reinterpret_cast<const float2*>(xp + (int64_t)ih * g.W + 2 * lane);
+        return v;
+    };
+    // taps of one input row in the reference's kw order: 2l-1, 2l, 2l+1
+    auto row_max = [&](float best, float2 v, bool valid) {
+        const float left = __shfl_up(v.y, 1, 64);
+        if (valid) {
+            if (lane > 0 && left > best) best = left;
+            if (v.x > best) best = v.x;
+            if (v.y > best) best = v.y;
+        }
+        return best;
+    };
+    if (oh0 >= oh1) return;
+    float2 prev = ldrow(2 * oh0 - 1);
+    for (int oh = oh0; oh < oh1; oh++) {
+        const float2 r0 = ldrow(2 * oh), r1 = ldrow(2 * oh + 1);
+        float best = ninf;
+        best = row_max(best, prev, 2 * oh - 1 >= 0);
+        best = row_max(best, r0, 2 * oh < g.H);
+        best = row_max(best, r1, 2 * oh + 1 < g.H);
+        if (live) yp[(int64_t)oh * g.OW + lane] = best;
+        prev = r1;
+    }
+}
+
 }  // namespace
 }  // namespace tohip
 
@@ -285,7 +393,7 @@ void softmax_forward(const Tensor* input, Tensor* output, int axis) {
     if (input->size) {
         // Split rows over G blocks when there are too few rows to fill the chip.
         int G = 1;
-        if (inner == 1 && outer < 2 * num_cus() && outer <= 65535) {
+        if (inner == 1 && outer < num_cus() / 2 && outer <= 65535) {
             G = (int)((4 * num_cus() + outer - 1) / outer);
             const int64_t gmax = (L + 1023) / 1024;            // at least ~1K elements per block
             if (G > gmax) G = (int)gmax;
@@ -294,15 +402,10 @@ void softmax_forward(const Tensor* input, Tensor* output, int axis) {
         if (inner == 1 && G > 1) {
             double* part = (double*)pool_alloc(sizeof(double) * 2 * (size_t)outer * G);
             if (!part) { st.finish(); return; }
-            const dim3 g((unsigned)G, (unsigned)outer), b(kSplitThreads);
-            if (dtx == kF32) {
-                hipLaunchKernelGGL((k_sm_part<kF32>), g, b, 0, s, x, dtx, L, G, part);
-                if (dty == kF32) hipLaunchKernelGGL((k_sm_out<kF32, kF32>), g, b, 0, s, x, dtx, y, dty, L, G, part);
-                else hipLaunchKernelGGL((k_sm_out<kF32, -1>), g, b, 0, s, x, dtx, y, dty, L, G, part);
-            } else {
-                hipLaunchKernelGGL((k_sm_part<-1>), g, b, 0, s, x, dtx, L, G, part);
-                hipLaunchKernelGGL((k_sm_out<-1, -1>), g, b, 0, s, x, dtx, y, dty, L, G, part);
-            }
+            const dim3 g((unsigned)G, (unsigned)outer);
+            if (dtx == kF32 && dty == kF32) launch_split<kF32, kF32>(x, dtx, y, dty, L, G, part, g, s);
+            else if (dtx == kF32) launch_split<kF32, -1>(x, dtx, y, dty, L, G, part, g, s);
+            else launch_split<-1, -1>(x, dtx, y, dty, L, G, part, g, s);
             const bool ok = check_launch(name);
             // Pool buffers are reused in stream order, so the partials can go back now.
             pool_free(part);
@@ -353,7 +456,10 @@ void max_pool_forward(const Tensor* X, Tensor* Y, PoolParams* p) {
         const bool res3s2 = f32 && g.KH == 3 && g.KW == 3 && g.sh == 2 && g.sw == 2 && g.dh == 1 && g.dw == 1 &&
                             g.pt == 1 && g.pl == 1 && g.W == 2 * g.OW && g.OW <= 64 && 2 * g.OH <= g.H + 2 &&
                             ((uintptr_t)x & 7) == 0;
-        if (res3s2)
+        if (res3s2 && planes <= 0x7FFFFFFF)
+            hipLaunchKernelGGL(k_maxpool_3s2_strip, dim3((unsigned)planes), blk, 0, s, (const float*)x, (float*)y, g,
+                               (g.OH + 3) / 4);
+        else if (res3s2)
             hipLaunchKernelGGL(k_maxpool_3s2, grid, blk, 0, s, (const float*)x, (float*)y, g, planes);
         else if (f32)
             hipLaunchKernelGGL((k_maxpool_rows<kF32, kF32>), grid, blk, 0, s, x, dtx, y, dty, g, planes);
