@@ -120,6 +120,23 @@ void gemm_forward(const Tensor* A, const Tensor* B, const Tensor* C, Tensor* Y,
 void softmax_forward(const Tensor* input, Tensor* output, int axis);
 
 /* ---------------------------------------------------------------------------
+ * Reference ABI (operators next to the hot path: the ops a ResNet-style graph
+ * needs between the conv blocks and the classifier, and dynamic quantization)
+ * ------------------------------------------------------------------------- */
+
+/* tensor_ops/tensor_ops.h:210 (tensor_ops.c:1289-1294): copies input->size
+ * elements of the input's width when the sizes match, else does nothing. */
+void flatten_forward(const Tensor* input, Tensor* output);
+/* tensor_ops/tensor_ops.h:216 (tensor_ops.c:1297-1299): same as flatten_forward. */
+void reshape_forward(const Tensor* input, Tensor* output);
+/* tensor_ops/tensor_ops.h:466 (tensor_ops.c:2844-2868): 4-D input only; each
+ * plane summed in double in index order, divided by H * W. */
+void global_average_pool_forward(const Tensor* input, Tensor* output);
+/* tensor_ops/tensor_ops.h:547 (tensor_ops.c:3760-3809): uint8 quantization
+ * with scale / zero point from the tensor's min and max (widened to 0). */
+void dynamic_quantize_linear_forward(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp);
+
+/* ---------------------------------------------------------------------------
  * Extensions (no counterpart in the reference)
  * ------------------------------------------------------------------------- */
 

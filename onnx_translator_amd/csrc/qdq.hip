@@ -1,4 +1,4 @@
-// qdq.hip — QuantizeLinear / DequantizeLinear for gfx950.
+// qdq.hip — QuantizeLinear / DequantizeLinear / DynamicQuantizeLinear for gfx950.
 //
 // tensor_ops/tensor_ops.c:999-1034:
 //   quantize:   y = s != 0 ? rint(x / s) + zp : zp   (double), then the output encoder
@@ -42,6 +42,9 @@
 // loads per thread, plain 4-byte stores (nontemporal 4-byte stores cost ~1 us),
 // 256-thread blocks, 8 blocks per CU; dequantize — one 4-byte code load and
 // one 16-byte nontemporal store per thread, 256-thread blocks, full grid.
+#include <algorithm>
+#include <cfloat>
+
 #include "runtime.h"
 
 namespace tohip {
@@ -504,6 +507,125 @@ void qdq_axis_entry(const char* name, const Tensor* X, const Tensor* S, const Te
     qdq_entry<QUANT>(name, X, &sv, &zv, &yv);
 }
 
+// ------------------------------------------------------- DynamicQuantizeLinear ---
+// tensor_ops.c:3760-3809.  Pass 1 (k_dql_minmax): each block reduces min / max
+// of its grid-stride share with the reference's compares (v < lo, v > hi:
+// NaN never enters), so the result does not depend on the order.  Pass 2
+// (k_dql_quant): every block folds the pass-1 partials itself (no atomics, no
+// cross-block waits), derives scale and zero point in double exactly as the
+// reference does, and quantizes its share; block 0 writes y_scale / y_zp.
+constexpr int kDqlThreads = 256, kDqlMaxParts = 256;
+
+template <int DIN> __device__ __forceinline__ double dql_ld(const void* p, int64_t i, int rdt) {
+    if constexpr (DIN >= 0) return ld_d<DIN>(p, i);
+    else return ld_d_rt(rdt, p, i);
+}
+
+__device__ __forceinline__ void dql_fold(double& lo, double& hi, double* lds) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const double a = __shfl_xor(lo, o, 64), b = __shfl_xor(hi, o, 64);
+        lo = a < lo ? a : lo;
+        hi = b > hi ? b : hi;
+    }
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) { lds[2 * w] = lo; lds[2 * w + 1] = hi; }
+    __syncthreads();
+    lo = lds[0];
+    hi = lds[1];
+#pragma unroll
+    for (int i = 1; i < kDqlThreads / 64; i++) {
+        lo = lds[2 * i] < lo ? lds[2 * i] : lo;
+        hi = lds[2 * i + 1] > hi ? lds[2 * i + 1] : hi;
+    }
+}
+
+template <int DIN>
+__global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const void* __restrict__ X, int dtx, int64_t n,
+                                                            double* __restrict__ part) {
+    __shared__ double lds[2 * kDqlThreads / 64];
+    double lo = DBL_MAX, hi = -DBL_MAX;
+    for (int64_t i = (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kDqlThreads) {
+        const double v = dql_ld<DIN>(X, i, dtx);
+        if (v < lo) lo = v;
+        if (v > hi) hi = v;
+    }
+    dql_fold(lo, hi, lds);
+    if (threadIdx.x == 0) { part[2 * blockIdx.x] = lo; part[2 * blockIdx.x + 1] = hi; }
+}
+
+template <int DIN, int DY>
+__global__ __launch_bounds__(kDqlThreads) void k_dql_quant(const void* __restrict__ X, int dtx, int64_t n,
+                                                           const double* __restrict__ part, int nparts,
+                                                           void* __restrict__ Y, int dty, void* __restrict__ ys, int dts,
+                                                           void* __restrict__ yz, int dtz) {
+    __shared__ double lds[2 * kDqlThreads / 64];
+    double lo = DBL_MAX, hi = -DBL_MAX;
+    for (int i = threadIdx.x; i < nparts; i += kDqlThreads) {
+        lo = part[2 * i] < lo ? part[2 * i] : lo;
+        hi = part[2 * i + 1] > hi ? part[2 * i + 1] : hi;
+    }
+    dql_fold(lo, hi, lds);
+    // fmin(lo, 0.0) / fmax(hi, 0.0) as x86 libm returns them (a zero gives +0)
+    lo = lo < 0.0 ? lo : 0.0;
+    hi = hi > 0.0 ? hi : 0.0;
+    double scale = (hi - lo) / 255.0;
+    if (scale == 0.0) scale = 1.0;
+    double zpd = round(0.0 - lo / scale);
+    if (zpd < 0.0) zpd = 0.0;
+    if (zpd > 255.0) zpd = 255.0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        st_d_rt(dts, ys, 0, scale);
+        st_d_rt(dtz, yz, 0, zpd);       // zpd is an integer in [0, 255]: the code is zpd itself
+    }
+    for (int64_t i = (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kDqlThreads) {
+        const double v = dql_ld<DIN>(X, i, dtx);
+        double q = __builtin_rint(v / scale) + zpd;
+        if (q < 0.0) q = 0.0;
+        if (q > 255.0) q = 255.0;
+        if constexpr (DY >= 0) st_d<DY>(Y, i, q);
+        else st_d_rt(dty, Y, i, q);
+    }
+}
+
+void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp) {
+    const char* name = "dynamic_quantize_linear_forward";
+    if (!tensor_sane(x, name) || !tensor_sane(y, name) || !tensor_sane(y_scale, name) || !tensor_sane(y_zp, name))
+        return;
+    if (y->size < x->size || y_scale->size < 1 || y_zp->size < 1) { set_error("%s: output too small", name); return; }
+    if (!ensure_device()) return;
+    const int64_t n = (int64_t)x->size;
+    Staging st;
+    const void* xd = st.in(x);
+    void* yd = st.out(y, (size_t)n * dt_bytes((int)y->dtype));
+    void* sd = st.out(y_scale, dt_bytes((int)y_scale->dtype));
+    void* zd = st.out(y_zp, dt_bytes((int)y_zp->dtype));
+    double* part = (double*)pool_alloc(sizeof(double) * 2 * kDqlMaxParts);
+    if (!xd || !yd || !sd || !zd || !part) { if (part) pool_free(part); st.finish(); return; }
+    const int nparts = (int)std::min<int64_t>(kDqlMaxParts, std::max<int64_t>(1, (n + 4095) / 4096));
+    const unsigned qblocks = grid_for((size_t)n, kDqlThreads, 4096);
+    const int dtx = (int)x->dtype, dty = (int)y->dtype;
+    hipStream_t s = stream();
+    if (dtx == kF32) {
+        hipLaunchKernelGGL((k_dql_minmax<kF32>), dim3(nparts), dim3(kDqlThreads), 0, s, xd, dtx, n, part);
+        if (dty == kU8)
+            hipLaunchKernelGGL((k_dql_quant<kF32, kU8>), dim3(qblocks), dim3(kDqlThreads), 0, s, xd, dtx, n, part,
+                               nparts, yd, dty, sd, (int)y_scale->dtype, zd, (int)y_zp->dtype);
+        else
+            hipLaunchKernelGGL((k_dql_quant<kF32, -1>), dim3(qblocks), dim3(kDqlThreads), 0, s, xd, dtx, n, part,
+                               nparts, yd, dty, sd, (int)y_scale->dtype, zd, (int)y_zp->dtype);
+    } else {
+        hipLaunchKernelGGL((k_dql_minmax<-1>), dim3(nparts), dim3(kDqlThreads), 0, s, xd, dtx, n, part);
+        hipLaunchKernelGGL((k_dql_quant<-1, -1>), dim3(qblocks), dim3(kDqlThreads), 0, s, xd, dtx, n, part, nparts,
+                           yd, dty, sd, (int)y_scale->dtype, zd, (int)y_zp->dtype);
+    }
+    const bool ok = check_launch(name);
+    pool_free(part);      // pool buffers are reused in stream order
+    if (!ok) { st.finish(); return; }
+    st.finish();
+}
+
 }  // namespace
 }  // namespace tohip
 
@@ -519,6 +641,9 @@ void dequantize_linear_forward(const Tensor* X, const Tensor* Scale, const Tenso
 void quantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint, Tensor* Y,
                                   int axis) {
     qdq_axis_entry<true>("quantize_linear_axis_forward", X, Scale, ZeroPoint, Y, axis);
+}
+void dynamic_quantize_linear_forward(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp) {
+    dql_entry(x, y, y_scale, y_zp);
 }
 void dequantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint, Tensor* Y,
                                     int axis) {

@@ -1,4 +1,4 @@
-// reduce.hip — Softmax and MaxPool for gfx950.
+// reduce.hip — Softmax, MaxPool and GlobalAveragePool for gfx950.
 //
 // Softmax (tensor_ops/tensor_ops.c:1231-1270): the tensor is viewed as
 // [outer, L, inner] around the axis; per (outer, inner) column the reference
@@ -16,6 +16,9 @@
 // reference's sequential loop); exp is sm_exp below (fp64 range reduction,
 // fp32 core) and the divide is a multiply by 1 / sum, so outputs agree with
 // the reference to ~1e-7 relative: a tolerance class (rtol 1e-5).
+//
+// GlobalAveragePool (tensor_ops.c:2844-2868): exact sequential plane sums,
+// one thread per plane over LDS-staged tiles.
 //
 // MaxPool (tensor_ops.c:1116-1165): -inf start, in-bounds taps only, strict >
 // in the reference's (kh, kw) order — NaN never wins, an all-padding window
@@ -366,12 +369,67 @@ __global__ __launch_bounds__(256) void k_maxpool_3s2_strip(const float* __restri
     }
 }
 
+// ------------------------------------------------------------ GlobalAveragePool ---
+// tensor_ops.c:2844-2868: each of the N*C planes summed in double in index
+// order, then divided by H*W.  A block takes 256 consecutive planes (thread t
+// owns plane p0 + t, so the sum keeps the reference's order and is bit-exact);
+// the planes, contiguous in memory, are staged through LDS 16 elements per
+// plane at a time with loads that are coalesced across the block.
+constexpr int kGapPlanes = 256, kGapChunk = 16;
+
+template <int DIN, int DOUT>
+__global__ __launch_bounds__(kGapPlanes) void k_gap(const void* __restrict__ X, int dtx, void* __restrict__ Y, int dty,
+                                                    int64_t planes, int hw) {
+    __shared__ double tile[kGapPlanes][kGapChunk + 1];
+    const int t = threadIdx.x;
+    const int64_t p0 = (int64_t)blockIdx.x * kGapPlanes;
+    const int64_t np = planes - p0 < kGapPlanes ? planes - p0 : kGapPlanes;
+    double sum = 0.0;
+    for (int c0 = 0; c0 < hw; c0 += kGapChunk) {
+        const int cn = hw - c0 < kGapChunk ? hw - c0 : kGapChunk;
+#pragma unroll
+        for (int i = 0; i < kGapChunk; i++) {
+            const int e = t + i * kGapPlanes;               // element e of the 256 x 16 tile
+            const int p = e / kGapChunk, k = e % kGapChunk;
+            if (p < np && k < cn) tile[p][k] = ldx<DIN>(X, (p0 + p) * hw + c0 + k, dtx);
+        }
+        __syncthreads();
+        for (int k = 0; k < cn; k++) sum += tile[t][k];
+        __syncthreads();
+    }
+    if (t < np) stx<DOUT>(Y, p0 + t, sum / hw, dty);
+}
+
 }  // namespace
 }  // namespace tohip
 
 using namespace tohip;
 
 extern "C" {
+
+void global_average_pool_forward(const Tensor* input, Tensor* output) {
+    const char* name = "global_average_pool_forward";
+    if (!tensor_sane(input, name) || !tensor_sane(output, name)) return;
+    if (input->ndim != 4) { set_error("%s: input must be 4-D (the reference leaves the output untouched)", name); return; }
+    const int64_t planes = (int64_t)input->shape[0] * input->shape[1];
+    const int hw = input->shape[2] * input->shape[3];
+    if (output->size < (size_t)planes) { set_error("%s: output holds %zu of %lld values", name, output->size, (long long)planes); return; }
+    if (!ensure_device()) return;
+    Staging st;
+    const void* x = st.in(input);
+    void* y = st.out(output, (size_t)planes * dt_bytes((int)output->dtype));
+    if (!x || !y) { st.finish(); return; }
+    if (planes > 0) {
+        const dim3 g((unsigned)((planes + kGapPlanes - 1) / kGapPlanes)), b(kGapPlanes);
+        const int dtx = (int)input->dtype, dty = (int)output->dtype;
+        hipStream_t s = stream();
+        if (dtx == kF32 && dty == kF32) hipLaunchKernelGGL((k_gap<kF32, kF32>), g, b, 0, s, x, dtx, y, dty, planes, hw);
+        else hipLaunchKernelGGL((k_gap<-1, -1>), g, b, 0, s, x, dtx, y, dty, planes, hw);
+        if (!check_launch(name)) { st.finish(); return; }
+    }
+    st.finish();
+}
+
 
 void softmax_forward(const Tensor* input, Tensor* output, int axis) {
     const char* name = "softmax_forward";

@@ -541,6 +541,27 @@ int tensor_from_host(Tensor* t, const void* host_src) {
     return 0;
 }
 
+// tensor_ops.c:1289-1299: a byte copy of input->size elements of the input's
+// width, done only when the element counts match.  Device tensors copy on the
+// library stream (asynchronous); a host operand makes the call synchronous.
+// Where the reference would silently do nothing (count mismatch) or overrun a
+// narrower output, an error is reported instead.
+static void copy_tensor(const Tensor* in, Tensor* out, const char* name) {
+    if (!tensor_sane(in, name) || !tensor_sane(out, name)) return;
+    if (in->size != out->size) { set_error("%s: %zu elements into %zu", name, in->size, out->size); return; }
+    const size_t b = in->size * dt_bytes((int)in->dtype);
+    if (b > tensor_bytes(out)) { set_error("%s: output holds fewer bytes than the input", name); return; }
+    if (!b || in->data == out->data) return;
+    const bool di = is_dev(classify(in->data)), dout = is_dev(classify(out->data));
+    if (!di && !dout) { memcpy(out->data, in->data, b); return; }
+    if (!ensure_device()) return;
+    if (!check_hip(hipMemcpyAsync(out->data, in->data, b, hipMemcpyDefault, stream()), name)) return;
+    if (!(di && dout)) (void)check_hip(hipStreamSynchronize(stream()), "stream synchronize");
+}
+
+void flatten_forward(const Tensor* input, Tensor* output) { copy_tensor(input, output, "flatten_forward"); }
+void reshape_forward(const Tensor* input, Tensor* output) { copy_tensor(input, output, "reshape_forward"); }
+
 int tensor_ops_hip_sync(void) {
     if (!ensure_device()) return -1;
     return check_hip(hipStreamSynchronize(stream()), "stream synchronize") ? 0 : -1;

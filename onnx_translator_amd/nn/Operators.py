@@ -1,4 +1,6 @@
-"""The 13 hot-path operator classes over libtensor_ops_hip.so.
+"""Operator classes over libtensor_ops_hip.so: the 13 hot-path operators and
+the ones a ResNet-style graph needs next to them (Flatten, Reshape,
+GlobalAveragePool, DynamicQuantizeLinear).
 
 Same class names, constructor signatures and ``forward`` / ``forward_``
 results as the reference (``nn/Operators.py:9-704``):
@@ -21,7 +23,8 @@ import numpy as np
 from . import DTYPE_TO_NUMPY, DeviceArray, Ops, Tensor, Tensor_, PT
 
 __all__ = ["CConvParams", "CPoolParams", "CReduceParams", "RELU", "COS", "ABS", "ADD", "SUB", "MUL", "DIV",
-           "QuantizeLinear", "DequantizeLinear", "Conv", "MaxPool", "Gemm", "Softmax"]
+           "QuantizeLinear", "DequantizeLinear", "Conv", "MaxPool", "Gemm", "Softmax", "Flatten", "Reshape",
+           "GlobalAveragePool", "DynamicQuantizeLinear"]
 
 
 class CConvParams(ctypes.Structure):
@@ -312,3 +315,111 @@ class Softmax(Ops):
 
     def forward_(self, input: Tensor_):
         return _values(self, Tensor_(*input.size, dtype=self.dtype))
+
+
+class Flatten(Ops):
+    """Collapse to 2-D around ``axis`` (nn/Operators.py:776-825 -> tensor_ops.c:1289-1294)."""
+
+    def __init__(self, inputs, outputs, axis=1, dtype="float32", version="17"):
+        super().__init__(inputs, outputs)
+        self.axis = axis
+        self.dtype = dtype
+        self.version = version
+
+    def _calc_shape(self, input_shape):
+        axis = self.axis if self.axis >= 0 else len(input_shape) + self.axis
+        d0 = int(np.prod(input_shape[:axis], dtype=np.int64)) if axis > 0 else 1
+        d1 = int(np.prod(input_shape[axis:], dtype=np.int64))
+        return (d0, d1)
+
+    def forward(self, input: Tensor):
+        return _values(self, self._run("flatten_forward", [input], self._calc_shape(input.size), self.dtype))
+
+    def forward_(self, input: Tensor_):
+        return _values(self, Tensor_(*self._calc_shape(input.size), dtype=self.dtype))
+
+
+class Reshape(Ops):
+    """Reshape to the shape held by the second input, -1 inferred
+    (nn/Operators.py:827-871 -> tensor_ops.c:1297-1299)."""
+
+    def __init__(self, inputs, outputs, dtype="float32", version="17"):
+        super().__init__(inputs, outputs)
+        self.dtype = dtype
+        self.version = version
+
+    @staticmethod
+    def _target(data_size, shape):
+        target = np.asarray(shape.numpy() if isinstance(shape, Tensor) else shape).astype(np.int64).reshape(-1).tolist()
+        known = 1
+        infer = -1
+        for i, v in enumerate(target):
+            if v == -1:
+                infer = i
+            else:
+                known *= v
+        if infer != -1:
+            target[infer] = data_size // known
+        return tuple(int(v) for v in target)
+
+    def forward(self, data: Tensor, shape: Tensor):
+        final = self._target(data.data_size, shape)
+        return _values(self, self._run("reshape_forward", [data], final, self.dtype))
+
+    def forward_(self, data: Tensor_, shape):
+        return _values(self, Tensor_(*self._target(data.data_size, shape), dtype=self.dtype))
+
+
+class GlobalAveragePool(Ops):
+    """Mean over the two trailing (spatial) dims: NCHW -> NC11
+    (nn/Operators.py:2997-3021 -> tensor_ops.c:2844-2868)."""
+
+    def __init__(self, inputs, outputs, dtype="float32", version="17"):
+        super().__init__(inputs, outputs)
+        self.dtype = dtype
+        self.version = version
+
+    def forward(self, x: Tensor):
+        out_shape = tuple(x.size[:-2]) + (1, 1)
+        return _values(self, self._run("global_average_pool_forward", [x], out_shape, self.dtype))
+
+    def forward_(self, x: Tensor_):
+        return _values(self, Tensor_(*(tuple(x.size[:-2]) + (1, 1)), dtype=self.dtype))
+
+
+class DynamicQuantizeLinear(Ops):
+    """uint8 quantization with scale / zero point computed from the data
+    (nn/Operators.py:3891-3927 -> tensor_ops.c:3760-3809).  ``forward`` returns
+    ``{"tensor": [y, y_scale, y_zero_point], "parameters": None}``."""
+
+    def __init__(self, inputs, outputs, dtype="uint8", version="17"):
+        super().__init__(inputs, outputs)
+        self.dtype = "uint8"
+        self.version = version
+
+    def forward(self, x: Tensor):
+        keep: list = []
+        dev = isinstance(x.data, DeviceArray)
+        outs = []
+        try:
+            cx = self._in_ctensor(x, keep)
+            for shape, dt in ((tuple(x.size), "uint8"), ((1,), "float32"), ((1,), "uint8")):
+                outs.append((shape, dt) + self._out_ctensor(shape, dt, dev))
+            self._call("dynamic_quantize_linear_forward", cx, *[o[3] for o in outs])
+        except Exception:
+            for shape, dt, d, c in outs:
+                if d is None:
+                    self.lib.free_tensor(c)
+            for c in keep:
+                self.lib.free_tensor(c)
+            raise
+        tensors = [self._finish(shape, dt, d, c, []) for shape, dt, d, c in outs]
+        for c in keep:
+            self.lib.free_tensor(c)
+        values = {"tensor": tensors, "parameters": None}
+        self.parameters = {"values": values}
+        return values
+
+    def forward_(self, x: Tensor_):
+        return {"tensor": [Tensor_(*x.size, dtype="uint8"), Tensor_(1, dtype="float32"), Tensor_(1, dtype="uint8")],
+                "parameters": None}

@@ -203,6 +203,9 @@ class Ops:
                         _sig(lib, n, None, [P, P, P, P])
                     for n in ("quantize_linear_axis_forward", "dequantize_linear_axis_forward"):
                         _sig(lib, n, None, [P, P, P, P, ctypes.c_int])
+                    for n in ("flatten_forward", "reshape_forward", "global_average_pool_forward"):
+                        _sig(lib, n, None, [P, P])
+                    _sig(lib, "dynamic_quantize_linear_forward", None, [P, P, P, P])
                     _sig(lib, "tensor_is_device", ctypes.c_int, [P])
                     _sig(lib, "tensor_to_host", ctypes.c_int, [P, ctypes.c_void_p])
                     _sig(lib, "tensor_from_host", ctypes.c_int, [P, ctypes.c_void_p])

@@ -96,6 +96,9 @@ class CpuLib:
         lib.gemm_forward.argtypes = [PT, PT, PT, PT, ctypes.c_float, ctypes.c_float,
                                      ctypes.c_int, ctypes.c_int]
         lib.softmax_forward.argtypes = [PT, PT, ctypes.c_int]
+        for n in ("flatten_forward", "reshape_forward", "global_average_pool_forward"):
+            getattr(lib, n).argtypes = [PT, PT]
+        lib.dynamic_quantize_linear_forward.argtypes = [PT, PT, PT, PT]
         lib.init_cos_lut.argtypes = []
         lib.init_cos_lut()
         self.lib = lib
@@ -196,6 +199,29 @@ class CpuLib:
 
     def softmax(self, x, dtx, dty, axis):
         return self._run(self.lib.softmax_forward, [(x, dtx)], x.shape, dty, int(axis))
+
+    def flatten(self, x, dtx, out_shape, dty=None, name="flatten"):
+        """flatten_forward / reshape_forward: byte copy into a tensor of out_shape."""
+        x = np.asarray(x)
+        return self._run(getattr(self.lib, name + "_forward"), [(x, dtx)], out_shape,
+                         dtx if dty is None else dty)
+
+    def gap(self, x, dtx, dty):
+        x = np.asarray(x)
+        return self._run(self.lib.global_average_pool_forward, [(x, dtx)],
+                         x.shape[:-2] + (1, 1), dty)
+
+    def dql(self, x, dtx, zdt="uint8"):
+        """dynamic_quantize_linear_forward -> (y uint8, scale float32 [1], zero point [1])."""
+        x = np.asarray(x)
+        tx = self.tensor(x, dtx)
+        ty, ts, tz = self.empty(x.shape, U8), self.empty((1,), F32), self.empty((1,), zdt)
+        try:
+            self.lib.dynamic_quantize_linear_forward(tx, ty, ts, tz)
+            return self.read(ty, U8), self.read(ts, F32), self.read(tz, zdt)
+        finally:
+            for t in (tx, ty, ts, tz):
+                self.lib.free_tensor(t)
 
     # -- oracle-only probes -------------------------------------------------
     def encode_f32(self, x, dt):

@@ -579,6 +579,62 @@ void softmax_forward(const Tensor* in, Tensor* out, int axis) {
     }
 }
 
+/* ---------------- Flatten / Reshape (tensor_ops.c:1289-1299) ---------------- */
+/* A byte copy of input->size elements of the input's width; sizes must match. */
+void flatten_forward(const Tensor* in, Tensor* out) {
+    if (!in || !out || in->size != out->size) return;
+    memcpy(out->data, in->data, in->size * elem_bytes(in->dtype));
+}
+void reshape_forward(const Tensor* in, Tensor* out) { flatten_forward(in, out); }
+
+/* ---------------- GlobalAveragePool (tensor_ops.c:2844-2868) ---------------- */
+/* 4-D input only (anything else leaves the output untouched); each of the
+ * N*C planes is summed in double in index order, then divided by H*W. */
+void global_average_pool_forward(const Tensor* in, Tensor* out) {
+    if (!in || !out || in->ndim != 4) return;
+    const int planes = in->shape[0] * in->shape[1];
+    const int hw = in->shape[2] * in->shape[3];
+    #pragma omp parallel for schedule(static)
+    for (int n = 0; n < planes; n++) {
+        double sum = 0.0;
+        for (int i = 0; i < hw; i++) sum += read_f64(in, (size_t)n * hw + i);
+        write_from_f64(out, (size_t)n, sum / hw);
+    }
+}
+
+/* ---------------- DynamicQuantizeLinear (tensor_ops.c:3760-3809) ---------------- */
+/* min / max over x (NaN never compares), widened to include 0; scale =
+ * (max - min) / 255 in double (1 when 0); zero point = round(-min / scale)
+ * (half away from zero) clamped to [0, 255]; y = clamp(rint(x / scale) + zp,
+ * 0, 255) with the double scale, written through the output encoder. */
+void dynamic_quantize_linear_forward(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp) {
+    if (!x || !y || !y_scale || !y_zp) return;
+    double lo = DBL_MAX, hi = -DBL_MAX;
+    for (size_t i = 0; i < x->size; i++) {
+        const double v = read_f64(x, i);
+        if (v < lo) lo = v;
+        if (v > hi) hi = v;
+    }
+    lo = fmin(lo, 0.0);
+    hi = fmax(hi, 0.0);
+    double scale = (hi - lo) / 255.0;
+    if (scale == 0.0) scale = 1.0;
+    double zpd = round(0.0 - lo / scale);
+    if (zpd < 0.0) zpd = 0.0;
+    if (zpd > 255.0) zpd = 255.0;
+    const uint8_t zp = (uint8_t)zpd;
+    write_from_f64(y_scale, 0, scale);
+    if (y_zp->dtype == DTYPE_UINT8) ((uint8_t*)y_zp->data)[0] = zp;
+    else write_from_f64(y_zp, 0, (double)zp);
+    #pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < x->size; i++) {
+        double q = rint(read_f64(x, i) / scale) + (double)zp;
+        if (q < 0.0) q = 0.0;
+        if (q > 255.0) q = 255.0;
+        write_from_f64(y, i, q);
+    }
+}
+
 /* ---------------- codec probes for exhaustive sweeps (oracle-only symbols) ---------------- */
 void oracle_encode_f32(const float* x, void* out, size_t n, int dtype) {
     #pragma omp parallel for schedule(static)

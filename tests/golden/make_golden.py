@@ -82,9 +82,15 @@ class Writer:
             k = f"{name}__in{i}"
             self.arrays[k] = np.asarray(a)
             keys.append(k)
-        self.arrays[f"{name}__out"] = out
+        if isinstance(out, (tuple, list)):          # several outputs (DynamicQuantizeLinear)
+            outk = [f"{name}__out{i}" for i in range(len(out))]
+            for k, a in zip(outk, out):
+                self.arrays[k] = np.asarray(a)
+        else:
+            outk = f"{name}__out"
+            self.arrays[outk] = out
         self.cases.append({"name": name, "op": op, "inputs": keys, "dtypes": dts,
-                           "out_dtype": out_dt, "out": f"{name}__out", "params": params})
+                           "out_dtype": out_dt, "out": outk, "params": params})
 
     def save(self):
         with open(os.path.join(HERE, "cases.json"), "w") as f:
@@ -129,6 +135,12 @@ def call(lib, op, ins, dts, out_dt, params):
                         params["alpha"], params["beta"], params["transA"], params["transB"])
     if op == "softmax":
         return lib.softmax(ins[0], dts[0], out_dt, params["axis"])
+    if op in ("flatten", "reshape"):
+        return lib.flatten(ins[0], dts[0], tuple(params["shape"]), out_dt, name=op)
+    if op == "global_average_pool":
+        return lib.gap(ins[0], dts[0], out_dt)
+    if op == "dynamic_quantize_linear":
+        return lib.dql(ins[0], dts[0], params.get("zp_dtype", "uint8"))
     raise ValueError(op)
 
 
@@ -386,6 +398,41 @@ def config_cases(ref, w):
     w.add("c5_softmax_f64out", "softmax", [x], ["float32"], "float64", out, axis=-1)
 
 
+def next_row_cases(ref, w):
+    """Operators next to the hot path: GlobalAveragePool, Flatten / Reshape and
+    DynamicQuantizeLinear (tensor_ops.c:1289-1299, 2844-2868, 3760-3809)."""
+    rng = np.random.default_rng(5)
+    for tag, shape, dt, ydt in (("f32_7x7", (2, 8, 7, 7), "float32", "float32"),
+                                ("f32_odd", (2, 3, 13, 11), "float32", "float32"),
+                                ("f32_56x56", (1, 4, 56, 56), "float32", "float32"),
+                                ("f16", (2, 4, 5, 6), "float16", "float16"),
+                                ("i8_to_f32", (2, 3, 4, 4), "int8", "float32"),
+                                ("f32_to_f64", (1, 5, 9, 9), "float32", "float64")):
+        x = gen(rng, shape, dt)
+        w.add(f"gap_{tag}", "global_average_pool", [x], [dt], ydt, ref.gap(x, dt, ydt))
+    for tag, shape, oshape, dt in (("f32", (2, 3, 4, 5), (2, 60), "float32"),
+                                   ("i8", (4, 6), (24,), "int8"),
+                                   ("f16_4d", (2, 8, 1, 1), (2, 8), "float16")):
+        x = gen(rng, shape, dt)
+        for op in ("flatten", "reshape"):
+            w.add(f"{op}_{tag}", op, [x], [dt], dt, ref.flatten(x, dt, oshape, dt, name=op),
+                  shape=list(oshape))
+    x = rng.normal(0, 1.5, (4, 16, 64))
+    x[rng.random(x.shape) < 0.01] *= 20
+    specials = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1.0], np.float32)
+    dql_inputs = [("normal", x.astype(np.float32), "float32"),
+                  ("positive", np.abs(x).astype(np.float32) + 0.5, "float32"),
+                  ("negative", -np.abs(x).astype(np.float32) - 0.5, "float32"),
+                  ("zeros", np.zeros((3, 5), np.float32), "float32"),
+                  ("ties", (np.arange(-300, 300) * 0.5).astype(np.float32), "float32"),
+                  ("nan", np.concatenate([x.reshape(-1)[:200].astype(np.float32), specials[:1]]), "float32"),
+                  ("inf", np.concatenate([x.reshape(-1)[:200].astype(np.float32), specials[1:3]]), "float32"),
+                  ("f16", x.astype(np.float16).view(np.uint16), "float16"),
+                  ("i32", rng.integers(-1000, 3000, (40, 9)).astype(np.int32), "int32")]
+    for tag, xin, dt in dql_inputs:
+        w.add(f"dql_{tag}", "dynamic_quantize_linear", [xin], [dt], "uint8", ref.dql(xin, dt))
+
+
 def make_cases(ref):
     w = Writer()
     rng = np.random.default_rng(12345)
@@ -393,6 +440,7 @@ def make_cases(ref):
         run_case(ref, w, f"plan{i:02d}_{op}", op, shapes, dts, out_dt, params, rng)
     edge_cases(ref, w)
     config_cases(ref, w)
+    next_row_cases(ref, w)
     w.save()
     print(f"wrote {len(w.cases)} cases")
 

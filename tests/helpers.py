@@ -133,7 +133,18 @@ def assert_close(out, ref, dt, rtol=1e-5, what=""):
 TOL_OPS = {"gemm", "conv2d", "softmax"}
 
 
+def out_dtypes(case):
+    """Output dtype per output key (DynamicQuantizeLinear: y, y_scale, y_zero_point)."""
+    if case["op"] == "dynamic_quantize_linear":
+        return ["uint8", "float32", case["params"].get("zp_dtype", "uint8")]
+    return [case["out_dtype"]]
+
+
 def check_case(out, case, arrays, exact):
+    if isinstance(case["out"], list):
+        for i, (o, k, dt) in enumerate(zip(out, case["out"], out_dtypes(case))):
+            assert_bitexact(o, arrays[k], dt, what=f"{case['name']} output {i}")
+        return
     ref = arrays[case["out"]]
     if case["op"] in TOL_OPS and not exact:
         assert_close(out, ref, case["out_dtype"], what=case["name"])
@@ -184,6 +195,14 @@ class HipLib(O.CpuLib):
     def _run(self, fn, ins, out_shape, out_dt, *extra):
         self.lib.tensor_ops_hip_clear_error()
         out = super()._run(fn, ins, out_shape, out_dt, *extra)
+        err = self.last_error()
+        if err:
+            raise RuntimeError(err)
+        return out
+
+    def dql(self, x, dtx, zdt="uint8"):
+        self.lib.tensor_ops_hip_clear_error()
+        out = super().dql(x, dtx, zdt)
         err = self.last_error()
         if err:
             raise RuntimeError(err)

@@ -294,3 +294,45 @@ def test_dequantize_all_codes(hip, oracle_lib, xdt):
         assert_bitexact(hip.qdq("dequantize", codes, xdt, sfull, O.F32, zfull, zdt, O.F32),
                         oracle_lib.qdq("dequantize", codes, xdt, sfull, O.F32, zfull, zdt, O.F32), O.F32,
                         what="DQ full-size")
+
+
+# ---------------------------------------------------------------- next rows ---
+def test_dynamic_quantize_linear_full_size(hip, oracle_lib, x2):
+    """DynamicQuantizeLinear on the config-2 activation tensor (16.8 M values), bit-exact."""
+    y, s, z = hip.dql(x2, O.F32)
+    ry, rs, rz = oracle_lib.dql(x2, O.F32)
+    assert_bitexact(s, rs, O.F32, what="dql scale")
+    assert_bitexact(z, rz, O.U8, what="dql zero point")
+    assert_bitexact(y, ry, O.U8, what="dql codes")
+
+
+@pytest.mark.parametrize("shape", [(64, 512, 7, 7), (8, 64, 56, 56), (3, 5, 1, 1), (1, 300, 3, 3)])
+def test_global_average_pool_sizes(hip, oracle_lib, shape):
+    rng = np.random.default_rng(sum(shape))
+    x = rng.normal(0, 1, shape).astype(np.float32)
+    for ydt in (O.F32, O.F64, O.F16):
+        assert_bitexact(hip.gap(x, O.F32, ydt), oracle_lib.gap(x, O.F32, ydt), ydt, what=f"gap {shape} -> {ydt}")
+
+
+def test_next_row_ops_device_resident(hip):
+    """Flatten / Reshape / GlobalAveragePool / DynamicQuantizeLinear through the
+    Python layer on device tensors give the host path's bits."""
+    from onnx_translator_amd.nn import Tensor
+    from onnx_translator_amd.nn.Operators import DynamicQuantizeLinear, Flatten, GlobalAveragePool, Reshape
+    rng = np.random.default_rng(8)
+    x = rng.normal(0, 1, (4, 32, 7, 7)).astype(np.float32)
+    host = Tensor(*x.shape, dtype="float32", data=x)
+    dev = host.to_device() if hasattr(host, "to_device") else None
+    assert dev is not None
+    for op, args in ((GlobalAveragePool(["x"], ["y"], dtype="float32"), ()),
+                     (Flatten(["x"], ["y"], axis=1, dtype="float32"), ()),
+                     (Reshape(["x", "s"], ["y"], dtype="float32"), (np.array([4, -1], np.int64),))):
+        h = op.forward(host, *args)["tensor"]
+        d = op.forward(dev, *args)["tensor"]
+        assert d.on_device and d.size == h.size
+        assert_bitexact(d.numpy(), h.numpy(), O.F32, what=type(op).__name__)
+    q = DynamicQuantizeLinear(["x"], ["y", "s", "z"])
+    hs = [t.numpy() for t in q.forward(host)["tensor"]]
+    ds = [t.numpy() for t in q.forward(dev)["tensor"]]
+    for a, b, dt in zip(ds, hs, (O.U8, O.F32, O.U8)):
+        assert_bitexact(a, b, dt, what="dql device")

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.helpers import assert_bitexact, load_cases, run_case, nan_mask
+from tests.helpers import assert_bitexact, check_case, load_cases, run_case, nan_mask
 
 CASES, ARRAYS = load_cases()
 
@@ -23,7 +23,7 @@ CASES, ARRAYS = load_cases()
 @pytest.mark.parametrize("case", CASES, ids=[c["name"] for c in CASES])
 def test_oracle_matches_reference_golden(oracle_lib, case):
     out = run_case(oracle_lib, case, ARRAYS)
-    assert_bitexact(out, ARRAYS[case["out"]], case["out_dtype"], what=case["name"])
+    check_case(out, case, ARRAYS, exact=True)
 
 
 # ------------------------------------------------------------------ codecs ---
@@ -222,6 +222,39 @@ def test_conv_gemm_softmax_pool_brute_force(oracle_lib):
     ref = np.stack([np.stack([pp[:, :, 2 * i:2 * i + 3, 2 * j:2 * j + 2].max(axis=(2, 3))
                               for j in range(got.shape[3])], -1) for i in range(got.shape[2])], -2)
     assert np.array_equal(got, ref)
+
+
+def test_gap_flatten_closed_form(oracle_lib):
+    """GlobalAveragePool = sequential double sum / (H*W) per plane; Flatten = bytes."""
+    rng = np.random.default_rng(21)
+    x = rng.normal(0, 1, (2, 3, 5, 7)).astype(np.float32)
+    got = oracle_lib.gap(x, O.F32, O.F64)
+    want = np.empty((2, 3, 1, 1))
+    for n in range(2):
+        for c in range(3):
+            acc = 0.0
+            for v in x[n, c].reshape(-1).tolist():
+                acc += v
+            want[n, c, 0, 0] = acc / 35
+    assert np.array_equal(got, want)
+    assert np.array_equal(oracle_lib.gap(x, O.F32, O.F32), want.astype(np.float32))
+    assert np.array_equal(oracle_lib.flatten(x, O.F32, (2, 105)), x.reshape(2, 105))
+    assert np.array_equal(oracle_lib.flatten(x, O.F32, (6, 35), name="reshape"), x.reshape(6, 35))
+
+
+def test_dql_closed_form(oracle_lib):
+    """DynamicQuantizeLinear against a numpy restatement of its formulas, including a
+    minimum exactly on a zero-point tie (round half away from zero) and all-equal input."""
+    rng = np.random.default_rng(22)
+    for x in (rng.normal(0, 2, 500).astype(np.float32), np.abs(rng.normal(0, 2, 100)).astype(np.float32),
+              np.full(7, -3.0, np.float32), np.array([-0.5, 127.0], np.float32)):
+        lo, hi = min(float(x.min()), 0.0), max(float(x.max()), 0.0)
+        scale = (hi - lo) / 255.0 or 1.0
+        t = 0.0 - lo / scale
+        zp = min(max(np.floor(abs(t) + 0.5) * np.sign(t), 0.0), 255.0)
+        q = np.clip(np.rint(x.astype(np.float64) / scale) + zp, 0, 255).astype(np.uint8)
+        y, s, z = oracle_lib.dql(x, O.F32)
+        assert np.array_equal(y, q) and s[0] == np.float32(scale) and z[0] == zp, (x[:4], s, z)
 
 
 def test_int_paths(oracle_lib):
