@@ -54,6 +54,10 @@ class CT(ctypes.Structure):
 PT = ctypes.POINTER(CT)
 
 
+class CStep(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_int), ("operand", ctypes.c_int), ("reversed", ctypes.c_int)]
+
+
 class Params(ctypes.Structure):
     _fields_ = [("a", ctypes.POINTER(ctypes.c_int)), ("b", ctypes.POINTER(ctypes.c_int)),
                 ("c", ctypes.POINTER(ctypes.c_int)), ("d", ctypes.POINTER(ctypes.c_int))]
@@ -90,6 +94,10 @@ class Lib:
         L.conv2d_forward.argtypes = [PT, PT, PT, PT, ctypes.POINTER(ConvP)]
         L.max_pool_forward.argtypes = [PT, PT, ctypes.POINTER(Params)]
         L.softmax_forward.argtypes = [PT, PT, ctypes.c_int]
+        L.elementwise_chain_forward.argtypes = [PT, ctypes.POINTER(PT), ctypes.c_int, ctypes.POINTER(CStep),
+                                                ctypes.c_int, PT]
+        L.global_average_pool_forward.argtypes = [PT, PT]
+        L.dynamic_quantize_linear_forward.argtypes = [PT, PT, PT, PT]
         L.init_cos_lut()
 
     def dev(self, arr, dt):
@@ -239,6 +247,13 @@ def run_suite(lib, torch):
     for name, fn in (("relu", L.relu_forward), ("abs", L.abs_forward), ("cos", L.cos_forward)):
         ms = bench_loop(torch, lambda i: fn(As[i % R], Os[i % R]), 200)
         out.append(op_line(f"{name}_f32", "config1 [8,64,56,56]", nb, ms, "hbm"))
+    # The same chain fused into one kernel (bit-identical to the op-by-op chain):
+    # 4 B in + 4 B out per element, plus the two [64,1,1] operands.
+    steps = (CStep * 7)(CStep(0, 0, 0), CStep(2, 0, 0), CStep(1, 0, 0), CStep(3, 1, 0), CStep(4, 0, 0),
+                        CStep(5, 0, 0), CStep(6, 0, 0))
+    opnds = (PT * 2)(tb, tbd)
+    ms = bench_loop(torch, lambda i: L.elementwise_chain_forward(As[i % R], opnds, 2, steps, 7, Os[i % R]), 200)
+    out.append(op_line("chain7_f32_fused", "config1 Add>Mul>Sub>Div>Relu>Abs>Cos, one pass", nb, ms, "hbm"))
     I = rng.integers(-(2 ** 31), 2 ** 31 - 1, A.shape, dtype=np.int64).astype(np.int32)
     Is = [lib.dev(I, I32) for _ in range(20)]
     O64 = [lib.empty(list(A.shape), F64) for _ in range(20)]
@@ -310,6 +325,27 @@ def run_suite(lib, torch):
     for t in ts + to:
         L.free_tensor(t)
     lib.check("config5")
+
+    # Next rows: GlobalAveragePool at the config-5 classifier input and
+    # DynamicQuantizeLinear over the config-2 activation tensor.
+    rng = np.random.default_rng(5)
+    g = rng.normal(0, 1, (64, 512, 7, 7)).astype(np.float32)
+    tg = [lib.dev(g, F32) for _ in range(20)]
+    to = [lib.empty([64, 512, 1, 1], F32) for _ in range(20)]
+    ms = bench_loop(torch, lambda i: L.global_average_pool_forward(tg[i % 20], to[i % 20]), 200)
+    out.append(op_line("global_avg_pool", "[64,512,7,7] -> [64,512,1,1]", g.size * 4 + 64 * 512 * 4, ms, "hbm"))
+    for t in tg + to:
+        L.free_tensor(t)
+    x = config2_input(np.random.default_rng(1))
+    tx = [lib.dev(x, F32) for _ in range(4)]
+    ty = [lib.empty(list(x.shape), U8) for _ in range(4)]
+    ts, tz = lib.empty([1], F32), lib.empty([1], U8)
+    ms = bench_loop(torch, lambda i: L.dynamic_quantize_linear_forward(tx[i % 4], ty[i % 4], ts, tz), 50)
+    # two reads of x (min / max, then quantize) and one write of the codes
+    out.append(op_line("dynamic_quantize_linear", "x f32 [32,512,1024] -> u8", x.size * 9, ms, "hbm"))
+    for t in tx + ty + [ts, tz]:
+        L.free_tensor(t)
+    lib.check("next rows")
     return out
 
 

@@ -165,6 +165,24 @@ const char* tensor_ops_hip_version(void);
 /* Gemm/Conv precision mode: 0 = MFMA fp32/fp16 accumulate (default, tolerance class);
  * 1 = exact replica of the reference (double accumulate, sequential k, bit-identical). */
 void tensor_ops_hip_set_exact(int exact);
+/* Fused elementwise chain: one pass over X that applies the steps in order to the
+ * running value v; binary steps take operands[operand] broadcast to X's shape and
+ * compute v op b (b op v when reversed).  Every step rounds to float32 as the
+ * standalone operator (add_forward, ..., cos_forward) writes its output, so Y equals
+ * the op-by-op chain bit for bit.  float32 only; at most 3 operands and 16 steps.
+ * Replaces a sequence of the reference's unary / binary calls on one tensor
+ * (tensor_ops/tensor_ops.h:85-143). */
+enum {
+    TENSOR_OPS_CHAIN_ADD = 0, TENSOR_OPS_CHAIN_SUB = 1, TENSOR_OPS_CHAIN_MUL = 2, TENSOR_OPS_CHAIN_DIV = 3,
+    TENSOR_OPS_CHAIN_RELU = 4, TENSOR_OPS_CHAIN_ABS = 5, TENSOR_OPS_CHAIN_COS = 6
+};
+typedef struct {
+    int op;         /* TENSOR_OPS_CHAIN_* */
+    int operand;    /* index into operands (binary steps) */
+    int reversed;   /* binary steps: 1 computes operand op v */
+} TensorOpsChainStep;
+void elementwise_chain_forward(const Tensor* X, const Tensor* const* operands, int noperands,
+                               const TensorOpsChainStep* steps, int nsteps, Tensor* Y);
 /* Per-axis quantize / dequantize with 1-D Scale / ZeroPoint of length X->shape[axis]. */
 void quantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint,
                                   Tensor* Y, int axis);

@@ -255,7 +255,7 @@ __device__ __forceinline__ void st_stream(uint32_t* p, uint32_t v) { __builtin_n
 // operand has one element stride per dim (0 where it broadcasts).
 // ----------------------------------------------------------------------------
 constexpr int kMaxDims = 8;
-constexpr int kMaxOperands = 3;
+constexpr int kMaxOperands = 4;
 
 // Division by a run-time invariant d >= 1 for 32-bit numerators:
 // q = (umulhi(n, m) + n) >> s with s = ceil(log2 d), m = 2^32 (2^s - d) / d + 1.

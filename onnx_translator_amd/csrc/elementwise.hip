@@ -1,4 +1,4 @@
-// elementwise.hip — Relu, Abs, Cos, Add, Sub, Mul, Div for gfx950.
+// elementwise.hip — Relu, Abs, Cos, Add, Sub, Mul, Div and their fused chain for gfx950.
 //
 // Memory-bound kernels: each thread moves 16-byte vectors along the
 // innermost (collapsed) dimension, broadcast operands are indexed through a
@@ -46,10 +46,25 @@ template <int OP> __device__ __forceinline__ int64_t iop(int64_t a, int64_t b) {
     }
 }
 
+// fmod(a, 2pi) for a = |x|, exactly.  Below 2^30 the quotient q = trunc(a / 2pi)
+// is found from a * (1 / 2pi) to within one, and fma(-q, 2pi, a) is exact
+// for the right q (the remainder of fmod is representable and the fma rounds
+// the exact value a - q * 2pi once); an off-by-one q shows as r < 0 or
+// r >= 2pi and is corrected the same way.  Larger (or non-finite) a uses fmod.
+__device__ __forceinline__ double fmod_two_pi(double a) {
+    const double two_pi = 2.0 * 3.141592653589793238462643383279502884197;
+    if (!(a < 0x1p30)) return fmod(a, two_pi);
+    const double q = __builtin_trunc(a * (1.0 / two_pi));
+    double r = __builtin_fma(-q, two_pi, a);
+    if (r < 0.0) r = __builtin_fma(-(q - 1.0), two_pi, a);
+    else if (r >= two_pi) r = __builtin_fma(-(q + 1.0), two_pi, a);
+    return r;
+}
+
 // tensor_ops.c:815-833: r = fmod(|x|, 2pi); pos = r * 4096 / 2pi; lerp.
 __device__ __forceinline__ double lut_cos(double x, const double* __restrict__ T) {
     const double two_pi = 2.0 * 3.141592653589793238462643383279502884197;
-    const double r = fmod(fabs(x), two_pi);
+    const double r = fmod_two_pi(fabs(x));
     if (r != r) return r;                              // NaN / inf input
     const double pos = r * 4096.0 / two_pi;
     int k = (int)pos;
@@ -286,12 +301,185 @@ void unary_entry(const char* name, const Tensor* X, Tensor* Y) {
     st.finish();
 }
 
+// ------------------------------------------------------------ fused chain ---
+// One pass over X applying a sequence of the operators above (the config-1
+// chain Add -> Mul -> Sub -> Div -> Relu -> Abs -> Cos, or any other), f32
+// throughout.  Each step rounds to f32 exactly as the standalone operator
+// writes its output (native fp32 + - * /, Relu / Abs bit rules, the Cos table
+// in fp64), so the result is the op-by-op result bit for bit while the
+// intermediates never leave registers.  Operand k (at most 3) is broadcast
+// to X's shape through the descriptor (operand k + 1 of d).
+// The program is packed 8 bits per step (op | operand << 3 | reversed << 5)
+// into two 64-bit words held in scalar registers, so the unrolled step loop
+// decodes it with shifts instead of indexing the kernel argument memory.
+constexpr int kChainMaxSteps = 16, kChainMaxOperands = kMaxOperands - 1;
+struct ChainProg {
+    int n;
+    uint64_t code[2];
+};
+
+// One step on the W values of a thread: one (uniform) dispatch per step.
+template <int W>
+__device__ __forceinline__ void chain_step(int op, float (&v)[W], const float (&b)[W], int rev, const double* T) {
+    switch (op) {
+    case TENSOR_OPS_CHAIN_ADD:
+#pragma unroll
+        for (int e = 0; e < W; e++) v[e] = rev ? b[e] + v[e] : v[e] + b[e];
+        break;
+    case TENSOR_OPS_CHAIN_SUB:
+#pragma unroll
+        for (int e = 0; e < W; e++) v[e] = rev ? b[e] - v[e] : v[e] - b[e];
+        break;
+    case TENSOR_OPS_CHAIN_MUL:
+#pragma unroll
+        for (int e = 0; e < W; e++) v[e] = rev ? b[e] * v[e] : v[e] * b[e];
+        break;
+    case TENSOR_OPS_CHAIN_DIV:
+#pragma unroll
+        for (int e = 0; e < W; e++) v[e] = rev ? b[e] / v[e] : v[e] / b[e];
+        break;
+    case TENSOR_OPS_CHAIN_RELU:
+#pragma unroll
+        for (int e = 0; e < W; e++) v[e] = unary_f32<U_RELU>(v[e], T);
+        break;
+    case TENSOR_OPS_CHAIN_ABS:
+#pragma unroll
+        for (int e = 0; e < W; e++) v[e] = unary_f32<U_ABS>(v[e], T);
+        break;
+    default:
+#pragma unroll
+        for (int e = 0; e < W; e++) v[e] = unary_f32<U_COS>(v[e], T);
+        break;
+    }
+}
+
+// V4: eight consecutive elements per thread as two float4 (inner dim % 8 == 0,
+// 16-byte aligned), which amortises the per-step dispatch; else one element.
+template <int ND, bool V4>
+__global__ __launch_bounds__(kBlock) void k_chain_f32(const float* __restrict__ X, const float* __restrict__ B0,
+                                                      const float* __restrict__ B1, const float* __restrict__ B2,
+                                                      float* __restrict__ Y, BDesc d, ChainProg prog, uint32_t nitems,
+                                                      int stream_x, const double* __restrict__ T) {
+    constexpr int W = V4 ? 8 : 1;
+    const float* Bp[3] = {B0, B1, B2};
+    const uint32_t stride = gridDim.x * kBlock;
+    for (uint32_t it = blockIdx.x * kBlock + threadIdx.x; it < nitems; it += stride) {
+        int64_t off[kMaxOperands];
+        bd_offsets32<kMaxOperands, ND>(d, it * W, off);
+        float v[W], b[kChainMaxOperands][W];
+        if constexpr (V4) {
+            const int64_t sx = d.st[0][d.nd - 1];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const float4 x = load4(X, off[0] + 4 * h * sx, sx, stream_x != 0);
+                v[4 * h] = x.x; v[4 * h + 1] = x.y; v[4 * h + 2] = x.z; v[4 * h + 3] = x.w;
+            }
+        } else {
+            v[0] = X[off[0]];
+        }
+#pragma unroll
+        for (int k = 0; k < kChainMaxOperands; k++) {
+            if (!Bp[k]) continue;
+            if constexpr (V4) {
+                const int64_t sb = d.st[k + 1][d.nd - 1];
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const float4 t = load4(Bp[k], off[k + 1] + 4 * h * sb, sb, false);
+                    b[k][4 * h] = t.x; b[k][4 * h + 1] = t.y; b[k][4 * h + 2] = t.z; b[k][4 * h + 3] = t.w;
+                }
+            } else {
+                b[k][0] = Bp[k][off[k + 1]];
+            }
+        }
+        for (int sidx = 0; sidx < prog.n; sidx++) {
+            const uint32_t c = (uint32_t)(prog.code[sidx >> 3] >> (8 * (sidx & 7))) & 0xFFu;
+            const int a = (c >> 3) & 3;
+            float bb[W];
+#pragma unroll
+            for (int e = 0; e < W; e++) bb[e] = a == 0 ? b[0][e] : (a == 1 ? b[1][e] : b[2][e]);
+            chain_step<W>((int)(c & 7u), v, bb, (int)((c >> 5) & 1u), T);
+        }
+        if constexpr (V4) {
+            st_stream(reinterpret_cast<float4*>(Y) + 2 * it, make_float4(v[0], v[1], v[2], v[3]));
+            st_stream(reinterpret_cast<float4*>(Y) + 2 * it + 1, make_float4(v[4], v[5], v[6], v[7]));
+        } else {
+            Y[it] = v[0];
+        }
+    }
+}
+
+void chain_entry(const Tensor* X, const Tensor* const* operands, int noperands, const TensorOpsChainStep* steps,
+                 int nsteps, Tensor* Y) {
+    const char* name = "elementwise_chain_forward";
+    if (!tensor_sane(X, name) || !tensor_sane(Y, name)) return;
+    if (noperands < 0 || noperands > kChainMaxOperands) { set_error("%s: at most %d operands", name, kChainMaxOperands); return; }
+    if (nsteps < 0 || nsteps > kChainMaxSteps || (nsteps && !steps)) { set_error("%s: 0..%d steps", name, kChainMaxSteps); return; }
+    if (X->dtype != DTYPE_FLOAT32 || Y->dtype != DTYPE_FLOAT32) { set_error("%s: float32 X and Y only", name); return; }
+    if (X->size != Y->size) { set_error("%s: X and Y sizes differ", name); return; }
+    ChainProg prog{};
+    prog.n = nsteps;
+    bool cos = false;
+    for (int i = 0; i < nsteps; i++) {
+        const int op = steps[i].op;
+        if (op < TENSOR_OPS_CHAIN_ADD || op > TENSOR_OPS_CHAIN_COS) { set_error("%s: step %d: unknown op %d", name, i, op); return; }
+        const bool bin = op <= TENSOR_OPS_CHAIN_DIV;
+        if (bin && (steps[i].operand < 0 || steps[i].operand >= noperands)) {
+            set_error("%s: step %d: operand %d out of range", name, i, steps[i].operand);
+            return;
+        }
+        const uint64_t c = (uint64_t)op | ((uint64_t)(bin ? steps[i].operand : 0) << 3) |
+                           ((uint64_t)(bin && steps[i].reversed ? 1 : 0) << 5);
+        prog.code[i >> 3] |= c << (8 * (i & 7));
+        cos |= op == TENSOR_OPS_CHAIN_COS;
+    }
+    const Tensor* ops[kMaxOperands] = {Y, nullptr, nullptr, nullptr};
+    ops[0] = X;
+    for (int k = 0; k < noperands; k++) {
+        if (!tensor_sane(operands[k], name)) return;
+        if (operands[k]->dtype != DTYPE_FLOAT32) { set_error("%s: float32 operands only", name); return; }
+        ops[k + 1] = operands[k];
+    }
+    if (!ensure_device()) return;
+    const double* T = nullptr;
+    if (cos && !(T = device_cos_lut())) return;
+    BDesc d;
+    if (!make_bdesc_for(d, Y, ops, 1 + noperands)) return;
+    Staging st;
+    const float* x = (const float*)st.in(X);
+    const float* b[kChainMaxOperands] = {nullptr, nullptr, nullptr};
+    for (int k = 0; k < noperands; k++)
+        if (!(b[k] = (const float*)st.in(operands[k]))) { st.finish(); return; }
+    float* y = (float*)st.out(Y, tensor_bytes(Y));
+    if (!x || !y) { st.finish(); return; }
+    const size_t n = Y->size;
+    if (n) {
+        if (n >= ((size_t)1 << 31)) { set_error("%s: more than 2^31 elements", name); st.finish(); return; }
+        bool v4 = d.dim[d.nd - 1] % 8u == 0 && aligned16(x) && aligned16(y);
+        for (int k = 0; k < noperands; k++) v4 = v4 && aligned16(b[k]);
+        hipStream_t s = stream();
+        if (v4) {
+            const uint32_t nv = (uint32_t)(n / 8);
+            ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, true>), dim3(grid_for(nv, kBlock)), dim3(kBlock), 0, s,
+                                               x, b[0], b[1], b[2], y, d, prog, nv, 1, T));
+        } else {
+            ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, false>), dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s,
+                                               x, b[0], b[1], b[2], y, d, prog, (uint32_t)n, 0, T));
+        }
+        if (!check_launch(name)) { st.finish(); return; }
+    }
+    st.finish();
+}
+
 }  // namespace
 }  // namespace tohip
 
 using namespace tohip;
 
 extern "C" {
+void elementwise_chain_forward(const Tensor* X, const Tensor* const* operands, int noperands,
+                               const TensorOpsChainStep* steps, int nsteps, Tensor* Y) {
+    chain_entry(X, operands, noperands, steps, nsteps, Y);
+}
 void relu_forward(const Tensor* input, Tensor* output) { unary_entry<U_RELU>("relu_forward", input, output); }
 void abs_forward(const Tensor* input, Tensor* output) { unary_entry<U_ABS>("abs_forward", input, output); }
 void cos_forward(const Tensor* input, Tensor* output) { unary_entry<U_COS>("cos_forward", input, output); }

@@ -508,13 +508,15 @@ void qdq_axis_entry(const char* name, const Tensor* X, const Tensor* S, const Te
 }
 
 // ------------------------------------------------------- DynamicQuantizeLinear ---
-// tensor_ops.c:3760-3809.  Pass 1 (k_dql_minmax): each block reduces min / max
-// of its grid-stride share with the reference's compares (v < lo, v > hi:
-// NaN never enters), so the result does not depend on the order.  Pass 2
-// (k_dql_quant): every block folds the pass-1 partials itself (no atomics, no
-// cross-block waits), derives scale and zero point in double exactly as the
-// reference does, and quantizes its share; block 0 writes y_scale / y_zp.
-constexpr int kDqlThreads = 256, kDqlMaxParts = 256;
+// tensor_ops.c:3760-3809.  Three launches:
+//  * k_dql_minmax: each block reduces min / max of its grid-stride share with
+//    the reference's compares (v < lo, v > hi: NaN never enters), so the
+//    result does not depend on the order; f32 input is read as float4;
+//  * k_dql_params: one block folds the partials and derives scale and zero
+//    point in double exactly as the reference (y_scale / y_zp written here);
+//  * k_dql_quant: y = clamp(rint(x / scale) + zp, 0, 255) with the double
+//    scale, four elements per thread.
+constexpr int kDqlThreads = 256, kDqlMaxParts = 2048;
 
 template <int DIN> __device__ __forceinline__ double dql_ld(const void* p, int64_t i, int rdt) {
     if constexpr (DIN >= 0) return ld_d<DIN>(p, i);
@@ -546,7 +548,23 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const void* __restri
                                                             double* __restrict__ part) {
     __shared__ double lds[2 * kDqlThreads / 64];
     double lo = DBL_MAX, hi = -DBL_MAX;
-    for (int64_t i = (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kDqlThreads) {
+    const int64_t stride = (int64_t)gridDim.x * kDqlThreads;
+    int64_t tail = 0;
+    if constexpr (DIN == kF32) {
+        const int64_t nv = n / 4;
+        for (int64_t v = (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; v < nv; v += stride) {
+            const float4 x = ld_stream(reinterpret_cast<const float4*>(X) + v);
+            const float e[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const double d = (double)e[k];
+                if (d < lo) lo = d;
+                if (d > hi) hi = d;
+            }
+        }
+        tail = nv * 4;
+    }
+    for (int64_t i = tail + (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; i < n; i += stride) {
         const double v = dql_ld<DIN>(X, i, dtx);
         if (v < lo) lo = v;
         if (v > hi) hi = v;
@@ -555,11 +573,10 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const void* __restri
     if (threadIdx.x == 0) { part[2 * blockIdx.x] = lo; part[2 * blockIdx.x + 1] = hi; }
 }
 
-template <int DIN, int DY>
-__global__ __launch_bounds__(kDqlThreads) void k_dql_quant(const void* __restrict__ X, int dtx, int64_t n,
-                                                           const double* __restrict__ part, int nparts,
-                                                           void* __restrict__ Y, int dty, void* __restrict__ ys, int dts,
-                                                           void* __restrict__ yz, int dtz) {
+// params[0] = scale, params[1] = zero point (an integer in [0, 255]).
+__global__ __launch_bounds__(kDqlThreads) void k_dql_params(const double* __restrict__ part, int nparts,
+                                                            double* __restrict__ params, void* __restrict__ ys,
+                                                            int dts, void* __restrict__ yz, int dtz) {
     __shared__ double lds[2 * kDqlThreads / 64];
     double lo = DBL_MAX, hi = -DBL_MAX;
     for (int i = threadIdx.x; i < nparts; i += kDqlThreads) {
@@ -567,6 +584,7 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(const void* __restric
         hi = part[2 * i + 1] > hi ? part[2 * i + 1] : hi;
     }
     dql_fold(lo, hi, lds);
+    if (threadIdx.x != 0) return;
     // fmin(lo, 0.0) / fmax(hi, 0.0) as x86 libm returns them (a zero gives +0)
     lo = lo < 0.0 ? lo : 0.0;
     hi = hi > 0.0 ? hi : 0.0;
@@ -575,15 +593,38 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(const void* __restric
     double zpd = round(0.0 - lo / scale);
     if (zpd < 0.0) zpd = 0.0;
     if (zpd > 255.0) zpd = 255.0;
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        st_d_rt(dts, ys, 0, scale);
-        st_d_rt(dtz, yz, 0, zpd);       // zpd is an integer in [0, 255]: the code is zpd itself
+    params[0] = scale;
+    params[1] = zpd;
+    st_d_rt(dts, ys, 0, scale);
+    st_d_rt(dtz, yz, 0, zpd);       // zpd is an integer in [0, 255]: the code is zpd itself
+}
+
+__device__ __forceinline__ double dql_q(double v, double scale, double zpd) {
+    double q = __builtin_rint(v / scale) + zpd;
+    if (q < 0.0) q = 0.0;
+    if (q > 255.0) q = 255.0;
+    return q;
+}
+
+template <int DIN, int DY>
+__global__ __launch_bounds__(kDqlThreads) void k_dql_quant(const void* __restrict__ X, int dtx, int64_t n,
+                                                           const double* __restrict__ params, void* __restrict__ Y,
+                                                           int dty) {
+    const double scale = params[0], zpd = params[1];
+    const int64_t stride = (int64_t)gridDim.x * kDqlThreads;
+    int64_t tail = 0;
+    if constexpr (DIN == kF32 && DY == kU8) {
+        const int64_t nv = n / 4;
+        for (int64_t v = (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; v < nv; v += stride) {
+            const float4 x = ld_stream(reinterpret_cast<const float4*>(X) + v);
+            const uint32_t c = (uint32_t)dql_q(x.x, scale, zpd) | ((uint32_t)dql_q(x.y, scale, zpd) << 8) |
+                               ((uint32_t)dql_q(x.z, scale, zpd) << 16) | ((uint32_t)dql_q(x.w, scale, zpd) << 24);
+            st_stream(reinterpret_cast<uint32_t*>(Y) + v, c);
+        }
+        tail = nv * 4;
     }
-    for (int64_t i = (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kDqlThreads) {
-        const double v = dql_ld<DIN>(X, i, dtx);
-        double q = __builtin_rint(v / scale) + zpd;
-        if (q < 0.0) q = 0.0;
-        if (q > 255.0) q = 255.0;
+    for (int64_t i = tail + (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; i < n; i += stride) {
+        const double q = dql_q(dql_ld<DIN>(X, i, dtx), scale, zpd);
         if constexpr (DY >= 0) st_d<DY>(Y, i, q);
         else st_d_rt(dty, Y, i, q);
     }
@@ -601,25 +642,26 @@ void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp) {
     void* yd = st.out(y, (size_t)n * dt_bytes((int)y->dtype));
     void* sd = st.out(y_scale, dt_bytes((int)y_scale->dtype));
     void* zd = st.out(y_zp, dt_bytes((int)y_zp->dtype));
-    double* part = (double*)pool_alloc(sizeof(double) * 2 * kDqlMaxParts);
+    double* part = (double*)pool_alloc(sizeof(double) * (2 * kDqlMaxParts + 2));
     if (!xd || !yd || !sd || !zd || !part) { if (part) pool_free(part); st.finish(); return; }
-    const int nparts = (int)std::min<int64_t>(kDqlMaxParts, std::max<int64_t>(1, (n + 4095) / 4096));
-    const unsigned qblocks = grid_for((size_t)n, kDqlThreads, 4096);
+    double* params = part + 2 * kDqlMaxParts;
     const int dtx = (int)x->dtype, dty = (int)y->dtype;
+    const bool v4 = dtx == kF32 && ((uintptr_t)xd & 15) == 0;
+    const int64_t items = v4 ? n / 4 : n;
+    const int nparts = (int)std::min<int64_t>(kDqlMaxParts, std::max<int64_t>(1, (items + 4 * kDqlThreads - 1) /
+                                                                                     (4 * kDqlThreads)));
+    const unsigned qblocks = grid_for((size_t)std::max<int64_t>(items, 1), kDqlThreads, 8192);
     hipStream_t s = stream();
-    if (dtx == kF32) {
-        hipLaunchKernelGGL((k_dql_minmax<kF32>), dim3(nparts), dim3(kDqlThreads), 0, s, xd, dtx, n, part);
-        if (dty == kU8)
-            hipLaunchKernelGGL((k_dql_quant<kF32, kU8>), dim3(qblocks), dim3(kDqlThreads), 0, s, xd, dtx, n, part,
-                               nparts, yd, dty, sd, (int)y_scale->dtype, zd, (int)y_zp->dtype);
-        else
-            hipLaunchKernelGGL((k_dql_quant<kF32, -1>), dim3(qblocks), dim3(kDqlThreads), 0, s, xd, dtx, n, part,
-                               nparts, yd, dty, sd, (int)y_scale->dtype, zd, (int)y_zp->dtype);
-    } else {
-        hipLaunchKernelGGL((k_dql_minmax<-1>), dim3(nparts), dim3(kDqlThreads), 0, s, xd, dtx, n, part);
-        hipLaunchKernelGGL((k_dql_quant<-1, -1>), dim3(qblocks), dim3(kDqlThreads), 0, s, xd, dtx, n, part, nparts,
-                           yd, dty, sd, (int)y_scale->dtype, zd, (int)y_zp->dtype);
-    }
+    if (v4) hipLaunchKernelGGL((k_dql_minmax<kF32>), dim3(nparts), dim3(kDqlThreads), 0, s, xd, dtx, n, part);
+    else hipLaunchKernelGGL((k_dql_minmax<-1>), dim3(nparts), dim3(kDqlThreads), 0, s, xd, dtx, n, part);
+    hipLaunchKernelGGL(k_dql_params, dim3(1), dim3(kDqlThreads), 0, s, part, nparts, params, sd, (int)y_scale->dtype,
+                       zd, (int)y_zp->dtype);
+    if (v4 && dty == kU8 && ((uintptr_t)yd & 3) == 0)
+        hipLaunchKernelGGL((k_dql_quant<kF32, kU8>), dim3(qblocks), dim3(kDqlThreads), 0, s, xd, dtx, n, params, yd, dty);
+    else if (dtx == kF32)
+        hipLaunchKernelGGL((k_dql_quant<kF32, -1>), dim3(qblocks), dim3(kDqlThreads), 0, s, xd, dtx, n, params, yd, dty);
+    else
+        hipLaunchKernelGGL((k_dql_quant<-1, -1>), dim3(qblocks), dim3(kDqlThreads), 0, s, xd, dtx, n, params, yd, dty);
     const bool ok = check_launch(name);
     pool_free(part);      // pool buffers are reused in stream order
     if (!ok) { st.finish(); return; }

@@ -371,11 +371,12 @@ __global__ __launch_bounds__(256) void k_maxpool_3s2_strip(const float* __restri
 
 // ------------------------------------------------------------ GlobalAveragePool ---
 // tensor_ops.c:2844-2868: each of the N*C planes summed in double in index
-// order, then divided by H*W.  A block takes 256 consecutive planes (thread t
+// order, then divided by H*W.  A block takes 64 consecutive planes (thread t
 // owns plane p0 + t, so the sum keeps the reference's order and is bit-exact);
-// the planes, contiguous in memory, are staged through LDS 16 elements per
-// plane at a time with loads that are coalesced across the block.
-constexpr int kGapPlanes = 256, kGapChunk = 16;
+// the planes, contiguous in memory, are staged through LDS 64 elements per
+// plane at a time (one pass for planes up to 8x8) with loads that are
+// coalesced across the wave.
+constexpr int kGapPlanes = 64, kGapChunk = 64;
 
 template <int DIN, int DOUT>
 __global__ __launch_bounds__(kGapPlanes) void k_gap(const void* __restrict__ X, int dtx, void* __restrict__ Y, int dty,
@@ -398,6 +399,50 @@ __global__ __launch_bounds__(kGapPlanes) void k_gap(const void* __restrict__ X, 
         __syncthreads();
     }
     if (t < np) stx<DOUT>(Y, p0 + t, sum / hw, dty);
+}
+
+// f32 planes of at most 128 values: a wave's 64 planes are one contiguous
+// region, copied into LDS with fully coalesced loads, then lane l sums plane
+// l from LDS in index order (the same exact sequential sum).
+constexpr int kGapSmallHW = 128;
+
+template <int DOUT>
+__global__ __launch_bounds__(64) void k_gap_small_f32(const float* __restrict__ X, void* __restrict__ Y, int dty,
+                                                      int64_t planes, int hw) {
+    __shared__ float tile[64 * kGapSmallHW];
+    const int lane = threadIdx.x;
+    const int64_t p0 = (int64_t)blockIdx.x * 64;
+    const int np = planes - p0 < 64 ? (int)(planes - p0) : 64;
+    const int cnt = np * hw;
+    // 16 loads in flight per lane before the LDS stores (buffer loads: reads
+    // past the region return 0 without touching memory)
+    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(X + p0 * hw, (uint32_t)cnt * 4u);
+    for (int base = 0; base < cnt; base += 64 * 16) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            v[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (uint32_t)(base + lane + 64 * j) * 4u, 0, 0));
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int i = base + lane + 64 * j;
+            if (i < cnt) tile[i] = v[j];
+        }
+    }
+    __syncthreads();
+    if (lane < np) {
+        const float* t = tile + lane * hw;
+        double sum = 0.0;
+        int k = 0;
+        for (; k + 4 <= hw; k += 4) {
+            const float a = t[k], b = t[k + 1], c = t[k + 2], d = t[k + 3];
+            sum += (double)a;
+            sum += (double)b;
+            sum += (double)c;
+            sum += (double)d;
+        }
+        for (; k < hw; k++) sum += (double)t[k];
+        stx<DOUT>(Y, p0 + lane, sum / hw, dty);
+    }
 }
 
 }  // namespace
@@ -423,8 +468,15 @@ void global_average_pool_forward(const Tensor* input, Tensor* output) {
         const dim3 g((unsigned)((planes + kGapPlanes - 1) / kGapPlanes)), b(kGapPlanes);
         const int dtx = (int)input->dtype, dty = (int)output->dtype;
         hipStream_t s = stream();
-        if (dtx == kF32 && dty == kF32) hipLaunchKernelGGL((k_gap<kF32, kF32>), g, b, 0, s, x, dtx, y, dty, planes, hw);
-        else hipLaunchKernelGGL((k_gap<-1, -1>), g, b, 0, s, x, dtx, y, dty, planes, hw);
+        const dim3 gs((unsigned)((planes + 63) / 64)), bs(64);
+        if (dtx == kF32 && hw <= kGapSmallHW && dty == kF32)
+            hipLaunchKernelGGL((k_gap_small_f32<kF32>), gs, bs, 0, s, (const float*)x, y, dty, planes, hw);
+        else if (dtx == kF32 && hw <= kGapSmallHW)
+            hipLaunchKernelGGL((k_gap_small_f32<-1>), gs, bs, 0, s, (const float*)x, y, dty, planes, hw);
+        else if (dtx == kF32 && dty == kF32)
+            hipLaunchKernelGGL((k_gap<kF32, kF32>), g, b, 0, s, x, dtx, y, dty, planes, hw);
+        else
+            hipLaunchKernelGGL((k_gap<-1, -1>), g, b, 0, s, x, dtx, y, dty, planes, hw);
         if (!check_launch(name)) { st.finish(); return; }
     }
     st.finish();

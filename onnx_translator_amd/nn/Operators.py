@@ -24,7 +24,7 @@ from . import DTYPE_TO_NUMPY, DeviceArray, Ops, Tensor, Tensor_, PT
 
 __all__ = ["CConvParams", "CPoolParams", "CReduceParams", "RELU", "COS", "ABS", "ADD", "SUB", "MUL", "DIV",
            "QuantizeLinear", "DequantizeLinear", "Conv", "MaxPool", "Gemm", "Softmax", "Flatten", "Reshape",
-           "GlobalAveragePool", "DynamicQuantizeLinear"]
+           "GlobalAveragePool", "DynamicQuantizeLinear", "ElementwiseChain", "CChainStep"]
 
 
 class CConvParams(ctypes.Structure):
@@ -423,3 +423,55 @@ class DynamicQuantizeLinear(Ops):
     def forward_(self, x: Tensor_):
         return {"tensor": [Tensor_(*x.size, dtype="uint8"), Tensor_(1, dtype="float32"), Tensor_(1, dtype="uint8")],
                 "parameters": None}
+
+
+class CChainStep(ctypes.Structure):
+    """``TensorOpsChainStep`` of include/tensor_ops.h."""
+    _fields_ = [("op", ctypes.c_int), ("operand", ctypes.c_int), ("reversed", ctypes.c_int)]
+
+
+CHAIN_OPS = {"Add": 0, "Sub": 1, "Mul": 2, "Div": 3, "Relu": 4, "Abs": 5, "Cos": 6}
+
+
+class ElementwiseChain(Ops):
+    """A run of elementwise operators on one float32 tensor in a single pass
+    (extension; replaces consecutive ADD / SUB / MUL / DIV / RELU / ABS / COS
+    calls).  ``steps`` is a list of ``(op, operand_index, reversed)`` with op in
+    Add, Sub, Mul, Div, Relu, Abs, Cos; binary steps compute ``v op operand``
+    (``operand op v`` when reversed).  Each step rounds to float32 as the
+    standalone operator does, so the result equals the op-by-op chain bit for bit."""
+
+    def __init__(self, inputs, outputs, steps, dtype="float32", version="17"):
+        super().__init__(inputs, outputs)
+        self.steps = [(op, None if arg is None else int(arg), bool(rev)) for op, arg, rev in steps]
+        self.dtype = dtype
+        self.version = version
+        self.lib.elementwise_chain_forward.argtypes = [PT, ctypes.POINTER(PT), ctypes.c_int,
+                                                       ctypes.POINTER(CChainStep), ctypes.c_int, PT]
+        self.lib.elementwise_chain_forward.restype = None
+
+    def forward(self, x: Tensor, *operands: Tensor):
+        keep: list = []
+        dev = isinstance(x.data, DeviceArray) or any(isinstance(o.data, DeviceArray) for o in operands)
+        try:
+            cx = self._in_ctensor(x, keep)
+            cops = (PT * max(1, len(operands)))(*[self._in_ctensor(o, keep) for o in operands])
+            csteps = (CChainStep * max(1, len(self.steps)))(
+                *[CChainStep(CHAIN_OPS[op], -1 if arg is None else arg, int(rev)) for op, arg, rev in self.steps])
+            dev_out, c_out = self._out_ctensor(tuple(x.size), self.dtype, dev)
+        except Exception:
+            for c in keep:
+                self.lib.free_tensor(c)
+            raise
+        try:
+            self._call("elementwise_chain_forward", cx, cops, len(operands), csteps, len(self.steps), c_out)
+        except Exception:
+            if dev_out is None:
+                self.lib.free_tensor(c_out)
+            for c in keep:
+                self.lib.free_tensor(c)
+            raise
+        return _values(self, self._finish(tuple(x.size), self.dtype, dev_out, c_out, keep))
+
+    def forward_(self, x: Tensor_, *operands):
+        return _values(self, Tensor_(*x.size, dtype=self.dtype))

@@ -336,3 +336,82 @@ def test_next_row_ops_device_resident(hip):
     ds = [t.numpy() for t in q.forward(dev)["tensor"]]
     for a, b, dt in zip(ds, hs, (O.U8, O.F32, O.U8)):
         assert_bitexact(a, b, dt, what="dql device")
+
+
+# ------------------------------------------------------------ fused chain ---
+CONFIG1_CHAIN = [("Add", 0, False), ("Mul", 0, False), ("Sub", 0, False), ("Div", 1, False), ("Relu", None, False),
+                 ("Abs", None, False), ("Cos", None, False)]
+
+
+def oracle_chain(o, x, operands, steps):
+    """The chain op by op through the oracle (each op pinned to the reference's golden vectors)."""
+    v = x
+    for op, arg, rev in steps:
+        if op in ("Relu", "Abs", "Cos"):
+            v = o.unary(op.lower(), v, O.F32, O.F32)
+        else:
+            b = operands[arg]
+            a0, a1 = (b, v) if rev else (v, b)
+            v = o.binary(op.lower(), a0, O.F32, a1, O.F32, O.F32)
+    return v
+
+
+def test_config1_chain_fused_full_size(hip, oracle_lib):
+    """The config-1 chain in one kernel equals the op-by-op reference chain bit for bit."""
+    from onnx_translator_amd.nn import Tensor
+    from onnx_translator_amd.nn.Operators import ElementwiseChain
+    rng = np.random.default_rng(0)
+    A = rng.uniform(-4, 4, (8, 64, 56, 56)).astype(np.float32)
+    B = rng.uniform(-4, 4, (64, 1, 1)).astype(np.float32)
+    Bd = (np.sign(B) * np.maximum(np.abs(B), 0.1)).astype(np.float32)
+    ref = oracle_chain(oracle_lib, A, [B, Bd], CONFIG1_CHAIN)
+    op = ElementwiseChain(["A", "B", "Bd"], ["Y"], CONFIG1_CHAIN)
+    got = op.forward(Tensor(*A.shape, dtype="float32", data=A), Tensor(*B.shape, dtype="float32", data=B),
+                     Tensor(*Bd.shape, dtype="float32", data=Bd))["tensor"]
+    assert_bitexact(got.numpy(), ref, O.F32, what="config1 chain (host)")
+    dev = op.forward(Tensor(*A.shape, dtype="float32", data=A).to_device(),
+                     Tensor(*B.shape, dtype="float32", data=B).to_device(),
+                     Tensor(*Bd.shape, dtype="float32", data=Bd).to_device())["tensor"]
+    assert dev.on_device
+    assert_bitexact(dev.numpy(), ref, O.F32, what="config1 chain (device)")
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_chains(hip, oracle_lib, seed):
+    """Random op sequences, reversed operands, operand shapes that broadcast along
+    inner / outer / all dims, the vector path (inner % 4 == 0) and the scalar one."""
+    from onnx_translator_amd.nn import Tensor
+    from onnx_translator_amd.nn.Operators import ElementwiseChain
+    rng = np.random.default_rng(100 + seed)
+    shape = [(3, 5, 8), (2, 7, 9), (4, 16), (6, 1, 12)][seed % 4]
+    x = rng.uniform(-3, 3, shape).astype(np.float32)
+    x.reshape(-1)[:3] = [np.nan, -0.0, np.inf]
+    cands = [shape[-1:], (1,) + tuple(shape[1:]), (1,), tuple(shape), (shape[0],) + (1,) * (len(shape) - 1)]
+    operands = [rng.uniform(0.5, 2, cands[int(rng.integers(len(cands)))]).astype(np.float32) for _ in range(3)]
+    ops = ["Add", "Sub", "Mul", "Div", "Relu", "Abs", "Cos"]
+    steps = []
+    for _ in range(int(rng.integers(3, 12))):
+        op = ops[int(rng.integers(len(ops)))]
+        steps.append((op, int(rng.integers(3)), bool(rng.integers(2))) if op in ops[:4] else (op, None, False))
+    with np.errstate(all="ignore"):
+        ref = oracle_chain(oracle_lib, x, operands, steps)
+    got = ElementwiseChain(["x"], ["y"], steps).forward(
+        Tensor(*x.shape, dtype="float32", data=x), *[Tensor(*o.shape, dtype="float32", data=o) for o in operands])
+    assert_bitexact(got["tensor"].numpy(), ref, O.F32, what=f"chain {steps}")
+
+
+def test_cos_near_multiples_of_two_pi(hip, oracle_lib):
+    """The exact fmod(|x|, 2pi) shortcut: inputs on and next to k * 2pi (where the
+    quotient estimate is off by one), random magnitudes below 2^30 and just above it."""
+    rng = np.random.default_rng(31)
+    k = np.unique(np.concatenate([np.arange(1, 2000), rng.integers(1, 2 ** 27, 4000)])).astype(np.float64)
+    base = (k * (2 * np.pi)).astype(np.float32)
+    near = np.concatenate([base, np.nextafter(base, 0), np.nextafter(base, np.inf)])
+    wide = np.concatenate([rng.uniform(0, 2.0 ** 30, 20000), rng.uniform(2.0 ** 30, 2.0 ** 34, 2000),
+                           -rng.uniform(0, 1e4, 2000)]).astype(np.float32)
+    x = np.concatenate([near, -near, wide]).astype(np.float32)
+    assert_bitexact(hip.unary("cos", x, O.F32, O.F32), oracle_lib.unary("cos", x, O.F32, O.F32), O.F32,
+                    what="cos near 2pi multiples")
+    xd = np.concatenate([k * 2 * np.pi, np.nextafter(k * 2 * np.pi, 0), rng.uniform(0, 2.0 ** 31, 5000)])
+    assert_bitexact(hip.unary("cos", xd, O.F64, O.F64), oracle_lib.unary("cos", xd, O.F64, O.F64), O.F64,
+                    what="cos f64 near 2pi multiples")
