@@ -142,6 +142,9 @@ void dynamic_quantize_linear_forward(const Tensor* x, Tensor* y, Tensor* y_scale
 
 /* Zero-filled tensor in device memory (HBM).  NULL on failure. */
 Tensor* create_tensor_device(int* shape, int ndim, DataType dtype);
+/* Device tensor with undefined contents, for an operator output that the next
+ * call writes in full (saves the fill of create_tensor_device).  NULL on failure. */
+Tensor* create_tensor_device_empty(int* shape, int ndim, DataType dtype);
 /* Tensor header over caller-owned device memory; free_tensor frees only the header. */
 Tensor* tensor_wrap_device(void* device_ptr, int* shape, int ndim, DataType dtype);
 /* 1 if t's data lives in device memory, else 0. */

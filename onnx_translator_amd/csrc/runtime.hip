@@ -470,14 +470,14 @@ Tensor* create_tensor(int* shape, int ndim, DataType dtype) {
     return t;
 }
 
-Tensor* create_tensor_device(int* shape, int ndim, DataType dtype) {
+static Tensor* device_tensor(int* shape, int ndim, DataType dtype, bool zero) {
     if (!ensure_device()) return nullptr;
     Tensor* t = new_header(shape, ndim, dtype);
     if (!t) return nullptr;
     const size_t bytes = t->size * dt_bytes((int)dtype);
     void* p = pool_alloc(bytes ? bytes : 1);
     if (!p) { free(t->shape); free(t); return nullptr; }
-    if (!check_hip(hipMemsetAsync(p, 0, bytes ? bytes : 1, stream()), "zero fill")) {
+    if (zero && !check_hip(hipMemsetAsync(p, 0, bytes ? bytes : 1, stream()), "zero fill")) {
         pool_free(p);
         free(t->shape);
         free(t);
@@ -486,6 +486,11 @@ Tensor* create_tensor_device(int* shape, int ndim, DataType dtype) {
     t->data = p;
     reg_put(p, Mem::kDevOwned);
     return t;
+}
+
+Tensor* create_tensor_device(int* shape, int ndim, DataType dtype) { return device_tensor(shape, ndim, dtype, true); }
+Tensor* create_tensor_device_empty(int* shape, int ndim, DataType dtype) {
+    return device_tensor(shape, ndim, dtype, false);
 }
 
 Tensor* tensor_wrap_device(void* device_ptr, int* shape, int ndim, DataType dtype) {

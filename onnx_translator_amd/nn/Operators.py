@@ -192,6 +192,8 @@ class DequantizeLinear(Ops):
         return _values(self, self._execute_ternary(x, x_scale, x_zero_point, "dequantize_linear_forward"))
 
     def forward_(self, x, x_scale, x_zero_point):
+        if self.axis is not None and len(tuple(x_scale.size)) == 1 and len(tuple(x.size)) > 1:
+            return _values(self, Tensor_(*x.size, dtype=self.dtype))      # per-axis scale: x's shape
         try:
             shape = np.broadcast_shapes(tuple(x.size), tuple(x_scale.size), tuple(x_zero_point.size))
         except ValueError:

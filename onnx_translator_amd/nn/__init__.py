@@ -81,13 +81,14 @@ def _shape_arr(shape):
 class DeviceArray:
     """An HBM-resident tensor owned by libtensor_ops_hip (``create_tensor_device``)."""
 
-    def __init__(self, lib, shape, dtype: str, ptr=None):
+    def __init__(self, lib, shape, dtype: str, ptr=None, zero: bool = True):
         self.lib = lib
         self.shape = tuple(int(s) for s in shape)
         self.dtype = dtype
         if ptr is None:
             shp = self.shape or (1,)
-            ptr = lib.create_tensor_device(_shape_arr(shp), len(shp), DTYPE_MAP[dtype])
+            make = lib.create_tensor_device if zero else lib.create_tensor_device_empty
+            ptr = make(_shape_arr(shp), len(shp), DTYPE_MAP[dtype])
             if not ptr:
                 raise RuntimeError("create_tensor_device failed: " + Ops._last_error(lib))
         self.ptr = ptr
@@ -192,6 +193,8 @@ class Ops:
                     _sig(lib, "create_tensor", P, [ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int])
                     _sig(lib, "create_tensor_device", P,
                          [ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int])
+                    _sig(lib, "create_tensor_device_empty", P,
+                         [ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int])
                     _sig(lib, "tensor_wrap_device", P,
                          [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int])
                     _sig(lib, "free_tensor", None, [P])
@@ -255,7 +258,8 @@ class Ops:
 
     def _out_ctensor(self, shape, dtype, device: bool):
         if device:
-            d = DeviceArray(self.lib, shape, dtype)
+            # operators write their whole output: no zero fill needed
+            d = DeviceArray(self.lib, shape, dtype, zero=False)
             return d, d.ptr
         shp = tuple(shape) or (1,)
         c = self.lib.create_tensor(_shape_arr(shp), len(shp), DTYPE_MAP[dtype])
@@ -346,3 +350,12 @@ class Ops:
         nbytes = c.size * np.dtype(np_dtype).itemsize
         arr = np.frombuffer((ctypes.c_byte * nbytes).from_address(c.data), dtype=np_dtype)
         return arr.reshape(shape).copy()
+
+
+def __getattr__(name):
+    """``nn.Graph`` as in the reference (``nn/__init__.py:346``), imported lazily
+    because the graph module builds on the operator classes."""
+    if name == "Graph":
+        from .graph import Graph
+        return Graph
+    raise AttributeError(name)

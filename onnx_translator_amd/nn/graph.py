@@ -1,0 +1,230 @@
+"""Graph executor (``nn/__init__.py:346-505`` of the reference), device-resident.
+
+Same constructor and naming as the reference ``Graph``; the differences fix its
+gaps and keep the data in HBM:
+
+* initializers are fed (the reference never feeds them, ``nn/__init__.py:423-424``);
+  ``to_device()`` uploads them once, so weights stay resident across calls;
+* ``forward`` returns the graph outputs (the reference returns nothing);
+* graph inputs are moved to the device once and every intermediate stays there
+  (each operator with a device operand writes a device tensor); an edge is
+  released when its last consumer has run;
+* ``fuse_elementwise()`` replaces runs of consecutive float32 Relu / Abs / Cos /
+  Add / Sub / Mul / Div nodes whose intermediates have no other consumer by one
+  :class:`~onnx_translator_amd.nn.Operators.ElementwiseChain` (bit-identical to
+  the unfused run).  Shapes are taken from a placeholder pass (``forward_``) at
+  the first call, when the input shapes are known;
+* a missing QuantizeLinear / DequantizeLinear zero point is a uint8 zero (the
+  ONNX default).
+"""
+from __future__ import annotations
+
+import sys
+from collections import OrderedDict
+from typing import Dict, List, Optional
+
+import numpy as np
+
+from . import NUMPY_TO_DTYPE, Tensor, Tensor_
+from . import Operators as Op
+
+_UNARY = {Op.RELU: "Relu", Op.ABS: "Abs", Op.COS: "Cos"}
+_BINARY = {Op.ADD: "Add", Op.SUB: "Sub", Op.MUL: "Mul", Op.DIV: "Div"}
+
+
+def _is_fusable(op) -> bool:
+    return type(op) in _UNARY or type(op) in _BINARY
+
+
+class Graph:
+    """Operators in topological order over named edges."""
+
+    def __init__(self, ops, input_name, output_name=None, model_name=None,
+                 initializers: Optional[Dict[str, Tensor]] = None):
+        self.input_name = list(input_name) if isinstance(input_name, (list, tuple)) else [input_name]
+        if output_name is None:
+            self.output_name: List[str] = []
+        else:
+            self.output_name = list(output_name) if isinstance(output_name, (list, tuple)) else [output_name]
+        self.model_name = model_name
+        self.initializers: Dict[str, Tensor] = dict(initializers or {})
+        self.ops: "OrderedDict[str, object]" = OrderedDict()
+        self._fuse_pending = False
+        self.device = False
+        self.fused_runs: List[List[str]] = []
+        self.update(ops)
+
+    # -- structure ---------------------------------------------------------------
+    def update(self, ops):
+        """Name the operators (``<Class>.<k>``) and check single assignment of edges."""
+        counts: Dict[str, int] = {}
+        produced = set(self.input_name) | set(self.initializers)
+        for op in ops:
+            cls = type(op).__name__
+            counts[cls] = counts.get(cls, -1) + 1
+            if not getattr(op, "name", None):
+                op.name = f"{cls}.{counts[cls]}"
+            self.ops[op.name] = op
+            for o in op.outputs:
+                if o in produced and o not in self.initializers:
+                    print(f"output edge name {o} repeat!!!")
+                    sys.exit()
+                produced.add(o)
+        if not self.output_name:
+            consumed = {i for op in self.ops.values() for i in op.inputs}
+            self.output_name = [o for op in self.ops.values() for o in op.outputs if o not in consumed]
+
+    def _consumers(self) -> Dict[str, int]:
+        c: Dict[str, int] = {}
+        for op in self.ops.values():
+            for i in op.inputs:
+                if i:
+                    c[i] = c.get(i, 0) + 1
+        for o in self.output_name:
+            c[o] = c.get(o, 0) + 1
+        return c
+
+    def to_device(self) -> "Graph":
+        """Upload the initializers to HBM once; inputs given to ``forward`` go to HBM too."""
+        self.initializers = {k: (v.to_device() if isinstance(v, Tensor) else v) for k, v in self.initializers.items()}
+        self.device = True
+        return self
+
+    # -- execution ----------------------------------------------------------------
+    @staticmethod
+    def _inputs_for(op, buf):
+        args = [buf[na] if na else None for na in op.inputs]
+        if type(op) in (Op.QuantizeLinear, Op.DequantizeLinear) and len(args) == 2:
+            args.append(Tensor(1, dtype="uint8", data=np.zeros(1, np.uint8)))
+        return args
+
+    def _run(self, inputs, method: str):
+        buf: Dict[str, object] = dict(self.initializers) if method == "forward" else {
+            k: Tensor_(*v.size, dtype=v.dtype) for k, v in self.initializers.items()}
+        for na, t in zip(self.input_name, inputs):
+            buf[na] = t
+        pending = self._consumers()
+        for op in self.ops.values():
+            outs = getattr(op, method)(*self._inputs_for(op, buf))
+            res = outs["tensor"]
+            if len(op.outputs) == 1:
+                buf[op.outputs[0]] = res
+            else:
+                for na, r in zip(op.outputs, res):
+                    buf[na] = r
+            for na in op.inputs:
+                if not na or na in self.initializers:
+                    continue
+                pending[na] -= 1
+                if pending[na] == 0:
+                    buf.pop(na, None)
+        out = tuple(buf[na] for na in self.output_name)
+        return out[0] if len(out) == 1 else out
+
+    def forward(self, *inputs):
+        """Run the graph; inputs may be numpy arrays or :class:`Tensor` objects.  Host
+        inputs are moved to the device after ``to_device()``.  Returns the output
+        tensor(s) (device-resident when computed there; ``.numpy()`` copies back)."""
+        ts = []
+        dev = self.device
+        for x in inputs:
+            if not isinstance(x, Tensor):
+                a = np.ascontiguousarray(x)
+                x = Tensor(*a.shape, dtype=NUMPY_TO_DTYPE.get(a.dtype.type, "float32"), data=a)
+            ts.append(x.to_device() if dev and not x.on_device else x)
+        if self._fuse_pending:
+            self._fuse(ts)
+        return self._run(ts, "forward")
+
+    def forward_(self, *inputs):
+        """Shape / dtype propagation with :class:`Tensor_` placeholders."""
+        return self._run(inputs, "forward_")
+
+    # -- fusion --------------------------------------------------------------------
+    def fuse_elementwise(self) -> "Graph":
+        """Request elementwise fusion; it is applied at the first ``forward`` (shapes needed)."""
+        self._fuse_pending = True
+        return self
+
+    def _edge_shapes(self, inputs) -> Dict[str, tuple]:
+        shapes: Dict[str, tuple] = {k: (tuple(v.size), v.dtype) for k, v in self.initializers.items()}
+        buf = {k: Tensor_(*v.size, dtype=v.dtype) for k, v in self.initializers.items()}
+        for na, t in zip(self.input_name, inputs):
+            buf[na] = Tensor_(*t.size, dtype=t.dtype)
+            shapes[na] = (tuple(t.size), t.dtype)
+        for op in self.ops.values():
+            res = op.forward_(*self._inputs_for(op, buf))["tensor"]
+            res = [res] if len(op.outputs) == 1 else list(res)
+            for na, r in zip(op.outputs, res):
+                buf[na] = r
+                shapes[na] = (tuple(r.size), r.dtype)
+        return shapes
+
+    def _fuse(self, inputs):
+        self._fuse_pending = False
+        shapes = self._edge_shapes(inputs)
+        consumers = self._consumers()
+        ops = list(self.ops.values())
+        out_ops = []
+        i = 0
+        while i < len(ops):
+            run = self._run_from(ops, i, shapes, consumers)
+            if run is None:
+                out_ops.append(ops[i])
+                i += 1
+                continue
+            n_ops, x_in, operands, steps, y_out = run
+            chain = Op.ElementwiseChain([x_in] + operands, [y_out], steps, dtype="float32")
+            chain.name = "ElementwiseChain." + "+".join(op.name for op in ops[i:i + n_ops])
+            self.fused_runs.append([op.name for op in ops[i:i + n_ops]])
+            out_ops.append(chain)
+            i += n_ops
+        self.ops = OrderedDict((op.name, op) for op in out_ops)
+
+    @staticmethod
+    def _run_from(ops, i, shapes, consumers):
+        """A fusable run starting at ops[i] of at least two nodes, or None."""
+        def f32(edge):
+            return edge in shapes and shapes[edge][1] == "float32"
+
+        def fits(edge, shape):   # operand broadcasts into the running shape without growing it
+            try:
+                return np.broadcast_shapes(shapes[edge][0], shape) == tuple(shape)
+            except ValueError:
+                return False
+
+        steps, operands = [], []
+        x_in, cur, shape = None, None, None
+        j = i
+        while j < len(ops) and len(steps) < 16:
+            op = ops[j]
+            if not _is_fusable(op) or op.dtype != "float32" or len(op.outputs) != 1 or not f32(op.outputs[0]):
+                break
+            out = op.outputs[0]
+            if cur is None:
+                # the running input is one with the output's shape
+                cand = [k for k, e in enumerate(op.inputs) if f32(e) and shapes[e][0] == shapes[out][0]]
+                if not cand:
+                    break
+                pos = cand[0]
+                x_in, shape = op.inputs[pos], shapes[out][0]
+            else:
+                if cur not in op.inputs or consumers.get(cur, 0) != 1 or shapes[out][0] != shape:
+                    break
+                pos = op.inputs.index(cur)
+            if type(op) in _UNARY:
+                steps.append((_UNARY[type(op)], None, False))
+            else:
+                other = op.inputs[1 - pos]
+                if other == cur or not f32(other) or not fits(other, shape):
+                    break
+                if other not in operands:
+                    if len(operands) == 3:
+                        break
+                    operands.append(other)
+                steps.append((_BINARY[type(op)], operands.index(other), pos == 1))
+            cur = out
+            j += 1
+        if len(steps) < 2:
+            return None
+        return j - i, x_in, operands, steps, cur

@@ -1,0 +1,70 @@
+"""Graph-level checker: evaluates an ONNX ModelProto node by node with the CPU
+oracle library (test infrastructure only).
+
+Each node maps to the oracle call that restates the reference operator, with
+the operands prepared as the reference's Python layer prepares them (numpy
+broadcasting; a 1-D Q / DQ scale reshaped onto its axis, nn/Operators.py:439-445;
+a 1-D Gemm bias reshaped to (1, N) or (M, 1), nn/Operators.py:638-645).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from onnx_translator_amd.nn import onnx_dtype_mapping
+from oracle import oracle as O
+
+
+def _on_axis(v, nd, axis):
+    shp = [1] * nd
+    shp[axis] = v.size
+    return v.reshape(shp)
+
+
+def run_model(o, model, feeds: dict):
+    """Returns {edge name: (array in storage form, dtype name)} for every edge."""
+    g = model.graph
+    env = {t.name: (t.numpy(), onnx_dtype_mapping[t.data_type]) for t in g.initializers}
+    env.update(feeds)
+    for n in g.nodes:
+        x, xdt = env[n.inputs[0]]
+        t = n.op_type
+        if t in ("Relu", "Abs", "Cos"):
+            out = (o.unary(t.lower(), x, xdt, xdt), xdt)
+        elif t in ("Add", "Sub", "Mul", "Div"):
+            y, ydt = env[n.inputs[1]]
+            out = (o.binary(t.lower(), x, xdt, y, ydt, xdt), xdt)
+        elif t == "Conv":
+            w, wdt = env[n.inputs[1]]
+            b, bdt = env[n.inputs[2]] if len(n.inputs) > 2 else (None, "float32")
+            out = (o.conv(x, xdt, w, wdt, b, bdt, xdt, n.attr("pads", [0] * 4), n.attr("strides", [1, 1]),
+                          n.attr("dilations", [1, 1]), n.attr("group", 1)), xdt)
+        elif t == "MaxPool":
+            out = (o.maxpool(x, xdt, xdt, n.attr("kernel_shape"), n.attr("pads", [0] * 4), n.attr("strides", [1, 1]),
+                             n.attr("dilations", [1, 1])), xdt)
+        elif t in ("QuantizeLinear", "DequantizeLinear"):
+            s, sdt = env[n.inputs[1]]
+            z, zdt = env[n.inputs[2]] if len(n.inputs) > 2 else (np.zeros(1, np.uint8), "uint8")
+            if s.ndim == 1 and s.size > 1 and x.ndim > 1:
+                axis = n.attr("axis", 1)
+                s, z = _on_axis(s, x.ndim, axis), _on_axis(z, x.ndim, axis)
+            if t == "QuantizeLinear":
+                out = (o.qdq("quantize", x, xdt, s, sdt, z, zdt, zdt), zdt)
+            else:
+                out = (o.qdq("dequantize", x, xdt, s, sdt, z, zdt, "float32"), "float32")
+        elif t == "GlobalAveragePool":
+            out = (o.gap(x, xdt, xdt), xdt)
+        elif t == "Flatten":
+            axis = n.attr("axis", 1)
+            shape = (int(np.prod(x.shape[:axis])), int(np.prod(x.shape[axis:])))
+            out = (o.flatten(x, xdt, shape), xdt)
+        elif t == "Gemm":
+            w, wdt = env[n.inputs[1]]
+            c, cdt = env[n.inputs[2]] if len(n.inputs) > 2 else (None, "float32")
+            ta, tb = n.attr("transA", 0), n.attr("transB", 0)
+            out = (o.gemm(x, xdt, w, wdt, c, cdt, xdt, n.attr("alpha", 1.0), n.attr("beta", 1.0), ta, tb), xdt)
+        elif t == "Softmax":
+            out = (o.softmax(x, xdt, xdt, n.attr("axis", -1)), xdt)
+        else:
+            raise NotImplementedError(t)
+        env[n.outputs[0]] = out
+    return env

@@ -1,0 +1,161 @@
+"""ONNX I/O, importer and graph executor (the config-5 path).
+
+CPU: the protobuf wire encoding is checked against the protobuf runtime itself
+(messages declared with onnx.proto's field numbers), models round-trip byte for
+byte, the importer maps nodes and attributes, placeholder propagation gives the
+graph's shapes, the fusion pass finds its runs, and the graph oracle agrees with a
+numpy closed form.  GPU: the toy model and the config-5 QDQ ResNet through the
+device-resident graph equal the oracle evaluated node by node.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from onnx_translator_amd.onnx import proto as P
+from onnx_translator_amd.onnx.create_model import comprehensive_model, resnet_qdq_model
+from tests.graph_oracle import run_model
+from tests.helpers import assert_bitexact, assert_close
+
+
+def _pb_classes():
+    """onnx.proto's messages (the fields used here) declared for the protobuf runtime."""
+    from google.protobuf import descriptor_pb2, descriptor_pool, message_factory
+    F = descriptor_pb2.FieldDescriptorProto
+    fd = descriptor_pb2.FileDescriptorProto(name="onnx_subset_check.proto", package="chk", syntax="proto2")
+
+    def msg(name, fields):
+        m = fd.message_type.add(name=name)
+        for fname, num, typ, label, tname, packed in fields:
+            f = m.field.add(name=fname, number=num, type=typ, label=label)
+            if tname:
+                f.type_name = ".chk." + tname
+            if packed:
+                f.options.packed = True
+
+    O_, R = F.LABEL_OPTIONAL, F.LABEL_REPEATED
+    msg("Tensor", [("dims", 1, F.TYPE_INT64, R, None, False), ("data_type", 2, F.TYPE_INT32, O_, None, False),
+                   ("float_data", 4, F.TYPE_FLOAT, R, None, True), ("int32_data", 5, F.TYPE_INT32, R, None, True),
+                   ("int64_data", 7, F.TYPE_INT64, R, None, True), ("name", 8, F.TYPE_STRING, O_, None, False),
+                   ("raw_data", 9, F.TYPE_BYTES, O_, None, False)])
+    msg("Attr", [("name", 1, F.TYPE_STRING, O_, None, False), ("f", 2, F.TYPE_FLOAT, O_, None, False),
+                 ("i", 3, F.TYPE_INT64, O_, None, False), ("s", 4, F.TYPE_BYTES, O_, None, False),
+                 ("t", 5, F.TYPE_MESSAGE, O_, "Tensor", False), ("floats", 7, F.TYPE_FLOAT, R, None, False),
+                 ("ints", 8, F.TYPE_INT64, R, None, False), ("type", 20, F.TYPE_INT32, O_, None, False)])
+    msg("Node", [("input", 1, F.TYPE_STRING, R, None, False), ("output", 2, F.TYPE_STRING, R, None, False),
+                 ("name", 3, F.TYPE_STRING, O_, None, False), ("op_type", 4, F.TYPE_STRING, O_, None, False),
+                 ("attribute", 5, F.TYPE_MESSAGE, R, "Attr", False), ("domain", 7, F.TYPE_STRING, O_, None, False)])
+    pool = descriptor_pool.DescriptorPool()
+    pool.Add(fd)
+    get = message_factory.GetMessageClass
+    return get(pool.FindMessageTypeByName("chk.Tensor")), get(pool.FindMessageTypeByName("chk.Node"))
+
+
+def test_wire_format_against_protobuf_runtime():
+    Tensor, Node = _pb_classes()
+    # ours -> protobuf
+    n = P.NodeProto("Conv", ["x", "w", "b"], ["y"], name="/Conv_7",
+                    attributes=[P.make_attribute("pads", [3, 3, -1, 0]), P.make_attribute("group", 2),
+                                P.make_attribute("alpha", 0.25), P.make_attribute("mode", "abc")])
+    pb = Node.FromString(n.serialize())
+    assert list(pb.input) == ["x", "w", "b"] and list(pb.output) == ["y"] and pb.op_type == "Conv"
+    a = {x.name: x for x in pb.attribute}
+    assert list(a["pads"].ints) == [3, 3, -1, 0] and a["group"].i == 2 and a["alpha"].f == 0.25
+    assert a["mode"].s == b"abc" and a["pads"].type == P.A_INTS
+    # protobuf -> ours, including packed and typed tensor payloads
+    t = Tensor(dims=[2, 3], data_type=P.INT64, name="shape", int64_data=[1, -2, 3, 4, -5, 6])
+    ours = P.TensorProto.parse(t.SerializeToString())
+    assert ours.name == "shape" and ours.dims == [2, 3]
+    assert ours.numpy().tolist() == [[1, -2, 3], [4, -5, 6]]
+    tf = Tensor(dims=[3], data_type=P.FLOAT, float_data=[0.5, -1.25, 3.0])
+    assert P.TensorProto.parse(tf.SerializeToString()).numpy().tolist() == [0.5, -1.25, 3.0]
+    raw = np.arange(6, dtype=np.int8).reshape(2, 3)
+    back = Tensor.FromString(P.TensorProto.from_numpy(raw, "r", P.INT8).serialize())
+    assert list(back.dims) == [2, 3] and back.raw_data == raw.tobytes() and back.data_type == P.INT8
+    pbn = Node(input=["a"], output=["b"], op_type="Softmax")
+    pbn.attribute.add(name="axis", i=-1, type=P.A_INT)
+    mine = P.NodeProto.parse(pbn.SerializeToString())
+    assert mine.op_type == "Softmax" and mine.attr("axis") == -1
+
+
+def test_model_round_trip():
+    for m in (resnet_qdq_model(batch=2, image=64), comprehensive_model()):
+        b = m.serialize()
+        m2 = P.ModelProto.parse(b)
+        assert m2.serialize() == b
+        assert [n.op_type for n in m2.graph.nodes] == [n.op_type for n in m.graph.nodes]
+        for t1, t2 in zip(m.graph.initializers, m2.graph.initializers):
+            assert t1.name == t2.name and np.array_equal(t1.numpy(), t2.numpy())
+        assert m2.opset_import == [("", 17)]
+
+
+def test_importer_mapping_and_shapes():
+    from onnx_translator_amd.nn import Graph, Tensor_
+    from onnx_translator_amd.nn import Operators as Op
+    from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
+    m = resnet_qdq_model(batch=2, image=64)
+    ops = ONNXImport(m)
+    assert [type(o).__name__ for o in ops[:6]] == ["Conv", "RELU", "MaxPool", "QuantizeLinear", "DequantizeLinear",
+                                                   "DequantizeLinear"]
+    stem = ops[0]
+    assert stem.pads == [3, 3, 3, 3] and stem.strides == [2, 2] and stem.group == 1
+    q, dq_act, dq_w = ops[3], ops[4], ops[5]
+    assert q.dtype == "uint8" and dq_act.axis is None and dq_w.axis == 0
+    gemm = [o for o in ops if isinstance(o, Op.Gemm)][0]
+    assert gemm.transB == 1 and gemm.alpha == 1.0
+    g = Graph(ops, ["input"], ["output"], initializers=initializers(m))
+    out = g.forward_(Tensor_(2, 3, 64, 64, dtype="float32"))
+    assert out.size == (2, 1000) and out.dtype == "float32"
+    g._fuse([Tensor_(2, 3, 64, 64, dtype="float32")])
+    assert g.fused_runs == [["RELU.1", "ADD.0"]]
+
+
+def test_toy_graph_oracle_closed_form(oracle_lib):
+    rng = np.random.default_rng(0)
+    x = rng.normal(0, 1, (1, 3, 32, 32)).astype(np.float32)
+    y = rng.normal(0, 1, (1, 1, 1, 32)).astype(np.float32)
+    env = run_model(oracle_lib, comprehensive_model(), {"input_x": (x, "float32"), "input_y": (y, "float32")})
+    want = np.cos(np.maximum(x, 0) + np.abs(y)).astype(np.float64)
+    np.testing.assert_allclose(env["output"][0], want, atol=4e-7)
+
+
+@pytest.mark.gpu
+def test_toy_graph_on_device(hip, oracle_lib):
+    from onnx_translator_amd.nn.ONNXImport import load_graph
+    m = comprehensive_model()
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 2, (1, 3, 32, 32)).astype(np.float32)
+    y = rng.normal(0, 2, (1, 1, 1, 32)).astype(np.float32)
+    g = load_graph(m)
+    out = g.forward(x, y)
+    assert out.on_device and g.fused_runs == [["ADD.0", "COS.0"]]
+    env = run_model(oracle_lib, m, {"input_x": (x, "float32"), "input_y": (y, "float32")})
+    assert_bitexact(out.numpy(), env["output"][0], O.F32, what="toy graph")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
+def test_resnet_qdq_graph(hip, oracle_lib, exact):
+    """Config-5 graph at batch 2: exact mode reproduces every node bit for bit
+    except the final Softmax (tolerance class); MFMA mode stays close."""
+    from onnx_translator_amd.nn.ONNXImport import load_graph
+    m = resnet_qdq_model(batch=2, image=224)
+    rng = np.random.default_rng(4)
+    x = rng.normal(0, 1, (2, 3, 224, 224)).astype(np.float32)
+    g = load_graph(m)
+    hip.set_exact(exact)
+    try:
+        out = g.forward(x)
+        probs = out.numpy()
+    finally:
+        hip.set_exact(False)
+    env = run_model(oracle_lib, m, {"input": (x, "float32")})
+    ref = env["output"][0]
+    assert probs.shape == (2, 1000)
+    if exact:
+        assert_close(probs, ref, O.F32, what="resnet_qdq exact")
+    else:
+        # fp32 MFMA accumulation flips a few uint8 activation codes near rounding
+        # ties, which moves the logits slightly: the probabilities stay close
+        np.testing.assert_allclose(probs.sum(axis=1), 1.0, rtol=1e-5)
+        assert np.abs(probs - ref).max() < 5e-3 * ref.max()
+        assert (probs.argmax(axis=1) == ref.argmax(axis=1)).all()
