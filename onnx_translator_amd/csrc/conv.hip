@@ -242,6 +242,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
     constexpr int KPT = EB / PPT;
     constexpr int PCOLS = BP / PPT;
     static_assert(MODE == 1 || PCOLS % 64 == 0, "a wave must share its k range");
+    static_assert(KPT >= 1 && KPT * PPT == EB, "every thread loads at least one k per tile");
     const int pc = (t % PCOLS) * PPT;
     const int kg = MODE == 0 ? __builtin_amdgcn_readfirstlane((t / PCOLS) * KPT) : (t / PCOLS) * KPT;
     const int p = p0 + pc;
@@ -492,14 +493,16 @@ bool launch_conv_tiled(const void* x, const void* w, const void* b, int dtb, voi
                         g.OH == g.H && g.OW == g.W && g.HW % 4 == 0;
     const float* xf = (const float*)x;
     const float* wf = (const float*)w;
-    if (direct && g.Mg >= 128)
-        launch_conv_tiled_cfg<128, 128, 16, 2, 2, 1>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, (uint32_t)yb, s);
-    else if (direct)
-        launch_conv_tiled_cfg<64, 256, 16, 1, 4, 1>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, (uint32_t)yb, s);
-    else if (g.Mg >= 128)
-        launch_conv_tiled_cfg<128, 128, 16, 2, 2, 0>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, (uint32_t)yb, s);
+    // Block shapes swept on MI355X over the config-4 layers: 64 channels x 256 pixels with
+    // 8 or 16 waves (wave tiles 32x64 / 32x32) keep 2-4 waves per SIMD on grids of a few
+    // hundred tiles; BK = 8 when K is short (the 7x7x3 stem: less padding, more tiles in flight).
+    const uint32_t ux = (uint32_t)xb, uw = (uint32_t)wb, uy = (uint32_t)yb;
+    if (direct)
+        launch_conv_tiled_cfg<64, 256, 16, 2, 4, 1>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, s);
+    else if (g.Kg <= 256)
+        launch_conv_tiled_cfg<64, 256, 8, 2, 4, 0>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, s);
     else
-        launch_conv_tiled_cfg<64, 256, 16, 1, 4, 0>(xf, wf, b, dtb, y, dty, g, cg.group, (uint32_t)xb, (uint32_t)wb, (uint32_t)yb, s);
+        launch_conv_tiled_cfg<64, 256, 16, 2, 8, 0>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, s);
     return true;
 }
 
