@@ -98,6 +98,8 @@ class Lib:
                                                 ctypes.c_int, PT]
         L.global_average_pool_forward.argtypes = [PT, PT]
         L.dynamic_quantize_linear_forward.argtypes = [PT, PT, PT, PT]
+        L.dequantize_gemm_forward.argtypes = [PT, PT, PT, PT, ctypes.c_int, PT, PT, ctypes.c_float, ctypes.c_float,
+                                              ctypes.c_int, ctypes.c_int]
         L.init_cos_lut()
 
     def dev(self, arr, dt):
@@ -212,10 +214,16 @@ def run_headline(lib, torch, steps, warmup):
             "dominant": dom, "bytes_per_launch": bytes_per_launch, "n": n}
 
 
-def bench_loop(torch, fn, iters, warm=3):
-    for i in range(warm):
+def bench_loop(torch, fn, iters, warm=3, warm_ms=50.0):
+    """Mean time of `iters` back-to-back calls.  The warm-up runs at least `warm`
+    calls and `warm_ms` of wall time, so the GPU clocks have ramped up (a cold
+    4096^3 Gemm runs ~20% slower for its first few milliseconds)."""
+    t0, i = time.perf_counter(), 0
+    while i < warm or (time.perf_counter() - t0) * 1e3 < warm_ms:
         fn(i)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        i += 1
+    warm = i
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for i in range(iters):
@@ -276,12 +284,37 @@ def run_suite(lib, torch):
         bb = b if dt == F32 else b.astype(np.float16)
         ta, tbb = lib.dev(aa, dt), lib.dev(bb, dt)
         ty = lib.empty([4096, 4096], dt)
-        ms = bench_loop(torch, lambda i: L.gemm_forward(ta, tbb, tc, ty, 1.0, 1.0, 0, 1), 5 if dt == F32 else 10, 1)
+        ms = bench_loop(torch, lambda i: L.gemm_forward(ta, tbb, tc, ty, 1.0, 1.0, 0, 1), 20, 1)
         out.append(op_line(f"gemm_{'f32' if dt == F32 else 'f16'}_4096", "config3 4096x4096x4096 transB=1 +bias",
                            flops, ms, "mfma", peak))
         for t in (ta, tbb, ty):
             L.free_tensor(t)
     lib.check("config3")
+    # Config 3 weight-only-quant variant: B int8 [4096,4096] with per-row (axis 0)
+    # scales, DequantizeLinear -> Gemm on A [256,4096]; fused (codes read in the
+    # Gemm) and unfused (f32 weight written, then read).
+    bw = rng.normal(0, 1 / 64, (4096, K))
+    sw = (np.abs(bw).max(axis=1) / 127).astype(np.float32)
+    bq = np.clip(np.rint(bw / sw[:, None]), -127, 127).astype(np.int8)
+    a = rng.normal(0, 1 / 64, (256, K)).astype(np.float32)
+    ta, tq, tbd = lib.dev(a, F32), lib.dev(bq, I8), lib.empty([4096, K], F32)
+    ts1, tz1 = lib.dev(sw, F32), lib.dev(np.zeros(4096, np.int8), I8)
+    ts2, tz2 = lib.dev(sw.reshape(-1, 1), F32), lib.dev(np.zeros((4096, 1), np.int8), I8)
+    ty = lib.empty([256, 4096], F32)
+    wflops = 2 * 256 * 4096 * K
+    ms = bench_loop(torch, lambda i: L.dequantize_gemm_forward(ta, tq, ts1, tz1, 0, tc, ty, 1.0, 1.0, 0, 1), 20, 2)
+    out.append(op_line("gemm_woq_int8_fused", "config3 WOQ A[256,4096] x int8 B[4096,4096]^T, axis-0 scales, +bias",
+                       wflops, ms, "mfma", MFMA_F32))
+
+    def unfused(i):
+        L.dequantize_linear_forward(tq, ts2, tz2, tbd)
+        L.gemm_forward(ta, tbd, tc, ty, 1.0, 1.0, 0, 1)
+    ms = bench_loop(torch, unfused, 20, 2)
+    out.append(op_line("gemm_woq_int8_unfused", "config3 WOQ DequantizeLinear -> Gemm (f32 weight in HBM)",
+                       wflops, ms, "mfma", MFMA_F32))
+    lib.check("config3 woq")
+    for t in (ta, tq, tbd, ts1, tz1, ts2, tz2, ty):
+        L.free_tensor(t)
     L.free_tensor(tc)
 
     # Config 4: conv layers + maxpool.

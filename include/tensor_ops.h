@@ -191,6 +191,14 @@ void quantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Te
                                   Tensor* Y, int axis);
 void dequantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint,
                                     Tensor* Y, int axis);
+/* Weight-only-quantized Gemm: Y = alpha * A' * DQ(Bq)' + beta * C with DQ(Bq) =
+ * dequantize_linear_axis_forward(Bq, Scale, ZeroPoint, ., axis), in one pass that reads
+ * Bq as int8 / uint8 codes (the f32 weight is never written).  Same arguments and output
+ * as dequantize_linear_axis_forward followed by gemm_forward (tensor_ops/tensor_ops.h:155,
+ * 173-174), and the same bits.  ZeroPoint may be NULL (zero). */
+void dequantize_gemm_forward(const Tensor* A, const Tensor* Bq, const Tensor* Scale, const Tensor* ZeroPoint,
+                             int axis, const Tensor* C, Tensor* Y, float alpha, float beta, int transA,
+                             int transB);
 
 #ifdef __cplusplus
 }

@@ -241,6 +241,9 @@ __device__ __forceinline__ uint32_t ld_stream(const uint32_t* p) { return __buil
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
+// A buffer offset past every resource built here (each covers < 2 GB): loads
+// through it return zero, which makes masked gathers branch-free.
+constexpr uint32_t kOOB = 0x80000000u;
 // 16-byte nontemporal load through a buffer resource.
 __device__ __forceinline__ float4 ld_buf_stream(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
     typedef unsigned int u32x4_t __attribute__((__vector_size__(16)));

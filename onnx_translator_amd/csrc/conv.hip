@@ -207,7 +207,6 @@ struct ConvTiled {
 };
 
 typedef __attribute__((address_space(1))) float gfloat;
-constexpr uint32_t kOOB = 0x80000000u;    // beyond every buffer resource here (< 2 GB)
 
 template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int YDT>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __restrict__ X, const float* __restrict__ Wt,

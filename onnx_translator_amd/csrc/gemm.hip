@@ -18,6 +18,8 @@
 //    reference for every dtype combination.  Used for f64 / int32 / int64
 //    operands and when exact mode is on.
 // The epilogue is shared: alpha * acc + beta * bias in double, then st_d.
+#include <algorithm>
+
 #include "runtime.h"
 
 namespace tohip {
@@ -541,6 +543,198 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_f16_nt(GemmArgs g) {
             }
 }
 
+// ------------------------------------------------------------- f32 NT tiled ---
+// Weight-only-quantized B: int8 / uint8 codes with a per-tensor or per-row
+// (per output column n) scale and zero point.
+struct WoqB {
+    const float* s;      // scale: 1 element, or N elements (per n)
+    const void* z;       // zero point of B's dtype, 1 or N elements, or null (zero)
+    int per_n;           // scale / zero point indexed by n
+    int zn;              // zero point elements (0, 1 or N)
+};
+
+// A [M, K] f32 and B [N, K] (transB = 1) with K % 4 == 0: v_mfma_f32_32x32x2f32
+// on BM x BN x BK tiles, operands through raw buffer loads one k-tile ahead into
+// registers, LDS double buffer, XCD-aware tile order.
+// BQ = 0: B is f32.  BQ = 1 / 2: B holds int8 / uint8 codes, turned into
+// (float)(q - zp) * s while staging into LDS.  (q - zp) is an integer of at
+// most 9 bits, so the fp32 product is the correctly rounded exact product, the
+// value DequantizeLinear writes (tensor_ops.c:1018-1034 computes it in double
+// and rounds once): the fused Gemm sees bit for bit the operand the unfused
+// DequantizeLinear -> Gemm pair sees, and with the same tile shape it returns
+// the same bits.
+// MFMA step s of a k-tile multiplies k = h * BK/2 + s in lane half h, so each
+// lane reads BK/2 consecutive floats of its row (b128 LDS reads); A and B use
+// the same order, so every product pairs equal k.
+// SPLIT: blockIdx.y takes k in [y * kchunk, (y + 1) * kchunk) (kchunk a
+// multiple of BK) and writes its raw fp32 sums to the workspace g.Y + y * M * N;
+// k_splitk_reduce adds the slices in order and applies the epilogue.
+template <int BM, int BN, int BK, int WGM, int WGN, int YDT, int BQ, int IGLP = -1, bool SPLIT = false>
+__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_f32_nt(GemmArgs g, WoqB q, int kchunk) {
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int LDK = BK + 4;
+    constexpr int WTM = BM / WGM, WTN = BN / WGN;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    constexpr int CPR = BK / 4;                   // 4-element chunks per tile row
+    constexpr int CA = BM * CPR / NT, CB = BN * CPR / NT;
+    constexpr int EB = BQ ? 1 : 4;                // bytes per B element
+    static_assert(CA * NT == BM * CPR && CB * NT == BN * CPR && CA >= 1 && CB >= 1, "tile / thread mismatch");
+    static_assert(TM >= 1 && TN >= 1 && BK % 8 == 0, "wave tile");
+    __shared__ float lds[2][(BM + BN) * LDK];
+
+    const int nbm = (g.M + BM - 1) / BM, nbn = (g.N + BN - 1) / BN;
+    int tm, tn;
+    tile_of_block(nbm, nbn, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+    // Rows past M / N read as zero; the host guarantees (rows + tile) * ld * size < 2^31.
+    const __amdgpu_buffer_rsrc_t ar = buffer_rsrc(g.A, (uint32_t)((int64_t)g.M * g.lda * 4));
+    const __amdgpu_buffer_rsrc_t br = buffer_rsrc(g.B, (uint32_t)((int64_t)g.N * g.ldb * EB));
+
+    // Per-row dequantisation constants of the B chunks this thread stages
+    // (a thread's chunk rows do not change across k-tiles).
+    float bs[BQ ? CB : 1];
+    int bz[BQ ? CB : 1];
+    if constexpr (BQ) {
+#pragma unroll
+        for (int i = 0; i < CB; i++) {
+            const int n = min(n0 + (t + i * NT) / CPR, g.N - 1);
+            bs[i] = q.s[q.per_n ? n : 0];
+            const int zi = q.zn > 1 ? n : 0;
+            bz[i] = q.zn == 0 ? 0 : (BQ == 1 ? (int)((const int8_t*)q.z)[zi] : (int)((const uint8_t*)q.z)[zi]);
+        }
+    }
+
+    u32x4 ra[CA];
+    uint32_t rq[BQ ? CB : 1];
+    u32x4 rb[BQ ? 1 : CB];
+    auto load_tile = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < CA; i++) {
+            const int c = t + i * NT;
+            const int k = k0 + (c % CPR) * 4;
+            ra[i] = ld_buf_b128(ar, k < g.K ? (uint32_t)(((m0 + c / CPR) * g.lda + k) * 4) : kOOB);
+        }
+#pragma unroll
+        for (int i = 0; i < CB; i++) {
+            const int c = t + i * NT;
+            const int k = k0 + (c % CPR) * 4;
+            const uint32_t off = k < g.K ? (uint32_t)(((n0 + c / CPR) * g.ldb + k) * EB) : kOOB;
+            if constexpr (BQ) rq[i] = __builtin_amdgcn_raw_buffer_load_b32(br, off, 0, 0);
+            else rb[i] = ld_buf_b128(br, off);
+        }
+    };
+    auto store_tile = [&](int buf, int k0) {
+#pragma unroll
+        for (int i = 0; i < CA; i++) {
+            const int c = t + i * NT;
+            *reinterpret_cast<u32x4*>(&lds[buf][(c / CPR) * LDK + (c % CPR) * 4]) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < CB; i++) {
+            const int c = t + i * NT;
+            float* dst = &lds[buf][(BM + c / CPR) * LDK + (c % CPR) * 4];
+            if constexpr (BQ) {
+                // Past K the A operand is zero, but (0 - zp) * s need not be: zero it.
+                const bool ok = k0 + (c % CPR) * 4 < g.K;
+                const uint32_t w = rq[i];
+                float4 v;
+                float* pv = reinterpret_cast<float*>(&v);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int code = BQ == 1 ? (int)(int8_t)(w >> (8 * e)) : (int)((w >> (8 * e)) & 255u);
+                    pv[e] = ok ? (float)(code - bz[i]) * bs[i] : 0.0f;
+                }
+                *reinterpret_cast<float4*>(dst) = v;
+            } else {
+                *reinterpret_cast<u32x4*>(dst) = rb[i];
+            }
+        }
+    };
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    const int lr = lane & 31, lh = (lane >> 5) * (BK / 2);
+    auto compute = [&](int buf) {
+        const float* As = &lds[buf][(wm * WTM + lr) * LDK + lh];
+        const float* Bs = &lds[buf][(BM + wn * WTN + lr) * LDK + lh];
+#pragma unroll
+        for (int s4 = 0; s4 < BK / 2; s4 += 4) {
+            float4 a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) a[i] = *reinterpret_cast<const float4*>(As + i * 32 * LDK + s4);
+#pragma unroll
+            for (int j = 0; j < TN; j++) b[j] = *reinterpret_cast<const float4*>(Bs + j * 32 * LDK + s4);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(reinterpret_cast<const float*>(&a[i])[e],
+                                                                         reinterpret_cast<const float*>(&b[j])[e],
+                                                                         acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // Tiles never straddle a split boundary, so masking against K stays exact.
+    const int kbeg = SPLIT ? (int)blockIdx.y * kchunk : 0;
+    const int kend = SPLIT ? min(g.K, kbeg + kchunk) : g.K;
+    const int nk = (kend - kbeg + BK - 1) / BK;
+    load_tile(kbeg);
+    store_tile(0, kbeg);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 1 < nk; kt++) {
+        const int cur = kt & 1;
+        const int k1 = kbeg + (kt + 1) * BK;
+        load_tile(k1);
+        compute(cur);
+        if constexpr (IGLP >= 0) __builtin_amdgcn_iglp_opt(IGLP);
+        store_tile(cur ^ 1, k1);
+        __syncthreads();
+    }
+    compute(kt & 1);
+    gfloat* part = (gfloat*)g.Y + (SPLIT ? (int64_t)blockIdx.y * g.M * g.N : 0);
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int n = n0 + wn * WTN + j * 32 + lr;
+                if (m < g.M && n < g.N) {
+                    if constexpr (SPLIT) part[(int64_t)m * g.N + n] = acc[i][j][r];
+                    else epilogue_fast<YDT>(g, m, n, (double)acc[i][j][r]);
+                }
+            }
+}
+
+// Sums the split-K slices of element (m, n) in slice order (in double) and
+// applies the Gemm epilogue.  Four consecutive n per thread.
+template <int YDT>
+__global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, const float* __restrict__ part, int nsplit) {
+    const int64_t mn = (int64_t)g.M * g.N;
+    const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (e0 >= mn) return;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int64_t i = e0 + e;
+        if (i >= mn) break;
+        double acc = 0.0;
+        for (int sp = 0; sp < nsplit; sp++) acc += (double)part[sp * mn + i];
+        epilogue_fast<YDT>(g, (int)(i / g.N), (int)(i % g.N), acc);
+    }
+}
+
 // -------------------------------------------------------------------- dispatch ---
 inline bool f32_exact_dtype(int dt) {
     return dt == kF32 || dt == kF16 || dt == kBF16 || dt == kE4M3 || dt == kE5M2 || dt == kI4 || dt == kI8 ||
@@ -594,6 +788,68 @@ bool launch_f16_nt(const GemmArgs& g, hipStream_t s) {
     if (big_tiles >= 192) launch_f16_nt_cfg<256, 256, 64, 2, 4, 2, 1>(g, s);
     else launch_f16_nt_cfg<128, 128, 64, 2, 2, 2, 0>(g, s);
     return true;
+}
+
+// f32 A [M, K] with B [N, K] (f32 codes or int8 / uint8 codes dequantised on
+// the fly): the tiled kernel.  128x256 tiles over 8 waves (64x64 each) when
+// they cover the CUs; otherwise 128x64 tiles with k split into up to 16
+// slices (each at least 512 deep) so that about 512 blocks run, the slices
+// summed by k_splitk_reduce.  The plan depends on M, N and K only, so the
+// fused weight-only-quantized Gemm and the unfused DequantizeLinear -> Gemm
+// pair run the same schedule and return the same bits.
+// Returns 1 when launched, 0 when the operands do not fit the kernel (caller
+// falls back), -1 on an allocation failure (error set).
+int nt_split_plan(int M, int N, int K, bool& big) {
+    const int64_t big_tiles = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
+    big = big_tiles >= 192;
+    if (big) return 1;
+    const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 63) / 64);
+    int64_t sp = std::min<int64_t>((512 + tiles - 1) / tiles, K / 512);
+    return (int)std::max<int64_t>(1, std::min<int64_t>(sp, 16));
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, int BQ, bool SPLIT>
+void launch_nt_kernel(const GemmArgs& g, const WoqB& q, int kchunk, int nsplit, int ydt, hipStream_t s) {
+    const dim3 grid(((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN), nsplit), block(64 * WGM * WGN);
+    if (SPLIT || ydt == kF32)
+        hipLaunchKernelGGL((k_gemm_f32_nt<BM, BN, BK, WGM, WGN, kF32, BQ, -1, SPLIT>), grid, block, 0, s, g, q, kchunk);
+    else if (ydt == kF16)
+        hipLaunchKernelGGL((k_gemm_f32_nt<BM, BN, BK, WGM, WGN, kF16, BQ, -1, SPLIT>), grid, block, 0, s, g, q, kchunk);
+    else
+        hipLaunchKernelGGL((k_gemm_f32_nt<BM, BN, BK, WGM, WGN, -1, BQ, -1, SPLIT>), grid, block, 0, s, g, q, kchunk);
+}
+
+template <int BQ>
+int launch_f32_nt(const GemmArgs& g, const WoqB& q, hipStream_t s) {
+    const int64_t reach = (int64_t)1 << 31;
+    const int eb = BQ ? 1 : 4;
+    if ((int64_t)(g.M + 256) * g.lda * 4 >= reach || (int64_t)(g.N + 256) * g.ldb * eb >= reach) return 0;
+    const bool fast_bias = g.c.mode == 0 || (g.c.dt == kF32 && g.c.mode <= 3);
+    const int ydt = fast_bias && (g.dty == kF32 || g.dty == kF16) ? g.dty : -1;
+    bool big = false;
+    const int split = nt_split_plan(g.M, g.N, g.K, big);
+    if (big) {
+        launch_nt_kernel<128, 256, 16, 2, 4, BQ, false>(g, q, 0, 1, ydt, s);
+        return 1;
+    }
+    if (split <= 1) {
+        launch_nt_kernel<128, 64, 16, 2, 2, BQ, false>(g, q, 0, 1, ydt, s);
+        return 1;
+    }
+    const int kchunk = ((g.K + split - 1) / split + 15) / 16 * 16;
+    const int nsplit = (g.K + kchunk - 1) / kchunk;
+    const int64_t mn = (int64_t)g.M * g.N;
+    float* part = (float*)pool_alloc((size_t)nsplit * mn * sizeof(float));
+    if (!part) return -1;
+    GemmArgs gp = g;
+    gp.Y = part;
+    launch_nt_kernel<128, 64, 16, 2, 2, BQ, true>(gp, q, kchunk, nsplit, kF32, s);
+    const dim3 rgrid((unsigned)((mn + 1023) / 1024));
+    if (ydt == kF32) hipLaunchKernelGGL((k_splitk_reduce<kF32>), rgrid, dim3(256), 0, s, g, (const float*)part, nsplit);
+    else if (ydt == kF16) hipLaunchKernelGGL((k_splitk_reduce<kF16>), rgrid, dim3(256), 0, s, g, (const float*)part, nsplit);
+    else hipLaunchKernelGGL((k_splitk_reduce<-1>), rgrid, dim3(256), 0, s, g, (const float*)part, nsplit);
+    pool_free(part);   // stream-ordered reuse: later work on this stream runs after the reduction
+    return 1;
 }
 
 // f32 x f32 uses typed (optionally vectorised) staging; every other pair of
@@ -673,7 +929,11 @@ extern "C" void gemm_forward(const Tensor* A, const Tensor* B, const Tensor* C, 
                 else launch_f16_y<true, false>(g, grid, vec, s);
                 done = true;
             } else if (f32_exact_dtype(dta) && f32_exact_dtype(dtb)) {
-                done = launch_f32_mfma(g, dta, dtb, transA, transB, s);
+                const bool nt = dta == kF32 && dtb == kF32 && !transA && transB && (g.lda % 4) == 0 &&
+                                (g.ldb % 4) == 0 && ((uintptr_t)g.A & 15) == 0 && ((uintptr_t)g.B & 15) == 0;
+                const int r = nt ? launch_f32_nt<0>(g, WoqB{nullptr, nullptr, 0, 0}, s) : 0;
+                if (r < 0) { st.finish(); return; }
+                done = r == 1 || launch_f32_mfma(g, dta, dtb, transA, transB, s);
             }
         }
         if (!done) {
@@ -682,5 +942,96 @@ extern "C" void gemm_forward(const Tensor* A, const Tensor* B, const Tensor* C, 
         }
         if (!check_launch(name)) { st.finish(); return; }
     }
+    st.finish();
+}
+
+namespace {
+// The unfused pair, for the cases the fused kernel does not cover.
+void dequantize_then_gemm(const Tensor* A, const Tensor* Bq, const Tensor* Scale, const Tensor* ZeroPoint, int axis,
+                          const Tensor* C, Tensor* Y, float alpha, float beta, int transA, int transB) {
+    int shp[2] = {Bq->shape[0], Bq->shape[1]};
+    Tensor* Bd = create_tensor_device_empty(shp, 2, DTYPE_FLOAT32);
+    if (!Bd) return;
+    tensor_ops_hip_clear_error();
+    dequantize_linear_axis_forward(Bq, Scale, ZeroPoint, Bd, axis);
+    if (tensor_ops_hip_last_error()[0] == 0) gemm_forward(A, Bd, C, Y, alpha, beta, transA, transB);
+    free_tensor(Bd);
+}
+}  // namespace
+
+// Weight-only-quantized Gemm: the DequantizeLinear -> Gemm pair of a quantized
+// ONNX graph (tensor_ops.c:1018-1034 then :1167-1228) in one pass.  The fused
+// kernel covers f32 A [M, K] (transA = 0) with B [N, K] (transB = 1) of int8 /
+// uint8 codes, an f32 Scale of 1 or N elements (axis 0) and a ZeroPoint of B's
+// dtype; everything else runs the two operators in sequence, which is also
+// what the fused kernel returns, bit for bit.
+extern "C" void dequantize_gemm_forward(const Tensor* A, const Tensor* Bq, const Tensor* Scale,
+                                        const Tensor* ZeroPoint, int axis, const Tensor* C, Tensor* Y, float alpha,
+                                        float beta, int transA, int transB) {
+    const char* name = "dequantize_gemm_forward";
+    if (!tensor_sane(A, name) || !tensor_sane(Bq, name) || !tensor_sane(Scale, name) || !tensor_sane(Y, name)) return;
+    const bool has_z = ZeroPoint && ZeroPoint->data;
+    if (has_z && !tensor_sane(ZeroPoint, name)) return;
+    if (A->ndim != 2 || Bq->ndim != 2) { set_error("%s: A and B must be 2-D", name); return; }
+    if (axis < 0) axis += 2;
+    if (axis < 0 || axis > 1) { set_error("%s: axis out of range", name); return; }
+    const size_t nax = (size_t)Bq->shape[axis];
+    if (Scale->size != 1 && Scale->size != nax) {
+        set_error("%s: Scale must have 1 or B.shape[axis] elements", name);
+        return;
+    }
+    if (has_z && ZeroPoint->size != 1 && ZeroPoint->size != nax) {
+        set_error("%s: ZeroPoint must have 1 or B.shape[axis] elements", name);
+        return;
+    }
+    const int M = transA ? A->shape[1] : A->shape[0];
+    const int K = transA ? A->shape[0] : A->shape[1];
+    const int N = transB ? Bq->shape[0] : Bq->shape[1];
+    const int KB = transB ? Bq->shape[1] : Bq->shape[0];
+    if (K != KB) { set_error("%s: inner dimensions differ (%d vs %d)", name, K, KB); return; }
+    if ((size_t)M * (size_t)N > Y->size) { set_error("%s: Y holds %zu elements, needs %d x %d", name, Y->size, M, N); return; }
+    const bool has_c = C && C->data;
+    if (has_c && !tensor_sane(C, name)) return;
+    if (!ensure_device()) return;
+
+    const int dtb = (int)Bq->dtype;
+    const int64_t reach = (int64_t)1 << 31;
+    const bool fused = !exact_mode() && A->dtype == kF32 && (dtb == kI8 || dtb == kU8) && Scale->dtype == kF32 &&
+                       (!has_z || (int)ZeroPoint->dtype == dtb) && !transA && transB &&
+                       (axis == 0 || (Scale->size == 1 && (!has_z || ZeroPoint->size == 1))) && (K % 4) == 0 &&
+                       M > 0 && N > 0 && ((uintptr_t)A->data & 15) == 0 && ((uintptr_t)Bq->data & 3) == 0 &&
+                       (int64_t)(M + 256) * K * 4 < reach && (int64_t)(N + 256) * K < reach;
+    if (!fused) {
+        dequantize_then_gemm(A, Bq, Scale, has_z ? ZeroPoint : nullptr, axis, C, Y, alpha, beta, transA, transB);
+        return;
+    }
+
+    GemmArgs g;
+    g.M = M; g.N = N; g.K = K;
+    g.lda = K; g.ldb = K;
+    g.alpha = (double)alpha; g.beta = (double)beta;
+    g.dty = (int)Y->dtype;
+    g.c = Bias{nullptr, has_c ? (int)C->dtype : 0, 0, 0, 0};
+    if (has_c) {
+        if (C->size == 1) g.c.mode = 1;
+        else if (C->ndim == 1) g.c.mode = (C->shape[0] == N) ? 2 : (C->shape[0] == M ? 3 : 5);
+        else { g.c.mode = 4; g.c.H = C->shape[C->ndim - 2]; g.c.W = C->shape[C->ndim - 1]; }
+        if (g.c.mode == 4 && C->size == (size_t)g.c.H * g.c.W) {
+            if (g.c.H == 1 && g.c.W == N) g.c.mode = 2;
+            else if (g.c.H == M && g.c.W == 1) g.c.mode = 3;
+        }
+    }
+    Staging st;
+    g.A = st.in(A);
+    g.B = st.in(Bq);
+    const void* sp = st.in(Scale);
+    const void* zp = has_z ? st.in(ZeroPoint) : nullptr;
+    if (has_c) g.c.p = st.in(C);
+    g.Y = st.out(Y, (size_t)M * N * dt_bytes((int)Y->dtype));
+    if (!g.A || !g.B || !sp || (has_z && !zp) || !g.Y || (has_c && !g.c.p)) { st.finish(); return; }
+    if (!has_c) g.c.mode = 0;
+    const WoqB q{(const float*)sp, zp, Scale->size > 1 ? 1 : 0, has_z ? (int)ZeroPoint->size : 0};
+    const int r = dtb == kI8 ? launch_f32_nt<1>(g, q, stream()) : launch_f32_nt<2>(g, q, stream());
+    if (r > 0) check_launch(name);
     st.finish();
 }

@@ -143,7 +143,8 @@ def ONNXParasGen(file_path, seed: int = 0) -> Tuple[List[str], List[Tensor]]:
 
 def load_graph(file_path, fuse: bool = True, device: bool = True):
     """A :class:`Graph` over the model's nodes with its initializers fed (on the device
-    when ``device``), elementwise runs fused when ``fuse``."""
+    when ``device``), with elementwise runs and DequantizeLinear -> Gemm pairs fused
+    when ``fuse``."""
     from .graph import Graph
     model = _model(file_path)
     inits = initializers(model)
@@ -153,5 +154,5 @@ def load_graph(file_path, fuse: bool = True, device: bool = True):
     if device:
         g.to_device()
     if fuse:
-        g.fuse_elementwise()
+        g.fuse()
     return g

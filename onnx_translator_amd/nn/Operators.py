@@ -301,6 +301,45 @@ class Gemm(Ops):
         return _values(self, Tensor_(M, N, dtype=self.dtype))
 
 
+class DequantizeGemm(Ops):
+    """Gemm(A, DequantizeLinear(Bq, scale, zero_point), C) in one call to
+    ``dequantize_gemm_forward``: the weight-only-quantized Gemm reads the int8 /
+    uint8 codes and never writes the f32 weight.  Output equals the
+    DequantizeLinear -> Gemm pair (nn/Operators.py:452-473 then :613-669) bit
+    for bit.  ``inputs`` = [A, Bq, scale, zero_point or "", C (optional)];
+    ``axis`` is the dequantisation axis of Bq (a 1-element scale is per-tensor)."""
+
+    def __init__(self, inputs, outputs, alpha, beta, transA, transB, axis, dtype, version="17"):
+        super().__init__(inputs, outputs)
+        self.alpha, self.beta, self.transA, self.transB, self.axis = alpha, beta, transA, transB, axis
+        self.dtype = dtype
+        self.version = version
+        self.lib.dequantize_gemm_forward.argtypes = [PT, PT, PT, PT, ctypes.c_int, PT, PT, ctypes.c_float,
+                                                     ctypes.c_float, ctypes.c_int, ctypes.c_int]
+        self.lib.dequantize_gemm_forward.restype = None
+
+    def _mn(self, A, B):
+        M = A.size[0] if self.transA == 0 else A.size[1]
+        N = B.size[1] if self.transB == 0 else B.size[0]
+        return M, N
+
+    def forward(self, A: Tensor, Bq: Tensor, scale: Tensor, zero_point: Tensor = None, C: Tensor = None):
+        M, N = self._mn(A, Bq)
+        args = (ctypes.c_int(self.axis), ctypes.c_float(self.alpha), ctypes.c_float(self.beta),
+                ctypes.c_int(self.transA), ctypes.c_int(self.transB))
+
+        def arrange(ins, out):
+            a, b, sc, zp, c = ins
+            return (a, b, sc, zp, args[0], c, out) + args[1:]
+        t = self._run("dequantize_gemm_forward", [A, Bq, scale, zero_point, C], (M, N), self.dtype,
+                      arrange=arrange)
+        return _values(self, t)
+
+    def forward_(self, A: Tensor_, Bq: Tensor_, scale: Tensor_ = None, zero_point: Tensor_ = None,
+                 C: Tensor_ = None):
+        return _values(self, Tensor_(*self._mn(A, Bq), dtype=self.dtype))
+
+
 class Softmax(Ops):
     """Softmax along one axis (nn/Operators.py:671-704 -> tensor_ops.c:1231-1270)."""
 

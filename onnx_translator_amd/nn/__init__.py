@@ -279,7 +279,9 @@ class Ops:
             for c in keep:
                 self.lib.free_tensor(c)
 
-    def _run(self, c_func_name, ins, out_shape, out_dtype, *extra):
+    def _run(self, c_func_name, ins, out_shape, out_dtype, *extra, arrange=None):
+        """Call c_func_name(*inputs, output, *extra) (or the argument list
+        ``arrange(inputs, output)`` builds) and wrap the output."""
         keep: list = []
         dev = any(isinstance(t.data, DeviceArray) for t in ins if t is not None)
         try:
@@ -290,7 +292,10 @@ class Ops:
                 self.lib.free_tensor(c)
             raise
         try:
-            self._call(c_func_name, *cins, c_out, *extra)
+            if arrange is None:
+                self._call(c_func_name, *cins, c_out, *extra)
+            else:
+                self._call(c_func_name, *arrange(cins, c_out))
         except Exception:
             if dev_out is None:
                 self.lib.free_tensor(c_out)

@@ -4,6 +4,10 @@
   ``z = Cos(Relu(x) + Abs(y))`` with x [1,3,32,32] and y [1,1,1,32] (the
   reference exports it with ``torch.onnx.export``, which needs the ``onnx``
   package; here the same graph is written directly, opset 17).
+* :func:`woq_gemm_model` — the config-3 weight-only-quantized Gemm:
+  ``Gemm(A, DequantizeLinear(Bq, s, zp, axis=0), C, transB=1)`` with A f32
+  [256, 4096], Bq int8 [4096, 4096] quantized per output row with scale
+  max|B_n| / 127 and zero point 0, and C f32 [4096] (seed 2).
 * :func:`resnet_qdq_model` — the QDQ ResNet-style graph: a conv 7x7 / stride 2
   stem with Relu, MaxPool 3x3 / stride 2, four QDQ conv 3x3 blocks (uint8
   per-tensor activations, int8 per-output-channel weights, Relu, residual Add;
@@ -65,6 +69,23 @@ def _quantized_weight(b: _Builder, rng, prefix, shape):
     return b.node("DequantizeLinear", [prefix + ".wq", prefix + ".ws", prefix + ".wz"], [prefix + ".w"], axis=0)
 
 
+def woq_gemm_model(M: int = 256, N: int = 4096, K: int = 4096, seed: int = 2) -> ModelProto:
+    rng = np.random.default_rng(seed)
+    b = _Builder()
+    bw = rng.normal(0, 1 / np.sqrt(K), (N, K))
+    s = (np.abs(bw).max(axis=1) / 127).astype(np.float32)
+    q = np.clip(np.rint(bw / s[:, None]), -127, 127).astype(np.int8)
+    b.init("fc.wq", q, INT8)
+    b.init("fc.ws", s, FLOAT)
+    b.init("fc.wz", np.zeros(N, np.int8), INT8)
+    b.init("fc.b", rng.normal(0, 1 / 64, N).astype(np.float32), FLOAT)
+    w = b.node("DequantizeLinear", ["fc.wq", "fc.ws", "fc.wz"], ["fc.w"], axis=0)
+    b.node("Gemm", ["input", w, "fc.b"], ["output"], alpha=1.0, beta=1.0, transB=1)
+    graph = GraphProto("woq_gemm", b.nodes, b.inits, [ValueInfoProto("input", FLOAT, [M, K])],
+                       [ValueInfoProto("output", FLOAT, [M, N])], b.vinfo)
+    return ModelProto(graph, producer_name="onnx_translator_amd")
+
+
 def resnet_qdq_model(batch: int = 64, image: int = 224, seed: int = 4, classes: int = 1000,
                      widths=(64, 128, 256, 512)) -> ModelProto:
     rng = np.random.default_rng(seed)
@@ -110,11 +131,12 @@ def resnet_qdq_model(batch: int = 64, image: int = 224, seed: int = 4, classes: 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("out")
-    ap.add_argument("--model", choices=["resnet_qdq", "comprehensive"], default="resnet_qdq")
+    ap.add_argument("--model", choices=["resnet_qdq", "woq_gemm", "comprehensive"], default="resnet_qdq")
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--image", type=int, default=224)
     args = ap.parse_args()
-    m = resnet_qdq_model(args.batch, args.image) if args.model == "resnet_qdq" else comprehensive_model()
+    m = {"resnet_qdq": lambda: resnet_qdq_model(args.batch, args.image), "woq_gemm": woq_gemm_model,
+         "comprehensive": comprehensive_model}[args.model]()
     save(m, args.out)
     print(f"wrote {args.out}: {len(m.graph.nodes)} nodes, {len(m.graph.initializers)} initializers")
 

@@ -181,6 +181,8 @@ class HipLib(O.CpuLib):
         lib.tensor_is_device.restype = ctypes.c_int
         for n in ("quantize_linear_axis_forward", "dequantize_linear_axis_forward"):
             getattr(lib, n).argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int]
+        lib.dequantize_gemm_forward.argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int, O.PT, O.PT, ctypes.c_float,
+                                                ctypes.c_float, ctypes.c_int, ctypes.c_int]
 
     def device_count(self):
         return int(self.lib.tensor_ops_hip_device_count())
@@ -207,6 +209,29 @@ class HipLib(O.CpuLib):
         if err:
             raise RuntimeError(err)
         return out
+
+    def dq_gemm(self, a, bq, dtb, s, z, axis, c, dty, alpha=1.0, beta=1.0, transA=0, transB=1):
+        """dequantize_gemm_forward on host tensors: A f32, Bq codes of dtb, 1-D Scale (f32)
+        and ZeroPoint (dtb, or None), bias c (f32 or None)."""
+        M = a.shape[1] if transA else a.shape[0]
+        N = bq.shape[0] if transB else bq.shape[1]
+        ins = [self.tensor(a, "float32"), self.tensor(bq, dtb), self.tensor(np.atleast_1d(s), "float32"),
+               self.tensor(np.atleast_1d(z), dtb) if z is not None else O.PT(),
+               self.tensor(c, "float32") if c is not None else O.PT()]
+        o = self.empty((M, N), dty)
+        try:
+            self.lib.tensor_ops_hip_clear_error()
+            self.lib.dequantize_gemm_forward(ins[0], ins[1], ins[2], ins[3], int(axis), ins[4], o,
+                                             ctypes.c_float(alpha), ctypes.c_float(beta), int(transA), int(transB))
+            err = self.last_error()
+            if err:
+                raise RuntimeError(err)
+            return self.read(o, dty)
+        finally:
+            for t in ins:
+                if t:
+                    self.lib.free_tensor(t)
+            self.lib.free_tensor(o)
 
     # device tensors --------------------------------------------------------
     def dev_from(self, arr, dt):

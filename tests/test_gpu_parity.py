@@ -71,6 +71,92 @@ def test_gemm_ragged_shapes(hip, oracle_lib, shape, trans):
         assert_close(got, ref, O.F32, what=f"gemm {dt} {shape} {trans}")
 
 
+# f32 x f32 with transB = 1 and K % 4 == 0 runs the tiled NT kernel: 128x256
+# tiles when the grid has >= 192 of them, else 128x64 tiles with the k range
+# split over up to 16 slices (partial sums reduced in a second pass).  The
+# cases cover one slice, several slices with a ragged last one, K % 16 != 0,
+# ragged M / N and every bias mode of the inline and out-of-line epilogues.
+F32_NT = [(300, 200, 136, "col"), (64, 256, 2048, "none"), (70, 130, 1100, "scalar"), (96, 72, 5200, "row"),
+          (3000, 3100, 68, "col"), (1000, 1000, 4, "2d"), (1, 1000, 512, "col")]
+
+
+@pytest.mark.parametrize("M,N,K,bias", F32_NT, ids=[f"{m}x{n}x{k}-{b}" for m, n, k, b in F32_NT])
+@pytest.mark.parametrize("ydt", ["float32", "float16"])
+def test_gemm_f32_tiled_kernel(hip, M, N, K, bias, ydt):
+    from tests.helpers import assert_close
+    rng = np.random.default_rng(M + 5 * N + 11 * K)
+    a = rng.normal(0, 1, (M, K)).astype(np.float32)
+    b = rng.normal(0, 1, (N, K)).astype(np.float32)
+    c = {"none": None, "scalar": rng.normal(0, 1, (1,)), "row": rng.normal(0, 1, (M,)),
+         "col": rng.normal(0, 1, (N,)), "2d": rng.normal(0, 1, (M, N))}[bias]
+    if c is not None:
+        c = c.astype(np.float32)
+    alpha, beta = 0.75, 1.5
+    y = hip.gemm(a, O.F32, b, O.F32, c, O.F32, ydt, alpha, beta, 0, 1)
+    rows = np.arange(M) if M * N <= 1 << 20 else np.unique(np.r_[rng.choice(M, 40, replace=False), 0, M - 1])
+    ref = alpha * (a[rows].astype(np.float64) @ b.astype(np.float64).T)
+    if c is not None:
+        cc = {"row": lambda: c[rows].reshape(-1, 1), "2d": lambda: c[rows]}.get(bias, lambda: c.reshape(1, -1))()
+        ref = ref + beta * cc.astype(np.float64)
+    if ydt == "float16":
+        assert_close(y[rows], O.oracle().encode_f32(ref.astype(np.float32), O.F16), O.F16,
+                     what=f"f32 nt {M}x{N}x{K} {bias}")
+    else:
+        assert_close(y[rows], ref.astype(np.float32), O.F32, what=f"f32 nt {M}x{N}x{K} {bias}")
+
+
+# dequantize_gemm_forward: the fused weight-only-quantized Gemm returns the
+# bits of dequantize_linear_axis_forward followed by gemm_forward (same
+# schedule, and the dequantised operand is the same fp32 value), and matches
+# the oracle's DequantizeLinear -> Gemm within the Gemm tolerance.  Cases: int8
+# per-row scales (split-K and single slice), uint8 with per-row zero points,
+# per-tensor parameters, no zero point, K % 16 != 0, ragged M / N, and cases
+# the fused kernel does not take (transB = 0, axis 1 scales, K % 4 != 0),
+# which run the unfused pair.
+DQ_GEMM = [("i8_row", 64, 256, 2048, "int8", "row", 1, 0), ("i8_row_big", 300, 2100, 96, "int8", "row", 1, 0),
+           ("u8_zp", 70, 130, 1100, "uint8", "row", 1, 0), ("u8_tensor", 33, 65, 260, "uint8", "tensor", 1, 0),
+           ("i8_nozp", 128, 64, 512, "int8", "nozp", 1, 0), ("i8_nn", 40, 50, 60, "int8", "row", 0, 1),
+           ("i8_axis1", 40, 50, 64, "int8", "col", 1, 1), ("i8_k_odd", 17, 19, 23, "int8", "row", 1, 0)]
+
+
+@pytest.mark.parametrize("case", DQ_GEMM, ids=[c[0] for c in DQ_GEMM])
+@pytest.mark.parametrize("ydt", ["float32", "float16"])
+def test_dequantize_gemm(hip, oracle_lib, case, ydt):
+    import ctypes
+    from tests.helpers import assert_close
+    tag, M, N, K, bdt, params, tb, axis = case
+    rng = np.random.default_rng(M * 3 + N + K)
+    shape = (N, K) if tb else (K, N)
+    lo, hi = (-128, 128) if bdt == "int8" else (0, 256)
+    bq = rng.integers(lo, hi, shape).astype(np.int8 if bdt == "int8" else np.uint8)
+    nax = shape[axis]
+    s = (rng.uniform(0.5, 2.0, nax) / 127).astype(np.float32)
+    z = rng.integers(-3, 4, nax) if bdt == "int8" else rng.integers(100, 156, nax)
+    z = z.astype(bq.dtype)
+    if params == "tensor":
+        s, z = s[:1], z[:1]
+    elif params == "nozp":
+        z = None
+    a = rng.normal(0, 1, (M, K)).astype(np.float32)
+    c = rng.normal(0, 1, (N,)).astype(np.float32)
+    got = hip.dq_gemm(a, bq, bdt, s, z, axis, c, ydt, 0.75, 1.25, 0, tb)
+    # unfused pair through the same library
+    zz = z if z is not None else np.zeros(1, bq.dtype)
+    bd = hip._run(hip.lib.dequantize_linear_axis_forward, [(bq, bdt), (s, O.F32), (zz, bdt)], bq.shape, O.F32,
+                  ctypes.c_int(axis))
+    two = hip.gemm(a, O.F32, bd, O.F32, c, O.F32, ydt, 0.75, 1.25, 0, tb)
+    assert np.array_equal(got.view(np.uint8), two.view(np.uint8)), f"{tag}: fused differs from the unfused pair"
+    # oracle: DequantizeLinear with the parameters on their axis, then Gemm
+    on_axis = [1, 1]
+    on_axis[axis] = -1
+    zo = zz if zz.size > 1 else np.broadcast_to(zz, s.shape)
+    ref_b = oracle_lib.qdq("dequantize", bq, bdt, s.reshape(on_axis) if s.size > 1 else s, O.F32,
+                           zo.reshape(on_axis) if zo.size > 1 else zo, bdt, O.F32)
+    assert np.array_equal(bd, ref_b), f"{tag}: dequantised weight differs from the oracle"
+    ref = oracle_lib.gemm(a, O.F32, ref_b, O.F32, c, O.F32, ydt, 0.75, 1.25, 0, tb)
+    assert_close(got, ref, ydt, what=f"dequantize_gemm {tag}")
+
+
 # f16 x f16 with transB = 1 and K % 8 == 0 runs the tiled kernel (buffer loads,
 # K tail masked in registers): 128x128 tiles for small grids, 256x256 tiles when
 # the grid has >= 192 of them.  Ragged M / N and K % 64 != 0 exercise the edges;

@@ -12,7 +12,7 @@ import pytest
 
 from oracle import oracle as O
 from onnx_translator_amd.onnx import proto as P
-from onnx_translator_amd.onnx.create_model import comprehensive_model, resnet_qdq_model
+from onnx_translator_amd.onnx.create_model import comprehensive_model, resnet_qdq_model, woq_gemm_model
 from tests.graph_oracle import run_model
 from tests.helpers import assert_bitexact, assert_close
 
@@ -105,7 +105,7 @@ def test_importer_mapping_and_shapes():
     g = Graph(ops, ["input"], ["output"], initializers=initializers(m))
     out = g.forward_(Tensor_(2, 3, 64, 64, dtype="float32"))
     assert out.size == (2, 1000) and out.dtype == "float32"
-    g._fuse([Tensor_(2, 3, 64, 64, dtype="float32")])
+    g.fuse()._fuse([Tensor_(2, 3, 64, 64, dtype="float32")])
     assert g.fused_runs == [["RELU.1", "ADD.0"]]
 
 
@@ -130,6 +130,45 @@ def test_toy_graph_on_device(hip, oracle_lib):
     assert out.on_device and g.fused_runs == [["ADD.0", "COS.0"]]
     env = run_model(oracle_lib, m, {"input_x": (x, "float32"), "input_y": (y, "float32")})
     assert_bitexact(out.numpy(), env["output"][0], O.F32, what="toy graph")
+
+
+def test_dq_gemm_fusion_pass():
+    """The fusion pass replaces the weight DequantizeLinear -> Gemm pair (placeholder
+    shapes only, no GPU) and keeps the graph's edges consistent."""
+    from onnx_translator_amd.nn import Tensor_
+    from onnx_translator_amd.nn.graph import Graph
+    from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
+    m = woq_gemm_model(M=8, N=64, K=32)
+    inits = initializers(m)
+    g = Graph(ONNXImport(m), ["input"], ["output"], initializers=inits).fuse()
+    shapes = g._edge_shapes([Tensor_(8, 32, dtype="float32")])
+    g._fuse_pending = None
+    g._fuse_dq_gemm(shapes, g._consumers())
+    ops = list(g.ops.values())
+    assert [type(o).__name__ for o in ops] == ["DequantizeGemm"]
+    assert ops[0].inputs == ["input", "fc.wq", "fc.ws", "fc.wz", "fc.b"] and ops[0].axis == 0
+    assert g.fused_runs == [["DequantizeLinear.0", "Gemm.0"]]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(256, 4096, 4096), (40, 300, 520)], ids=["config3", "ragged"])
+def test_woq_gemm_graph(hip, oracle_lib, shape):
+    """Config-3 WOQ graph: the fused DequantizeGemm returns the unfused pair's bits,
+    and both match the oracle's DequantizeLinear -> Gemm within the Gemm tolerance
+    (oracle on sampled rows at the full size)."""
+    from onnx_translator_amd.nn.ONNXImport import load_graph
+    M, N, K = shape
+    m = woq_gemm_model(M=M, N=N, K=K)
+    x = np.random.default_rng(2).normal(0, 1 / 64, (M, K)).astype(np.float32)
+    fused = load_graph(m)
+    y = fused.forward(x).numpy()
+    assert fused.fused_runs == [["DequantizeLinear.0", "Gemm.0"]]
+    plain = load_graph(m, fuse=False)
+    y2 = plain.forward(x).numpy()
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+    rows = np.arange(M) if M <= 64 else np.r_[0, 1, 97, 128, M - 1]
+    env = run_model(oracle_lib, m, {"input": (x[rows], "float32")})
+    assert_close(y[rows], env["output"][0], O.F32, what=f"woq graph {shape}")
 
 
 @pytest.mark.gpu
