@@ -199,6 +199,13 @@ void dequantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const 
 void dequantize_gemm_forward(const Tensor* A, const Tensor* Bq, const Tensor* Scale, const Tensor* ZeroPoint,
                              int axis, const Tensor* C, Tensor* Y, float alpha, float beta, int transA,
                              int transB);
+/* Convolution with the residual block's epilogue: Y = [Skip +] [Relu](Conv(X, W, B)), the
+ * conv2d_forward -> relu_forward -> add_forward(., Skip) sequence (tensor_ops/tensor_ops.h:161,
+ * 85, 116) in one pass over Y.  Each step rounds to the output dtype as the standalone
+ * operator does, so Y equals the sequence bit for bit.  relu != 0 applies Relu; Skip may be
+ * NULL (no Add) and broadcasts to Y as add_forward's B does. */
+void conv2d_fused_forward(const Tensor* X, const Tensor* W, const Tensor* B, const Tensor* Skip, int relu,
+                          Tensor* Y, ConvParams* params);
 
 #ifdef __cplusplus
 }

@@ -16,6 +16,8 @@
 //    coalesced; the (c, kh, kw) decode of k is uniform across the block.
 //    fp32 accumulate: tolerance class vs the reference.
 //  * k_conv_exact — fp64, reference summation order, bit-identical.
+#include <algorithm>
+
 #include "runtime.h"
 
 namespace tohip {
@@ -208,11 +210,26 @@ struct ConvTiled {
 
 typedef __attribute__((address_space(1))) float gfloat;
 
-template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int YDT>
+// Fused epilogue of conv2d_fused_forward (f32 output): y = conv + bias, then
+// Relu (v > 0 ? v : 0, as relu_forward), then + skip (an f32 tensor of Y's
+// shape, as add_forward).  Each step rounds to f32 exactly as the standalone
+// operator does, so the result equals the three calls bit for bit.
+struct ConvEpi {
+    const float* skip;
+    int relu;
+};
+__device__ __forceinline__ float relu_f(float v) { return v > 0.0f ? v : 0.0f; }
+
+// SPLIT: blockIdx.z = slice * groups + group; slice s covers k in
+// [s * kchunk, (s + 1) * kchunk) (kchunk a multiple of BK) and stores its raw
+// fp32 sums, without bias, to Y + s * N * M * OH * OW (Y is then the f32
+// workspace); k_conv_splitk_reduce adds the slices in order with the bias.
+template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int YDT, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __restrict__ X, const float* __restrict__ Wt,
                                                                const float* __restrict__ Bv, void* __restrict__ Y,
                                                                int dty, int dtb, ConvTiled g, uint32_t xbytes,
-                                                               uint32_t wbytes, uint32_t ybytes) {
+                                                               uint32_t wbytes, uint32_t ybytes, ConvEpi epi,
+                                                               int kchunk = 0, int groups = 1) {
     constexpr int NT = 64 * WGM * WGN;
     constexpr int WTM = BM / WGM, WTP = BP / WGN, TM = WTM / 32, TP = WTP / 32;
     constexpr int EA = BM * BK / NT;              // weights per thread per k-tile (consecutive k)
@@ -223,7 +240,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
-    const int grp = blockIdx.z;
+    const int grp = SPLIT ? (int)blockIdx.z % groups : (int)blockIdx.z;
+    const int slice = SPLIT ? (int)blockIdx.z / groups : 0;
     const int m0 = blockIdx.y * BM, p0 = blockIdx.x * BP;
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, xbytes);
     const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(Wt, wbytes);
@@ -388,16 +406,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
         }
     };
 
-    const int nk = (g.Kg + BK - 1) / BK;
-    load_tile(0);
+    // Tiles never straddle a slice boundary, so masking against Kg stays exact.
+    const int kbeg = SPLIT ? slice * kchunk : 0;
+    const int nk = ((SPLIT ? min(g.Kg, kbeg + kchunk) : g.Kg) - kbeg + BK - 1) / BK;
+    load_tile(kbeg);
     store_tile(0);
     __syncthreads();
     int kt = 0;
     for (; kt + 1 < nk; kt++) {
         if constexpr (MODE == 0) {
-            compute_and_gather(kt & 1, (kt + 1) * BK);
+            compute_and_gather(kt & 1, kbeg + (kt + 1) * BK);
         } else {
-            load_tile((kt + 1) * BK);
+            load_tile(kbeg + (kt + 1) * BK);
             compute(kt & 1);
         }
         store_tile((kt & 1) ^ 1);
@@ -408,11 +428,29 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
     // Output row m of the 32x32 tile (i, j), register r: m = mw + i*32 + 8*(r/4) + (r%4) + 4*lk,
     // pixel q = qw + j*32 + lr.
     const int mw = m0 + wm * WTM;
+    if constexpr (SPLIT) {
+        gfloat* part = (gfloat*)Y + (int64_t)slice * g.P * g.M;
+#pragma unroll
+        for (int j = 0; j < TP; j++) {
+            const int q = p0 + wn * WTP + j * 32 + lr;
+            if (q >= g.P) continue;
+            const int qn = (int)g.fd_ohw.div((uint32_t)q), qr = q - qn * g.OHW;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int mloc = mw + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+                    if (mloc < g.Mg) part[((int64_t)qn * g.M + grp * g.Mg + mloc) * g.OHW + qr] = acc[i][j][r];
+                }
+        }
+        return;
+    }
     if (YDT == kF32 && mw + WTM <= g.Mg) {
         // Raw buffer stores: per-lane byte offset of (m = mw + 4*lk, pixel q) plus
         // a uniform offset for the tile row, so the 16 x TM x TP stores need no
         // address arithmetic.
         const __amdgpu_buffer_rsrc_t yr = buffer_rsrc(Y, ybytes);
+        const __amdgpu_buffer_rsrc_t zr = buffer_rsrc(epi.skip, epi.skip ? ybytes : 0u);
         float bv[TM][16];
 #pragma unroll
         for (int i = 0; i < TM; i++)
@@ -431,8 +469,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
                     for (int r = 0; r < 16; r++) {
                         const uint32_t so = (uint32_t)((i * 32 + 8 * (r >> 2) + (r & 3)) * g.OHW) * 4u;
                         // + 0.0f without a bias, as the reference adds bias_val = 0.0 (-0 -> +0)
-                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc[i][j][r] + bv[i][r]),
-                                                              yr, vo, so, 0);
+                        float v = acc[i][j][r] + bv[i][r];
+                        if (epi.relu) v = relu_f(v);
+                        if (epi.skip)
+                            v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(zr, vo, so, 0));
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, vo, so, 0);
                     }
             }
         }
@@ -452,7 +493,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
                 const int m = grp * g.Mg + mloc;
                 const int64_t yi = ((int64_t)qn * g.M + m) * g.OHW + qr;
                 if constexpr (YDT == kF32) {
-                    ((gfloat*)Y)[yi] = acc[i][j][r] + (Bv ? ((const gfloat*)Bv)[m] : 0.0f);
+                    float v = acc[i][j][r] + (Bv ? ((const gfloat*)Bv)[m] : 0.0f);
+                    if (epi.relu) v = relu_f(v);
+                    if (epi.skip) v += ((const gfloat*)epi.skip)[yi];
+                    ((gfloat*)Y)[yi] = v;
                 } else {
                     conv_store_rt(Y, dty, yi, Bv, dtb, m, acc[i][j][r]);
                 }
@@ -462,20 +506,57 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
 
 template <int BM, int BP, int BK, int WGM, int WGN, int MODE>
 void launch_conv_tiled_cfg(const float* x, const float* w, const void* b, int dtb, void* y, int dty, const ConvTiled& g,
-                           int group, uint32_t xbytes, uint32_t wbytes, uint32_t ybytes, hipStream_t s) {
+                           int group, uint32_t xbytes, uint32_t wbytes, uint32_t ybytes, ConvEpi epi, hipStream_t s) {
     const dim3 grid((g.P + BP - 1) / BP, (g.Mg + BM - 1) / BM, group), block(64 * WGM * WGN);
     if (dty == kF32 && (!b || dtb == kF32))
         hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32>), grid, block, 0, s, x, w, (const float*)b,
-                           y, dty, dtb, g, xbytes, wbytes, ybytes);
+                           y, dty, dtb, g, xbytes, wbytes, ybytes, epi, 0, 1);
     else
         hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, -1>), grid, block, 0, s, x, w, (const float*)b, y,
-                           dty, dtb, g, xbytes, wbytes, ybytes);
+                           dty, dtb, g, xbytes, wbytes, ybytes, ConvEpi{nullptr, 0}, 0, 1);
+}
+
+// Sum of the split-K slices of each output element, in slice order (double),
+// plus the bias, rounded once to f32.
+// One element per thread (coalesced); total < 2^31 (the caller's reach check).
+__global__ __launch_bounds__(256) void k_conv_splitk_reduce(const float* __restrict__ part, const float* __restrict__ Bv,
+                                                            float* __restrict__ Y, int total, FastDiv fd_ohw,
+                                                            FastDiv fd_m, int nsplit, ConvEpi epi) {
+    const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (i >= total) return;
+    double acc = 0.0;
+    for (int s = 0; s < nsplit; s++) acc += (double)part[(int64_t)s * total + i];
+    if (Bv) {
+        const uint32_t r = fd_ohw.div((uint32_t)i);
+        acc += (double)Bv[r - fd_m.div(r) * fd_m.d];
+    }
+    float v = (float)acc;
+    if (epi.relu) v = relu_f(v);
+    if (epi.skip) v += epi.skip[i];
+    Y[i] = v;
+}
+
+template <int BM, int BP, int BK, int WGM, int WGN, int MODE>
+bool launch_conv_split_cfg(const float* x, const float* w, const float* b, float* y, const ConvTiled& g, int group,
+                           uint32_t xbytes, uint32_t wbytes, int nsplit_req, ConvEpi epi, hipStream_t s) {
+    const int kchunk = ((g.Kg + nsplit_req - 1) / nsplit_req + BK - 1) / BK * BK;
+    const int nsplit = (g.Kg + kchunk - 1) / kchunk;
+    const int64_t total = (int64_t)g.P * g.M;
+    float* part = (float*)pool_alloc((size_t)nsplit * total * sizeof(float));
+    if (!part) return false;
+    const dim3 grid((g.P + BP - 1) / BP, (g.Mg + BM - 1) / BM, group * nsplit), block(64 * WGM * WGN);
+    hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32, true>), grid, block, 0, s, x, w, b, part, kF32,
+                       kF32, g, xbytes, wbytes, 0u, ConvEpi{nullptr, 0}, kchunk, group);
+    hipLaunchKernelGGL(k_conv_splitk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, b, y,
+                       (int)total, make_fastdiv((uint32_t)g.OHW), make_fastdiv((uint32_t)g.M), nsplit, epi);
+    pool_free(part);   // stream-ordered reuse: later work on this stream runs after the reduction
+    return true;
 }
 
 // Returns false (caller falls back) when a tensor is beyond the 2 GB reach of
 // 32-bit buffer offsets.
 bool launch_conv_tiled(const void* x, const void* w, const void* b, int dtb, void* y, int dty, const ConvGeom& cg,
-                       hipStream_t s) {
+                       ConvEpi epi, hipStream_t s) {
     const int64_t xb = (int64_t)cg.N * cg.C * cg.H * cg.W * 4, wb = (int64_t)cg.M * cg.Kg * 4;
     const int64_t P = (int64_t)cg.N * cg.OH * cg.OW;
     const int64_t yb = P * cg.M * 4;
@@ -496,12 +577,26 @@ bool launch_conv_tiled(const void* x, const void* w, const void* b, int dtb, voi
     // 8 or 16 waves (wave tiles 32x64 / 32x32) keep 2-4 waves per SIMD on grids of a few
     // hundred tiles; BK = 8 when K is short (the 7x7x3 stem: less padding, more tiles in flight).
     const uint32_t ux = (uint32_t)xb, uw = (uint32_t)wb, uy = (uint32_t)yb;
+    // Grids of fewer blocks than CUs with a long k range (late, strided layers:
+    // few pixels, many channels) split k into up to 8 slices.
+    const int64_t blocks = ((P + 255) / 256) * ((g.Mg + 63) / 64) * cg.group;
+    const int split = blocks >= 256 ? 1 : (int)std::min<int64_t>(std::min<int64_t>((512 + blocks - 1) / blocks, g.Kg / 128), 8);
+    if (split > 1 && dty == kF32 && (!b || dtb == kF32) && yb * split < ((int64_t)1 << 31)) {
+        if (direct)
+            return launch_conv_split_cfg<64, 256, 16, 2, 4, 1>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
+                                                               split, epi, s);
+        if (g.Kg <= 256)
+            return launch_conv_split_cfg<64, 256, 8, 2, 4, 0>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
+                                                              split, epi, s);
+        return launch_conv_split_cfg<64, 256, 16, 2, 8, 0>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
+                                                           split, epi, s);
+    }
     if (direct)
-        launch_conv_tiled_cfg<64, 256, 16, 2, 4, 1>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, s);
+        launch_conv_tiled_cfg<64, 256, 16, 2, 4, 1>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, s);
     else if (g.Kg <= 256)
-        launch_conv_tiled_cfg<64, 256, 8, 2, 4, 0>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, s);
+        launch_conv_tiled_cfg<64, 256, 8, 2, 4, 0>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, s);
     else
-        launch_conv_tiled_cfg<64, 256, 16, 2, 8, 0>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, s);
+        launch_conv_tiled_cfg<64, 256, 16, 2, 8, 0>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, s);
     return true;
 }
 
@@ -526,11 +621,15 @@ void launch_conv_mfma(const void* x, int dtx, const void* w, int dtw, const void
 
 using namespace tohip;
 
-extern "C" void conv2d_forward(const Tensor* X, const Tensor* W, const Tensor* B, Tensor* Y, ConvParams* params) {
-    const char* name = "conv2d_forward";
-    if (!tensor_sane(X, name) || !tensor_sane(W, name) || !tensor_sane(Y, name)) return;
-    if (!params || !params->pads || !params->strides || !params->dilations) { set_error("%s: NULL params", name); return; }
-    if (X->ndim != 4 || W->ndim != 4 || Y->ndim != 4) { set_error("%s: X, W and Y must be 4-D", name); return; }
+namespace {
+// Shared by conv2d_forward and conv2d_fused_forward.  Returns false when the
+// fused epilogue (skip / relu) could not be applied in the kernel: the caller
+// then applies it with the standalone operators.
+bool conv_entry(const char* name, const Tensor* X, const Tensor* W, const Tensor* B, Tensor* Y, ConvParams* params,
+                const void* skip, int relu) {
+    if (!tensor_sane(X, name) || !tensor_sane(W, name) || !tensor_sane(Y, name)) return true;
+    if (!params || !params->pads || !params->strides || !params->dilations) { set_error("%s: NULL params", name); return true; }
+    if (X->ndim != 4 || W->ndim != 4 || Y->ndim != 4) { set_error("%s: X, W and Y must be 4-D", name); return true; }
     ConvGeom g;
     g.N = X->shape[0]; g.C = X->shape[1]; g.H = X->shape[2]; g.W = X->shape[3];
     g.M = W->shape[0]; g.KH = W->shape[2]; g.KW = W->shape[3];
@@ -539,21 +638,23 @@ extern "C" void conv2d_forward(const Tensor* X, const Tensor* W, const Tensor* B
     g.sh = params->strides[0]; g.sw = params->strides[1];
     g.dh = params->dilations[0]; g.dw = params->dilations[1];
     g.group = params->group;
-    if (g.group < 1 || g.C % g.group || g.M % g.group) { set_error("%s: bad group %d", name, g.group); return; }
+    if (g.group < 1 || g.C % g.group || g.M % g.group) { set_error("%s: bad group %d", name, g.group); return true; }
     g.Cg = g.C / g.group; g.Mg = g.M / g.group;
-    if (W->shape[1] != g.Cg) { set_error("%s: W.shape[1]=%d but C/group=%d", name, W->shape[1], g.Cg); return; }
-    if (Y->shape[0] != g.N || Y->shape[1] != g.M) { set_error("%s: Y shape does not match N, M", name); return; }
+    if (W->shape[1] != g.Cg) { set_error("%s: W.shape[1]=%d but C/group=%d", name, W->shape[1], g.Cg); return true; }
+    if (Y->shape[0] != g.N || Y->shape[1] != g.M) { set_error("%s: Y shape does not match N, M", name); return true; }
     g.Kg = g.Cg * g.KH * g.KW;
     const bool has_b = B && B->data;
-    if (has_b && (!tensor_sane(B, name) || B->size < (size_t)g.M)) { set_error("%s: bias needs M elements", name); return; }
-    if (!ensure_device()) return;
+    if (has_b && (!tensor_sane(B, name) || B->size < (size_t)g.M)) { set_error("%s: bias needs M elements", name); return true; }
+    if (!ensure_device()) return true;
     const int64_t total = (int64_t)g.N * g.M * g.OH * g.OW;
     Staging st;
     const void* x = st.in(X);
     const void* w = st.in(W);
     const void* b = has_b ? st.in(B) : nullptr;
     void* y = st.out(Y, (size_t)total * dt_bytes((int)Y->dtype));
-    if (!x || !w || !y || (has_b && !b)) { st.finish(); return; }
+    const void* z = skip ? st.in((const Tensor*)skip) : nullptr;
+    if (!x || !w || !y || (has_b && !b) || (skip && !z)) { st.finish(); return true; }
+    bool fused = !skip && !relu;   // epilogue applied in the kernel (or none requested)
     hipStream_t s = stream();
     const int dtx = (int)X->dtype, dtw = (int)W->dtype, dty = (int)Y->dtype, dtb = has_b ? (int)B->dtype : kF32;
     if (total > 0) {
@@ -561,8 +662,10 @@ extern "C" void conv2d_forward(const Tensor* X, const Tensor* W, const Tensor* B
         bool done = false;
         if (!exact_mode() && !big && g.Kg > 0 && f32_exact_dtype(dtx) && f32_exact_dtype(dtw)) {
             if (dtx == kF32 && dtw == kF32) {
-                if (!launch_conv_tiled(x, w, b, dtb, y, dty, g, s))
-                    launch_conv_mfma<kF32, kF32>(x, dtx, w, dtw, b, dtb, y, dty, g, s);
+                const bool epi_ok = dty == kF32 && (!has_b || dtb == kF32);
+                const ConvEpi epi{epi_ok ? (const float*)z : nullptr, epi_ok ? relu : 0};
+                if (launch_conv_tiled(x, w, b, dtb, y, dty, g, epi, s)) fused = fused || epi_ok;
+                else launch_conv_mfma<kF32, kF32>(x, dtx, w, dtw, b, dtb, y, dty, g, s);
             } else {
                 launch_conv_mfma<-1, -1>(x, dtx, w, dtw, b, dtb, y, dty, g, s);
             }
@@ -571,7 +674,31 @@ extern "C" void conv2d_forward(const Tensor* X, const Tensor* W, const Tensor* B
         if (!done)
             hipLaunchKernelGGL(k_conv_exact, dim3(grid_for((size_t)total, 256)), dim3(256), 0, s, x, dtx, w, dtw, b, dtb,
                                y, dty, g, total);
-        if (!check_launch(name)) { st.finish(); return; }
+        if (!check_launch(name)) { st.finish(); return true; }
     }
     st.finish();
+    return fused || total == 0;
+}
+}  // namespace
+
+extern "C" void conv2d_forward(const Tensor* X, const Tensor* W, const Tensor* B, Tensor* Y, ConvParams* params) {
+    conv_entry("conv2d_forward", X, W, B, Y, params, nullptr, 0);
+}
+
+// Conv -> Relu -> Add(., Skip) in one pass (the QDQ ResNet block's epilogue);
+// see tensor_ops.h.  The kernel epilogue covers f32 X / W / Y with an f32 or no
+// bias and an f32 Skip of Y's size; otherwise the standalone operators run after
+// the convolution, which is also what the fused epilogue equals.
+extern "C" void conv2d_fused_forward(const Tensor* X, const Tensor* W, const Tensor* B, const Tensor* Skip, int relu,
+                                     Tensor* Y, ConvParams* params) {
+    const char* name = "conv2d_fused_forward";
+    const bool has_skip = Skip && Skip->data;
+    if (has_skip && !tensor_sane(Skip, name)) return;
+    if (!Y) { set_error("%s: NULL output", name); return; }
+    const bool skip_in_kernel = has_skip && Skip->dtype == kF32 && Skip->size == Y->size;
+    tensor_ops_hip_clear_error();
+    const bool fused = conv_entry(name, X, W, B, Y, params, skip_in_kernel ? Skip : nullptr, relu ? 1 : 0);
+    if (tensor_ops_hip_last_error()[0]) return;
+    if (!fused && relu) relu_forward(Y, Y);
+    if ((!fused || !skip_in_kernel) && has_skip && !tensor_ops_hip_last_error()[0]) add_forward(Y, Skip, Y);
 }

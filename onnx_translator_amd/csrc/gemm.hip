@@ -719,20 +719,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_f32_nt(GemmArgs g, WoqB
 }
 
 // Sums the split-K slices of element (m, n) in slice order (in double) and
-// applies the Gemm epilogue.  Four consecutive n per thread.
+// applies the Gemm epilogue.  One element per thread, coalesced; M * N < 2^31
+// (the caller's reach check bounds it).
 template <int YDT>
-__global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, const float* __restrict__ part, int nsplit) {
-    const int64_t mn = (int64_t)g.M * g.N;
-    const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-    if (e0 >= mn) return;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const int64_t i = e0 + e;
-        if (i >= mn) break;
-        double acc = 0.0;
-        for (int sp = 0; sp < nsplit; sp++) acc += (double)part[sp * mn + i];
-        epilogue_fast<YDT>(g, (int)(i / g.N), (int)(i % g.N), acc);
-    }
+__global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g, const float* __restrict__ part, int nsplit,
+                                                       FastDiv fd_n) {
+    const int mn = g.M * g.N;
+    const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (i >= mn) return;
+    double acc = 0.0;
+    for (int sp = 0; sp < nsplit; sp++) acc += (double)part[(int64_t)sp * mn + i];
+    const int m = (int)fd_n.div((uint32_t)i);
+    epilogue_fast<YDT>(g, m, i - m * g.N, acc);
 }
 
 // -------------------------------------------------------------------- dispatch ---
@@ -793,7 +791,7 @@ bool launch_f16_nt(const GemmArgs& g, hipStream_t s) {
 // f32 A [M, K] with B [N, K] (f32 codes or int8 / uint8 codes dequantised on
 // the fly): the tiled kernel.  128x256 tiles over 8 waves (64x64 each) when
 // they cover the CUs; otherwise 128x64 tiles with k split into up to 16
-// slices (each at least 512 deep) so that about 512 blocks run, the slices
+// slices (each at least 64 deep) so that about 512 blocks run, the slices
 // summed by k_splitk_reduce.  The plan depends on M, N and K only, so the
 // fused weight-only-quantized Gemm and the unfused DequantizeLinear -> Gemm
 // pair run the same schedule and return the same bits.
@@ -804,7 +802,7 @@ int nt_split_plan(int M, int N, int K, bool& big) {
     big = big_tiles >= 192;
     if (big) return 1;
     const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 63) / 64);
-    int64_t sp = std::min<int64_t>((512 + tiles - 1) / tiles, K / 512);
+    int64_t sp = std::min<int64_t>((512 + tiles - 1) / tiles, K / 64);
     return (int)std::max<int64_t>(1, std::min<int64_t>(sp, 16));
 }
 
@@ -844,10 +842,14 @@ int launch_f32_nt(const GemmArgs& g, const WoqB& q, hipStream_t s) {
     GemmArgs gp = g;
     gp.Y = part;
     launch_nt_kernel<128, 64, 16, 2, 2, BQ, true>(gp, q, kchunk, nsplit, kF32, s);
-    const dim3 rgrid((unsigned)((mn + 1023) / 1024));
-    if (ydt == kF32) hipLaunchKernelGGL((k_splitk_reduce<kF32>), rgrid, dim3(256), 0, s, g, (const float*)part, nsplit);
-    else if (ydt == kF16) hipLaunchKernelGGL((k_splitk_reduce<kF16>), rgrid, dim3(256), 0, s, g, (const float*)part, nsplit);
-    else hipLaunchKernelGGL((k_splitk_reduce<-1>), rgrid, dim3(256), 0, s, g, (const float*)part, nsplit);
+    const dim3 rgrid((unsigned)((mn + 255) / 256));
+    const FastDiv fd_n = make_fastdiv((uint32_t)g.N);
+    if (ydt == kF32)
+        hipLaunchKernelGGL((k_splitk_reduce<kF32>), rgrid, dim3(256), 0, s, g, (const float*)part, nsplit, fd_n);
+    else if (ydt == kF16)
+        hipLaunchKernelGGL((k_splitk_reduce<kF16>), rgrid, dim3(256), 0, s, g, (const float*)part, nsplit, fd_n);
+    else
+        hipLaunchKernelGGL((k_splitk_reduce<-1>), rgrid, dim3(256), 0, s, g, (const float*)part, nsplit, fd_n);
     pool_free(part);   // stream-ordered reuse: later work on this stream runs after the reduction
     return 1;
 }

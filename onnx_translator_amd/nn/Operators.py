@@ -242,6 +242,35 @@ class Conv(Ops):
         return _values(self, Tensor_(N, M, OH, OW, dtype=self.dtype))
 
 
+class FusedConv(Conv):
+    """Conv -> Relu -> Add(., skip) of a residual block in one call to
+    ``conv2d_fused_forward``: y = [skip +] [Relu](Conv(x, w, b)), equal to the
+    three operators (nn/Operators.py:475-548, :32-79, :170-219) bit for bit.
+    ``inputs`` = [x, w, b or "", skip or ""]."""
+
+    def __init__(self, inputs, outputs, pads, strides, dilations, group, dtype, relu, version="17"):
+        super().__init__(inputs, outputs, pads, strides, dilations, group, dtype, version)
+        self.relu = 1 if relu else 0
+        self.lib.conv2d_fused_forward.argtypes = [PT, PT, PT, PT, ctypes.c_int, PT, ctypes.POINTER(CConvParams)]
+        self.lib.conv2d_fused_forward.restype = None
+
+    def forward(self, x: Tensor, w: Tensor, b: Tensor = None, skip: Tensor = None):
+        N, _, H, W = x.size
+        M, _, KH, KW = w.size
+        OH, OW = _pool_out(H, W, self.pads, self.strides, self.dilations, KH, KW)
+        p, keep = self._params()
+        relu = ctypes.c_int(self.relu)
+
+        def arrange(ins, out):
+            return (ins[0], ins[1], ins[2], ins[3], relu, out, ctypes.byref(p))
+        t = self._run("conv2d_fused_forward", [x, w, b, skip], (N, M, OH, OW), self.dtype, arrange=arrange)
+        del keep
+        return _values(self, t)
+
+    def forward_(self, x: Tensor_, w: Tensor_, b: Tensor_ = None, skip: Tensor_ = None):
+        return super().forward_(x, w, b)
+
+
 class MaxPool(Ops):
     """2-D max pooling (nn/Operators.py:550-611 -> tensor_ops.c:1116-1165)."""
 

@@ -18,6 +18,12 @@ gaps and keep the data in HBM:
   consumer is a Gemm's B input by one
   :class:`~onnx_translator_amd.nn.Operators.DequantizeGemm` (the
   weight-only-quantized Gemm reads the codes; bit-identical to the pair);
+* ``fuse()`` also folds a Conv whose output feeds only a Relu, and that
+  Relu's (or the Conv's) output feeds only an Add with an operand of the same
+  shape, into one :class:`~onnx_translator_amd.nn.Operators.FusedConv`
+  (``conv2d_fused_forward``; bit-identical to the sequence), placed where the
+  last folded node was, and evaluates DequantizeLinear nodes whose inputs are
+  all initializers once (their outputs become initializers);
 * a missing QuantizeLinear / DequantizeLinear zero point is a uint8 zero (the
   ONNX default).
 """
@@ -53,9 +59,10 @@ class Graph:
         self.model_name = model_name
         self.initializers: Dict[str, Tensor] = dict(initializers or {})
         self.ops: "OrderedDict[str, object]" = OrderedDict()
-        self._fuse_pending = None      # (elementwise, dequantize_gemm) requested, applied at the first forward
+        self._fuse_pending = None      # passes requested by fuse(), applied at the first forward
         self.device = False
         self.fused_runs: List[List[str]] = []
+        self.folded: List[str] = []
         self.update(ops)
 
     # -- structure ---------------------------------------------------------------
@@ -145,14 +152,15 @@ class Graph:
         return self._run(inputs, "forward_")
 
     # -- fusion --------------------------------------------------------------------
-    def fuse(self, elementwise: bool = True, dequantize_gemm: bool = True) -> "Graph":
-        """Request the fusion passes; they are applied at the first ``forward`` (shapes needed)."""
-        self._fuse_pending = (elementwise, dequantize_gemm)
+    def fuse(self, elementwise: bool = True, dequantize_gemm: bool = True, conv_epilogue: bool = True,
+             fold_constants: bool = True) -> "Graph":
+        """Request the graph passes; they are applied at the first ``forward`` (shapes needed)."""
+        self._fuse_pending = (elementwise, dequantize_gemm, conv_epilogue, fold_constants)
         return self
 
     def fuse_elementwise(self) -> "Graph":
         """Request elementwise fusion only."""
-        return self.fuse(True, False)
+        return self.fuse(True, False, False, False)
 
     def _edge_shapes(self, inputs) -> Dict[str, tuple]:
         shapes: Dict[str, tuple] = {k: (tuple(v.size), v.dtype) for k, v in self.initializers.items()}
@@ -169,13 +177,73 @@ class Graph:
         return shapes
 
     def _fuse(self, inputs):
-        elementwise, dq_gemm = self._fuse_pending
+        elementwise, dq_gemm, conv_epi, fold = self._fuse_pending
         self._fuse_pending = None
         shapes = self._edge_shapes(inputs)
         if dq_gemm:
             self._fuse_dq_gemm(shapes, self._consumers())
+        if fold:
+            self._fold_constants()
+        if conv_epi:
+            self._fuse_conv_epilogue(shapes, self._consumers())
         if elementwise:
             self._fuse_runs(shapes, self._consumers())
+
+    def _fold_constants(self):
+        """DequantizeLinear nodes over initializers only are evaluated once."""
+        out = []
+        for op in self.ops.values():
+            ins = [na for na in op.inputs if na]
+            if type(op) is Op.DequantizeLinear and ins and all(na in self.initializers for na in ins):
+                args = self._inputs_for(op, self.initializers)
+                self.initializers[op.outputs[0]] = op.forward(*args)["tensor"]
+                self.folded.append(op.name)
+                continue
+            out.append(op)
+        self.ops = OrderedDict((o.name, o) for o in out)
+
+    def _fuse_conv_epilogue(self, shapes, consumers):
+        ops = list(self.ops.values())
+        users: Dict[str, list] = {}
+        for op in ops:
+            for na in op.inputs:
+                if na:
+                    users.setdefault(na, []).append(op)
+
+        def only_user(edge):
+            u = users.get(edge, [])
+            return u[0] if len(u) == 1 and consumers.get(edge, 0) == 1 and edge not in self.output_name else None
+
+        def f32(edge):
+            return edge in shapes and shapes[edge][1] == "float32"
+
+        replace, drop = {}, set()
+        for op in ops:
+            if type(op) is not Op.Conv or op.dtype != "float32" or not f32(op.outputs[0]):
+                continue
+            chain, cur, relu, skip = [op], op.outputs[0], False, ""
+            nxt = only_user(cur)
+            if type(nxt) is Op.RELU and f32(nxt.outputs[0]) and nxt.dtype in (None, "float32"):
+                chain.append(nxt)
+                cur, relu = nxt.outputs[0], True
+                nxt = only_user(cur)
+            if (type(nxt) is Op.ADD and nxt.dtype in (None, "float32") and len(nxt.inputs) == 2 and
+                    nxt.inputs.count(cur) == 1):
+                other = nxt.inputs[1 - nxt.inputs.index(cur)]
+                if f32(other) and shapes[other][0] == shapes[cur][0] == shapes[nxt.outputs[0]][0]:
+                    chain.append(nxt)
+                    cur, skip = nxt.outputs[0], other
+            if len(chain) == 1 or any(o.name in drop or o.name in replace for o in chain):
+                continue
+            b = op.inputs[2] if len(op.inputs) > 2 else ""
+            fc = Op.FusedConv([op.inputs[0], op.inputs[1], b, skip], [cur], op.pads, op.strides, op.dilations,
+                              op.group, op.dtype, relu)
+            fc.name = "FusedConv." + "+".join(o.name for o in chain)
+            replace[chain[-1].name] = fc
+            drop.update(o.name for o in chain[:-1])
+            self.fused_runs.append([o.name for o in chain])
+        out = [replace.get(o.name, o) for o in ops if o.name not in drop]
+        self.ops = OrderedDict((o.name, o) for o in out)
 
     @staticmethod
     def _dq_axis(dq, shapes):

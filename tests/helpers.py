@@ -181,6 +181,7 @@ class HipLib(O.CpuLib):
         lib.tensor_is_device.restype = ctypes.c_int
         for n in ("quantize_linear_axis_forward", "dequantize_linear_axis_forward"):
             getattr(lib, n).argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int]
+        lib.conv2d_fused_forward.argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int, O.PT, ctypes.POINTER(O.CConvParams)]
         lib.dequantize_gemm_forward.argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int, O.PT, O.PT, ctypes.c_float,
                                                 ctypes.c_float, ctypes.c_int, ctypes.c_int]
 
@@ -223,6 +224,33 @@ class HipLib(O.CpuLib):
             self.lib.tensor_ops_hip_clear_error()
             self.lib.dequantize_gemm_forward(ins[0], ins[1], ins[2], ins[3], int(axis), ins[4], o,
                                              ctypes.c_float(alpha), ctypes.c_float(beta), int(transA), int(transB))
+            err = self.last_error()
+            if err:
+                raise RuntimeError(err)
+            return self.read(o, dty)
+        finally:
+            for t in ins:
+                if t:
+                    self.lib.free_tensor(t)
+            self.lib.free_tensor(o)
+
+    def conv_fused(self, x, w, b, skip, relu, dty, pads, strides, dilations=(1, 1), group=1, skip_dt="float32"):
+        """conv2d_fused_forward on host tensors (f32 x / w / b; skip of skip_dt or None)."""
+        N, C, H, W = x.shape
+        M, _, KH, KW = w.shape
+        OH = (H + pads[0] + pads[2] - dilations[0] * (KH - 1) - 1) // strides[0] + 1
+        OW = (W + pads[1] + pads[3] - dilations[1] * (KW - 1) - 1) // strides[1] + 1
+        p = O.CConvParams()
+        keep = [O._ints(pads), O._ints(strides), O._ints(dilations)]
+        p.pads, p.strides, p.dilations = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep]
+        p.group = int(group)
+        ins = [self.tensor(x, "float32"), self.tensor(w, "float32"),
+               self.tensor(b, "float32") if b is not None else O.PT(),
+               self.tensor(skip, skip_dt) if skip is not None else O.PT()]
+        o = self.empty((N, M, OH, OW), dty)
+        try:
+            self.lib.tensor_ops_hip_clear_error()
+            self.lib.conv2d_fused_forward(ins[0], ins[1], ins[2], ins[3], int(relu), o, ctypes.byref(p))
             err = self.last_error()
             if err:
                 raise RuntimeError(err)

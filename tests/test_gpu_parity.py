@@ -207,6 +207,11 @@ CONV_TILED = [
     ("stem_like", (2, 3, 37, 41), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2], [1, 1], 1, True, "float32"),
     ("f16_out", (2, 5, 13, 11), (7, 5, 3, 2), [1, 0, 2, 1], [2, 1], [1, 2], 1, True, "float16"),
     ("direct_f16_out", (2, 64, 12, 12), (160, 64, 1, 1), [0, 0, 0, 0], [1, 1], [1, 1], 1, False, "float16"),
+    # few pixels, long k: the k range is split over slices reduced in a second pass
+    ("split_3x3_s2", (2, 256, 14, 14), (512, 256, 3, 3), [1, 1, 1, 1], [2, 2], [1, 1], 1, True, "float32"),
+    ("split_direct", (1, 512, 8, 8), (256, 512, 1, 1), [0, 0, 0, 0], [1, 1], [1, 1], 1, True, "float32"),
+    ("split_grouped_nobias", (2, 256, 9, 9), (256, 128, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 2, False, "float32"),
+    ("split_ragged_k", (3, 37, 11, 11), (70, 37, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 1, True, "float32"),
 ]
 
 
@@ -221,6 +226,59 @@ def test_conv_tiled_kernel(hip, oracle_lib, case):
     got = hip.conv(x, O.F32, w, O.F32, b, O.F32, ydt, pads, strides, dil, group)
     ref = oracle_lib.conv(x, O.F32, w, O.F32, b, O.F32, ydt, pads, strides, dil, group)
     assert_close(got, ref, ydt, what=f"conv {tag}")
+
+
+# conv2d_fused_forward = conv2d_forward -> relu_forward -> add_forward(., Skip)
+# bit for bit, through the kernel epilogue (gather, direct 1x1 and split-k
+# paths, with / without bias, Relu only, Skip only) and through the fallbacks
+# (f16 output, broadcast Skip, exact mode); and close to the oracle's sequence.
+CONV_FUSED = [
+    ("gather_relu_skip", (2, 16, 13, 11), (24, 16, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, "full", "float32"),
+    ("direct_relu_skip", (2, 64, 12, 12), (96, 64, 1, 1), [0, 0, 0, 0], [1, 1], 1, True, True, "full", "float32"),
+    ("split_relu_skip", (2, 256, 14, 14), (512, 256, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, "full", "float32"),
+    ("stem_relu_only", (2, 3, 37, 41), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2], 1, True, True, None, "float32"),
+    ("skip_only_nobias", (2, 12, 10, 9), (18, 4, 3, 3), [0, 1, 1, 0], [1, 2], 3, False, False, "full", "float32"),
+    ("tail_rows_m200", (1, 30, 9, 9), (200, 30, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, "full", "float32"),
+    ("f16_out_fallback", (2, 5, 13, 11), (7, 5, 3, 2), [1, 0, 2, 1], [2, 1], 1, True, True, "full", "float16"),
+    ("bcast_skip_fallback", (2, 16, 13, 11), (24, 16, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, "chan", "float32"),
+]
+
+
+@pytest.mark.parametrize("case", CONV_FUSED, ids=[c[0] for c in CONV_FUSED])
+@pytest.mark.parametrize("exact", [False, True], ids=["mfma", "exact"])
+def test_conv_fused_epilogue(hip, oracle_lib, case, exact):
+    from tests.helpers import assert_close
+    tag, xs, ws, pads, strides, group, has_b, relu, skip_kind, ydt = case
+    rng = np.random.default_rng(len(tag) * 17 + xs[1])
+    x = rng.normal(0, 1, xs).astype(np.float32)
+    w = rng.normal(0, np.sqrt(2 / (ws[1] * ws[2] * ws[3])), ws).astype(np.float32)
+    b = rng.normal(0, 1, (ws[0],)).astype(np.float32) if has_b else None
+    y0 = oracle_lib.conv(x, O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], group)
+    skip = None
+    if skip_kind == "full":
+        skip = rng.normal(0, 1, y0.shape).astype(np.float32)
+    elif skip_kind == "chan":
+        skip = rng.normal(0, 1, (y0.shape[1], 1, 1)).astype(np.float32)
+    if ydt == "float16" and skip is not None:
+        skip = skip.astype(np.float16).view(np.uint16)
+    sdt = ydt
+    hip.set_exact(exact)
+    try:
+        got = hip.conv_fused(x, w, b, skip, relu, ydt, pads, strides, [1, 1], group, skip_dt=sdt)
+        seq = hip.conv(x, O.F32, w, O.F32, b, O.F32, ydt, pads, strides, [1, 1], group)
+        if relu:
+            seq = hip.unary("relu", seq, ydt, ydt)
+        if skip is not None:
+            seq = hip.binary("add", seq, ydt, skip, sdt, ydt)
+    finally:
+        hip.set_exact(False)
+    assert np.array_equal(got.view(np.uint8), seq.view(np.uint8)), f"{tag}: fused differs from the sequence"
+    ref = oracle_lib.conv(x, O.F32, w, O.F32, b, O.F32, ydt, pads, strides, [1, 1], group)
+    if relu:
+        ref = oracle_lib.unary("relu", ref, ydt, ydt)
+    if skip is not None:
+        ref = oracle_lib.binary("add", ref, ydt, skip, sdt, ydt)
+    assert_close(got, ref, ydt, what=f"conv fused {tag}")
 
 
 def test_device_path_matches_host_path(hip):

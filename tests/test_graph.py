@@ -105,8 +105,39 @@ def test_importer_mapping_and_shapes():
     g = Graph(ops, ["input"], ["output"], initializers=initializers(m))
     out = g.forward_(Tensor_(2, 3, 64, 64, dtype="float32"))
     assert out.size == (2, 1000) and out.dtype == "float32"
-    g.fuse()._fuse([Tensor_(2, 3, 64, 64, dtype="float32")])
+    g.fuse_elementwise()._fuse([Tensor_(2, 3, 64, 64, dtype="float32")])
     assert g.fused_runs == [["RELU.1", "ADD.0"]]
+
+
+def test_conv_epilogue_and_fold_passes(monkeypatch):
+    """Placeholder-shape run of the passes on the config-5 graph: every block's
+    Conv -> Relu -> Add and the stem's Conv -> Relu become FusedConv nodes at the
+    position of the last folded node; the projection convs stay; the weight
+    DequantizeLinear nodes are folded into initializers (evaluated here by the
+    shape pass, as no GPU is present)."""
+    from onnx_translator_amd.nn import Graph, Tensor_
+    from onnx_translator_amd.nn import Operators as Op
+    from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
+    monkeypatch.setattr(Op.DequantizeLinear, "forward", lambda self, *a: self.forward_(*a))
+    m = resnet_qdq_model(batch=1, image=32)
+    g = Graph(ONNXImport(m), ["input"], ["output"], initializers=initializers(m))
+    g.fuse()
+    shapes = g._edge_shapes([Tensor_(1, 3, 32, 32, dtype="float32")])
+    g._fuse_pending = None
+    g._fold_constants()
+    g._fuse_conv_epilogue(shapes, g._consumers())
+    names = [type(o).__name__ for o in g.ops.values()]
+    assert names.count("FusedConv") == 5 and names.count("Conv") == 3 and "RELU" not in names and "ADD" not in names
+    assert len(g.folded) == 7 and names.count("DequantizeLinear") == 4
+    fc = [o for o in g.ops.values() if type(o).__name__ == "FusedConv"]
+    assert fc[0].relu == 1 and fc[0].inputs[3] == "" and fc[0].outputs == ["stem.relu"]
+    assert all(o.relu == 1 and o.inputs[3] for o in fc[1:])
+    assert fc[2].inputs[3] == "block2.proj" and fc[2].outputs == ["block2.out"]
+    # every edge is produced before it is consumed
+    seen = {"input"} | set(g.initializers)
+    for o in g.ops.values():
+        assert all((not na) or na in seen for na in o.inputs), o.name
+        seen.update(o.outputs)
 
 
 def test_toy_graph_oracle_closed_form(oracle_lib):
@@ -181,12 +212,18 @@ def test_resnet_qdq_graph(hip, oracle_lib, exact):
     rng = np.random.default_rng(4)
     x = rng.normal(0, 1, (2, 3, 224, 224)).astype(np.float32)
     g = load_graph(m)
+    plain = load_graph(m, fuse=False)
     hip.set_exact(exact)
     try:
         out = g.forward(x)
         probs = out.numpy()
+        unfused = plain.forward(x).numpy()
     finally:
         hip.set_exact(False)
+    # every pass (conv epilogue, elementwise runs, folded weight dequantisation)
+    # keeps the node-by-node bits
+    assert len(g.fused_runs) == 5 and len(g.folded) == 7
+    assert np.array_equal(probs.view(np.uint32), unfused.view(np.uint32))
     env = run_model(oracle_lib, m, {"input": (x, "float32")})
     ref = env["output"][0]
     assert probs.shape == (2, 1000)
