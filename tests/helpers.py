@@ -121,7 +121,8 @@ def assert_close(out, ref, dt, rtol=1e-5, what=""):
     else:
         tol = rtol * np.abs(r) + rtol * rms
     fin = np.isfinite(r)
-    err = np.abs(g - r)
+    with np.errstate(invalid="ignore"):        # inf - inf where both are infinite
+        err = np.abs(g - r)
     bad = fin & ~(err <= tol)
     bad |= ~fin & ~rn & (g != r)
     if bad.any():

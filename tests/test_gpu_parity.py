@@ -361,3 +361,14 @@ def test_errors_are_reported_not_faulted(hip):
 def test_zero_size_tensors(hip):
     out = hip.binary("add", np.zeros((0, 3), np.float32), O.F32, np.zeros((0, 3), np.float32), O.F32, O.F32)
     assert out.shape == (0, 3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("exact", [False, True], ids=["mfma", "exact"])
+def test_verifier_plans(hip, oracle_lib, exact):
+    """The verifier harness (tests/verify.py) over all 45 reference plans with
+    fresh seeded inputs: every iteration inside its parity class."""
+    from tests.verify import verify
+    failures, stats = verify(hip, oracle_lib, iterations=3, seed=7, exact=exact, log=lambda *a: None)
+    assert not failures, failures[:3]
+    assert sum(len(s["abs"]) for s in stats.values()) == 45 * 3
