@@ -327,12 +327,15 @@ __global__ __launch_bounds__(256) void k_maxpool_3s2(const float* __restrict__ X
     }
 }
 
-// f32, 3x3 window, stride 2, top/left pad 1, W == 2 * OW, OW <= 64: one
-// block per plane, wave w walks a strip of output rows.  Output row oh reads
-// input rows 2oh-1, 2oh, 2oh+1; the last is carried to the next iteration as
-// its first, so every input row is loaded once, as one 8-byte load per lane
-// (columns 2l, 2l+1; column 2l-1 comes from lane l-1).
-__global__ __launch_bounds__(256) void k_maxpool_3s2_strip(const float* __restrict__ X, float* __restrict__ Y,
+constexpr int kPoolStrip = 8;           // output rows per wave of the strip kernel
+constexpr int kPoolStripWaves = 8;      // waves per plane: OH <= 64
+
+// f32, 3x3 window, stride 2, top/left pad 1, W == 2 * OW, OW <= 64, OH <= 64:
+// one block per plane, wave w takes a strip of output rows.  Output row oh reads
+// input rows 2oh-1, 2oh, 2oh+1; consecutive output rows share one, so every
+// input row of the strip is loaded once, as one 8-byte load per lane (columns
+// 2l, 2l+1; column 2l-1 comes from lane l-1).
+__global__ __launch_bounds__(64 * kPoolStripWaves) void k_maxpool_3s2_strip(const float* __restrict__ X, float* __restrict__ Y,
                                                            PoolGeom g, int rows_per_wave) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t plane = blockIdx.x;
@@ -343,7 +346,13 @@ __global__ __launch_bounds__(256) void k_maxpool_3s2_strip(const float* __restri
     const float ninf = -__builtin_inff();
     auto ldrow = [&](int ih) {
         float2 v = make_float2(ninf, ninf);
-        if ((unsigned)ih < (unsigned)g.H && live) v = *reinterpret_cast<const float2*>(xp + (int64_t)ih * g.W + 2 * lane);
+        // each input row is read once: streaming (nontemporal) loads
+        if ((unsigned)ih < (unsigned)g.H && live)
+        {
+            typedef float f32x2 __attribute__((ext_vector_type(2)));
+            const f32x2 t = __builtin_nontemporal_load(reinterpret_cast<const f32x2*>(xp + (int64_t)ih * g.W + 2 * lane));
+            v = make_float2(t.x, t.y);
+        }
         return v;
     };
     // taps of one input row in the reference's kw order: 2l-1, 2l, 2l+1
@@ -357,15 +366,22 @@ __global__ __launch_bounds__(256) void k_maxpool_3s2_strip(const float* __restri
         return best;
     };
     if (oh0 >= oh1) return;
-    float2 prev = ldrow(2 * oh0 - 1);
-    for (int oh = oh0; oh < oh1; oh++) {
-        const float2 r0 = ldrow(2 * oh), r1 = ldrow(2 * oh + 1);
+    // The whole strip (2 * rows + 1 input rows) is loaded up front: a wave
+    // waits for memory once instead of once per output row.
+    float2 rows[2 * kPoolStrip + 1];
+    const int nrows = 2 * (oh1 - oh0) + 1;
+#pragma unroll
+    for (int j = 0; j < 2 * kPoolStrip + 1; j++)
+        rows[j] = j < nrows ? ldrow(2 * oh0 - 1 + j) : make_float2(ninf, ninf);
+#pragma unroll
+    for (int o = 0; o < kPoolStrip; o++) {
+        const int oh = oh0 + o;
+        if (oh >= oh1) break;
         float best = ninf;
-        best = row_max(best, prev, 2 * oh - 1 >= 0);
-        best = row_max(best, r0, 2 * oh < g.H);
-        best = row_max(best, r1, 2 * oh + 1 < g.H);
+        best = row_max(best, rows[2 * o], 2 * oh - 1 >= 0);
+        best = row_max(best, rows[2 * o + 1], 2 * oh < g.H);
+        best = row_max(best, rows[2 * o + 2], 2 * oh + 1 < g.H);
         if (live) yp[(int64_t)oh * g.OW + lane] = best;
-        prev = r1;
     }
 }
 
@@ -566,9 +582,10 @@ void max_pool_forward(const Tensor* X, Tensor* Y, PoolParams* p) {
         const bool res3s2 = f32 && g.KH == 3 && g.KW == 3 && g.sh == 2 && g.sw == 2 && g.dh == 1 && g.dw == 1 &&
                             g.pt == 1 && g.pl == 1 && g.W == 2 * g.OW && g.OW <= 64 && 2 * g.OH <= g.H + 2 &&
                             ((uintptr_t)x & 7) == 0;
-        if (res3s2 && planes <= 0x7FFFFFFF)
-            hipLaunchKernelGGL(k_maxpool_3s2_strip, dim3((unsigned)planes), blk, 0, s, (const float*)x, (float*)y, g,
-                               (g.OH + 3) / 4);
+        const int strip = (g.OH + kPoolStripWaves - 1) / kPoolStripWaves;
+        if (res3s2 && planes <= 0x7FFFFFFF && strip <= kPoolStrip)
+            hipLaunchKernelGGL(k_maxpool_3s2_strip, dim3((unsigned)planes), dim3(64 * kPoolStripWaves), 0, s,
+                               (const float*)x, (float*)y, g, strip);
         else if (res3s2)
             hipLaunchKernelGGL(k_maxpool_3s2, grid, blk, 0, s, (const float*)x, (float*)y, g, planes);
         else if (f32)
