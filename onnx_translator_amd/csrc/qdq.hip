@@ -553,7 +553,8 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const void* __restri
     if constexpr (DIN == kF32) {
         const int64_t nv = n / 4;
         for (int64_t v = (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; v < nv; v += stride) {
-            const float4 x = ld_stream(reinterpret_cast<const float4*>(X) + v);
+            // ordinary loads: the quantize pass reads x again, from the Infinity Cache when it fits
+            const float4 x = reinterpret_cast<const float4*>(X)[v];
             const float e[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
             for (int k = 0; k < 4; k++) {
@@ -599,8 +600,17 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_params(const double* __rest
     st_d_rt(dtz, yz, 0, zpd);       // zpd is an integer in [0, 255]: the code is zpd itself
 }
 
-__device__ __forceinline__ double dql_q(double v, double scale, double zpd) {
-    double q = __builtin_rint(v / scale) + zpd;
+// rint(v / scale) + zp, clamped to [0, 255].  The quotient is formed as
+// p = RN(v * RN(1 / scale)), within 2^-52 |v / scale| of the exact quotient;
+// rint(p) equals rint(v / scale) unless the quotient lies within that distance
+// of a half-integer.  Lanes whose p is within 2^-40 |p| of one (and NaN / inf,
+// whose comparisons fail) take the correctly rounded fp64 division instead, so
+// every code equals the reference's.
+__device__ __forceinline__ double dql_q(double v, double scale, double inv, double zpd) {
+    const double p = v * inv;
+    double r = __builtin_rint(p);
+    if (!(__builtin_fabs(__builtin_fabs(p - r) - 0.5) > 0x1p-40 * __builtin_fabs(p))) r = __builtin_rint(v / scale);
+    double q = r + zpd;
     if (q < 0.0) q = 0.0;
     if (q > 255.0) q = 255.0;
     return q;
@@ -610,21 +620,22 @@ template <int DIN, int DY>
 __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(const void* __restrict__ X, int dtx, int64_t n,
                                                            const double* __restrict__ params, void* __restrict__ Y,
                                                            int dty) {
-    const double scale = params[0], zpd = params[1];
+    const double scale = params[0], zpd = params[1], inv = 1.0 / scale;
     const int64_t stride = (int64_t)gridDim.x * kDqlThreads;
     int64_t tail = 0;
     if constexpr (DIN == kF32 && DY == kU8) {
         const int64_t nv = n / 4;
         for (int64_t v = (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; v < nv; v += stride) {
             const float4 x = ld_stream(reinterpret_cast<const float4*>(X) + v);
-            const uint32_t c = (uint32_t)dql_q(x.x, scale, zpd) | ((uint32_t)dql_q(x.y, scale, zpd) << 8) |
-                               ((uint32_t)dql_q(x.z, scale, zpd) << 16) | ((uint32_t)dql_q(x.w, scale, zpd) << 24);
+            const uint32_t c = (uint32_t)dql_q(x.x, scale, inv, zpd) | ((uint32_t)dql_q(x.y, scale, inv, zpd) << 8) |
+                               ((uint32_t)dql_q(x.z, scale, inv, zpd) << 16) |
+                               ((uint32_t)dql_q(x.w, scale, inv, zpd) << 24);
             st_stream(reinterpret_cast<uint32_t*>(Y) + v, c);
         }
         tail = nv * 4;
     }
     for (int64_t i = tail + (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; i < n; i += stride) {
-        const double q = dql_q(dql_ld<DIN>(X, i, dtx), scale, zpd);
+        const double q = dql_q(dql_ld<DIN>(X, i, dtx), scale, inv, zpd);
         if constexpr (DY >= 0) st_d<DY>(Y, i, q);
         else st_d_rt(dty, Y, i, q);
     }

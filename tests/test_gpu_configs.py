@@ -297,6 +297,23 @@ def test_dequantize_all_codes(hip, oracle_lib, xdt):
 
 
 # ---------------------------------------------------------------- next rows ---
+def test_dql_reciprocal_path_ties(hip, oracle_lib):
+    """The quantize pass multiplies by 1/scale and falls back to the division
+    near half-integers: with scale = 3 (1/3 inexact), inputs 3k + 1.5 are exact
+    ties of x / scale and their float neighbours sit next to them."""
+    k = np.arange(-2, 253, dtype=np.float64)
+    t = (3 * k + 1.5).astype(np.float32)
+    x = np.concatenate([np.array([-6.0, 759.0], np.float32), t, np.nextafter(t, np.float32(np.inf)),
+                        np.nextafter(t, np.float32(-np.inf)), (3 * k).astype(np.float32)])
+    x = np.tile(x, 64)
+    y, s, z = hip.dql(x, O.F32)
+    ry, rs, rz = oracle_lib.dql(x, O.F32)
+    assert float(rs[0]) == 3.0 and int(rz[0]) == 2
+    assert_bitexact(s, rs, O.F32, what="dql scale")
+    assert_bitexact(z, rz, O.U8, what="dql zero point")
+    assert_bitexact(y, ry, O.U8, what="dql codes at ties")
+
+
 def test_dynamic_quantize_linear_full_size(hip, oracle_lib, x2):
     """DynamicQuantizeLinear on the config-2 activation tensor (16.8 M values), bit-exact."""
     y, s, z = hip.dql(x2, O.F32)
