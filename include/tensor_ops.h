@@ -206,6 +206,13 @@ void dequantize_gemm_forward(const Tensor* A, const Tensor* Bq, const Tensor* Sc
  * NULL (no Add) and broadcasts to Y as add_forward's B does. */
 void conv2d_fused_forward(const Tensor* X, const Tensor* W, const Tensor* B, const Tensor* Skip, int relu,
                           Tensor* Y, ConvParams* params);
+/* The QDQ convolution: Y = [Skip +] [Relu](Conv(DequantizeLinear(Xq, XScale, XZero), W, B)), the
+ * dequantize_linear_forward -> conv2d_fused_forward sequence (tensor_ops/tensor_ops.h:155, 161)
+ * in one pass that reads the uint8 / int8 activation codes directly; the same bits as the
+ * sequence.  XScale / XZero hold one element (per-tensor); XZero may be NULL (zero). */
+void dequantize_conv2d_fused_forward(const Tensor* Xq, const Tensor* XScale, const Tensor* XZero,
+                                     const Tensor* W, const Tensor* B, const Tensor* Skip, int relu,
+                                     Tensor* Y, ConvParams* params);
 
 #ifdef __cplusplus
 }

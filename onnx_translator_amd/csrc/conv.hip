@@ -220,16 +220,38 @@ struct ConvEpi {
 };
 __device__ __forceinline__ float relu_f(float v) { return v > 0.0f ? v : 0.0f; }
 
+// Quantized input of dequantize_conv2d_fused_forward: X holds uint8 (XQ = 1) or
+// int8 (XQ = 2) codes with a per-tensor scale and zero point; the gather forms
+// (float)(q - z) * s, which is the value DequantizeLinear writes (q - z has at
+// most 9 bits, so the fp32 product is the correctly rounded exact product, as
+// the reference's double product rounded once).  Padding taps stay 0.
+struct ConvXQ {
+    const float* s;      // scale (one element)
+    const void* z;       // zero point of the codes' dtype (one element), or null for 0
+};
+template <int XQ> __device__ __forceinline__ float xq_value(uint32_t code, float s, int z) {
+    const int c = XQ == 2 ? (int)(int8_t)(uint8_t)code : (int)(code & 0xFFu);
+    return (float)(c - z) * s;
+}
+
 // SPLIT: blockIdx.z = slice * groups + group; slice s covers k in
 // [s * kchunk, (s + 1) * kchunk) (kchunk a multiple of BK) and stores its raw
 // fp32 sums, without bias, to Y + s * N * M * OH * OW (Y is then the f32
 // workspace); k_conv_splitk_reduce adds the slices in order with the bias.
-template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int YDT, bool SPLIT = false>
+// XQ: 0 f32 input; 1 / 2 uint8 / int8 codes dequantised in the gather (ConvXQ).
+template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int YDT, bool SPLIT = false, int XQ = 0>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __restrict__ X, const float* __restrict__ Wt,
                                                                const float* __restrict__ Bv, void* __restrict__ Y,
                                                                int dty, int dtb, ConvTiled g, uint32_t xbytes,
                                                                uint32_t wbytes, uint32_t ybytes, ConvEpi epi,
-                                                               int kchunk = 0, int groups = 1) {
+                                                               ConvXQ xq, int kchunk = 0, int groups = 1) {
+    constexpr uint32_t XES = XQ ? 1u : 4u;        // bytes per input element
+    float xs = 1.0f;
+    int xz = 0;
+    if constexpr (XQ != 0) {
+        xs = xq.s[0];
+        xz = xq.z ? (XQ == 2 ? (int)((const int8_t*)xq.z)[0] : (int)((const uint8_t*)xq.z)[0]) : 0;
+    }
     constexpr int NT = 64 * WGM * WGN;
     constexpr int WTM = BM / WGM, WTP = BP / WGN, TM = WTM / 32, TP = WTP / 32;
     constexpr int EA = BM * BK / NT;              // weights per thread per k-tile (consecutive k)
@@ -286,15 +308,23 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
 #pragma unroll
             for (int e = 0; e < KPT; e++) {
                 const int k = k0 + kg + e;
-                const uint32_t off = (ih0 >= 0 && k < g.Kg) ? (uint32_t)(pix + k * g.HW) * 4u : kOOB;
-                typedef unsigned int u32x4 __attribute__((__vector_size__(16)));
-                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+                const bool ok = ih0 >= 0 && k < g.Kg;
+                const uint32_t off = ok ? (uint32_t)(pix + k * g.HW) * XES : kOOB;
+                if constexpr (XQ) {
+                    // four codes of four consecutive pixels in one word
+                    const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0);
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    // element copied to a scalar first: hipcc 7.2 folds
-                    // __builtin_bit_cast of a vector subscript to element 0
-                    const uint32_t u = v[q];
-                    rb[e * 4 + q] = __builtin_bit_cast(float, u);
+                    for (int q = 0; q < 4; q++) rb[e * 4 + q] = ok ? xq_value<XQ>(w >> (8 * q), xs, xz) : 0.0f;
+                } else {
+                    typedef unsigned int u32x4 __attribute__((__vector_size__(16)));
+                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        // element copied to a scalar first: hipcc 7.2 folds
+                        // __builtin_bit_cast of a vector subscript to element 0
+                        const uint32_t u = v[q];
+                        rb[e * 4 + q] = __builtin_bit_cast(float, u);
+                    }
                 }
             }
         } else {
@@ -308,8 +338,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
                 const int sdh = kh * g.dh, sdw = kw * g.dw;
                 const int koff = c * g.HW + sdh * g.W + sdw;
                 const bool ok = k < g.Kg && (unsigned)(ih0 + sdh) < (unsigned)g.H && (unsigned)(iw0 + sdw) < (unsigned)g.W;
-                const uint32_t off = ok ? (uint32_t)(pix + koff) * 4u : kOOB;
-                rb[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
+                const uint32_t off = ok ? (uint32_t)(pix + koff) * XES : kOOB;
+                if constexpr (XQ) rb[e] = ok ? xq_value<XQ>(__builtin_amdgcn_raw_buffer_load_b8(xr, off, 0, 0), xs, xz) : 0.0f;
+                else rb[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
                 k++;
                 if (++kw == g.KW) { kw = 0; if (++kh == g.KH) { kh = 0; c++; } }
             }
@@ -371,8 +402,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
         const int sdh = q.kh * g.dh, sdw = q.kw * g.dw;
         const int koff = q.c * g.HW + sdh * g.W + sdw;
         const bool ok = q.k < g.Kg && (unsigned)(ih0 + sdh) < (unsigned)g.H && (unsigned)(iw0 + sdw) < (unsigned)g.W;
-        const uint32_t off = ok ? (uint32_t)(pix + koff) * 4u : kOOB;
-        rb[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
+        const uint32_t off = ok ? (uint32_t)(pix + koff) * XES : kOOB;
+        if constexpr (XQ) rb[e] = ok ? xq_value<XQ>(__builtin_amdgcn_raw_buffer_load_b8(xr, off, 0, 0), xs, xz) : 0.0f;
+        else rb[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
         q.k++;
         if (++q.kw == g.KW) { q.kw = 0; if (++q.kh == g.KH) { q.kh = 0; q.c++; } }
     };
@@ -504,16 +536,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
     }
 }
 
-template <int BM, int BP, int BK, int WGM, int WGN, int MODE>
+// XQ != 0 (quantized input) runs with an f32 output and an f32 or no bias only.
+template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int XQ = 0>
 void launch_conv_tiled_cfg(const float* x, const float* w, const void* b, int dtb, void* y, int dty, const ConvTiled& g,
-                           int group, uint32_t xbytes, uint32_t wbytes, uint32_t ybytes, ConvEpi epi, hipStream_t s) {
+                           int group, uint32_t xbytes, uint32_t wbytes, uint32_t ybytes, ConvEpi epi, ConvXQ xq,
+                           hipStream_t s) {
     const dim3 grid((g.P + BP - 1) / BP, (g.Mg + BM - 1) / BM, group), block(64 * WGM * WGN);
-    if (dty == kF32 && (!b || dtb == kF32))
-        hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32>), grid, block, 0, s, x, w, (const float*)b,
-                           y, dty, dtb, g, xbytes, wbytes, ybytes, epi, 0, 1);
+    if (XQ || (dty == kF32 && (!b || dtb == kF32)))
+        hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32, false, XQ>), grid, block, 0, s, x, w,
+                           (const float*)b, y, dty, dtb, g, xbytes, wbytes, ybytes, epi, xq, 0, 1);
     else
         hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, -1>), grid, block, 0, s, x, w, (const float*)b, y,
-                           dty, dtb, g, xbytes, wbytes, ybytes, ConvEpi{nullptr, 0}, 0, 1);
+                           dty, dtb, g, xbytes, wbytes, ybytes, ConvEpi{nullptr, 0}, xq, 0, 1);
 }
 
 // Sum of the split-K slices of each output element, in slice order (double),
@@ -536,17 +570,17 @@ __global__ __launch_bounds__(256) void k_conv_splitk_reduce(const float* __restr
     Y[i] = v;
 }
 
-template <int BM, int BP, int BK, int WGM, int WGN, int MODE>
+template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int XQ = 0>
 bool launch_conv_split_cfg(const float* x, const float* w, const float* b, float* y, const ConvTiled& g, int group,
-                           uint32_t xbytes, uint32_t wbytes, int nsplit_req, ConvEpi epi, hipStream_t s) {
+                           uint32_t xbytes, uint32_t wbytes, int nsplit_req, ConvEpi epi, ConvXQ xq, hipStream_t s) {
     const int kchunk = ((g.Kg + nsplit_req - 1) / nsplit_req + BK - 1) / BK * BK;
     const int nsplit = (g.Kg + kchunk - 1) / kchunk;
     const int64_t total = (int64_t)g.P * g.M;
     float* part = (float*)pool_alloc((size_t)nsplit * total * sizeof(float));
     if (!part) return false;
     const dim3 grid((g.P + BP - 1) / BP, (g.Mg + BM - 1) / BM, group * nsplit), block(64 * WGM * WGN);
-    hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32, true>), grid, block, 0, s, x, w, b, part, kF32,
-                       kF32, g, xbytes, wbytes, 0u, ConvEpi{nullptr, 0}, kchunk, group);
+    hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32, true, XQ>), grid, block, 0, s, x, w, b, part,
+                       kF32, kF32, g, xbytes, wbytes, 0u, ConvEpi{nullptr, 0}, xq, kchunk, group);
     hipLaunchKernelGGL(k_conv_splitk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, b, y,
                        (int)total, make_fastdiv((uint32_t)g.OHW), make_fastdiv((uint32_t)g.M), nsplit, epi);
     pool_free(part);   // stream-ordered reuse: later work on this stream runs after the reduction
@@ -555,9 +589,10 @@ bool launch_conv_split_cfg(const float* x, const float* w, const float* b, float
 
 // Returns false (caller falls back) when a tensor is beyond the 2 GB reach of
 // 32-bit buffer offsets.
-bool launch_conv_tiled(const void* x, const void* w, const void* b, int dtb, void* y, int dty, const ConvGeom& cg,
-                       ConvEpi epi, hipStream_t s) {
-    const int64_t xb = (int64_t)cg.N * cg.C * cg.H * cg.W * 4, wb = (int64_t)cg.M * cg.Kg * 4;
+template <int XQ>
+bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, void* y, int dty, const ConvGeom& cg,
+                          ConvEpi epi, ConvXQ xq, hipStream_t s) {
+    const int64_t xb = (int64_t)cg.N * cg.C * cg.H * cg.W * (XQ ? 1 : 4), wb = (int64_t)cg.M * cg.Kg * 4;
     const int64_t P = (int64_t)cg.N * cg.OH * cg.OW;
     const int64_t yb = P * cg.M * 4;
     if (xb >= ((int64_t)1 << 31) || wb >= ((int64_t)1 << 31) || yb >= ((int64_t)1 << 31)) return false;
@@ -570,7 +605,7 @@ bool launch_conv_tiled(const void* x, const void* w, const void* b, int dtb, voi
     g.fd_khw = make_fastdiv((uint32_t)(g.KH * g.KW));
     g.fd_kw = make_fastdiv((uint32_t)g.KW);
     const bool direct = g.KH == 1 && g.KW == 1 && g.sh == 1 && g.sw == 1 && g.pt == 0 && g.pl == 0 &&
-                        g.OH == g.H && g.OW == g.W && g.HW % 4 == 0;
+                        g.OH == g.H && g.OW == g.W && g.HW % 4 == 0 && (((uintptr_t)x) & (XQ ? 3 : 15)) == 0;
     const float* xf = (const float*)x;
     const float* wf = (const float*)w;
     // Block shapes swept on MI355X over the config-4 layers: 64 channels x 256 pixels with
@@ -582,22 +617,28 @@ bool launch_conv_tiled(const void* x, const void* w, const void* b, int dtb, voi
     const int64_t blocks = ((P + 255) / 256) * ((g.Mg + 63) / 64) * cg.group;
     const int split = blocks >= 256 ? 1 : (int)std::min<int64_t>(std::min<int64_t>((512 + blocks - 1) / blocks, g.Kg / 128), 8);
     if (split > 1 && dty == kF32 && (!b || dtb == kF32) && yb * split < ((int64_t)1 << 31)) {
+        // (an XQ launch always has an f32 output and an f32 or no bias)
         if (direct)
-            return launch_conv_split_cfg<64, 256, 16, 2, 4, 1>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
-                                                               split, epi, s);
+            return launch_conv_split_cfg<64, 256, 16, 2, 4, 1, XQ>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
+                                                               split, epi, xq, s);
         if (g.Kg <= 256)
-            return launch_conv_split_cfg<64, 256, 8, 2, 4, 0>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
-                                                              split, epi, s);
-        return launch_conv_split_cfg<64, 256, 16, 2, 8, 0>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
-                                                           split, epi, s);
+            return launch_conv_split_cfg<64, 256, 8, 2, 4, 0, XQ>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
+                                                              split, epi, xq, s);
+        return launch_conv_split_cfg<64, 256, 16, 2, 8, 0, XQ>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
+                                                           split, epi, xq, s);
     }
     if (direct)
-        launch_conv_tiled_cfg<64, 256, 16, 2, 4, 1>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, s);
+        launch_conv_tiled_cfg<64, 256, 16, 2, 4, 1, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else if (g.Kg <= 256)
-        launch_conv_tiled_cfg<64, 256, 8, 2, 4, 0>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, s);
+        launch_conv_tiled_cfg<64, 256, 8, 2, 4, 0, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else
-        launch_conv_tiled_cfg<64, 256, 16, 2, 8, 0>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, s);
+        launch_conv_tiled_cfg<64, 256, 16, 2, 8, 0, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     return true;
+}
+
+bool launch_conv_tiled(const void* x, const void* w, const void* b, int dtb, void* y, int dty, const ConvGeom& cg,
+                       ConvEpi epi, hipStream_t s) {
+    return launch_conv_tiled_xq<0>(x, w, b, dtb, y, dty, cg, epi, ConvXQ{nullptr, nullptr}, s);
 }
 
 inline bool f32_exact_dtype(int dt) {
@@ -625,8 +666,11 @@ namespace {
 // Shared by conv2d_forward and conv2d_fused_forward.  Returns false when the
 // fused epilogue (skip / relu) could not be applied in the kernel: the caller
 // then applies it with the standalone operators.
+// xq_kind 1 / 2: X holds uint8 / int8 codes dequantised in the kernel with the
+// one-element scale xs and zero point xz (xz may be null); the caller has
+// checked that this is the tiled f32 path (f32 W / Y, f32 or no bias).
 bool conv_entry(const char* name, const Tensor* X, const Tensor* W, const Tensor* B, Tensor* Y, ConvParams* params,
-                const void* skip, int relu) {
+                const void* skip, int relu, int xq_kind = 0, const Tensor* xs = nullptr, const Tensor* xz = nullptr) {
     if (!tensor_sane(X, name) || !tensor_sane(W, name) || !tensor_sane(Y, name)) return true;
     if (!params || !params->pads || !params->strides || !params->dilations) { set_error("%s: NULL params", name); return true; }
     if (X->ndim != 4 || W->ndim != 4 || Y->ndim != 4) { set_error("%s: X, W and Y must be 4-D", name); return true; }
@@ -653,14 +697,27 @@ bool conv_entry(const char* name, const Tensor* X, const Tensor* W, const Tensor
     const void* b = has_b ? st.in(B) : nullptr;
     void* y = st.out(Y, (size_t)total * dt_bytes((int)Y->dtype));
     const void* z = skip ? st.in((const Tensor*)skip) : nullptr;
-    if (!x || !w || !y || (has_b && !b) || (skip && !z)) { st.finish(); return true; }
+    const void* xsd = xq_kind ? st.in(xs) : nullptr;
+    const void* xzd = (xq_kind && xz) ? st.in(xz) : nullptr;
+    if (!x || !w || !y || (has_b && !b) || (skip && !z) || (xq_kind && !xsd) || (xq_kind && xz && !xzd)) {
+        st.finish();
+        return true;
+    }
     bool fused = !skip && !relu;   // epilogue applied in the kernel (or none requested)
     hipStream_t s = stream();
     const int dtx = (int)X->dtype, dtw = (int)W->dtype, dty = (int)Y->dtype, dtb = has_b ? (int)B->dtype : kF32;
     if (total > 0) {
         const bool big = (int64_t)g.N * g.OH * g.OW > 0x7FFFFFFF;
         bool done = false;
-        if (!exact_mode() && !big && g.Kg > 0 && f32_exact_dtype(dtx) && f32_exact_dtype(dtw)) {
+        if (xq_kind) {
+            const ConvEpi epi{(const float*)z, relu};
+            const ConvXQ xq{(const float*)xsd, xzd};
+            const bool ok = xq_kind == 1 ? launch_conv_tiled_xq<1>(x, w, b, dtb, y, dty, g, epi, xq, s)
+                                         : launch_conv_tiled_xq<2>(x, w, b, dtb, y, dty, g, epi, xq, s);
+            if (!ok) set_error("%s: operands beyond the quantized-input kernel's reach", name);
+            fused = true;
+            done = true;
+        } else if (!exact_mode() && !big && g.Kg > 0 && f32_exact_dtype(dtx) && f32_exact_dtype(dtw)) {
             if (dtx == kF32 && dtw == kF32) {
                 const bool epi_ok = dty == kF32 && (!has_b || dtb == kF32);
                 const ConvEpi epi{epi_ok ? (const float*)z : nullptr, epi_ok ? relu : 0};
@@ -685,7 +742,7 @@ extern "C" void conv2d_forward(const Tensor* X, const Tensor* W, const Tensor* B
     conv_entry("conv2d_forward", X, W, B, Y, params, nullptr, 0);
 }
 
-// Conv -> Relu -> Add(., Skip) in one pass (the QDQ ResNet block's epilogue);
+// Conv -> Relu -> Add(., Skip) in one pass (the ResNet block's epilogue);
 // see tensor_ops.h.  The kernel epilogue covers f32 X / W / Y with an f32 or no
 // bias and an f32 Skip of Y's size; otherwise the standalone operators run after
 // the convolution, which is also what the fused epilogue equals.
@@ -701,4 +758,56 @@ extern "C" void conv2d_fused_forward(const Tensor* X, const Tensor* W, const Ten
     if (tensor_ops_hip_last_error()[0]) return;
     if (!fused && relu) relu_forward(Y, Y);
     if ((!fused || !skip_in_kernel) && has_skip && !tensor_ops_hip_last_error()[0]) add_forward(Y, Skip, Y);
+}
+
+namespace {
+bool conv_xq_fast(const Tensor* Xq, const Tensor* XScale, const Tensor* XZero, const Tensor* W, const Tensor* B,
+                  const Tensor* Skip, const Tensor* Y) {
+    const int dx = (int)Xq->dtype;
+    if (exact_mode() || (dx != kU8 && dx != kI8) || XScale->dtype != kF32 || XScale->size != 1) return false;
+    if (XZero && XZero->data && ((int)XZero->dtype != dx || XZero->size != 1)) return false;
+    if (W->dtype != kF32 || Y->dtype != kF32 || (B && B->data && B->dtype != kF32)) return false;
+    if (Skip && Skip->data && (Skip->dtype != kF32 || Skip->size != Y->size)) return false;
+    if (Xq->ndim != 4 || W->ndim != 4 || Y->ndim != 4) return false;
+    return (int64_t)Xq->shape[0] * Xq->shape[1] * Xq->shape[2] * Xq->shape[3] < ((int64_t)1 << 31);
+}
+}  // namespace
+
+// DequantizeLinear -> Conv -> Relu -> Add(., Skip): the QDQ convolution of a
+// quantized ResNet block in one pass; see tensor_ops.h.  The kernel covers
+// uint8 / int8 codes with a one-element f32 scale and zero point, f32 weights,
+// output and skip; otherwise the standalone operators run in sequence, which
+// is also what the fused kernel returns.
+extern "C" void dequantize_conv2d_fused_forward(const Tensor* Xq, const Tensor* XScale, const Tensor* XZero,
+                                                const Tensor* W, const Tensor* B, const Tensor* Skip, int relu,
+                                                Tensor* Y, ConvParams* params) {
+    const char* name = "dequantize_conv2d_fused_forward";
+    if (!tensor_sane(Xq, name) || !tensor_sane(XScale, name) || !tensor_sane(W, name) || !tensor_sane(Y, name)) return;
+    const bool has_z = XZero && XZero->data;
+    if (has_z && !tensor_sane(XZero, name)) return;
+    if (!ensure_device()) return;
+    if (conv_xq_fast(Xq, XScale, has_z ? XZero : nullptr, W, B, Skip, Y)) {
+        tensor_ops_hip_clear_error();
+        conv_entry(name, Xq, W, B, Y, params, (Skip && Skip->data) ? Skip : nullptr, relu ? 1 : 0,
+                   Xq->dtype == kU8 ? 1 : 2, XScale, has_z ? XZero : nullptr);
+        return;
+    }
+    // the unfused sequence: DequantizeLinear into an f32 tensor, then the convolution
+    int shp[8];
+    for (int i = 0; i < Xq->ndim && i < 8; i++) shp[i] = Xq->shape[i];
+    Tensor* Xd = create_tensor_device_empty(shp, Xq->ndim, DTYPE_FLOAT32);
+    if (!Xd) return;
+    tensor_ops_hip_clear_error();
+    if (has_z) {
+        dequantize_linear_forward(Xq, XScale, XZero, Xd);
+    } else {
+        int one = 1;
+        Tensor* z0 = create_tensor(&one, 1, DTYPE_UINT8);
+        if (z0) {
+            dequantize_linear_forward(Xq, XScale, z0, Xd);
+            free_tensor(z0);
+        }
+    }
+    if (tensor_ops_hip_last_error()[0] == 0) conv2d_fused_forward(Xd, W, B, Skip, relu, Y, params);
+    free_tensor(Xd);
 }

@@ -143,8 +143,9 @@ def ONNXParasGen(file_path, seed: int = 0) -> Tuple[List[str], List[Tensor]]:
 
 def load_graph(file_path, fuse: bool = True, device: bool = True):
     """A :class:`Graph` over the model's nodes with its initializers fed (on the device
-    when ``device``), with elementwise runs and DequantizeLinear -> Gemm pairs fused
-    when ``fuse``."""
+    when ``device``) and, when ``fuse``, the default graph passes of ``Graph.fuse``
+    (DequantizeLinear -> Gemm, Conv -> Relu -> Add epilogues, weight DequantizeLinear
+    folding, elementwise runs)."""
     from .graph import Graph
     model = _model(file_path)
     inits = initializers(model)

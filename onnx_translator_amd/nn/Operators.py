@@ -271,6 +271,40 @@ class FusedConv(Conv):
         return super().forward_(x, w, b)
 
 
+class DequantizeConv(FusedConv):
+    """DequantizeLinear -> Conv [-> Relu] [-> Add(., skip)] of a QDQ block in one call
+    to ``dequantize_conv2d_fused_forward``: the convolution reads the uint8 / int8
+    activation codes and never materialises the float32 activation; equal to the
+    operator sequence (nn/Operators.py:452-473, :475-548, :32-79, :170-219) bit for
+    bit.  ``inputs`` = [x codes, x scale, x zero point or "", w, b or "", skip or ""];
+    the scale and zero point hold one element."""
+
+    def __init__(self, inputs, outputs, pads, strides, dilations, group, dtype, relu, version="17"):
+        super().__init__(inputs, outputs, pads, strides, dilations, group, dtype, relu, version)
+        self.lib.dequantize_conv2d_fused_forward.argtypes = [PT, PT, PT, PT, PT, PT, ctypes.c_int, PT,
+                                                             ctypes.POINTER(CConvParams)]
+        self.lib.dequantize_conv2d_fused_forward.restype = None
+
+    def forward(self, xq: Tensor, x_scale: Tensor, x_zero_point: Tensor = None, w: Tensor = None, b: Tensor = None,
+                skip: Tensor = None):
+        N, _, H, W = xq.size
+        M, _, KH, KW = w.size
+        OH, OW = _pool_out(H, W, self.pads, self.strides, self.dilations, KH, KW)
+        p, keep = self._params()
+        relu = ctypes.c_int(self.relu)
+
+        def arrange(ins, out):
+            return (ins[0], ins[1], ins[2], ins[3], ins[4], ins[5], relu, out, ctypes.byref(p))
+        t = self._run("dequantize_conv2d_fused_forward", [xq, x_scale, x_zero_point, w, b, skip], (N, M, OH, OW),
+                      self.dtype, arrange=arrange)
+        del keep
+        return _values(self, t)
+
+    def forward_(self, xq: Tensor_, x_scale: Tensor_ = None, x_zero_point: Tensor_ = None, w: Tensor_ = None,
+                 b: Tensor_ = None, skip: Tensor_ = None):
+        return Conv.forward_(self, xq, w, b)
+
+
 class MaxPool(Ops):
     """2-D max pooling (nn/Operators.py:550-611 -> tensor_ops.c:1116-1165)."""
 

@@ -22,8 +22,13 @@ gaps and keep the data in HBM:
   Relu's (or the Conv's) output feeds only an Add with an operand of the same
   shape, into one :class:`~onnx_translator_amd.nn.Operators.FusedConv`
   (``conv2d_fused_forward``; bit-identical to the sequence), placed where the
-  last folded node was, and evaluates DequantizeLinear nodes whose inputs are
-  all initializers once (their outputs become initializers);
+  last folded node was; and evaluates DequantizeLinear nodes whose inputs are
+  all initializers once (their outputs become initializers).  On request
+  (``fuse(dequantize_conv=True)``) it also folds a per-tensor DequantizeLinear
+  of uint8 / int8 codes whose consumers are all convolutions into each of them
+  (:class:`~onnx_translator_amd.nn.Operators.DequantizeConv`, which reads the
+  codes: 4x smaller activations, but on MI355X the byte gather costs more than
+  the separate DequantizeLinear pass it saves, so it is off by default);
 * a missing QuantizeLinear / DequantizeLinear zero point is a uint8 zero (the
   ONNX default).
 """
@@ -153,14 +158,14 @@ class Graph:
 
     # -- fusion --------------------------------------------------------------------
     def fuse(self, elementwise: bool = True, dequantize_gemm: bool = True, conv_epilogue: bool = True,
-             fold_constants: bool = True) -> "Graph":
+             fold_constants: bool = True, dequantize_conv: bool = False) -> "Graph":
         """Request the graph passes; they are applied at the first ``forward`` (shapes needed)."""
-        self._fuse_pending = (elementwise, dequantize_gemm, conv_epilogue, fold_constants)
+        self._fuse_pending = (elementwise, dequantize_gemm, conv_epilogue, fold_constants, dequantize_conv)
         return self
 
     def fuse_elementwise(self) -> "Graph":
         """Request elementwise fusion only."""
-        return self.fuse(True, False, False, False)
+        return self.fuse(True, False, False, False, False)
 
     def _edge_shapes(self, inputs) -> Dict[str, tuple]:
         shapes: Dict[str, tuple] = {k: (tuple(v.size), v.dtype) for k, v in self.initializers.items()}
@@ -177,7 +182,7 @@ class Graph:
         return shapes
 
     def _fuse(self, inputs):
-        elementwise, dq_gemm, conv_epi, fold = self._fuse_pending
+        elementwise, dq_gemm, conv_epi, fold, dq_conv = self._fuse_pending
         self._fuse_pending = None
         shapes = self._edge_shapes(inputs)
         if dq_gemm:
@@ -186,6 +191,8 @@ class Graph:
             self._fold_constants()
         if conv_epi:
             self._fuse_conv_epilogue(shapes, self._consumers())
+        if dq_conv:
+            self._fuse_dq_conv(shapes)
         if elementwise:
             self._fuse_runs(shapes, self._consumers())
 
@@ -292,6 +299,47 @@ class Graph:
                     self.fused_runs.append([dq.name, op.name])
             out.append(fused or op)
         self.ops = OrderedDict((o.name, o) for o in out if o.name not in drop)
+
+    def _fuse_dq_conv(self, shapes):
+        """DequantizeLinear (per-tensor, uint8 / int8 codes) -> every consuming
+        Conv / FusedConv becomes a DequantizeConv; the DequantizeLinear goes."""
+        ops = list(self.ops.values())
+        users: Dict[str, list] = {}
+        for op in ops:
+            for na in op.inputs:
+                if na:
+                    users.setdefault(na, []).append(op)
+
+        def one(edge):
+            return edge and edge in shapes and int(np.prod(shapes[edge][0] or (1,))) == 1
+
+        replace, drop = {}, set()
+        for dq in ops:
+            if type(dq) is not Op.DequantizeLinear or not dq.outputs[0] or dq.outputs[0] in self.output_name:
+                continue
+            xe, out = dq.inputs[0], dq.outputs[0]
+            code_dt = shapes.get(xe, ((), ""))[1]
+            zp = dq.inputs[2] if len(dq.inputs) > 2 else ""
+            if code_dt not in ("uint8", "int8") or not one(dq.inputs[1]) or shapes[dq.inputs[1]][1] != "float32":
+                continue
+            if zp and (not one(zp) or shapes[zp][1] != code_dt):
+                continue
+            cons = users.get(out, [])
+            if not cons or any(type(c) not in (Op.Conv, Op.FusedConv) or c.inputs[0] != out or
+                               out in c.inputs[1:] or c.dtype != "float32" for c in cons):
+                continue
+            for c in cons:
+                b = c.inputs[2] if len(c.inputs) > 2 else ""
+                skip = c.inputs[3] if type(c) is Op.FusedConv else ""
+                relu = c.relu if type(c) is Op.FusedConv else 0
+                dc = Op.DequantizeConv([xe, dq.inputs[1], zp, c.inputs[1], b, skip], list(c.outputs), c.pads,
+                                       c.strides, c.dilations, c.group, c.dtype, relu)
+                dc.name = f"DequantizeConv.{dq.name}+{c.name}"
+                replace[c.name] = dc
+                self.fused_runs.append([dq.name, c.name])
+            drop.add(dq.name)
+        out_ops = [replace.get(o.name, o) for o in ops if o.name not in drop]
+        self.ops = OrderedDict((o.name, o) for o in out_ops)
 
     def _fuse_runs(self, shapes, consumers):
         ops = list(self.ops.values())

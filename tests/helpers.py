@@ -183,6 +183,8 @@ class HipLib(O.CpuLib):
         for n in ("quantize_linear_axis_forward", "dequantize_linear_axis_forward"):
             getattr(lib, n).argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int]
         lib.conv2d_fused_forward.argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int, O.PT, ctypes.POINTER(O.CConvParams)]
+        lib.dequantize_conv2d_fused_forward.argtypes = [O.PT, O.PT, O.PT, O.PT, O.PT, O.PT, ctypes.c_int, O.PT,
+                                                        ctypes.POINTER(O.CConvParams)]
         lib.dequantize_gemm_forward.argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int, O.PT, O.PT, ctypes.c_float,
                                                 ctypes.c_float, ctypes.c_int, ctypes.c_int]
 
@@ -256,6 +258,36 @@ class HipLib(O.CpuLib):
             if err:
                 raise RuntimeError(err)
             return self.read(o, dty)
+        finally:
+            for t in ins:
+                if t:
+                    self.lib.free_tensor(t)
+            self.lib.free_tensor(o)
+
+    def dq_conv_fused(self, xq, xdt, s, z, w, b, skip, relu, pads, strides, dilations=(1, 1), group=1):
+        """dequantize_conv2d_fused_forward on host tensors: codes xq of xdt, scale s (f32) and
+        zero point z (xdt, or None), f32 w / b / skip."""
+        N, C, H, W = xq.shape
+        M, _, KH, KW = w.shape
+        OH = (H + pads[0] + pads[2] - dilations[0] * (KH - 1) - 1) // strides[0] + 1
+        OW = (W + pads[1] + pads[3] - dilations[1] * (KW - 1) - 1) // strides[1] + 1
+        p = O.CConvParams()
+        keep = [O._ints(pads), O._ints(strides), O._ints(dilations)]
+        p.pads, p.strides, p.dilations = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep]
+        p.group = int(group)
+        ins = [self.tensor(xq, xdt), self.tensor(np.atleast_1d(s), "float32"),
+               self.tensor(np.atleast_1d(z), xdt) if z is not None else O.PT(), self.tensor(w, "float32"),
+               self.tensor(b, "float32") if b is not None else O.PT(),
+               self.tensor(skip, "float32") if skip is not None else O.PT()]
+        o = self.empty((N, M, OH, OW), "float32")
+        try:
+            self.lib.tensor_ops_hip_clear_error()
+            self.lib.dequantize_conv2d_fused_forward(ins[0], ins[1], ins[2], ins[3], ins[4], ins[5], int(relu), o,
+                                                     ctypes.byref(p))
+            err = self.last_error()
+            if err:
+                raise RuntimeError(err)
+            return self.read(o, "float32")
         finally:
             for t in ins:
                 if t:

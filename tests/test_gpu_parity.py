@@ -281,6 +281,68 @@ def test_conv_fused_epilogue(hip, oracle_lib, case, exact):
     assert_close(got, ref, ydt, what=f"conv fused {tag}")
 
 
+# dequantize_conv2d_fused_forward = dequantize_linear_forward -> conv2d_fused_forward
+# bit for bit: uint8 / int8 codes read by the gather (zero points that make the
+# padding taps differ from (0 - zp) * s), the direct 1x1 path, the split-k path,
+# stride / groups, no zero point; and the fallbacks (exact mode, a per-channel
+# scale).  Against the oracle: DequantizeLinear then Conv / Relu / Add.
+DQ_CONV = [
+    ("u8_pad_relu_skip", (2, 16, 13, 11), "uint8", 37, (24, 16, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, True),
+    ("i8_pad", (2, 8, 9, 10), "int8", -5, (12, 8, 3, 3), [1, 0, 2, 1], [2, 1], 1, True, False, False),
+    ("u8_direct_1x1", (2, 64, 12, 12), "uint8", 128, (96, 64, 1, 1), [0, 0, 0, 0], [1, 1], 1, True, True, True),
+    ("u8_split", (2, 256, 14, 14), "uint8", 3, (512, 256, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, True),
+    ("u8_groups_nozp", (2, 12, 10, 9), "uint8", None, (18, 4, 3, 3), [0, 1, 1, 0], [1, 2], 3, False, True, False),
+    ("u8_stride2_proj", (2, 32, 14, 14), "uint8", 0, (64, 32, 1, 1), [0, 0, 0, 0], [2, 2], 1, False, False, False),
+]
+
+
+@pytest.mark.parametrize("case", DQ_CONV, ids=[c[0] for c in DQ_CONV])
+@pytest.mark.parametrize("mode", ["mfma", "exact", "per_channel_fallback"])
+def test_dequantize_conv_fused(hip, oracle_lib, case, mode):
+    import ctypes
+    from tests.helpers import assert_close
+    tag, xs, xdt, zp, ws, pads, strides, group, has_b, relu, has_skip = case
+    rng = np.random.default_rng(len(tag) * 29 + xs[1])
+    lo, hi = (0, 256) if xdt == "uint8" else (-128, 128)
+    xq = rng.integers(lo, hi, xs).astype(np.uint8 if xdt == "uint8" else np.int8)
+    sc = np.array([0.037], np.float32)
+    z = None if zp is None else np.array([zp], xq.dtype)
+    w = rng.normal(0, np.sqrt(2 / (ws[1] * ws[2] * ws[3])), ws).astype(np.float32)
+    b = rng.normal(0, 1, (ws[0],)).astype(np.float32) if has_b else None
+    # dequantised input, as DequantizeLinear writes it (the oracle)
+    zz = z if z is not None else np.zeros(1, xq.dtype)
+    if mode == "per_channel_fallback":
+        sc = (0.02 + 0.01 * rng.random(xs[1])).astype(np.float32)
+        zz = np.full(xs[1], zp if zp is not None else 0, xq.dtype)
+        z = zz
+        xd = oracle_lib.qdq("dequantize", xq, xdt, sc.reshape(1, -1, 1, 1), O.F32, zz.reshape(1, -1, 1, 1), xdt, O.F32)
+    else:
+        xd = oracle_lib.qdq("dequantize", xq, xdt, sc, O.F32, zz, xdt, O.F32)
+    y0 = oracle_lib.conv(xd, O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], group)
+    skip = rng.normal(0, 1, y0.shape).astype(np.float32) if has_skip else None
+    hip.set_exact(mode == "exact")
+    try:
+        if mode == "per_channel_fallback":
+            with pytest.raises(RuntimeError):
+                # a 1-D per-channel scale does not broadcast against [N, C, H, W] in
+                # DequantizeLinear (numpy alignment): the sequence reports the error
+                hip.dq_conv_fused(xq, xdt, sc, z, w, b, skip, relu, pads, strides, [1, 1], group)
+            return
+        got = hip.dq_conv_fused(xq, xdt, sc, z, w, b, skip, relu, pads, strides, [1, 1], group)
+        xdh = hip.qdq("dequantize", xq, xdt, sc, O.F32, zz, xdt, O.F32)
+        seq = hip.conv_fused(xdh, w, b, skip, relu, O.F32, pads, strides, [1, 1], group)
+    finally:
+        hip.set_exact(False)
+    assert np.array_equal(xdh, xd), f"{tag}: DequantizeLinear differs from the oracle"
+    assert np.array_equal(got.view(np.uint32), seq.view(np.uint32)), f"{tag}: fused differs from the sequence"
+    ref = y0
+    if relu:
+        ref = oracle_lib.unary("relu", ref, O.F32, O.F32)
+    if skip is not None:
+        ref = oracle_lib.binary("add", ref, O.F32, skip, O.F32, O.F32)
+    assert_close(got, ref, O.F32, what=f"dq conv {tag}")
+
+
 def test_device_path_matches_host_path(hip):
     """Config-1 chain with device-resident tensors (no host round trips between ops)."""
     from onnx_translator_amd.nn import Tensor

@@ -138,6 +138,17 @@ def test_conv_epilogue_and_fold_passes(monkeypatch):
     for o in g.ops.values():
         assert all((not na) or na in seen for na in o.inputs), o.name
         seen.update(o.outputs)
+    g._fuse_dq_conv(shapes)
+    names = [type(o).__name__ for o in g.ops.values()]
+    # each block's activation DequantizeLinear folds into its conv(s): 4 main + 3 projections
+    assert "DequantizeLinear" not in names and names.count("DequantizeConv") == 7
+    assert names.count("FusedConv") == 1 and names.count("Conv") == 0
+    dcs = [o for o in g.ops.values() if type(o).__name__ == "DequantizeConv"]
+    assert dcs[0].inputs[:3] == ["block1.xq", "act.scale", "act.zp"] and dcs[0].relu == 1 and dcs[0].inputs[5]
+    seen = {"input"} | set(g.initializers)
+    for o in g.ops.values():
+        assert all((not na) or na in seen for na in o.inputs), o.name
+        seen.update(o.outputs)
 
 
 def test_toy_graph_oracle_closed_form(oracle_lib):
@@ -220,10 +231,19 @@ def test_resnet_qdq_graph(hip, oracle_lib, exact):
         unfused = plain.forward(x).numpy()
     finally:
         hip.set_exact(False)
-    # every pass (conv epilogue, elementwise runs, folded weight dequantisation)
+    # every pass (conv epilogue, elementwise runs, folded weight dequantisation,
+    # and on request the activation dequantisation folded into the convolutions)
     # keeps the node-by-node bits
     assert len(g.fused_runs) == 5 and len(g.folded) == 7
     assert np.array_equal(probs.view(np.uint32), unfused.view(np.uint32))
+    gq = load_graph(m, fuse=False).fuse(dequantize_conv=True)
+    hip.set_exact(exact)
+    try:
+        with_dq = gq.forward(x).numpy()
+    finally:
+        hip.set_exact(False)
+    assert len(gq.fused_runs) == 12
+    assert np.array_equal(with_dq.view(np.uint32), unfused.view(np.uint32))
     env = run_model(oracle_lib, m, {"input": (x, "float32")})
     ref = env["output"][0]
     assert probs.shape == (2, 1000)
