@@ -17,6 +17,7 @@
 //    fp32 accumulate: tolerance class vs the reference.
 //  * k_conv_exact — fp64, reference summation order, bit-identical.
 #include <algorithm>
+#include <cmath>
 
 #include "runtime.h"
 
@@ -615,6 +616,14 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
     // Grids of fewer blocks than CUs with a long k range (late, strided layers:
     // few pixels, many channels) split k into up to 8 slices.
     const int64_t blocks = ((P + 255) / 256) * ((g.Mg + 63) / 64) * cg.group;
+    // Tiles do equal work, so a grid of t tiles keeps the CUs busy for a share
+    // (t / CUs) / ceil(t / CUs) of the time; 64x128 tiles (8 waves) replace
+    // 64x256 ones (16 waves, same wave tile) when that share improves by > 5%
+    // (config-5 block 1: 784 -> 1568 tiles, 0.77 -> 0.88; measured 0.43 -> 0.49).
+    auto balance = [](int64_t t) {
+        const double r = (double)t / (double)num_cus();
+        return r / std::ceil(r);
+    };
     const int split = blocks >= 256 ? 1 : (int)std::min<int64_t>(std::min<int64_t>((512 + blocks - 1) / blocks, g.Kg / 128), 8);
     if (split > 1 && dty == kF32 && (!b || dtb == kF32) && yb * split < ((int64_t)1 << 31)) {
         // (an XQ launch always has an f32 output and an f32 or no bias)
@@ -631,6 +640,8 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
         launch_conv_tiled_cfg<64, 256, 16, 2, 4, 1, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else if (g.Kg <= 256)
         launch_conv_tiled_cfg<64, 256, 8, 2, 4, 0, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
+    else if (balance(((P + 127) / 128) * ((g.Mg + 63) / 64) * cg.group) > 1.05 * balance(blocks))
+        launch_conv_tiled_cfg<64, 128, 16, 2, 4, 0, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else
         launch_conv_tiled_cfg<64, 256, 16, 2, 8, 0, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     return true;
