@@ -571,6 +571,37 @@ __global__ __launch_bounds__(256) void k_conv_splitk_reduce(const float* __restr
     Y[i] = v;
 }
 
+// Four consecutive outputs per thread with 16-byte loads and stores (total,
+// Y and the skip tensor 16-byte aligned); per element the same slice order,
+// fp64 sum, bias, relu and skip as k_conv_splitk_reduce.
+__global__ __launch_bounds__(256) void k_conv_splitk_reduce4(const float* __restrict__ part, const float* __restrict__ Bv,
+                                                             float* __restrict__ Y, int total, FastDiv fd_ohw,
+                                                             FastDiv fd_m, int nsplit, ConvEpi epi) {
+    const int i = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 4;
+    if (i >= total) return;
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int s = 0; s < nsplit; s++) {
+        const float4 p = *(const float4*)(part + (int64_t)s * total + i);
+        acc[0] += (double)p.x; acc[1] += (double)p.y; acc[2] += (double)p.z; acc[3] += (double)p.w;
+    }
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        double a = acc[j];
+        if (Bv) {
+            const uint32_t r = fd_ohw.div((uint32_t)(i + j));
+            a += (double)Bv[r - fd_m.div(r) * fd_m.d];
+        }
+        v[j] = (float)a;
+        if (epi.relu) v[j] = relu_f(v[j]);
+    }
+    if (epi.skip) {
+        const float4 k = *(const float4*)(epi.skip + i);
+        v[0] += k.x; v[1] += k.y; v[2] += k.z; v[3] += k.w;
+    }
+    *(float4*)(Y + i) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
 template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int XQ = 0>
 bool launch_conv_split_cfg(const float* x, const float* w, const float* b, float* y, const ConvTiled& g, int group,
                            uint32_t xbytes, uint32_t wbytes, int nsplit_req, ConvEpi epi, ConvXQ xq, hipStream_t s) {
@@ -582,8 +613,13 @@ bool launch_conv_split_cfg(const float* x, const float* w, const float* b, float
     const dim3 grid((g.P + BP - 1) / BP, (g.Mg + BM - 1) / BM, group * nsplit), block(64 * WGM * WGN);
     hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32, true, XQ>), grid, block, 0, s, x, w, b, part,
                        kF32, kF32, g, xbytes, wbytes, 0u, ConvEpi{nullptr, 0}, xq, kchunk, group);
-    hipLaunchKernelGGL(k_conv_splitk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, b, y,
-                       (int)total, make_fastdiv((uint32_t)g.OHW), make_fastdiv((uint32_t)g.M), nsplit, epi);
+    const bool vec4 = total % 4 == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)epi.skip & 15) == 0;
+    if (vec4)
+        hipLaunchKernelGGL(k_conv_splitk_reduce4, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0, s, part, b,
+                           y, (int)total, make_fastdiv((uint32_t)g.OHW), make_fastdiv((uint32_t)g.M), nsplit, epi);
+    else
+        hipLaunchKernelGGL(k_conv_splitk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, b, y,
+                           (int)total, make_fastdiv((uint32_t)g.OHW), make_fastdiv((uint32_t)g.M), nsplit, epi);
     pool_free(part);   // stream-ordered reuse: later work on this stream runs after the reduction
     return true;
 }
@@ -624,7 +660,21 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
         const double r = (double)t / (double)num_cus();
         return r / std::ceil(r);
     };
-    const int split = blocks >= 256 ? 1 : (int)std::min<int64_t>(std::min<int64_t>((512 + blocks - 1) / blocks, g.Kg / 128), 8);
+    // Split-k slice count: at least one block per CU, each slice >= 128 deep,
+    // at most 8; among those, the count whose block total balances best over
+    // the CUs (fewer slices on near ties: each slice adds a write and a read of
+    // the output).  Config-5 block 4: 104 tiles -> 7 slices (0.95) rather than 5 (0.68).
+    int split = 1;
+    if (blocks < num_cus()) {
+        const int smax = (int)std::min<int64_t>(g.Kg / 128, 8);
+        const int smin = (int)std::max<int64_t>(2, (num_cus() + blocks - 1) / blocks);
+        double best = 0.0;
+        for (int sp = smin; sp <= smax; sp++) {
+            const double bal = balance(blocks * sp);
+            if (bal > best + 0.02) { best = bal; split = sp; }
+        }
+        if (split == 1 && smax >= 2) split = std::min(smax, smin);
+    }
     if (split > 1 && dty == kF32 && (!b || dtb == kF32) && yb * split < ((int64_t)1 << 31)) {
         // (an XQ launch always has an f32 output and an f32 or no bias)
         if (direct)
