@@ -206,7 +206,7 @@ struct ConvTiled {
     int C, H, W, M, KH, KW, OH, OW;
     int pt, pl, sh, sw, dh, dw;
     int Cg, Mg, Kg, HW, OHW, P;
-    FastDiv fd_ohw, fd_ow, fd_khw, fd_kw;
+    FastDiv fd_ohw, fd_ow, fd_khw, fd_kw, fd_cg;
 };
 
 typedef __attribute__((address_space(1))) float gfloat;
@@ -240,7 +240,16 @@ template <int XQ> __device__ __forceinline__ float xq_value(uint32_t code, float
 // fp32 sums, without bias, to Y + s * N * M * OH * OW (Y is then the f32
 // workspace); k_conv_splitk_reduce adds the slices in order with the bias.
 // XQ: 0 f32 input; 1 / 2 uint8 / int8 codes dequantised in the gather (ConvXQ).
-template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int YDT, bool SPLIT = false, int XQ = 0>
+// MODE 0: k = (c, kh, kw) as the weights store it, one gathered element per
+// (pixel, k) with its own padding test.  MODE 1: 1x1 stride-1 layers, four
+// pixels per float4.  MODE 2 (Cg a multiple of BK): k runs in (channel block
+// of BK, kh, kw, channel) order, so a k-tile holds BK channels of one tap; the
+// padding test and the pixel's address are computed once per tile and each channel is one load
+// with a wave-uniform scalar offset (c * H * W).  Its LDS tiles keep k
+// contiguous ([row][k]), and lane half h feeds MFMA step s with k = h*BK/2 + s,
+// so each operand is read as 16-byte vectors covering four steps.  DEPTH 2
+// (MODE 2 only) keeps a second loaded tile in registers.
+template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int YDT, bool SPLIT = false, int XQ = 0, int DEPTH = 1>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __restrict__ X, const float* __restrict__ Wt,
                                                                const float* __restrict__ Bv, void* __restrict__ Y,
                                                                int dty, int dtb, ConvTiled g, uint32_t xbytes,
@@ -258,8 +267,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
     constexpr int EA = BM * BK / NT;              // weights per thread per k-tile (consecutive k)
     constexpr int EB = BK * BP / NT;              // im2col values per thread per k-tile
     static_assert(EA >= 1 && BK % EA == 0 && EB >= 1, "tile / thread mismatch");
-    __shared__ float As[2][BK][BM + 4];
-    __shared__ float Bs[2][BK][BP + 4];
+    constexpr bool TAP = MODE == 2;
+    static_assert(!TAP || BK % 8 == 0, "MODE 2 reads four k per lane half and vector");
+    static_assert(DEPTH == 1 || (TAP && DEPTH == 2), "two register sets are a MODE 2 option");
+    // MODE 0 / 1: [k][row]; MODE 2: [row][k] (rows of BK + 4 floats: 16-byte
+    // reads and writes of consecutive rows fall in distinct bank groups)
+    __shared__ float As[2][TAP ? BM : BK][TAP ? BK + 4 : BM + 4];
+    __shared__ float Bs[2][TAP ? BP : BK][TAP ? BK + 4 : BP + 4];
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
@@ -284,7 +298,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
     static_assert(MODE == 1 || PCOLS % 64 == 0, "a wave must share its k range");
     static_assert(KPT >= 1 && KPT * PPT == EB, "every thread loads at least one k per tile");
     const int pc = (t % PCOLS) * PPT;
-    const int kg = MODE == 0 ? __builtin_amdgcn_readfirstlane((t / PCOLS) * KPT) : (t / PCOLS) * KPT;
+    const int kg = MODE != 1 ? __builtin_amdgcn_readfirstlane((t / PCOLS) * KPT) : (t / PCOLS) * KPT;
     const int p = p0 + pc;
     int ih0 = -(1 << 29), iw0 = 0, pix = 0;
     if (p < g.P) {
@@ -296,20 +310,24 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
         pix = (n * g.C + grp * g.Cg) * g.HW + (MODE == 1 ? r : ih0 * g.W + iw0);
     }
 
+    // Tiles never straddle a slice boundary, so masking against kend stays exact.
+    const int kbeg = SPLIT ? slice * kchunk : 0;
+    const int kend = SPLIT ? min(g.Kg, kbeg + kchunk) : g.Kg;
+    const int nk = (kend - kbeg + BK - 1) / BK;
     float ra[EA];
     float rb[EB];
     auto load_tile = [&](int k0) {
 #pragma unroll
         for (int e = 0; e < EA; e++) {
             const int k = k0 + ak + e;
-            const uint32_t off = (am_ok && k < g.Kg) ? (uint32_t)(wrow * g.Kg + k) * 4u : kOOB;
+            const uint32_t off = (am_ok && k < kend) ? (uint32_t)(wrow * g.Kg + k) * 4u : kOOB;
             ra[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0));
         }
         if constexpr (MODE == 1) {
 #pragma unroll
             for (int e = 0; e < KPT; e++) {
                 const int k = k0 + kg + e;
-                const bool ok = ih0 >= 0 && k < g.Kg;
+                const bool ok = ih0 >= 0 && k < kend;
                 const uint32_t off = ok ? (uint32_t)(pix + k * g.HW) * XES : kOOB;
                 if constexpr (XQ) {
                     // four codes of four consecutive pixels in one word
@@ -338,7 +356,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
             for (int e = 0; e < KPT; e++) {
                 const int sdh = kh * g.dh, sdw = kw * g.dw;
                 const int koff = c * g.HW + sdh * g.W + sdw;
-                const bool ok = k < g.Kg && (unsigned)(ih0 + sdh) < (unsigned)g.H && (unsigned)(iw0 + sdw) < (unsigned)g.W;
+                const bool ok = k < kend && (unsigned)(ih0 + sdh) < (unsigned)g.H && (unsigned)(iw0 + sdw) < (unsigned)g.W;
                 const uint32_t off = ok ? (uint32_t)(pix + koff) * XES : kOOB;
                 if constexpr (XQ) rb[e] = ok ? xq_value<XQ>(__builtin_amdgcn_raw_buffer_load_b8(xr, off, 0, 0), xs, xz) : 0.0f;
                 else rb[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
@@ -399,28 +417,30 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
         q.kw = rem - q.kh * g.KW;
         return q;
     };
-    auto gather_one = [&](Gather& q, int e) {
+    // kend bounds the loads: k at or past the end of this block's k range
+    // reads zero through the out-of-range offset.
+    auto gather_one = [&](Gather& q, float (&dst)[EB], int e) {
         const int sdh = q.kh * g.dh, sdw = q.kw * g.dw;
         const int koff = q.c * g.HW + sdh * g.W + sdw;
-        const bool ok = q.k < g.Kg && (unsigned)(ih0 + sdh) < (unsigned)g.H && (unsigned)(iw0 + sdw) < (unsigned)g.W;
+        const bool ok = q.k < kend && (unsigned)(ih0 + sdh) < (unsigned)g.H && (unsigned)(iw0 + sdw) < (unsigned)g.W;
         const uint32_t off = ok ? (uint32_t)(pix + koff) * XES : kOOB;
-        if constexpr (XQ) rb[e] = ok ? xq_value<XQ>(__builtin_amdgcn_raw_buffer_load_b8(xr, off, 0, 0), xs, xz) : 0.0f;
-        else rb[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
+        if constexpr (XQ) dst[e] = ok ? xq_value<XQ>(__builtin_amdgcn_raw_buffer_load_b8(xr, off, 0, 0), xs, xz) : 0.0f;
+        else dst[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
         q.k++;
         if (++q.kw == g.KW) { q.kw = 0; if (++q.kh == g.KH) { q.kh = 0; q.c++; } }
     };
-    auto load_weights = [&](int k0) {
+    auto load_weights = [&](int k0, float (&dst)[EA]) {
 #pragma unroll
         for (int e = 0; e < EA; e++) {
             const int k = k0 + ak + e;
-            const uint32_t off = (am_ok && k < g.Kg) ? (uint32_t)(wrow * g.Kg + k) * 4u : kOOB;
-            ra[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0));
+            const uint32_t off = (am_ok && k < kend) ? (uint32_t)(wrow * g.Kg + k) * 4u : kOOB;
+            dst[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0));
         }
     };
-    auto compute_and_gather = [&](int buf, int k1) {
+    auto compute_and_gather = [&](int buf, int k1, float (&da)[EA], float (&db)[EB]) {
         constexpr int PER = (KPT + BK / 2 - 1) / (BK / 2);
         Gather q = gather_start(k1);
-        load_weights(k1);
+        load_weights(k1, da);
 #pragma unroll
         for (int ks = 0; ks < BK; ks += 2) {
             float a[TM], b[TP];
@@ -435,28 +455,133 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
 #pragma unroll
             for (int e = (ks / 2) * PER; e < (ks / 2 + 1) * PER; e++)
-                if (e < KPT) gather_one(q, e);
+                if (e < KPT) gather_one(q, db, e);
         }
     };
 
-    // Tiles never straddle a slice boundary, so masking against Kg stays exact.
-    const int kbeg = SPLIT ? slice * kchunk : 0;
-    const int nk = ((SPLIT ? min(g.Kg, kbeg + kchunk) : g.Kg) - kbeg + BK - 1) / BK;
-    load_tile(kbeg);
-    store_tile(0);
-    __syncthreads();
-    int kt = 0;
-    for (; kt + 1 < nk; kt++) {
-        if constexpr (MODE == 0) {
-            compute_and_gather(kt & 1, kbeg + (kt + 1) * BK);
-        } else {
-            load_tile(kbeg + (kt + 1) * BK);
-            compute(kt & 1);
+    // MODE 2 tile k0 / BK = cb * KH*KW + tap: channels [cb*BK, cb*BK + BK) of
+    // tap (kh, kw), so the KH*KW tiles of a channel block run back to back
+    // over the same input rows.  Weights W[m][c][tap], input
+    // X[n][c][ih0 + kh*dh][iw0 + kw*dw].
+    // Lanes of rows past Mg get the out-of-range base; adding a tile offset
+    // (< 2^31) keeps it out of range.
+    const uint32_t wtap = am_ok ? (uint32_t)(wrow * g.Kg + ak * (g.KH * g.KW)) * 4u : kOOB;
+    auto tap_load = [&](int k0, float (&da)[EA], float (&db)[EB]) {
+        k0 = min(k0, kend - 1) / BK * BK;     // DEPTH 2 prefetch past the end: reload the last tile (unused)
+        const int khw = g.KH * g.KW;
+        const int kt0 = k0 / BK;
+        const int cb = (int)g.fd_khw.div((uint32_t)kt0);
+        const int tap = kt0 - cb * khw;
+        const int c0 = cb * BK;
+        const int kh = (int)g.fd_kw.div((uint32_t)tap), kw = tap - kh * g.KW;
+#pragma unroll
+        for (int e = 0; e < EA; e++) {
+            const uint32_t wuni = (uint32_t)((c0 + e) * khw + tap) * 4u;   // wave-uniform
+            da[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, wtap + wuni, 0, 0));
         }
-        store_tile((kt & 1) ^ 1);
+        const int sdh = kh * g.dh, sdw = kw * g.dw;
+        const bool ok = (unsigned)(ih0 + sdh) < (unsigned)g.H && (unsigned)(iw0 + sdw) < (unsigned)g.W;
+        const uint32_t voff = ok ? (uint32_t)(pix + sdh * g.W + sdw) * XES : kOOB;
+#pragma unroll
+        for (int e = 0; e < KPT; e++) {
+            const uint32_t soff = (uint32_t)((c0 + kg + e) * g.HW) * XES;   // wave-uniform
+            if constexpr (XQ)
+                db[e] = ok ? xq_value<XQ>(__builtin_amdgcn_raw_buffer_load_b8(xr, voff, soff, 0), xs, xz) : 0.0f;
+            else
+                db[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, voff, soff, 0));
+        }
+        // keep the loads ahead of the MFMA steps that follow
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto tap_store = [&](int buf, const float (&sa)[EA], const float (&sb)[EB]) {
+#pragma unroll
+        for (int e = 0; e < EA; e++) As[buf][am][ak + e] = sa[e];
+        if constexpr (KPT % 4 == 0) {
+#pragma unroll
+            for (int e = 0; e < KPT; e += 4)
+                *reinterpret_cast<float4*>(&Bs[buf][pc][kg + e]) = make_float4(sb[e], sb[e + 1], sb[e + 2], sb[e + 3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < KPT; e++) Bs[buf][pc][kg + e] = sb[e];
+        }
+    };
+    auto tap_compute = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < BK / 8; j++) {
+            typedef float f32x4 __attribute__((ext_vector_type(4)));
+            f32x4 a4[TM], b4[TP];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                a4[i] = *reinterpret_cast<const f32x4*>(&As[buf][wm * WTM + i * 32 + lr][lk * (BK / 2) + 4 * j]);
+#pragma unroll
+            for (int jj = 0; jj < TP; jj++)
+                b4[jj] = *reinterpret_cast<const f32x4*>(&Bs[buf][wn * WTP + jj * 32 + lr][lk * (BK / 2) + 4 * j]);
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int jj = 0; jj < TP; jj++)
+                        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[i][q], b4[jj][q], acc[i][jj], 0, 0, 0);
+        }
+    };
+
+    int kt = 0;
+    if constexpr (TAP) {
+        // Two tiles per trip with fixed LDS buffers: tile kt (even) sits in
+        // buffer 0 at the top of each trip.  DEPTH 2 keeps tile kt + 1 in a
+        // second register set, loaded one trip earlier.
+        float ra2[EA], rb2[EB];
+        tap_load(kbeg, ra, rb);
+        tap_store(0, ra, rb);
+        if constexpr (DEPTH == 2) tap_load(kbeg + BK, ra2, rb2);
         __syncthreads();
+        for (; kt + 2 < nk; kt += 2) {
+            if constexpr (DEPTH == 2) {
+                tap_load(kbeg + (kt + 2) * BK, ra, rb);
+                tap_compute(0);
+                tap_store(1, ra2, rb2);
+                __syncthreads();
+                tap_load(kbeg + (kt + 3) * BK, ra2, rb2);
+                tap_compute(1);
+                tap_store(0, ra, rb);
+                __syncthreads();
+            } else {
+                tap_load(kbeg + (kt + 1) * BK, ra, rb);
+                tap_compute(0);
+                tap_store(1, ra, rb);
+                __syncthreads();
+                tap_load(kbeg + (kt + 2) * BK, ra, rb);
+                tap_compute(1);
+                tap_store(0, ra, rb);
+                __syncthreads();
+            }
+        }
+        if (kt + 1 < nk) {
+            if constexpr (DEPTH != 2) tap_load(kbeg + (kt + 1) * BK, ra2, rb2);
+            tap_compute(0);
+            tap_store(1, ra2, rb2);
+            __syncthreads();
+            tap_compute(1);
+        } else {
+            tap_compute(0);
+        }
+    } else {
+        load_tile(kbeg);
+        store_tile(0);
+        __syncthreads();
+        for (; kt + 1 < nk; kt++) {
+            if constexpr (MODE == 0) {
+                compute_and_gather(kt & 1, kbeg + (kt + 1) * BK, ra, rb);
+            } else {
+                load_tile(kbeg + (kt + 1) * BK);
+                compute(kt & 1);
+            }
+            store_tile((kt & 1) ^ 1);
+            __syncthreads();
+        }
+        compute(kt & 1);
     }
-    compute(kt & 1);
 
     // Output row m of the 32x32 tile (i, j), register r: m = mw + i*32 + 8*(r/4) + (r%4) + 4*lk,
     // pixel q = qw + j*32 + lr.
@@ -490,24 +615,58 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
 #pragma unroll
             for (int r = 0; r < 16; r++)
                 bv[i][r] = Bv ? ((const gfloat*)Bv)[grp * g.Mg + mw + i * 32 + 8 * (r >> 2) + (r & 3) + 4 * lk] : 0.0f;
+        if constexpr (TAP) {
+            // Pixels past P get the out-of-range offset: their loads read zero
+            // and their stores are dropped.  The skip values of each 32x32
+            // tile are loaded before its first store, so those loads are not
+            // ordered behind the stores (Y and Skip may alias as far as the
+            // compiler knows).
 #pragma unroll
-        for (int j = 0; j < TP; j++) {
-            const int q = p0 + wn * WTP + j * 32 + lr;
-            if (q < g.P) {
+            for (int j = 0; j < TP; j++) {
+                const int q = p0 + wn * WTP + j * 32 + lr;
                 const int qn = (int)g.fd_ohw.div((uint32_t)q), qr = q - qn * g.OHW;
-                const uint32_t vo = (uint32_t)((qn * g.M + grp * g.Mg + mw + 4 * lk) * g.OHW + qr) * 4u;
+                const uint32_t vo =
+                    q < g.P ? (uint32_t)((qn * g.M + grp * g.Mg + mw + 4 * lk) * g.OHW + qr) * 4u : kOOB;
 #pragma unroll
-                for (int i = 0; i < TM; i++)
+                for (int i = 0; i < TM; i++) {
+                    float sk[16];
+                    if (epi.skip) {
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const uint32_t so = (uint32_t)((i * 32 + 8 * (r >> 2) + (r & 3)) * g.OHW) * 4u;
+                            sk[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(zr, vo, so, 0));
+                        }
+                    }
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
                         const uint32_t so = (uint32_t)((i * 32 + 8 * (r >> 2) + (r & 3)) * g.OHW) * 4u;
-                        // + 0.0f without a bias, as the reference adds bias_val = 0.0 (-0 -> +0)
                         float v = acc[i][j][r] + bv[i][r];
                         if (epi.relu) v = relu_f(v);
-                        if (epi.skip)
-                            v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(zr, vo, so, 0));
+                        if (epi.skip) v += sk[r];
                         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, vo, so, 0);
                     }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < TP; j++) {
+                const int q = p0 + wn * WTP + j * 32 + lr;
+                if (q < g.P) {
+                    const int qn = (int)g.fd_ohw.div((uint32_t)q), qr = q - qn * g.OHW;
+                    const uint32_t vo = (uint32_t)((qn * g.M + grp * g.Mg + mw + 4 * lk) * g.OHW + qr) * 4u;
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const uint32_t so = (uint32_t)((i * 32 + 8 * (r >> 2) + (r & 3)) * g.OHW) * 4u;
+                            // + 0.0f without a bias, as the reference adds bias_val = 0.0 (-0 -> +0)
+                            float v = acc[i][j][r] + bv[i][r];
+                            if (epi.relu) v = relu_f(v);
+                            if (epi.skip)
+                                v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(zr, vo, so, 0));
+                            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, vo, so, 0);
+                        }
+                }
             }
         }
         return;
@@ -538,16 +697,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
 }
 
 // XQ != 0 (quantized input) runs with an f32 output and an f32 or no bias only.
-template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int XQ = 0>
+template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int XQ = 0, int DEPTH = 1>
 void launch_conv_tiled_cfg(const float* x, const float* w, const void* b, int dtb, void* y, int dty, const ConvTiled& g,
                            int group, uint32_t xbytes, uint32_t wbytes, uint32_t ybytes, ConvEpi epi, ConvXQ xq,
                            hipStream_t s) {
     const dim3 grid((g.P + BP - 1) / BP, (g.Mg + BM - 1) / BM, group), block(64 * WGM * WGN);
     if (XQ || (dty == kF32 && (!b || dtb == kF32)))
-        hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32, false, XQ>), grid, block, 0, s, x, w,
+        hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32, false, XQ, DEPTH>), grid, block, 0, s, x, w,
                            (const float*)b, y, dty, dtb, g, xbytes, wbytes, ybytes, epi, xq, 0, 1);
     else
-        hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, -1>), grid, block, 0, s, x, w, (const float*)b, y,
+        hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, -1, false, 0, DEPTH>), grid, block, 0, s, x, w,
+                           (const float*)b, y,
                            dty, dtb, g, xbytes, wbytes, ybytes, ConvEpi{nullptr, 0}, xq, 0, 1);
 }
 
@@ -602,7 +762,7 @@ __global__ __launch_bounds__(256) void k_conv_splitk_reduce4(const float* __rest
     *(float4*)(Y + i) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
-template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int XQ = 0>
+template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int XQ = 0, int DEPTH = 1>
 bool launch_conv_split_cfg(const float* x, const float* w, const float* b, float* y, const ConvTiled& g, int group,
                            uint32_t xbytes, uint32_t wbytes, int nsplit_req, ConvEpi epi, ConvXQ xq, hipStream_t s) {
     const int kchunk = ((g.Kg + nsplit_req - 1) / nsplit_req + BK - 1) / BK * BK;
@@ -611,7 +771,7 @@ bool launch_conv_split_cfg(const float* x, const float* w, const float* b, float
     float* part = (float*)pool_alloc((size_t)nsplit * total * sizeof(float));
     if (!part) return false;
     const dim3 grid((g.P + BP - 1) / BP, (g.Mg + BM - 1) / BM, group * nsplit), block(64 * WGM * WGN);
-    hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32, true, XQ>), grid, block, 0, s, x, w, b, part,
+    hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32, true, XQ, DEPTH>), grid, block, 0, s, x, w, b, part,
                        kF32, kF32, g, xbytes, wbytes, 0u, ConvEpi{nullptr, 0}, xq, kchunk, group);
     const bool vec4 = total % 4 == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)epi.skip & 15) == 0;
     if (vec4)
@@ -641,56 +801,80 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
     g.fd_ow = make_fastdiv((uint32_t)g.OW);
     g.fd_khw = make_fastdiv((uint32_t)(g.KH * g.KW));
     g.fd_kw = make_fastdiv((uint32_t)g.KW);
+    g.fd_cg = make_fastdiv((uint32_t)g.Cg);
     const bool direct = g.KH == 1 && g.KW == 1 && g.sh == 1 && g.sw == 1 && g.pt == 0 && g.pl == 0 &&
                         g.OH == g.H && g.OW == g.W && g.HW % 4 == 0 && (((uintptr_t)x) & (XQ ? 3 : 15)) == 0;
     const float* xf = (const float*)x;
     const float* wf = (const float*)w;
-    // Block shapes swept on MI355X over the config-4 layers: 64 channels x 256 pixels with
-    // 8 or 16 waves (wave tiles 32x64 / 32x32) keep 2-4 waves per SIMD on grids of a few
-    // hundred tiles; BK = 8 when K is short (the 7x7x3 stem: less padding, more tiles in flight).
+    // MODE 0 block shapes: 64 channels x 256 pixels with 8 or 16 waves (wave
+    // tiles 32x64 / 32x32); BK = 8 when K is short (the 7x7x3 stem: less
+    // padding, more tiles in flight).
     const uint32_t ux = (uint32_t)xb, uw = (uint32_t)wb, uy = (uint32_t)yb;
-    // Grids of fewer blocks than CUs with a long k range (late, strided layers:
-    // few pixels, many channels) split k into up to 8 slices.
-    const int64_t blocks = ((P + 255) / 256) * ((g.Mg + 63) / 64) * cg.group;
+    // Plan: MODE 1 for 1x1 stride-1 layers; MODE 2 when Cg is a multiple of 16
+    // and a tile's input stays local (1x1 kernels, or >= 128 output pixels per
+    // image, so 256 pixels span at most two images); MODE 0 otherwise (the
+    // 3-channel stem, 7x7 outputs of 3x3 kernels: there 16 channels of one tap
+    // over five images miss L1, while 16 consecutive (c, kh, kw) stay in it).
+    // Swept on MI355X over the config-4 / config-5 layers.  MODE 2 plans use
+    // BK = 16, so Cg % 16 == 0 keeps every k-tile inside one tap.
+    const int khw = g.KH * g.KW;
+    const bool tap = !direct && g.Cg % 16 == 0 && (khw == 1 || g.OHW >= 128);
+    const int bm = tap && khw > 1 && g.Mg >= 128 ? 128 : 64;
+    const int bp = tap && khw == 1 ? 128 : 256;
+    const int64_t blocks = ((P + bp - 1) / bp) * ((g.Mg + bm - 1) / bm) * cg.group;
     // Tiles do equal work, so a grid of t tiles keeps the CUs busy for a share
-    // (t / CUs) / ceil(t / CUs) of the time; 64x128 tiles (8 waves) replace
-    // 64x256 ones (16 waves, same wave tile) when that share improves by > 5%
-    // (config-5 block 1: 784 -> 1568 tiles, 0.77 -> 0.88; measured 0.43 -> 0.49).
+    // (t / CUs) / ceil(t / CUs) of the time (fewer tiles than CUs: t / CUs).
     auto balance = [](int64_t t) {
         const double r = (double)t / (double)num_cus();
         return r / std::ceil(r);
     };
-    // Split-k slice count: at least one block per CU, each slice >= 128 deep,
-    // at most 8; among those, the count whose block total balances best over
+    // Split-k slice count for grids smaller than the CU count: each slice
+    // >= 128 deep, at most 8; the count whose block total balances best over
     // the CUs (fewer slices on near ties: each slice adds a write and a read of
-    // the output).  Config-5 block 4: 104 tiles -> 7 slices (0.95) rather than 5 (0.68).
+    // the output), and only if that beats the unsplit grid by 5%.
+    // Config-5 block 4: 104 tiles -> 7 slices (0.95 of the CUs busy, not 0.41).
     int split = 1;
     if (blocks < num_cus()) {
         const int smax = (int)std::min<int64_t>(g.Kg / 128, 8);
-        const int smin = (int)std::max<int64_t>(2, (num_cus() + blocks - 1) / blocks);
-        double best = 0.0;
-        for (int sp = smin; sp <= smax; sp++) {
+        const double base = balance(blocks);
+        double best = base;
+        for (int sp = 2; sp <= smax; sp++) {
             const double bal = balance(blocks * sp);
-            if (bal > best + 0.02) { best = bal; split = sp; }
+            if (bal > best * 1.02) { best = bal; split = sp; }
         }
-        if (split == 1 && smax >= 2) split = std::min(smax, smin);
+        if (best < base * 1.05) split = 1;
     }
     if (split > 1 && dty == kF32 && (!b || dtb == kF32) && yb * split < ((int64_t)1 << 31)) {
         // (an XQ launch always has an f32 output and an f32 or no bias)
+        const float* bf = (const float*)b;
+        float* yf = (float*)y;
         if (direct)
-            return launch_conv_split_cfg<64, 256, 16, 2, 4, 1, XQ>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
-                                                               split, epi, xq, s);
+            return launch_conv_split_cfg<64, 256, 16, 2, 4, 1, XQ>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi, xq, s);
+        if (tap && khw == 1)
+            return launch_conv_split_cfg<64, 128, 16, 2, 4, 2, XQ, 2>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi, xq,
+                                                                      s);
+        if (tap && bm == 128)
+            return launch_conv_split_cfg<128, 256, 16, 2, 8, 2, XQ, 2>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi,
+                                                                       xq, s);
+        if (tap)
+            return launch_conv_split_cfg<64, 256, 16, 2, 4, 2, XQ>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi, xq, s);
         if (g.Kg <= 256)
-            return launch_conv_split_cfg<64, 256, 8, 2, 4, 0, XQ>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
-                                                              split, epi, xq, s);
-        return launch_conv_split_cfg<64, 256, 16, 2, 8, 0, XQ>(xf, wf, (const float*)b, (float*)y, g, cg.group, ux, uw,
-                                                           split, epi, xq, s);
+            return launch_conv_split_cfg<64, 256, 8, 2, 4, 0, XQ>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi, xq, s);
+        return launch_conv_split_cfg<64, 256, 16, 2, 8, 0, XQ>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi, xq, s);
     }
     if (direct)
         launch_conv_tiled_cfg<64, 256, 16, 2, 4, 1, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
+    else if (tap && khw == 1)
+        launch_conv_tiled_cfg<64, 128, 16, 2, 4, 2, XQ, 2>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
+    else if (tap && bm == 128)
+        launch_conv_tiled_cfg<128, 256, 16, 2, 8, 2, XQ, 2>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
+    else if (tap)
+        launch_conv_tiled_cfg<64, 256, 16, 2, 4, 2, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else if (g.Kg <= 256)
         launch_conv_tiled_cfg<64, 256, 8, 2, 4, 0, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else if (balance(((P + 127) / 128) * ((g.Mg + 63) / 64) * cg.group) > 1.05 * balance(blocks))
+        // 64x128 tiles (8 waves) when they fill the CUs better than 64x256 ones
+        // (config-5-like 56x56 layers of 64 channels: 784 -> 1568 tiles, 0.77 -> 0.88)
         launch_conv_tiled_cfg<64, 128, 16, 2, 4, 0, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else
         launch_conv_tiled_cfg<64, 256, 16, 2, 8, 0, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);

@@ -191,8 +191,9 @@ def test_gemm_f16_tiled_kernel(hip, M, N, K, bias, ydt):
         assert_close(y[rows], ref.astype(np.float32), O.F32, rtol=2e-5, what=f"f16 nt {M}x{N}x{K} {bias}")
 
 
-# f32 x f32 Conv runs the tiled implicit GEMM: MODE 0 (gathered im2col) and
-# MODE 1 (1x1 / stride 1 / no padding with HW % 4 == 0), 64-channel and
+# f32 x f32 Conv runs the tiled implicit GEMM: MODE 0 (gathered im2col),
+# MODE 1 (1x1 / stride 1 / no padding with HW % 4 == 0) and MODE 2 (channel
+# counts a multiple of 16, tap-blocked k order), 64-channel and
 # 128-channel block tiles, groups, dilation, asymmetric padding, ragged channel
 # and pixel counts, no bias, and a narrow output through the generic epilogue.
 CONV_TILED = [
@@ -212,6 +213,15 @@ CONV_TILED = [
     ("split_direct", (1, 512, 8, 8), (256, 512, 1, 1), [0, 0, 0, 0], [1, 1], [1, 1], 1, True, "float32"),
     ("split_grouped_nobias", (2, 256, 9, 9), (256, 128, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 2, False, "float32"),
     ("split_ragged_k", (3, 37, 11, 11), (70, 37, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 1, True, "float32"),
+    # MODE 2 (channels a multiple of 16; (channel block, kh, kw, channel) k order):
+    # 128-row tiles with ragged rows and a split k range, groups with dilation
+    # and asymmetric padding, a strided 1x1 with ragged rows, a narrow output
+    ("tap_m144_split", (2, 32, 16, 16), (144, 32, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 1, True, "float32"),
+    ("tap_groups_dil", (2, 32, 20, 19), (40, 16, 3, 3), [2, 1, 1, 2], [1, 1], [2, 1], 2, True, "float32"),
+    ("tap_1x1_s2_m96", (3, 48, 15, 15), (96, 48, 1, 1), [0, 0, 0, 0], [2, 2], [1, 1], 1, False, "float32"),
+    ("tap_m128_s2", (4, 64, 30, 30), (128, 64, 3, 3), [1, 1, 1, 1], [2, 2], [1, 1], 1, True, "float32"),
+    ("tap_m160_k144", (2, 16, 24, 24), (160, 16, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 1, True, "float32"),
+    ("tap_f16_out", (2, 32, 16, 16), (40, 32, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 1, True, "float16"),
 ]
 
 
@@ -241,6 +251,8 @@ CONV_FUSED = [
     ("tail_rows_m200", (1, 30, 9, 9), (200, 30, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, "full", "float32"),
     ("f16_out_fallback", (2, 5, 13, 11), (7, 5, 3, 2), [1, 0, 2, 1], [2, 1], 1, True, True, "full", "float16"),
     ("bcast_skip_fallback", (2, 16, 13, 11), (24, 16, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, "chan", "float32"),
+    ("tap_split_relu_skip", (2, 32, 16, 16), (144, 32, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, "full", "float32"),
+    ("tap_m128_relu_skip", (4, 64, 30, 30), (128, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, "full", "float32"),
 ]
 
 
@@ -293,6 +305,8 @@ DQ_CONV = [
     ("u8_split", (2, 256, 14, 14), "uint8", 3, (512, 256, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, True),
     ("u8_groups_nozp", (2, 12, 10, 9), "uint8", None, (18, 4, 3, 3), [0, 1, 1, 0], [1, 2], 3, False, True, False),
     ("u8_stride2_proj", (2, 32, 14, 14), "uint8", 0, (64, 32, 1, 1), [0, 0, 0, 0], [2, 2], 1, False, False, False),
+    ("u8_tap_split", (2, 32, 16, 16), "uint8", 7, (144, 32, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, True),
+    ("i8_tap_m128_s2", (4, 64, 30, 30), "int8", -3, (128, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, False),
 ]
 
 
