@@ -191,6 +191,16 @@ void quantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Te
                                   Tensor* Y, int axis);
 void dequantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint,
                                     Tensor* Y, int axis);
+/* Fake quantization: Y = DequantizeLinear(QuantizeLinear(X, QScale, QZeroPoint), DScale,
+ * DZeroPoint), the quantize_linear_forward -> dequantize_linear_forward pair
+ * (tensor_ops/tensor_ops.h:149, 155) with the codes of dtype code_dtype kept in registers
+ * (never written), for the QuantizeLinear -> DequantizeLinear pairs of QDQ graphs whose codes
+ * feed nothing else.  Y (float32, X's shape) equals the pair bit for bit.  The one-pass
+ * kernel takes f32 X, one-element f32 scales and one-element zero points of code_dtype
+ * (uint8 / int8 / e4m3 / e5m2); other operands run the pair through a temporary. */
+void quantize_dequantize_linear_forward(const Tensor* X, const Tensor* QScale, const Tensor* QZeroPoint,
+                                        const Tensor* DScale, const Tensor* DZeroPoint, Tensor* Y,
+                                        int code_dtype);
 /* Weight-only-quantized Gemm: Y = alpha * A' * DQ(Bq)' + beta * C with DQ(Bq) =
  * dequantize_linear_axis_forward(Bq, Scale, ZeroPoint, ., axis), in one pass that reads
  * Bq as int8 / uint8 codes (the f32 weight is never written).  Same arguments and output

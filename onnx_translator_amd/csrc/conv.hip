@@ -6,7 +6,10 @@
 // extent comes from Y's shape; pads[0] / pads[1] are top / left.
 //
 //  * k_conv_tiled — f32 x f32: implicit GEMM with register prefetch, buffer
-//    loads and an LDS double buffer (described at the kernel).
+//    loads and an LDS double buffer; three gathers (MODE 0 per-element
+//    (c, kh, kw), MODE 1 1x1 float4, MODE 2 tap-blocked channels with
+//    b128 LDS reads), split-K for small grids, fused Relu / residual
+//    epilogue (described at the kernel and at launch_conv_tiled_xq).
 //  * k_conv_mfma_f32 — other fp32-exact dtypes (decoded while staging):
 //    implicit GEMM on v_mfma_f32_32x32x2f32.  Per group:
 //    M = out channels, N = batch * OH * OW pixels, K = Cin/g * KH * KW.  The

@@ -350,6 +350,38 @@ __global__ __launch_bounds__(kBlock) void k_dequant_v(const uint8_t* __restrict_
     }
 }
 
+// QuantizeLinear then DequantizeLinear, one scale / zero point each, in one
+// pass (tensor_ops.c:999-1016 then :1018-1034): the codes stay in registers.
+// The quantize step is k_quant_v's (MODE 0) and the dequantize step
+// k_dequant_v's (MODE 0), so Y equals the two operators' result bit for bit.
+// The zero points have the code's dtype (as ONNX requires); two float4 units
+// per thread per iteration.
+template <int CDT>
+__global__ __launch_bounds__(kBlock) void k_qdq_fused(const float* __restrict__ X, const float* __restrict__ SQ,
+                                                      const void* __restrict__ ZQ, const float* __restrict__ SD,
+                                                      const void* __restrict__ ZD, float* __restrict__ Y, uint32_t nv) {
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, nv * 16u);
+    const QParm pu = qparm<CDT>(SQ[0], ld_d<CDT>(ZQ, 0));
+    const double sd = (double)SD[0], zd = ld_d<CDT>(ZD, 0);
+    const Params<CDT, 0> none{};
+    float4* Y4 = reinterpret_cast<float4*>(Y);
+    for (uint32_t v0 = blockIdx.x * (kBlock * 2) + threadIdx.x; v0 < nv; v0 += gridDim.x * (kBlock * 2)) {
+        float4 xv[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) xv[u] = ld_buf_stream(xr, (v0 + u * kBlock) * 16u);   // past nv: zero
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const uint32_t v = v0 + u * kBlock;
+            if (v >= nv) continue;
+            float c[4], y[4];
+            decode4<CDT>(quant_unit<CDT, CDT, 0>(xv[u], none, pu), c);
+#pragma unroll
+            for (int b = 0; b < 4; b++) y[b] = (float)(((double)c[b] - zd) * sd);
+            st_stream(Y4 + v, make_float4(y[0], y[1], y[2], y[3]));
+        }
+    }
+}
+
 // Generic: any dtypes, one element per thread, 64-bit indexing.
 template <bool QUANT>
 __global__ __launch_bounds__(kBlock) void k_qdq_rt(const void* __restrict__ X, int dtx, const void* __restrict__ S,
@@ -679,6 +711,62 @@ void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp) {
     st.finish();
 }
 
+// QuantizeLinear(X, QScale, QZeroPoint) as code_dtype, then DequantizeLinear
+// with DScale / DZeroPoint.  The one-pass kernel covers f32 X and Y of one
+// shape, one-element f32 scales and one-element zero points of the code dtype
+// (uint8 / int8 / e4m3 / e5m2); anything else runs the two operators through
+// a temporary code tensor, which is also what the kernel returns.
+void qdq_fused_entry(const Tensor* X, const Tensor* QS, const Tensor* QZ, const Tensor* DS, const Tensor* DZ, Tensor* Y,
+                     int code_dtype) {
+    const char* name = "quantize_dequantize_linear_forward";
+    if (!tensor_sane(X, name) || !tensor_sane(QS, name) || !tensor_sane(QZ, name) || !tensor_sane(DS, name) ||
+        !tensor_sane(DZ, name) || !tensor_sane(Y, name))
+        return;
+    if (Y->size != X->size) { set_error("%s: Y must have X's size", name); return; }
+    const size_t n = X->size;
+    const bool fast = X->dtype == DTYPE_FLOAT32 && Y->dtype == DTYPE_FLOAT32 && is_code8(code_dtype) &&
+                      QS->dtype == DTYPE_FLOAT32 && DS->dtype == DTYPE_FLOAT32 && QS->size == 1 && DS->size == 1 &&
+                      QZ->size == 1 && DZ->size == 1 && (int)QZ->dtype == code_dtype &&
+                      (int)DZ->dtype == code_dtype && n % 4 == 0 && n < (size_t(1) << 31);
+    if (fast && ensure_device()) {
+        Staging st;
+        const void* x = st.in(X);
+        const void* qs = st.in(QS);
+        const void* qz = st.in(QZ);
+        const void* ds = st.in(DS);
+        const void* dz = st.in(DZ);
+        void* y = st.out(Y, tensor_bytes(Y));
+        if (!x || !qs || !qz || !ds || !dz || !y) { st.finish(); return; }
+        if (((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0) {
+            if (n) {
+                const uint32_t nv = (uint32_t)(n / 4);
+                const dim3 g(grid_for(nv, kBlock * 2)), b(kBlock);
+                hipStream_t sm = stream();
+                const float *xf = (const float*)x, *qsf = (const float*)qs, *dsf = (const float*)ds;
+                float* yf = (float*)y;
+                switch (code_dtype) {
+                case kU8: hipLaunchKernelGGL((k_qdq_fused<kU8>), g, b, 0, sm, xf, qsf, qz, dsf, dz, yf, nv); break;
+                case kI8: hipLaunchKernelGGL((k_qdq_fused<kI8>), g, b, 0, sm, xf, qsf, qz, dsf, dz, yf, nv); break;
+                case kE4M3: hipLaunchKernelGGL((k_qdq_fused<kE4M3>), g, b, 0, sm, xf, qsf, qz, dsf, dz, yf, nv); break;
+                default: hipLaunchKernelGGL((k_qdq_fused<kE5M2>), g, b, 0, sm, xf, qsf, qz, dsf, dz, yf, nv); break;
+                }
+                if (!check_launch(name)) { st.finish(); return; }
+            }
+            st.finish();
+            return;
+        }
+        st.finish();
+    }
+    if (code_dtype < 0 || code_dtype > DTYPE_INT64) { set_error("%s: unknown code dtype %d", name, code_dtype); return; }
+    Tensor* C = (X->data && tensor_is_device(X)) ? create_tensor_device_empty(X->shape, X->ndim, (DataType)code_dtype)
+                                                 : create_tensor(X->shape, X->ndim, (DataType)code_dtype);
+    if (!C) { set_error("%s: no memory for the codes", name); return; }
+    tensor_ops_hip_clear_error();
+    qdq_entry<true>("quantize_linear_forward", X, QS, QZ, C);
+    if (tensor_ops_hip_last_error()[0] == 0) qdq_entry<false>("dequantize_linear_forward", C, DS, DZ, Y);
+    free_tensor(C);
+}
+
 }  // namespace
 }  // namespace tohip
 
@@ -701,5 +789,9 @@ void dynamic_quantize_linear_forward(const Tensor* x, Tensor* y, Tensor* y_scale
 void dequantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint, Tensor* Y,
                                     int axis) {
     qdq_axis_entry<false>("dequantize_linear_axis_forward", X, Scale, ZeroPoint, Y, axis);
+}
+void quantize_dequantize_linear_forward(const Tensor* X, const Tensor* QScale, const Tensor* QZeroPoint,
+                                        const Tensor* DScale, const Tensor* DZeroPoint, Tensor* Y, int code_dtype) {
+    qdq_fused_entry(X, QScale, QZeroPoint, DScale, DZeroPoint, Y, code_dtype);
 }
 }

@@ -20,7 +20,7 @@ import ctypes
 
 import numpy as np
 
-from . import DTYPE_TO_NUMPY, DeviceArray, Ops, Tensor, Tensor_, PT
+from . import DTYPE_MAP, DTYPE_TO_NUMPY, DeviceArray, Ops, Tensor, Tensor_, PT
 
 __all__ = ["CConvParams", "CPoolParams", "CReduceParams", "RELU", "COS", "ABS", "ADD", "SUB", "MUL", "DIV",
            "QuantizeLinear", "DequantizeLinear", "Conv", "MaxPool", "Gemm", "Softmax", "Flatten", "Reshape",
@@ -362,6 +362,32 @@ class Gemm(Ops):
         M = A.size[0] if self.transA == 0 else A.size[1]
         N = B.size[1] if self.transB == 0 else B.size[0]
         return _values(self, Tensor_(M, N, dtype=self.dtype))
+
+
+class QuantizeDequantize(Ops):
+    """DequantizeLinear(QuantizeLinear(x, q_scale, q_zero_point), d_scale,
+    d_zero_point) in one call to ``quantize_dequantize_linear_forward``: the
+    codes (dtype ``code_dtype``) stay in registers and are never written.
+    Output equals the QuantizeLinear -> DequantizeLinear pair
+    (nn/Operators.py:427-473) bit for bit.  ``inputs`` = [x, q_scale,
+    q_zero_point, d_scale, d_zero_point]."""
+
+    def __init__(self, inputs, outputs, code_dtype, dtype="float32", version="17"):
+        super().__init__(inputs, outputs)
+        self.code_dtype = code_dtype
+        self.dtype = dtype
+        self.version = version
+        self.lib.quantize_dequantize_linear_forward.argtypes = [PT] * 6 + [ctypes.c_int]
+        self.lib.quantize_dequantize_linear_forward.restype = None
+
+    def forward(self, x: Tensor, q_scale: Tensor, q_zero_point: Tensor, d_scale: Tensor, d_zero_point: Tensor):
+        code = ctypes.c_int(DTYPE_MAP[self.code_dtype])
+        t = self._run("quantize_dequantize_linear_forward", [x, q_scale, q_zero_point, d_scale, d_zero_point],
+                      tuple(x.size), self.dtype, code)
+        return _values(self, t)
+
+    def forward_(self, x: Tensor_, *params):
+        return _values(self, Tensor_(*x.size, dtype=self.dtype))
 
 
 class DequantizeGemm(Ops):

@@ -158,14 +158,18 @@ class Graph:
 
     # -- fusion --------------------------------------------------------------------
     def fuse(self, elementwise: bool = True, dequantize_gemm: bool = True, conv_epilogue: bool = True,
-             fold_constants: bool = True, dequantize_conv: bool = False) -> "Graph":
-        """Request the graph passes; they are applied at the first ``forward`` (shapes needed)."""
-        self._fuse_pending = (elementwise, dequantize_gemm, conv_epilogue, fold_constants, dequantize_conv)
+             fold_constants: bool = True, dequantize_conv: bool = False,
+             quantize_dequantize: bool = True) -> "Graph":
+        """Request the graph passes; they are applied at the first ``forward`` (shapes needed).
+        ``dequantize_conv`` folds activation DequantizeLinear nodes into their convolutions
+        and so takes precedence over ``quantize_dequantize`` for those pairs."""
+        self._fuse_pending = (elementwise, dequantize_gemm, conv_epilogue, fold_constants, dequantize_conv,
+                              quantize_dequantize)
         return self
 
     def fuse_elementwise(self) -> "Graph":
         """Request elementwise fusion only."""
-        return self.fuse(True, False, False, False, False)
+        return self.fuse(True, False, False, False, False, False)
 
     def _edge_shapes(self, inputs) -> Dict[str, tuple]:
         shapes: Dict[str, tuple] = {k: (tuple(v.size), v.dtype) for k, v in self.initializers.items()}
@@ -182,7 +186,7 @@ class Graph:
         return shapes
 
     def _fuse(self, inputs):
-        elementwise, dq_gemm, conv_epi, fold, dq_conv = self._fuse_pending
+        elementwise, dq_gemm, conv_epi, fold, dq_conv, qdq = self._fuse_pending
         self._fuse_pending = None
         shapes = self._edge_shapes(inputs)
         if dq_gemm:
@@ -193,6 +197,8 @@ class Graph:
             self._fuse_conv_epilogue(shapes, self._consumers())
         if dq_conv:
             self._fuse_dq_conv(shapes)
+        if qdq:
+            self._fuse_qdq(shapes, self._consumers())
         if elementwise:
             self._fuse_runs(shapes, self._consumers())
 
@@ -299,6 +305,44 @@ class Graph:
                     self.fused_runs.append([dq.name, op.name])
             out.append(fused or op)
         self.ops = OrderedDict((o.name, o) for o in out if o.name not in drop)
+
+    def _fuse_qdq(self, shapes, consumers):
+        """QuantizeLinear -> DequantizeLinear with one-element f32 scales and
+        zero points of the code dtype, the codes read by that DequantizeLinear
+        only: one QuantizeDequantize at the DequantizeLinear's place (the codes
+        are never written)."""
+        ops = list(self.ops.values())
+        producer = {o: op for op in ops for o in op.outputs}
+
+        def one(edge, dt):
+            return bool(edge) and edge in shapes and int(np.prod(shapes[edge][0] or (1,))) == 1 and shapes[edge][1] == dt
+
+        replace, drop = {}, set()
+        for dq in ops:
+            if type(dq) is not Op.DequantizeLinear or len(dq.inputs) < 3 or not dq.outputs[0]:
+                continue
+            codes = dq.inputs[0]
+            q = producer.get(codes)
+            if type(q) is not Op.QuantizeLinear or len(q.inputs) < 3 or q.name in drop:
+                continue
+            if consumers.get(codes, 0) != 1 or codes in self.output_name or codes in dq.inputs[1:]:
+                continue
+            cdt = shapes.get(codes, ((), ""))[1]
+            if cdt not in ("uint8", "int8", "float8_e4m3", "float8_e5m2"):
+                continue
+            x, qs, qz = q.inputs[:3]
+            ds, dz = dq.inputs[1:3]
+            if not (one(qs, "float32") and one(qz, cdt) and one(ds, "float32") and one(dz, cdt)):
+                continue
+            if shapes.get(x, ((), ""))[1] != "float32" or shapes[dq.outputs[0]][1] != "float32":
+                continue
+            fused = Op.QuantizeDequantize([x, qs, qz, ds, dz], list(dq.outputs), cdt)
+            fused.name = f"QuantizeDequantize.{q.name}+{dq.name}"
+            replace[dq.name] = fused
+            drop.add(q.name)
+            self.fused_runs.append([q.name, dq.name])
+        out = [replace.get(o.name, o) for o in ops if o.name not in drop]
+        self.ops = OrderedDict((o.name, o) for o in out)
 
     def _fuse_dq_conv(self, shapes):
         """DequantizeLinear (per-tensor, uint8 / int8 codes) -> every consuming

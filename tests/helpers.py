@@ -187,6 +187,7 @@ class HipLib(O.CpuLib):
                                                         ctypes.POINTER(O.CConvParams)]
         lib.dequantize_gemm_forward.argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int, O.PT, O.PT, ctypes.c_float,
                                                 ctypes.c_float, ctypes.c_int, ctypes.c_int]
+        lib.quantize_dequantize_linear_forward.argtypes = [O.PT] * 6 + [ctypes.c_int]
 
     def device_count(self):
         return int(self.lib.tensor_ops_hip_device_count())
@@ -205,6 +206,22 @@ class HipLib(O.CpuLib):
         if err:
             raise RuntimeError(err)
         return out
+
+    def qdq1(self, name, x, dtx, s, z, dtz, dty):
+        """quantize / dequantize_linear_forward with Scale and ZeroPoint passed as
+        given (not broadcast to X's shape: one-element tensors stay per-tensor)."""
+        return self._run(getattr(self.lib, name + "_linear_forward"),
+                         [(np.asarray(x), dtx), (np.atleast_1d(s), O.F32), (np.atleast_1d(z), dtz)],
+                         np.asarray(x).shape, dty)
+
+    def qdq_fused(self, x, qs, qz, ds, dz, code_dt):
+        """quantize_dequantize_linear_forward on host tensors (f32 x and scales,
+        zero points of code_dt)."""
+        x = np.asarray(x)
+        return self._run(self.lib.quantize_dequantize_linear_forward,
+                         [(x, O.F32), (np.atleast_1d(qs), O.F32), (np.atleast_1d(qz), code_dt),
+                          (np.atleast_1d(ds), O.F32), (np.atleast_1d(dz), code_dt)], x.shape, O.F32,
+                         ctypes.c_int(O.NAMES[code_dt] if isinstance(code_dt, str) else int(code_dt)))
 
     def dql(self, x, dtx, zdt="uint8"):
         self.lib.tensor_ops_hip_clear_error()

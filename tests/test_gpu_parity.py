@@ -157,6 +157,47 @@ def test_dequantize_gemm(hip, oracle_lib, case, ydt):
     assert_close(got, ref, ydt, what=f"dequantize_gemm {tag}")
 
 
+# quantize_dequantize_linear_forward = quantize_linear_forward ->
+# dequantize_linear_forward bit for bit: the one-pass kernel (one-element
+# scales, zero points of the code dtype, f32, n % 4 == 0) for every 1-byte code
+# format, with special values (NaN, +-inf, +-0, ties of the rounding, values
+# that saturate) and different quantize / dequantize parameters; the fallback
+# through a temporary (n % 4 != 0, a per-channel scale).  The oracle's pair
+# gives the same bits.
+QDQ_FUSED = [("u8", "uint8", 128, 0.037, 128, 0.037, (64, 64, 4)),
+             ("i8_zp", "int8", -3, 0.02, 5, 0.031, (3, 1000, 4)),
+             ("e4m3", "float8_e4m3", 0, 0.011, 0, 0.011, (4096,)),
+             ("e5m2", "float8_e5m2", 0, 0.5, 0, 0.25, (2, 2048)),
+             ("u8_tail_fallback", "uint8", 7, 0.05, 7, 0.05, (3, 5, 7)),
+             ("i8_per_channel_fallback", "int8", 0, None, 0, 0.02, (2, 6, 8, 8))]
+
+
+@pytest.mark.parametrize("case", QDQ_FUSED, ids=[c[0] for c in QDQ_FUSED])
+def test_quantize_dequantize_fused(hip, oracle_lib, case):
+    tag, cdt, qz, qs, dz, ds, shape = case
+    rng = np.random.default_rng(len(tag) * 7 + len(shape))
+    x = rng.normal(0, 3, shape).astype(np.float32)
+    flat = x.reshape(-1)
+    specials = [np.nan, np.inf, -np.inf, 0.0, -0.0, 1e30, -1e30]
+    flat[:len(specials)] = specials
+    sq = np.float32(qs if qs is not None else 0.03)
+    flat[len(specials):len(specials) + 64] = (np.arange(-32, 32) + 0.5) * sq      # ties of rint
+    npz = np.int8 if cdt == "int8" else np.uint8
+    zq, zd = np.array([qz], npz), np.array([dz], npz)
+    if qs is None:   # per-channel quantize scale [1, C, 1, 1]: the library runs the pair
+        qsv = (0.01 + 0.02 * rng.random(shape[1])).astype(np.float32).reshape(1, -1, 1, 1)
+    else:
+        qsv = np.array([qs], np.float32)
+    dsv = np.array([ds], np.float32)
+    got = hip.qdq_fused(x, qsv, zq, dsv, zd, cdt)
+    codes = hip.qdq1("quantize", x, O.F32, qsv, zq, cdt, cdt)
+    pair = hip.qdq1("dequantize", codes, cdt, dsv, zd, cdt, O.F32)
+    assert np.array_equal(got.view(np.uint32), pair.view(np.uint32)), f"{tag}: fused differs from the pair"
+    ref_codes = oracle_lib.qdq("quantize", x, O.F32, qsv, O.F32, zq, cdt, cdt)
+    ref = oracle_lib.qdq("dequantize", ref_codes, cdt, dsv, O.F32, zd, cdt, O.F32)
+    assert_bitexact(got, ref, O.F32, what=f"qdq fused {tag}")
+
+
 # f16 x f16 with transB = 1 and K % 8 == 0 runs the tiled kernel (buffer loads,
 # K tail masked in registers): 128x128 tiles for small grids, 256x256 tiles when
 # the grid has >= 192 of them.  Ragged M / N and K % 64 != 0 exercise the edges;

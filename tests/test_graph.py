@@ -151,6 +151,35 @@ def test_conv_epilogue_and_fold_passes(monkeypatch):
         seen.update(o.outputs)
 
 
+def test_quantize_dequantize_pass(monkeypatch):
+    """Placeholder-shape run of the passes on the config-5 graph: each block's
+    activation QuantizeLinear -> DequantizeLinear pair (uint8 codes read only by
+    the DequantizeLinear) becomes one QuantizeDequantize at the
+    DequantizeLinear's place; with dequantize_conv the pairs go to the
+    convolutions instead."""
+    from onnx_translator_amd.nn import Graph, Tensor_
+    from onnx_translator_amd.nn import Operators as Op
+    from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
+    monkeypatch.setattr(Op.DequantizeLinear, "forward", lambda self, *a: self.forward_(*a))
+    m = resnet_qdq_model(batch=1, image=32)
+    g = Graph(ONNXImport(m), ["input"], ["output"], initializers=initializers(m))
+    shapes = g._edge_shapes([Tensor_(1, 3, 32, 32, dtype="float32")])
+    g._fold_constants()
+    g._fuse_conv_epilogue(shapes, g._consumers())
+    g._fuse_qdq(shapes, g._consumers())
+    names = [type(o).__name__ for o in g.ops.values()]
+    assert names.count("QuantizeDequantize") == 4
+    assert "QuantizeLinear" not in names and "DequantizeLinear" not in names
+    qd = [o for o in g.ops.values() if type(o).__name__ == "QuantizeDequantize"]
+    assert qd[0].inputs == ["pool", "act.scale", "act.zp", "act.scale", "act.zp"]
+    assert qd[0].outputs == ["block1.xd"] and qd[0].code_dtype == "uint8"
+    seen = {"input"} | set(g.initializers)
+    for o in g.ops.values():
+        assert all((not na) or na in seen for na in o.inputs), o.name
+        seen.update(o.outputs)
+    assert not any("block1.xq" in o.inputs or "block1.xq" in o.outputs for o in g.ops.values())
+
+
 def test_toy_graph_oracle_closed_form(oracle_lib):
     rng = np.random.default_rng(0)
     x = rng.normal(0, 1, (1, 3, 32, 32)).astype(np.float32)
@@ -232,9 +261,11 @@ def test_resnet_qdq_graph(hip, oracle_lib, exact):
     finally:
         hip.set_exact(False)
     # every pass (conv epilogue, elementwise runs, folded weight dequantisation,
-    # and on request the activation dequantisation folded into the convolutions)
-    # keeps the node-by-node bits
-    assert len(g.fused_runs) == 5 and len(g.folded) == 7
+    # the activation QuantizeLinear -> DequantizeLinear pairs in one pass, and on
+    # request the activation dequantisation folded into the convolutions) keeps
+    # the node-by-node bits
+    assert len(g.fused_runs) == 9 and len(g.folded) == 7
+    assert sum(type(o).__name__ == "QuantizeDequantize" for o in g.ops.values()) == 4
     assert np.array_equal(probs.view(np.uint32), unfused.view(np.uint32))
     gq = load_graph(m, fuse=False).fuse(dequantize_conv=True)
     hip.set_exact(exact)
