@@ -813,17 +813,31 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
     // tiles 32x64 / 32x32); BK = 8 when K is short (the 7x7x3 stem: less
     // padding, more tiles in flight).
     const uint32_t ux = (uint32_t)xb, uw = (uint32_t)wb, uy = (uint32_t)yb;
-    // Plan: MODE 1 for 1x1 stride-1 layers; MODE 2 when Cg is a multiple of 16
-    // and a tile's input stays local (1x1 kernels, or >= 128 output pixels per
-    // image, so 256 pixels span at most two images); MODE 0 otherwise (the
-    // 3-channel stem, 7x7 outputs of 3x3 kernels: there 16 channels of one tap
-    // over five images miss L1, while 16 consecutive (c, kh, kw) stay in it).
-    // Swept on MI355X over the config-4 / config-5 layers.  MODE 2 plans use
-    // BK = 16, so Cg % 16 == 0 keeps every k-tile inside one tap.
+    // Plan: MODE 1 for 1x1 stride-1 layers; MODE 2 (BK = 16, so Cg % 16 == 0
+    // keeps every k-tile inside one tap) for
+    //   * 1x1 strided layers: 128x128 tiles (16 waves of 32x32, two register
+    //     sets) when >= 256 output channels still give >= 192 blocks, else 64x128;
+    //   * >= 128 output pixels per image: 128x256 (16 waves of 64x32, two
+    //     register sets) for >= 128 output channels, else 64x256 (8 waves of 32x64);
+    //   * smaller images with >= 128 output channels: 128x256 tiles would span
+    //     five or more images and miss L1 on the tap-blocked order, 128x128
+    //     tiles (16 waves of 32x32, two register sets) keep it (block 4 of
+    //     config 5: 109 -> 92 us at split 5);
+    // MODE 0 otherwise (the 3-channel stem, few output channels on small
+    // images).  Swept on MI355X over the config-4 / config-5 layers.
+    enum { kNone, kT64x128, kT128x128, kT64x256, kT128x256 };
     const int khw = g.KH * g.KW;
-    const bool tap = !direct && g.Cg % 16 == 0 && (khw == 1 || g.OHW >= 128);
-    const int bm = tap && khw > 1 && g.Mg >= 128 ? 128 : 64;
-    const int bp = tap && khw == 1 ? 128 : 256;
+    int plan = kNone;
+    if (!direct && g.Cg % 16 == 0) {
+        if (khw == 1)
+            plan = (g.Mg >= 256 && ((P + 127) / 128) * ((g.Mg + 127) / 128) * cg.group >= 192) ? kT128x128 : kT64x128;
+        else if (g.OHW >= 128)
+            plan = g.Mg >= 128 ? kT128x256 : kT64x256;
+        else if (g.Mg >= 128)
+            plan = kT128x128;
+    }
+    const int bm = (plan == kT128x128 || plan == kT128x256) ? 128 : 64;
+    const int bp = (plan == kT64x128 || plan == kT128x128) ? 128 : 256;
     const int64_t blocks = ((P + bp - 1) / bp) * ((g.Mg + bm - 1) / bm) * cg.group;
     // Tiles do equal work, so a grid of t tiles keeps the CUs busy for a share
     // (t / CUs) / ceil(t / CUs) of the time (fewer tiles than CUs: t / CUs).
@@ -835,7 +849,7 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
     // >= 128 deep, at most 8; the count whose block total balances best over
     // the CUs (fewer slices on near ties: each slice adds a write and a read of
     // the output), and only if that beats the unsplit grid by 5%.
-    // Config-5 block 4: 104 tiles -> 7 slices (0.95 of the CUs busy, not 0.41).
+    // Config-5 block 4: 100 tiles -> 5 slices (0.98 of the CUs busy, not 0.39).
     int split = 1;
     if (blocks < num_cus()) {
         const int smax = (int)std::min<int64_t>(g.Kg / 128, 8);
@@ -853,13 +867,16 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
         float* yf = (float*)y;
         if (direct)
             return launch_conv_split_cfg<64, 256, 16, 2, 4, 1, XQ>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi, xq, s);
-        if (tap && khw == 1)
+        if (plan == kT64x128)
             return launch_conv_split_cfg<64, 128, 16, 2, 4, 2, XQ, 2>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi, xq,
                                                                       s);
-        if (tap && bm == 128)
+        if (plan == kT128x128)
+            return launch_conv_split_cfg<128, 128, 16, 4, 4, 2, XQ, 2>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi,
+                                                                       xq, s);
+        if (plan == kT128x256)
             return launch_conv_split_cfg<128, 256, 16, 2, 8, 2, XQ, 2>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi,
                                                                        xq, s);
-        if (tap)
+        if (plan == kT64x256)
             return launch_conv_split_cfg<64, 256, 16, 2, 4, 2, XQ>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi, xq, s);
         if (g.Kg <= 256)
             return launch_conv_split_cfg<64, 256, 8, 2, 4, 0, XQ>(xf, wf, bf, yf, g, cg.group, ux, uw, split, epi, xq, s);
@@ -867,11 +884,13 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
     }
     if (direct)
         launch_conv_tiled_cfg<64, 256, 16, 2, 4, 1, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
-    else if (tap && khw == 1)
+    else if (plan == kT64x128)
         launch_conv_tiled_cfg<64, 128, 16, 2, 4, 2, XQ, 2>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
-    else if (tap && bm == 128)
+    else if (plan == kT128x128)
+        launch_conv_tiled_cfg<128, 128, 16, 4, 4, 2, XQ, 2>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
+    else if (plan == kT128x256)
         launch_conv_tiled_cfg<128, 256, 16, 2, 8, 2, XQ, 2>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
-    else if (tap)
+    else if (plan == kT64x256)
         launch_conv_tiled_cfg<64, 256, 16, 2, 4, 2, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else if (g.Kg <= 256)
         launch_conv_tiled_cfg<64, 256, 8, 2, 4, 0, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);

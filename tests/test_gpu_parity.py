@@ -263,6 +263,10 @@ CONV_TILED = [
     ("tap_m128_s2", (4, 64, 30, 30), (128, 64, 3, 3), [1, 1, 1, 1], [2, 2], [1, 1], 1, True, "float32"),
     ("tap_m160_k144", (2, 16, 24, 24), (160, 16, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 1, True, "float32"),
     ("tap_f16_out", (2, 32, 16, 16), (40, 32, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 1, True, "float16"),
+    # 128x128 MODE 2 tiles: small images with >= 128 output channels (split k),
+    # and a strided 1x1 with 256 output channels over >= 192 tiles
+    ("tap_small_img_m192_split", (2, 64, 14, 14), (192, 64, 3, 3), [1, 1, 1, 1], [2, 2], [1, 1], 1, True, "float32"),
+    ("tap_1x1_m256_wide", (12, 16, 64, 64), (256, 16, 1, 1), [0, 0, 0, 0], [2, 2], [1, 1], 1, True, "float32"),
 ]
 
 
@@ -294,6 +298,7 @@ CONV_FUSED = [
     ("bcast_skip_fallback", (2, 16, 13, 11), (24, 16, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, "chan", "float32"),
     ("tap_split_relu_skip", (2, 32, 16, 16), (144, 32, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, "full", "float32"),
     ("tap_m128_relu_skip", (4, 64, 30, 30), (128, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, "full", "float32"),
+    ("tap_small_img_relu_skip", (2, 64, 14, 14), (192, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, "full", "float32"),
 ]
 
 
@@ -348,6 +353,7 @@ DQ_CONV = [
     ("u8_stride2_proj", (2, 32, 14, 14), "uint8", 0, (64, 32, 1, 1), [0, 0, 0, 0], [2, 2], 1, False, False, False),
     ("u8_tap_split", (2, 32, 16, 16), "uint8", 7, (144, 32, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, True),
     ("i8_tap_m128_s2", (4, 64, 30, 30), "int8", -3, (128, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, False),
+    ("u8_tap_small_img", (2, 64, 14, 14), "uint8", 9, (192, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, True),
 ]
 
 
