@@ -818,13 +818,20 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
     //   * 1x1 strided layers: 128x128 tiles (16 waves of 32x32, two register
     //     sets) when >= 256 output channels still give >= 192 blocks, else 64x128;
     //   * >= 128 output pixels per image: 128x256 (16 waves of 64x32, two
-    //     register sets) for >= 128 output channels, else 64x256 (8 waves of 32x64);
+    //     register sets) for >= 128 output channels, else 64x256 (8 waves of
+    //     32x64) or 64x128 (8 waves of 32x32, two register sets) by balance;
     //   * smaller images with >= 128 output channels: 128x256 tiles would span
     //     five or more images and miss L1 on the tap-blocked order, 128x128
     //     tiles (16 waves of 32x32, two register sets) keep it (block 4 of
     //     config 5: 109 -> 92 us at split 5);
     // MODE 0 otherwise (the 3-channel stem, few output channels on small
     // images).  Swept on MI355X over the config-4 / config-5 layers.
+    // Tiles do equal work, so a grid of t tiles keeps the CUs busy for a share
+    // (t / CUs) / ceil(t / CUs) of the time (fewer tiles than CUs: t / CUs).
+    auto balance = [](int64_t t) {
+        const double r = (double)t / (double)num_cus();
+        return r / std::ceil(r);
+    };
     enum { kNone, kT64x128, kT128x128, kT64x256, kT128x256 };
     const int khw = g.KH * g.KW;
     int plan = kNone;
@@ -835,16 +842,16 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
             plan = g.Mg >= 128 ? kT128x256 : kT64x256;
         else if (g.Mg >= 128)
             plan = kT128x128;
+        // 64x128 tiles (two register sets) when they fill the CUs better than
+        // 64x256 ones (config-5 block 1: 784 -> 1568 tiles, 0.77 -> 0.87; 163 -> 159 us)
+        if (plan == kT64x256 &&
+            balance(((P + 127) / 128) * ((g.Mg + 63) / 64) * cg.group) >
+                1.05 * balance(((P + 255) / 256) * ((g.Mg + 63) / 64) * cg.group))
+            plan = kT64x128;
     }
     const int bm = (plan == kT128x128 || plan == kT128x256) ? 128 : 64;
     const int bp = (plan == kT64x128 || plan == kT128x128) ? 128 : 256;
     const int64_t blocks = ((P + bp - 1) / bp) * ((g.Mg + bm - 1) / bm) * cg.group;
-    // Tiles do equal work, so a grid of t tiles keeps the CUs busy for a share
-    // (t / CUs) / ceil(t / CUs) of the time (fewer tiles than CUs: t / CUs).
-    auto balance = [](int64_t t) {
-        const double r = (double)t / (double)num_cus();
-        return r / std::ceil(r);
-    };
     // Split-k slice count for grids smaller than the CU count: each slice
     // >= 128 deep, at most 8; the count whose block total balances best over
     // the CUs (fewer slices on near ties: each slice adds a write and a read of
