@@ -282,7 +282,22 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
     const int wm = wave / WGN, wn = wave % WGN;
     const int grp = SPLIT ? (int)blockIdx.z % groups : (int)blockIdx.z;
     const int slice = SPLIT ? (int)blockIdx.z / groups : 0;
-    const int m0 = blockIdx.y * BM, p0 = blockIdx.x * BP;
+    // Tile order: the dispatcher deals consecutive workgroups to the 8 XCDs in
+    // turn (each with its own L2), so the block index L becomes a tile index
+    // that gives XCD class L % 8 a contiguous run of tiles, and within it the
+    // channel tile varies fastest: the channel tiles of one pixel tile share
+    // their input through one L2 (config-5 block 4: its 4 channel tiles had
+    // fetched the input 4x past L2).  A bijection on [0, tiles) for any count.
+    int m0, p0;
+    {
+        const int ntm = (int)gridDim.y, tiles = (int)gridDim.x * ntm;
+        const int L = (int)blockIdx.x + (int)blockIdx.y * (int)gridDim.x;
+        const int cls = L & 7, q = tiles >> 3, rem = tiles & 7;
+        const int tid = cls * q + min(cls, rem) + (L >> 3);
+        const int tp = tid / ntm;
+        m0 = (tid - tp * ntm) * BM;
+        p0 = tp * BP;
+    }
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, xbytes);
     const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(Wt, wbytes);
 

@@ -267,6 +267,7 @@ CONV_TILED = [
     # and a strided 1x1 with 256 output channels over >= 192 tiles
     ("tap_small_img_m192_split", (2, 64, 14, 14), (192, 64, 3, 3), [1, 1, 1, 1], [2, 2], [1, 1], 1, True, "float32"),
     ("tap_1x1_m256_wide", (12, 16, 64, 64), (256, 16, 1, 1), [0, 0, 0, 0], [2, 2], [1, 1], 1, True, "float32"),
+    ("tap_groups_m128_split", (1, 64, 10, 10), (256, 32, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 2, True, "float32"),
 ]
 
 
