@@ -719,6 +719,7 @@ template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int XQ = 0, int DE
 void launch_conv_tiled_cfg(const float* x, const float* w, const void* b, int dtb, void* y, int dty, const ConvTiled& g,
                            int group, uint32_t xbytes, uint32_t wbytes, uint32_t ybytes, ConvEpi epi, ConvXQ xq,
                            hipStream_t s) {
+    if (MODE == 2 && g.Cg % BK) { set_error("conv: tap-blocked plan needs Cg %% %d == 0", BK); return; }
     const dim3 grid((g.P + BP - 1) / BP, (g.Mg + BM - 1) / BM, group), block(64 * WGM * WGN);
     if (XQ || (dty == kF32 && (!b || dtb == kF32)))
         hipLaunchKernelGGL((k_conv_tiled<BM, BP, BK, WGM, WGN, MODE, kF32, false, XQ, DEPTH>), grid, block, 0, s, x, w,
@@ -783,6 +784,7 @@ __global__ __launch_bounds__(256) void k_conv_splitk_reduce4(const float* __rest
 template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int XQ = 0, int DEPTH = 1>
 bool launch_conv_split_cfg(const float* x, const float* w, const float* b, float* y, const ConvTiled& g, int group,
                            uint32_t xbytes, uint32_t wbytes, int nsplit_req, ConvEpi epi, ConvXQ xq, hipStream_t s) {
+    if (MODE == 2 && g.Cg % BK) { set_error("conv: tap-blocked plan needs Cg %% %d == 0", BK); return true; }
     const int kchunk = ((g.Kg + nsplit_req - 1) / nsplit_req + BK - 1) / BK * BK;
     const int nsplit = (g.Kg + kchunk - 1) / kchunk;
     const int64_t total = (int64_t)g.P * g.M;

@@ -738,12 +738,14 @@ void qdq_fused_entry(const Tensor* X, const Tensor* QS, const Tensor* QZ, const 
         void* y = st.out(Y, tensor_bytes(Y));
         if (!x || !qs || !qz || !ds || !dz || !y) { st.finish(); return; }
         if (((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0) {
-            if (n) {
-                const uint32_t nv = (uint32_t)(n / 4);
+            // chunks of at most kMaxUnitsPerLaunch float4 units: buffer byte offsets stay below 2^32
+            const uint32_t nv_all = (uint32_t)(n / 4);
+            hipStream_t sm = stream();
+            for (uint32_t vbase = 0; vbase < nv_all; vbase += kMaxUnitsPerLaunch) {
+                const uint32_t nv = nv_all - vbase < kMaxUnitsPerLaunch ? nv_all - vbase : kMaxUnitsPerLaunch;
                 const dim3 g(grid_for(nv, kBlock * 2)), b(kBlock);
-                hipStream_t sm = stream();
-                const float *xf = (const float*)x, *qsf = (const float*)qs, *dsf = (const float*)ds;
-                float* yf = (float*)y;
+                const float *xf = (const float*)x + (size_t)vbase * 4, *qsf = (const float*)qs, *dsf = (const float*)ds;
+                float* yf = (float*)y + (size_t)vbase * 4;
                 switch (code_dtype) {
                 case kU8: hipLaunchKernelGGL((k_qdq_fused<kU8>), g, b, 0, sm, xf, qsf, qz, dsf, dz, yf, nv); break;
                 case kI8: hipLaunchKernelGGL((k_qdq_fused<kI8>), g, b, 0, sm, xf, qsf, qz, dsf, dz, yf, nv); break;
