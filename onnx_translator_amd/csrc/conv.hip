@@ -714,6 +714,202 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
     }
 }
 
+// Few-channel convolution (the 7x7 / stride-2 stem over 3 channels): a block
+// computes 64 output channels x 256 consecutive output pixels of one image with
+// the whole k range resident in LDS, loaded once: the weights as [channel][k]
+// and, for each input channel, the input rows the pixels touch with the zero
+// halo of the padding.  k runs in the reference's (c, kh, kw) order and is
+// unrolled at compile time, so each MFMA operand is one LDS read at a per-lane
+// base plus an immediate offset: no address arithmetic, bounds tests or
+// barriers inside the k loop.  v_mfma_f32_32x32x1f32 takes one k per step for
+// two 32x32 blocks (lanes 0-31 and 32-63), which here are the same 32 output
+// channels over two 32-pixel groups: a 32x64 wave tile per instruction, and no
+// padded k slots (a padded slot would multiply a zero weight by a real, possibly
+// non-finite, input).  Output register r of lane l: block r / 16, channel
+// 8*((r%16)/4) + r%4 + 4*(l/32), pixel l%32 of that block's group.
+constexpr int kStemRows = 13, kStemCols = 232;   // LDS patch per input channel: rows x columns
+template <int C, int KH, int KW, int S>
+__global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ X, const float* __restrict__ Wt,
+                                                   const float* __restrict__ Bv, float* __restrict__ Y, ConvTiled g,
+                                                   int tiles_per_img, int ntm, int tiles, uint32_t xbytes,
+                                                   uint32_t wbytes, uint32_t ybytes, ConvEpi epi) {
+    typedef float floatx32 __attribute__((ext_vector_type(32)));
+    constexpr int BM = 64, BP = 256, WGN = 4, K = C * KH * KW, KA = K + (K % 2 == 0 ? 1 : 2);   // odd row pitch
+    constexpr int PRM = kStemRows, PCM = kStemCols, PATCH = C * PRM * PCM;
+    __shared__ float As[BM * KA];
+    __shared__ float Ps[PATCH];
+    __shared__ float Bs[BM];
+    const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), lr = lane & 31,
+              lk = lane >> 5;
+    const int wm = wave / WGN, wn = wave % WGN, pw = wn * 64;
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, xbytes);
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(Wt, wbytes);
+    const __amdgpu_buffer_rsrc_t yr = buffer_rsrc(Y, ybytes);
+    const __amdgpu_buffer_rsrc_t zr = buffer_rsrc(epi.skip, epi.skip ? ybytes : 0u);
+
+    // Persistent blocks: block b takes tile slots b, b + G, b + 2G, ... (G =
+    // gridDim.x, a multiple of 8, so one XCD); a slot maps to a tile with the
+    // k_conv_tiled order (each XCD class a contiguous run, channel tile fastest).
+    struct Tile { int m0, n, q0, ih_lo; };
+    auto tile_of = [&](int slot) {
+        const int cls = slot & 7, q = tiles >> 3, rem = tiles & 7;
+        const int tid = cls * q + min(cls, rem) + (slot >> 3);
+        const int tp = tid / ntm;
+        Tile T;
+        T.m0 = (tid - tp * ntm) * BM;
+        T.n = tp / tiles_per_img;
+        T.q0 = (tp - T.n * tiles_per_img) * BP;
+        T.ih_lo = (int)g.fd_ow.div((uint32_t)T.q0) * S - g.pt;
+        return T;
+    };
+    // A tile's operands: weights [m][k] (rows past Mg read zero) and the input
+    // patch [c][row][col] (row r <-> input row ih_lo + r, col <-> column col - pl).
+    // Wave w moves rows w, w + 8, ... (a wave-uniform row index: its address
+    // math is scalar), lanes move columns lane, lane + 64, ...: a thread keeps
+    // only the loaded values across the multiply.
+    constexpr int NW = 8, WROWS = BM / NW, WCOLJ = (K + 63) / 64;
+    constexpr int PROWS = C * PRM, PRW = (PROWS + NW - 1) / NW, PCOLJ = (PCM + 63) / 64;
+    float wv[WROWS][WCOLJ], pv[PRW][PCOLJ], bv = 0.0f;
+    auto load = [&](const Tile& T) {
+        if (t < BM) bv = (Bv && T.m0 + t < g.Mg) ? Bv[T.m0 + t] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < WROWS; i++) {
+            const int m = wave + i * NW;
+            const bool mok = T.m0 + m < g.Mg;
+#pragma unroll
+            for (int j = 0; j < WCOLJ; j++) {
+                const int k = lane + 64 * j;
+                const uint32_t off = (mok && k < K) ? (uint32_t)((T.m0 + m) * K + k) * 4u : kOOB;
+                wv[i][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PRW; i++) {
+            const int row = wave + i * NW;
+            const int c = row / PRM, ih = T.ih_lo + (row - c * PRM);
+            const bool rok = row < PROWS && (unsigned)ih < (unsigned)g.H;
+#pragma unroll
+            for (int j = 0; j < PCOLJ; j++) {
+                const int col = lane + 64 * j, iw = col - g.pl;
+                const bool ok = rok && col < PCM && (unsigned)iw < (unsigned)g.W;
+                const uint32_t off = ok ? (uint32_t)(((T.n * C + c) * g.H + ih) * g.W + iw) * 4u : kOOB;
+                pv[i][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
+            }
+        }
+    };
+    auto store = [&]() {
+        if (t < BM) Bs[t] = bv;
+#pragma unroll
+        for (int i = 0; i < WROWS; i++)
+#pragma unroll
+            for (int j = 0; j < WCOLJ; j++) {
+                const int k = lane + 64 * j;
+                if (k < K) As[(wave + i * NW) * KA + k] = wv[i][j];
+            }
+#pragma unroll
+        for (int i = 0; i < PRW; i++)
+#pragma unroll
+            for (int j = 0; j < PCOLJ; j++) {
+                const int row = wave + i * NW, col = lane + 64 * j;
+                if (row < PROWS && col < PCM) Ps[row * PCM + col] = pv[i][j];
+            }
+    };
+
+    int slot = blockIdx.x;
+    if (slot >= tiles) return;
+    Tile T = tile_of(slot);
+    load(T);
+    store();
+    __syncthreads();
+    const float* pa = &As[(wm * 32 + lr) * KA];
+    while (true) {
+        // the next tile's operands go to registers while this one is multiplied
+        const int next = slot + (int)gridDim.x;
+        Tile Tn = T;
+        if (next < tiles) {
+            Tn = tile_of(next);
+            load(Tn);
+        }
+        const int q = min(T.q0 + pw + lk * 32 + lr, g.OHW - 1);
+        const int oh = (int)g.fd_ow.div((uint32_t)q), ow = q - oh * g.OW;
+        const float* pb = &Ps[(oh * S - g.pt - T.ih_lo) * PCM + ow * S];
+        floatx32 acc;
+#pragma unroll
+        for (int r = 0; r < 32; r++) acc[r] = 0.0f;
+        // k = (c, kh, kw): one rolled trip per input channel (bounded read-ahead,
+        // so the next tile's operands fit beside it), its KH x KW taps unrolled
+#pragma nounroll
+        for (int c = 0; c < C; c++) {
+            const float* ac = pa + c * KH * KW;
+            const float* bc = pb + c * PRM * PCM;
+#pragma unroll
+            for (int kh = 0; kh < KH; kh++)
+#pragma unroll
+                for (int kw = 0; kw < KW; kw++)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x1f32(ac[kh * KW + kw], bc[kh * PCM + kw], acc, 0, 0, 0);
+        }
+
+        // epilogue (f32 output): bias, Relu, residual; pixels past the image and
+        // channels past Mg take the out-of-range offset (loads zero, stores
+        // dropped); residual values loaded four at a time ahead of their stores
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const int qq = T.q0 + pw + b * 32 + lr;
+            const bool qok = qq < g.OHW;
+#pragma unroll
+            for (int r0 = 0; r0 < 16; r0 += 4) {
+                float sk[4];
+                if (epi.skip) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int m = T.m0 + wm * 32 + 8 * ((r0 + u) >> 2) + ((r0 + u) & 3) + 4 * lk;
+                        const uint32_t vo = (qok && m < g.Mg) ? (uint32_t)(((T.n * g.M + m) * g.OHW + qq) * 4) : kOOB;
+                        sk[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(zr, vo, 0, 0));
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int r = r0 + u;
+                    const int m = T.m0 + wm * 32 + 8 * (r >> 2) + (r & 3) + 4 * lk;
+                    const uint32_t vo = (qok && m < g.Mg) ? (uint32_t)(((T.n * g.M + m) * g.OHW + qq) * 4) : kOOB;
+                    // + 0.0f without a bias, as the reference adds bias_val = 0.0 (-0 -> +0)
+                    float v = acc[b * 16 + r] + Bs[wm * 32 + 8 * (r >> 2) + (r & 3) + 4 * lk];
+                    if (epi.relu) v = relu_f(v);
+                    if (epi.skip) v += sk[u];
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, vo, 0, 0);
+                }
+            }
+        }
+        if (next >= tiles) break;
+        __syncthreads();   // every wave is done reading this tile's operands
+        store();
+        __syncthreads();
+        slot = next;
+        T = Tn;
+    }
+}
+
+// The few-channel plan: 3 input channels, 7x7, stride 2, no dilation, one
+// group, and a patch that fits (256 consecutive output pixels touch at most
+// kStemRows input rows of at most kStemCols columns).
+inline bool stem_plan(const ConvTiled& g, int group) {
+    if (group != 1 || g.Cg != 3 || g.KH != 7 || g.KW != 7 || g.sh != 2 || g.sw != 2 || g.dh != 1 || g.dw != 1) return false;
+    const int rows_out = std::min((256 + g.OW - 1) / g.OW + 1, g.OH);
+    const int PR = (rows_out - 1) * 2 + 7, PC = (g.OW - 1) * 2 + 7 + 1;   // + 1: the last column read stays in the row
+    return PR <= kStemRows && PC <= kStemCols;
+}
+
+template <int C, int KH, int KW, int S>
+void launch_conv_stem(const float* x, const float* w, const float* b, float* y, const ConvTiled& g, uint32_t xbytes,
+                      uint32_t wbytes, uint32_t ybytes, ConvEpi epi, hipStream_t s) {
+    const int tiles_per_img = (g.OHW + 255) / 256, N = g.P / g.OHW, ntm = (g.Mg + 63) / 64;
+    const int tiles = N * tiles_per_img * ntm;
+    // persistent grid: two blocks per CU (the LDS footprint allows two), a multiple of 8
+    const int grid = std::min(2 * num_cus(), (tiles + 7) / 8 * 8);
+    hipLaunchKernelGGL((k_conv_stem<C, KH, KW, S>), dim3((unsigned)grid), dim3(512), 0, s, x, w, b, y, g,
+                       tiles_per_img, ntm, tiles, xbytes, wbytes, ybytes, epi);
+}
+
 // XQ != 0 (quantized input) runs with an f32 output and an f32 or no bias only.
 template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int XQ = 0, int DEPTH = 1>
 void launch_conv_tiled_cfg(const float* x, const float* w, const void* b, int dtb, void* y, int dty, const ConvTiled& g,
@@ -830,6 +1026,15 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
     // tiles 32x64 / 32x32); BK = 8 when K is short (the 7x7x3 stem: less
     // padding, more tiles in flight).
     const uint32_t ux = (uint32_t)xb, uw = (uint32_t)wb, uy = (uint32_t)yb;
+    // The 3-channel 7x7 / stride-2 stem: its whole k range in LDS (k_conv_stem).
+    // Quantized inputs never get here for it (conv_xq_fast sends them through
+    // DequantizeLinear and this plan, which keeps the two paths' bits equal).
+    if constexpr (XQ == 0) {
+        if (stem_plan(g, cg.group) && dty == kF32 && (!b || dtb == kF32)) {
+            launch_conv_stem<3, 7, 7, 2>(xf, wf, (const float*)b, (float*)y, g, ux, uw, uy, epi, s);
+            return true;
+        }
+    }
     // Plan: MODE 1 for 1x1 stride-1 layers; MODE 2 (BK = 16, so Cg % 16 == 0
     // keeps every k-tile inside one tap) for
     //   * 1x1 strided layers: 128x128 tiles (16 waves of 32x32, two register
@@ -1053,8 +1258,12 @@ extern "C" void conv2d_fused_forward(const Tensor* X, const Tensor* W, const Ten
 
 namespace {
 bool conv_xq_fast(const Tensor* Xq, const Tensor* XScale, const Tensor* XZero, const Tensor* W, const Tensor* B,
-                  const Tensor* Skip, const Tensor* Y) {
+                  const Tensor* Skip, const Tensor* Y, const ConvParams* params) {
     const int dx = (int)Xq->dtype;
+    // 3-channel 7x7 stride-2 layers take the f32 stem plan: run them as the pair
+    if (W->ndim == 4 && W->shape[1] == 3 && W->shape[2] == 7 && W->shape[3] == 7 && params && params->strides &&
+        params->strides[0] == 2 && params->strides[1] == 2)
+        return false;
     if (exact_mode() || (dx != kU8 && dx != kI8) || XScale->dtype != kF32 || XScale->size != 1) return false;
     if (XZero && XZero->data && ((int)XZero->dtype != dx || XZero->size != 1)) return false;
     if (W->dtype != kF32 || Y->dtype != kF32 || (B && B->data && B->dtype != kF32)) return false;
@@ -1077,7 +1286,7 @@ extern "C" void dequantize_conv2d_fused_forward(const Tensor* Xq, const Tensor* 
     const bool has_z = XZero && XZero->data;
     if (has_z && !tensor_sane(XZero, name)) return;
     if (!ensure_device()) return;
-    if (conv_xq_fast(Xq, XScale, has_z ? XZero : nullptr, W, B, Skip, Y)) {
+    if (conv_xq_fast(Xq, XScale, has_z ? XZero : nullptr, W, B, Skip, Y, params)) {
         tensor_ops_hip_clear_error();
         conv_entry(name, Xq, W, B, Y, params, (Skip && Skip->data) ? Skip : nullptr, relu ? 1 : 0,
                    Xq->dtype == kU8 ? 1 : 2, XScale, has_z ? XZero : nullptr);

@@ -268,6 +268,10 @@ CONV_TILED = [
     ("tap_small_img_m192_split", (2, 64, 14, 14), (192, 64, 3, 3), [1, 1, 1, 1], [2, 2], [1, 1], 1, True, "float32"),
     ("tap_1x1_m256_wide", (12, 16, 64, 64), (256, 16, 1, 1), [0, 0, 0, 0], [2, 2], [1, 1], 1, True, "float32"),
     ("tap_groups_m128_split", (1, 64, 10, 10), (256, 32, 3, 3), [1, 1, 1, 1], [1, 1], [1, 1], 2, True, "float32"),
+    # the 3-channel 7x7 / stride-2 stem plan (whole k range in LDS): a second, partial
+    # channel tile; asymmetric padding without bias
+    ("stem_plan_m80", (2, 3, 20, 180), (80, 3, 7, 7), [3, 3, 3, 3], [2, 2], [1, 1], 1, True, "float32"),
+    ("stem_plan_asym_nobias", (1, 3, 17, 224), (64, 3, 7, 7), [2, 3, 4, 1], [2, 2], [1, 1], 1, False, "float32"),
 ]
 
 
@@ -300,6 +304,7 @@ CONV_FUSED = [
     ("tap_split_relu_skip", (2, 32, 16, 16), (144, 32, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, "full", "float32"),
     ("tap_m128_relu_skip", (4, 64, 30, 30), (128, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, "full", "float32"),
     ("tap_small_img_relu_skip", (2, 64, 14, 14), (192, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, "full", "float32"),
+    ("stem_plan_relu_skip", (2, 3, 20, 180), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2], 1, True, True, "full", "float32"),
 ]
 
 
@@ -355,6 +360,7 @@ DQ_CONV = [
     ("u8_tap_split", (2, 32, 16, 16), "uint8", 7, (144, 32, 3, 3), [1, 1, 1, 1], [1, 1], 1, True, True, True),
     ("i8_tap_m128_s2", (4, 64, 30, 30), "int8", -3, (128, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, False),
     ("u8_tap_small_img", (2, 64, 14, 14), "uint8", 9, (192, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, True),
+    ("u8_stem_shape", (2, 3, 20, 180), "uint8", 5, (64, 3, 7, 7), [3, 3, 3, 3], [2, 2], 1, True, True, False),
 ]
 
 
