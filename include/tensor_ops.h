@@ -216,6 +216,18 @@ void dequantize_gemm_forward(const Tensor* A, const Tensor* Bq, const Tensor* Sc
  * NULL (no Add) and broadcasts to Y as add_forward's B does. */
 void conv2d_fused_forward(const Tensor* X, const Tensor* W, const Tensor* B, const Tensor* Skip, int relu,
                           Tensor* Y, ConvParams* params);
+/* Convolution with the residual block's epilogue and the next block's activation fake
+ * quantization: Y = DequantizeLinear(QuantizeLinear(conv2d_fused_forward's Y, QScale,
+ * QZeroPoint), DScale, DZeroPoint), the conv2d_fused_forward -> quantize_linear_forward ->
+ * dequantize_linear_forward sequence (tensor_ops/tensor_ops.h:161, 85, 116, 149, 155) in one
+ * pass over Y (the pre-quantization activation is never written), with the same bits as
+ * conv2d_fused_forward followed by quantize_dequantize_linear_forward.  code_dtype names the
+ * intermediate codes' dtype as there; the one-pass epilogue covers uint8 / int8 codes with
+ * one-element f32 scales and zero points of the code dtype, other arguments run the
+ * sequence. */
+void conv2d_fused_qdq_forward(const Tensor* X, const Tensor* W, const Tensor* B, const Tensor* Skip, int relu,
+                              const Tensor* QScale, const Tensor* QZeroPoint, const Tensor* DScale,
+                              const Tensor* DZeroPoint, int code_dtype, Tensor* Y, ConvParams* params);
 /* The QDQ convolution: Y = [Skip +] [Relu](Conv(DequantizeLinear(Xq, XScale, XZero), W, B)), the
  * dequantize_linear_forward -> conv2d_fused_forward sequence (tensor_ops/tensor_ops.h:155, 161)
  * in one pass that reads the uint8 / int8 activation codes directly; the same bits as the

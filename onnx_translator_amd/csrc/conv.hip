@@ -22,6 +22,7 @@
 #include <algorithm>
 #include <cmath>
 
+#include "quant.h"
 #include "runtime.h"
 
 namespace tohip {
@@ -221,6 +222,7 @@ typedef __attribute__((address_space(1))) float gfloat;
 struct ConvEpi {
     const float* skip;
     int relu;
+    FakeQuant fq;   // applied last (kind 0: none)
 };
 __device__ __forceinline__ float relu_f(float v) { return v > 0.0f ? v : 0.0f; }
 
@@ -627,6 +629,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
         // address arithmetic.
         const __amdgpu_buffer_rsrc_t yr = buffer_rsrc(Y, ybytes);
         const __amdgpu_buffer_rsrc_t zr = buffer_rsrc(epi.skip, epi.skip ? ybytes : 0u);
+        FQParm fqp;
+        if (epi.fq.kind) fqp = fq_parm(epi.fq);
         float bv[TM][16];
 #pragma unroll
         for (int i = 0; i < TM; i++)
@@ -661,6 +665,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
                         float v = acc[i][j][r] + bv[i][r];
                         if (epi.relu) v = relu_f(v);
                         if (epi.skip) v += sk[r];
+                        if (epi.fq.kind) v = fq_apply(v, fqp);
                         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, vo, so, 0);
                     }
                 }
@@ -682,6 +687,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
                             if (epi.relu) v = relu_f(v);
                             if (epi.skip)
                                 v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(zr, vo, so, 0));
+                            if (epi.fq.kind) v = fq_apply(v, fqp);
                             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, vo, so, 0);
                         }
                 }
@@ -706,6 +712,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
                     float v = acc[i][j][r] + (Bv ? ((const gfloat*)Bv)[m] : 0.0f);
                     if (epi.relu) v = relu_f(v);
                     if (epi.skip) v += ((const gfloat*)epi.skip)[yi];
+                    if (epi.fq.kind) v = fq_apply(v, fq_parm(epi.fq));
                     ((gfloat*)Y)[yi] = v;
                 } else {
                     conv_store_rt(Y, dty, yi, Bv, dtb, m, acc[i][j][r]);
@@ -943,6 +950,7 @@ __global__ __launch_bounds__(256) void k_conv_splitk_reduce(const float* __restr
     float v = (float)acc;
     if (epi.relu) v = relu_f(v);
     if (epi.skip) v += epi.skip[i];
+    if (epi.fq.kind) v = fq_apply(v, fq_parm(epi.fq));
     Y[i] = v;
 }
 
@@ -974,6 +982,11 @@ __global__ __launch_bounds__(256) void k_conv_splitk_reduce4(const float* __rest
         const float4 k = *(const float4*)(epi.skip + i);
         v[0] += k.x; v[1] += k.y; v[2] += k.z; v[3] += k.w;
     }
+    if (epi.fq.kind) {
+        const FQParm fqp = fq_parm(epi.fq);
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = fq_apply(v[j], fqp);
+    }
     *(float4*)(Y + i) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
@@ -1003,8 +1016,11 @@ bool launch_conv_split_cfg(const float* x, const float* w, const float* b, float
 // Returns false (caller falls back) when a tensor is beyond the 2 GB reach of
 // 32-bit buffer offsets.
 template <int XQ>
+// *fq_applied (when given) tells whether the kernels applied epi.fq: the stem
+// plan leaves it to the caller.
 bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, void* y, int dty, const ConvGeom& cg,
-                          ConvEpi epi, ConvXQ xq, hipStream_t s) {
+                          ConvEpi epi, ConvXQ xq, hipStream_t s, bool* fq_applied = nullptr) {
+    if (fq_applied) *fq_applied = epi.fq.kind != 0;
     const int64_t xb = (int64_t)cg.N * cg.C * cg.H * cg.W * (XQ ? 1 : 4), wb = (int64_t)cg.M * cg.Kg * 4;
     const int64_t P = (int64_t)cg.N * cg.OH * cg.OW;
     const int64_t yb = P * cg.M * 4;
@@ -1032,6 +1048,7 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
     if constexpr (XQ == 0) {
         if (stem_plan(g, cg.group) && dty == kF32 && (!b || dtb == kF32)) {
             launch_conv_stem<3, 7, 7, 2>(xf, wf, (const float*)b, (float*)y, g, ux, uw, uy, epi, s);
+            if (fq_applied) *fq_applied = false;
             return true;
         }
     }
@@ -1133,8 +1150,8 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
 }
 
 bool launch_conv_tiled(const void* x, const void* w, const void* b, int dtb, void* y, int dty, const ConvGeom& cg,
-                       ConvEpi epi, hipStream_t s) {
-    return launch_conv_tiled_xq<0>(x, w, b, dtb, y, dty, cg, epi, ConvXQ{nullptr, nullptr}, s);
+                       ConvEpi epi, hipStream_t s, bool* fq_applied = nullptr) {
+    return launch_conv_tiled_xq<0>(x, w, b, dtb, y, dty, cg, epi, ConvXQ{nullptr, nullptr}, s, fq_applied);
 }
 
 inline bool f32_exact_dtype(int dt) {
@@ -1165,8 +1182,14 @@ namespace {
 // xq_kind 1 / 2: X holds uint8 / int8 codes dequantised in the kernel with the
 // one-element scale xs and zero point xz (xz may be null); the caller has
 // checked that this is the tiled f32 path (f32 W / Y, f32 or no bias).
+// fq_kind 1 / 2: fake quantization with uint8 / int8 codes after the skip add,
+// parameters fq_t = {q scale, q zero point, d scale, d zero point} (one-element
+// f32 scales, zero points of the code dtype); *fq_done tells whether the kernel
+// applied it, which it does only where it also applied relu and skip.
 bool conv_entry(const char* name, const Tensor* X, const Tensor* W, const Tensor* B, Tensor* Y, ConvParams* params,
-                const void* skip, int relu, int xq_kind = 0, const Tensor* xs = nullptr, const Tensor* xz = nullptr) {
+                const void* skip, int relu, int xq_kind = 0, const Tensor* xs = nullptr, const Tensor* xz = nullptr,
+                int fq_kind = 0, const Tensor* const* fq_t = nullptr, bool* fq_done = nullptr) {
+    if (fq_done) *fq_done = false;
     if (!tensor_sane(X, name) || !tensor_sane(W, name) || !tensor_sane(Y, name)) return true;
     if (!params || !params->pads || !params->strides || !params->dilations) { set_error("%s: NULL params", name); return true; }
     if (X->ndim != 4 || W->ndim != 4 || Y->ndim != 4) { set_error("%s: X, W and Y must be 4-D", name); return true; }
@@ -1195,10 +1218,15 @@ bool conv_entry(const char* name, const Tensor* X, const Tensor* W, const Tensor
     const void* z = skip ? st.in((const Tensor*)skip) : nullptr;
     const void* xsd = xq_kind ? st.in(xs) : nullptr;
     const void* xzd = (xq_kind && xz) ? st.in(xz) : nullptr;
-    if (!x || !w || !y || (has_b && !b) || (skip && !z) || (xq_kind && !xsd) || (xq_kind && xz && !xzd)) {
+    const void* fqd[4] = {nullptr, nullptr, nullptr, nullptr};
+    if (fq_kind)
+        for (int k = 0; k < 4; k++) fqd[k] = st.in(fq_t[k]);
+    if (!x || !w || !y || (has_b && !b) || (skip && !z) || (xq_kind && !xsd) || (xq_kind && xz && !xzd) ||
+        (fq_kind && (!fqd[0] || !fqd[1] || !fqd[2] || !fqd[3]))) {
         st.finish();
         return true;
     }
+    const FakeQuant fq{(const float*)fqd[0], fqd[1], (const float*)fqd[2], fqd[3], fq_kind};
     bool fused = !skip && !relu;   // epilogue applied in the kernel (or none requested)
     hipStream_t s = stream();
     const int dtx = (int)X->dtype, dtw = (int)W->dtype, dty = (int)Y->dtype, dtb = has_b ? (int)B->dtype : kF32;
@@ -1206,18 +1234,25 @@ bool conv_entry(const char* name, const Tensor* X, const Tensor* W, const Tensor
         const bool big = (int64_t)g.N * g.OH * g.OW > 0x7FFFFFFF;
         bool done = false;
         if (xq_kind) {
-            const ConvEpi epi{(const float*)z, relu};
+            const ConvEpi epi{(const float*)z, relu, fq};
             const ConvXQ xq{(const float*)xsd, xzd};
-            const bool ok = xq_kind == 1 ? launch_conv_tiled_xq<1>(x, w, b, dtb, y, dty, g, epi, xq, s)
-                                         : launch_conv_tiled_xq<2>(x, w, b, dtb, y, dty, g, epi, xq, s);
+            bool fq_applied = false;
+            const bool ok = xq_kind == 1 ? launch_conv_tiled_xq<1>(x, w, b, dtb, y, dty, g, epi, xq, s, &fq_applied)
+                                         : launch_conv_tiled_xq<2>(x, w, b, dtb, y, dty, g, epi, xq, s, &fq_applied);
             if (!ok) set_error("%s: operands beyond the quantized-input kernel's reach", name);
             fused = true;
+            if (fq_done) *fq_done = ok && fq_applied;
             done = true;
         } else if (!exact_mode() && !big && g.Kg > 0 && f32_exact_dtype(dtx) && f32_exact_dtype(dtw)) {
             if (dtx == kF32 && dtw == kF32) {
                 const bool epi_ok = dty == kF32 && (!has_b || dtb == kF32);
-                const ConvEpi epi{epi_ok ? (const float*)z : nullptr, epi_ok ? relu : 0};
-                if (launch_conv_tiled(x, w, b, dtb, y, dty, g, epi, s)) fused = fused || epi_ok;
+                const ConvEpi epi{epi_ok ? (const float*)z : nullptr, epi_ok ? relu : 0,
+                                  epi_ok ? fq : FakeQuant{nullptr, nullptr, nullptr, nullptr, 0}};
+                bool fq_applied = false;
+                if (launch_conv_tiled(x, w, b, dtb, y, dty, g, epi, s, &fq_applied)) {
+                    fused = fused || epi_ok;
+                    if (fq_done) *fq_done = fq_applied;
+                }
                 else launch_conv_mfma<kF32, kF32>(x, dtx, w, dtw, b, dtb, y, dty, g, s);
             } else {
                 launch_conv_mfma<-1, -1>(x, dtx, w, dtw, b, dtb, y, dty, g, s);
@@ -1254,6 +1289,40 @@ extern "C" void conv2d_fused_forward(const Tensor* X, const Tensor* W, const Ten
     if (tensor_ops_hip_last_error()[0]) return;
     if (!fused && relu) relu_forward(Y, Y);
     if ((!fused || !skip_in_kernel) && has_skip && !tensor_ops_hip_last_error()[0]) add_forward(Y, Skip, Y);
+}
+
+// Conv -> Relu -> Add(., Skip) -> QuantizeLinear -> DequantizeLinear in one
+// pass; see tensor_ops.h.  The kernel epilogue covers what conv2d_fused_forward's
+// does, with uint8 / int8 codes and one-element f32 scales and zero points of
+// the code dtype; otherwise the fused convolution runs and then
+// quantize_dequantize_linear_forward in place on Y, which is also what the
+// epilogue equals.
+extern "C" void conv2d_fused_qdq_forward(const Tensor* X, const Tensor* W, const Tensor* B, const Tensor* Skip,
+                                         int relu, const Tensor* QScale, const Tensor* QZeroPoint,
+                                         const Tensor* DScale, const Tensor* DZeroPoint, int code_dtype, Tensor* Y,
+                                         ConvParams* params) {
+    const char* name = "conv2d_fused_qdq_forward";
+    const bool has_skip = Skip && Skip->data;
+    if (has_skip && !tensor_sane(Skip, name)) return;
+    if (!tensor_sane(QScale, name) || !tensor_sane(QZeroPoint, name) || !tensor_sane(DScale, name) ||
+        !tensor_sane(DZeroPoint, name) || !tensor_sane(Y, name))
+        return;
+    const bool skip_in_kernel = has_skip && Skip->dtype == kF32 && Skip->size == Y->size;
+    const int kind = code_dtype == kU8 ? 1 : (code_dtype == kI8 ? 2 : 0);
+    const bool fq_ok = kind && Y->dtype == kF32 && (!has_skip || skip_in_kernel) && QScale->dtype == kF32 &&
+                       DScale->dtype == kF32 && QScale->size == 1 && DScale->size == 1 && QZeroPoint->size == 1 &&
+                       DZeroPoint->size == 1 && (int)QZeroPoint->dtype == code_dtype &&
+                       (int)DZeroPoint->dtype == code_dtype;
+    const Tensor* fq_t[4] = {QScale, QZeroPoint, DScale, DZeroPoint};
+    tensor_ops_hip_clear_error();
+    bool fq_done = false;
+    const bool fused = conv_entry(name, X, W, B, Y, params, skip_in_kernel ? Skip : nullptr, relu ? 1 : 0, 0, nullptr,
+                                  nullptr, fq_ok ? kind : 0, fq_t, &fq_done);
+    if (tensor_ops_hip_last_error()[0]) return;
+    if (!fused && relu) relu_forward(Y, Y);
+    if ((!fused || !skip_in_kernel) && has_skip && !tensor_ops_hip_last_error()[0]) add_forward(Y, Skip, Y);
+    if (!fq_done && !tensor_ops_hip_last_error()[0])
+        quantize_dequantize_linear_forward(Y, QScale, QZeroPoint, DScale, DZeroPoint, Y, code_dtype);
 }
 
 namespace {

@@ -45,51 +45,13 @@
 #include <algorithm>
 #include <cfloat>
 
+#include "quant.h"
 #include "runtime.h"
 
 namespace tohip {
 namespace {
 
 constexpr int kBlock = 256;
-
-template <int YDT> __device__ __forceinline__ uint8_t code8(double r) {
-    if constexpr (YDT == kU8) return (uint8_t)sat(cvt_i64(__builtin_rint(r)), 0, 255);
-    else if constexpr (YDT == kI8) return (uint8_t)(int8_t)sat(cvt_i64(__builtin_rint(r)), -128, 127);
-    else if constexpr (YDT == kI4) return (uint8_t)(int8_t)sat(cvt_i64(__builtin_rint(r)), -8, 7);
-    else if constexpr (YDT == kE4M3) return enc_e4m3((float)r);
-    else return enc_e5m2((float)r);
-}
-
-__device__ __forceinline__ double qval(double x, double s, double z) { return s != 0.0 ? __builtin_rint(x / s) + z : z; }
-
-// Quantization parameters of one scale / zero-point pair.
-struct QParm {
-    float s, rs, hs, zf;   // scale, ~1/s, |s|/2, zero point (+128 for i8 outputs)
-    double zd;             // zero point as the reference reads it
-    bool fast;             // zero point integral with |zp| < 2^22
-};
-
-template <int YDT>
-__device__ __forceinline__ QParm qparm(float s, double zd) {
-    QParm p;
-    p.s = s;
-    p.rs = __builtin_amdgcn_rcpf(s);
-    p.hs = __builtin_fabsf(s) * 0.5f;
-    p.zd = zd;
-    const float zf = (float)p.zd;
-    p.fast = (double)zf == p.zd && __builtin_rintf(zf) == zf && __builtin_fabsf(zf) < 0x1p22f;
-    p.zf = (YDT == kI8) ? zf + 128.0f : zf;
-    return p;
-}
-
-// r + zp of one element through the fast path; good becomes false when the
-// lane must be recomputed exactly.
-__device__ __forceinline__ float qfast(float x, const QParm& p, bool& good) {
-    const float r = __builtin_rintf(x * p.rs);
-    const float rho = __builtin_fmaf(-r, p.s, x);
-    good = good && p.fast && (__builtin_fabsf(rho) < p.hs);
-    return r + p.zf;
-}
 
 // Codes of four fast-path values, little-endian in one word.
 template <int YDT>

@@ -271,6 +271,41 @@ class FusedConv(Conv):
         return super().forward_(x, w, b)
 
 
+class FusedConvQDQ(FusedConv):
+    """Conv -> Relu -> Add(., skip) -> QuantizeLinear -> DequantizeLinear in one
+    call to ``conv2d_fused_qdq_forward``: y = DQ(Q([skip +] [Relu](Conv(x, w, b)))),
+    the fake quantization applied in the convolution's epilogue, so neither the
+    block output before quantization nor the codes are written.  Equal to the
+    operator sequence (nn/Operators.py:475-548, :32-79, :170-219, :427-473) bit
+    for bit.  ``inputs`` = [x, w, b or "", skip or "", q_scale, q_zero_point,
+    d_scale, d_zero_point]; codes of dtype ``code_dtype``."""
+
+    def __init__(self, inputs, outputs, pads, strides, dilations, group, dtype, relu, code_dtype, version="17"):
+        super().__init__(inputs, outputs, pads, strides, dilations, group, dtype, relu, version)
+        self.code_dtype = code_dtype
+        self.lib.conv2d_fused_qdq_forward.argtypes = [PT, PT, PT, PT, ctypes.c_int, PT, PT, PT, PT, ctypes.c_int, PT,
+                                                      ctypes.POINTER(CConvParams)]
+        self.lib.conv2d_fused_qdq_forward.restype = None
+
+    def forward(self, x: Tensor, w: Tensor, b: Tensor = None, skip: Tensor = None, q_scale: Tensor = None,
+                q_zero_point: Tensor = None, d_scale: Tensor = None, d_zero_point: Tensor = None):
+        N, _, H, W = x.size
+        M, _, KH, KW = w.size
+        OH, OW = _pool_out(H, W, self.pads, self.strides, self.dilations, KH, KW)
+        p, keep = self._params()
+        relu, code = ctypes.c_int(self.relu), ctypes.c_int(DTYPE_MAP[self.code_dtype])
+
+        def arrange(ins, out):
+            return (ins[0], ins[1], ins[2], ins[3], relu, ins[4], ins[5], ins[6], ins[7], code, out, ctypes.byref(p))
+        t = self._run("conv2d_fused_qdq_forward", [x, w, b, skip, q_scale, q_zero_point, d_scale, d_zero_point],
+                      (N, M, OH, OW), self.dtype, arrange=arrange)
+        del keep
+        return _values(self, t)
+
+    def forward_(self, x: Tensor_, w: Tensor_, b: Tensor_ = None, *rest):
+        return super().forward_(x, w, b)
+
+
 class DequantizeConv(FusedConv):
     """DequantizeLinear -> Conv [-> Relu] [-> Add(., skip)] of a QDQ block in one call
     to ``dequantize_conv2d_fused_forward``: the convolution reads the uint8 / int8

@@ -199,6 +199,8 @@ class Graph:
             self._fuse_dq_conv(shapes)
         if qdq:
             self._fuse_qdq(shapes, self._consumers())
+            if conv_epi:
+                self._fuse_conv_qdq(shapes, self._consumers())
         if elementwise:
             self._fuse_runs(shapes, self._consumers())
 
@@ -341,6 +343,35 @@ class Graph:
             replace[dq.name] = fused
             drop.add(q.name)
             self.fused_runs.append([q.name, dq.name])
+        out = [replace.get(o.name, o) for o in ops if o.name not in drop]
+        self.ops = OrderedDict((o.name, o) for o in out)
+
+    def _fuse_conv_qdq(self, shapes, consumers):
+        """Conv / FusedConv (f32) whose output is read only by a QuantizeDequantize
+        with uint8 / int8 codes: one FusedConvQDQ in the convolution's place that
+        writes the QuantizeDequantize's output (the pre-quantization tensor is
+        never written)."""
+        ops = list(self.ops.values())
+        producer = {o: op for op in ops for o in op.outputs}
+        replace, drop = {}, set()
+        for fq in ops:
+            if type(fq) is not Op.QuantizeDequantize or fq.code_dtype not in ("uint8", "int8"):
+                continue
+            x = fq.inputs[0]
+            c = producer.get(x)
+            if type(c) not in (Op.Conv, Op.FusedConv) or c.dtype != "float32" or c.name in replace:
+                continue
+            if consumers.get(x, 0) != 1 or x in self.output_name or x in fq.inputs[1:]:
+                continue
+            b = c.inputs[2] if len(c.inputs) > 2 else ""
+            skip = c.inputs[3] if type(c) is Op.FusedConv and len(c.inputs) > 3 else ""
+            relu = c.relu if type(c) is Op.FusedConv else 0
+            fused = Op.FusedConvQDQ([c.inputs[0], c.inputs[1], b, skip] + list(fq.inputs[1:5]), list(fq.outputs),
+                                    c.pads, c.strides, c.dilations, c.group, c.dtype, relu, fq.code_dtype)
+            fused.name = f"FusedConvQDQ.{c.name}+{fq.name}"
+            replace[c.name] = fused
+            drop.add(fq.name)
+            self.fused_runs.append([c.name, fq.name])
         out = [replace.get(o.name, o) for o in ops if o.name not in drop]
         self.ops = OrderedDict((o.name, o) for o in out)
 

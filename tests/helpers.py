@@ -188,6 +188,8 @@ class HipLib(O.CpuLib):
         lib.dequantize_gemm_forward.argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int, O.PT, O.PT, ctypes.c_float,
                                                 ctypes.c_float, ctypes.c_int, ctypes.c_int]
         lib.quantize_dequantize_linear_forward.argtypes = [O.PT] * 6 + [ctypes.c_int]
+        lib.conv2d_fused_qdq_forward.argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int, O.PT, O.PT, O.PT, O.PT,
+                                                 ctypes.c_int, O.PT, ctypes.POINTER(O.CConvParams)]
 
     def device_count(self):
         return int(self.lib.tensor_ops_hip_device_count())
@@ -275,6 +277,38 @@ class HipLib(O.CpuLib):
             if err:
                 raise RuntimeError(err)
             return self.read(o, dty)
+        finally:
+            for t in ins:
+                if t:
+                    self.lib.free_tensor(t)
+            self.lib.free_tensor(o)
+
+    def conv_fused_qdq(self, x, w, b, skip, relu, qs, qz, ds, dz, code_dt, pads, strides, dilations=(1, 1),
+                       group=1):
+        """conv2d_fused_qdq_forward on host tensors: f32 x / w / b / skip (b, skip may be
+        None), f32 scales and zero points of code_dt; f32 output."""
+        N, C, H, W = x.shape
+        M, _, KH, KW = w.shape
+        OH = (H + pads[0] + pads[2] - dilations[0] * (KH - 1) - 1) // strides[0] + 1
+        OW = (W + pads[1] + pads[3] - dilations[1] * (KW - 1) - 1) // strides[1] + 1
+        p = O.CConvParams()
+        keep = [O._ints(pads), O._ints(strides), O._ints(dilations)]
+        p.pads, p.strides, p.dilations = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep]
+        p.group = int(group)
+        ins = [self.tensor(x, "float32"), self.tensor(w, "float32"),
+               self.tensor(b, "float32") if b is not None else O.PT(),
+               self.tensor(skip, "float32") if skip is not None else O.PT(),
+               self.tensor(np.atleast_1d(qs), "float32"), self.tensor(np.atleast_1d(qz), code_dt),
+               self.tensor(np.atleast_1d(ds), "float32"), self.tensor(np.atleast_1d(dz), code_dt)]
+        o = self.empty((N, M, OH, OW), "float32")
+        try:
+            self.lib.tensor_ops_hip_clear_error()
+            self.lib.conv2d_fused_qdq_forward(*ins[:4], int(relu), *ins[4:], ctypes.c_int(O.NAMES[code_dt]), o,
+                                              ctypes.byref(p))
+            err = self.last_error()
+            if err:
+                raise RuntimeError(err)
+            return self.read(o, "float32")
         finally:
             for t in ins:
                 if t:

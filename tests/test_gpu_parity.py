@@ -345,6 +345,74 @@ def test_conv_fused_epilogue(hip, oracle_lib, case, exact):
     assert_close(got, ref, ydt, what=f"conv fused {tag}")
 
 
+# conv2d_fused_qdq_forward = conv2d_fused_forward -> quantize_dequantize_linear_forward
+# bit for bit on every conv plan: tap-blocked tiles (64x128, 128x128, 128x256), the
+# split-k reductions (16-byte and scalar), the gather and direct 1x1 plans, the
+# generic epilogue of partial channel tiles, the stem plan (fake quantization in a
+# second pass), and the sequence fallbacks (fp8 codes, exact mode).  Output channel 0
+# has zero weights and bias, so with Relu its value is the skip tensor's, which holds
+# rint ties and non-finite values there (the fp64 fallback of the quantize step).
+CONV_QDQ = [
+    ("tap_u8_relu_skip", (2, 64, 28, 28), (64, 64, 3, 3), [1, 1, 1, 1], [1, 1], "uint8", 0, 8 / 255, 0, 8 / 255),
+    ("tap_i8_m128_s2", (2, 64, 30, 30), (128, 64, 3, 3), [1, 1, 1, 1], [2, 2], "int8", -3, 0.05, 2, 0.04),
+    ("tap_m256_small_img", (2, 128, 14, 14), (256, 128, 3, 3), [1, 1, 1, 1], [2, 2], "uint8", 3, 0.03, 3, 0.03),
+    ("split4_u8", (2, 256, 14, 14), (512, 256, 3, 3), [1, 1, 1, 1], [2, 2], "uint8", 0, 8 / 255, 0, 8 / 255),
+    ("split_scalar_i8", (1, 256, 9, 9), (129, 256, 3, 3), [1, 1, 1, 1], [2, 2], "int8", 0, 0.05, 0, 0.05),
+    ("gather_u8", (2, 12, 13, 11), (24, 12, 3, 3), [1, 1, 1, 1], [1, 1], "uint8", 9, 0.02, 9, 0.02),
+    ("direct_1x1_u8", (2, 40, 12, 12), (96, 40, 1, 1), [0, 0, 0, 0], [1, 1], "uint8", 0, 0.04, 0, 0.04),
+    ("tail_rows_m200_i8", (1, 30, 9, 9), (200, 30, 3, 3), [1, 1, 1, 1], [1, 1], "int8", 1, 0.03, 1, 0.03),
+    ("stem_u8", (2, 3, 20, 180), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2], "uint8", 0, 8 / 255, 0, 8 / 255),
+    ("e4m3_fallback", (2, 64, 12, 12), (64, 64, 3, 3), [1, 1, 1, 1], [1, 1], "float8_e4m3", 0, 0.01, 0, 0.01),
+]
+
+
+@pytest.mark.parametrize("case", CONV_QDQ, ids=[c[0] for c in CONV_QDQ])
+@pytest.mark.parametrize("exact", [False, True], ids=["mfma", "exact"])
+def test_conv_fused_qdq(hip, oracle_lib, case, exact):
+    tag, xs, ws, pads, strides, cdt, qz, qs, dz, ds = case
+    rng = np.random.default_rng(len(tag) * 13 + ws[0])
+    x = rng.normal(0, 1, xs).astype(np.float32)
+    w = rng.normal(0, np.sqrt(2 / (ws[1] * ws[2] * ws[3])), ws).astype(np.float32)
+    b = rng.normal(0, 0.1, (ws[0],)).astype(np.float32)
+    w[0], b[0] = 0.0, 0.0
+    OH = (xs[2] + pads[0] + pads[2] - ws[2]) // strides[0] + 1
+    OW = (xs[3] + pads[1] + pads[3] - ws[3]) // strides[1] + 1
+    skip = rng.normal(0, 1, (xs[0], ws[0], OH, OW)).astype(np.float32)
+    c0 = skip[0, 0].reshape(-1)
+    specials = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1e30, -1e30], np.float32)
+    c0[:7] = specials
+    ties = ((np.arange(-16, 16) + 0.5) * np.float32(qs)).astype(np.float32)
+    c0[7:7 + min(32, c0.size - 7)] = ties[:c0.size - 7]
+    npz = {"int8": np.int8, "uint8": np.uint8}.get(cdt, np.uint8)
+    qsv, dsv = np.array([qs], np.float32), np.array([ds], np.float32)
+    zq, zd = np.array([qz], npz), np.array([dz], npz)
+    hip.set_exact(exact)
+    try:
+        got = hip.conv_fused_qdq(x, w, b, skip, True, qsv, zq, dsv, zd, cdt, pads, strides)
+        y = hip.conv_fused(x, w, b, skip, True, "float32", pads, strides)
+        seq = hip.qdq_fused(y, qsv, zq, dsv, zd, cdt)
+    finally:
+        hip.set_exact(False)
+    assert np.array_equal(got.view(np.uint32), seq.view(np.uint32)), f"{tag}: fused differs from the sequence"
+    # against the oracle: Conv -> Relu -> Add -> QuantizeLinear -> DequantizeLinear
+    yr = oracle_lib.conv(x, O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], 1)
+    yr = oracle_lib.binary("add", oracle_lib.unary("relu", yr, O.F32, O.F32), O.F32, skip, O.F32, O.F32)
+    codes = oracle_lib.qdq("quantize", yr, O.F32, qsv, O.F32, zq, cdt, cdt)
+    ref = oracle_lib.qdq("dequantize", codes, cdt, dsv, O.F32, zd, cdt, O.F32)
+    if exact:
+        assert_bitexact(got, ref, O.F32, what=f"conv qdq {tag}")
+    else:
+        # fp32 MFMA accumulation moves a few values across a rounding boundary of
+        # the quantizer: those differ by one code step, everything else is exact
+        assert_bitexact(got[0, 0], ref[0, 0], O.F32, what=f"conv qdq {tag} channel 0")
+        fin = np.isfinite(ref)
+        assert np.array_equal(np.isfinite(got), fin)
+        diff = np.abs(got[fin].astype(np.float64) - ref[fin])
+        if not cdt.startswith("float8"):   # integer codes: one step of the dequantize scale
+            assert diff.max() <= np.float64(np.float32(ds)) * 1.0001
+        assert (diff > 0).mean() < 0.01, f"{tag}: {(diff > 0).mean():.4f} of the values differ"
+
+
 # dequantize_conv2d_fused_forward = dequantize_linear_forward -> conv2d_fused_forward
 # bit for bit: uint8 / int8 codes read by the gather (zero points that make the
 # padding taps differ from (0 - zp) * s), the direct 1x1 path, the split-k path,

@@ -180,6 +180,37 @@ def test_quantize_dequantize_pass(monkeypatch):
     assert not any("block1.xq" in o.inputs or "block1.xq" in o.outputs for o in g.ops.values())
 
 
+def test_conv_qdq_pass(monkeypatch):
+    """Placeholder-shape run of the passes on the config-5 graph: the
+    QuantizeDequantize of blocks 2-4 reads the output of block 1-3's fused
+    convolution and nothing else does, so each pair becomes one FusedConvQDQ
+    that writes the quantized activation; block 1's reads the MaxPool output,
+    which is also block 1's residual, and stays."""
+    from onnx_translator_amd.nn import Graph, Tensor_
+    from onnx_translator_amd.nn import Operators as Op
+    from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
+    monkeypatch.setattr(Op.DequantizeLinear, "forward", lambda self, *a: self.forward_(*a))
+    m = resnet_qdq_model(batch=1, image=32)
+    g = Graph(ONNXImport(m), ["input"], ["output"], initializers=initializers(m))
+    shapes = g._edge_shapes([Tensor_(1, 3, 32, 32, dtype="float32")])
+    g._fold_constants()
+    g._fuse_conv_epilogue(shapes, g._consumers())
+    g._fuse_qdq(shapes, g._consumers())
+    g._fuse_conv_qdq(shapes, g._consumers())
+    names = [type(o).__name__ for o in g.ops.values()]
+    assert names.count("QuantizeDequantize") == 1 and names.count("FusedConvQDQ") == 3
+    fc = [o for o in g.ops.values() if type(o).__name__ == "FusedConvQDQ"]
+    assert fc[0].inputs[3] == "pool" and fc[0].relu == 1 and fc[0].code_dtype == "uint8"
+    assert fc[0].inputs[4:] == ["act.scale", "act.zp", "act.scale", "act.zp"]
+    assert fc[0].outputs == ["block2.xd"] and fc[2].outputs == ["block4.xd"]
+    assert [o.inputs[3] for o in fc[1:]] == ["block2.proj", "block3.proj"]
+    assert not any("block1.out" in o.inputs or "block1.out" in o.outputs for o in g.ops.values())
+    seen = {"input"} | set(g.initializers)
+    for o in g.ops.values():
+        assert all((not na) or na in seen for na in o.inputs), o.name
+        seen.update(o.outputs)
+
+
 def test_toy_graph_oracle_closed_form(oracle_lib):
     rng = np.random.default_rng(0)
     x = rng.normal(0, 1, (1, 3, 32, 32)).astype(np.float32)
@@ -264,8 +295,9 @@ def test_resnet_qdq_graph(hip, oracle_lib, exact):
     # the activation QuantizeLinear -> DequantizeLinear pairs in one pass, and on
     # request the activation dequantisation folded into the convolutions) keeps
     # the node-by-node bits
-    assert len(g.fused_runs) == 9 and len(g.folded) == 7
-    assert sum(type(o).__name__ == "QuantizeDequantize" for o in g.ops.values()) == 4
+    assert len(g.fused_runs) == 12 and len(g.folded) == 7
+    assert sum(type(o).__name__ == "QuantizeDequantize" for o in g.ops.values()) == 1
+    assert sum(type(o).__name__ == "FusedConvQDQ" for o in g.ops.values()) == 3
     assert np.array_equal(probs.view(np.uint32), unfused.view(np.uint32))
     gq = load_graph(m, fuse=False).fuse(dequantize_conv=True)
     hip.set_exact(exact)
