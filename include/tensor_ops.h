@@ -216,6 +216,16 @@ void dequantize_gemm_forward(const Tensor* A, const Tensor* Bq, const Tensor* Sc
  * NULL (no Add) and broadcasts to Y as add_forward's B does. */
 void conv2d_fused_forward(const Tensor* X, const Tensor* W, const Tensor* B, const Tensor* Skip, int relu,
                           Tensor* Y, ConvParams* params);
+/* MaxPool with a second output: Y = max_pool_forward(X) and Yq = DequantizeLinear(
+ * QuantizeLinear(Y, QScale, QZeroPoint), DScale, DZeroPoint), the max_pool_forward ->
+ * quantize_linear_forward -> dequantize_linear_forward sequence (tensor_ops/tensor_ops.h:166,
+ * 149, 155) with Y read once; Yq has the bits of quantize_dequantize_linear_forward(Y).  The
+ * one-pass kernel covers f32 3x3 / stride-2 pooling (top / left pad 1) with uint8 / int8 codes
+ * and one-element f32 scales and zero points of the code dtype; other arguments run the
+ * sequence. */
+void max_pool_qdq_forward(const Tensor* X, Tensor* Y, PoolParams* params, const Tensor* QScale,
+                          const Tensor* QZeroPoint, const Tensor* DScale, const Tensor* DZeroPoint,
+                          int code_dtype, Tensor* Yq);
 /* Convolution with the residual block's epilogue and the next block's activation fake
  * quantization: Y = DequantizeLinear(QuantizeLinear(conv2d_fused_forward's Y, QScale,
  * QZeroPoint), DScale, DZeroPoint), the conv2d_fused_forward -> quantize_linear_forward ->

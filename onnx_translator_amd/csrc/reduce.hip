@@ -27,6 +27,7 @@
 // window has a block-per-plane strip kernel that loads each input row once.
 #include <cfloat>
 
+#include "quant.h"
 #include "runtime.h"
 
 namespace tohip {
@@ -334,9 +335,12 @@ constexpr int kPoolStripWaves = 8;      // waves per plane: OH <= 64
 // one block per plane, wave w takes a strip of output rows.  Output row oh reads
 // input rows 2oh-1, 2oh, 2oh+1; consecutive output rows share one, so every
 // input row of the strip is loaded once, as one 8-byte load per lane (columns
-// 2l, 2l+1; column 2l-1 comes from lane l-1).
+// 2l, 2l+1; column 2l-1 comes from lane l-1).  FQ: each output value is also
+// written fake-quantized (fq_apply) to Yq.
+template <bool FQ>
 __global__ __launch_bounds__(64 * kPoolStripWaves) void k_maxpool_3s2_strip(const float* __restrict__ X, float* __restrict__ Y,
-                                                           PoolGeom g, int rows_per_wave) {
+                                                           PoolGeom g, int rows_per_wave, float* __restrict__ Yq,
+                                                           FakeQuant fq) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t plane = blockIdx.x;
     const float* xp = X + plane * (int64_t)g.H * g.W;
@@ -366,6 +370,8 @@ __global__ __launch_bounds__(64 * kPoolStripWaves) void k_maxpool_3s2_strip(cons
         return best;
     };
     if (oh0 >= oh1) return;
+    FQParm fqp;
+    if constexpr (FQ) fqp = fq_parm(fq);
     // The whole strip (2 * rows + 1 input rows) is loaded up front: a wave
     // waits for memory once instead of once per output row.
     float2 rows[2 * kPoolStrip + 1];
@@ -381,7 +387,10 @@ __global__ __launch_bounds__(64 * kPoolStripWaves) void k_maxpool_3s2_strip(cons
         best = row_max(best, rows[2 * o], 2 * oh - 1 >= 0);
         best = row_max(best, rows[2 * o + 1], 2 * oh < g.H);
         best = row_max(best, rows[2 * o + 2], 2 * oh + 1 < g.H);
-        if (live) yp[(int64_t)oh * g.OW + lane] = best;
+        if (live) {
+            yp[(int64_t)oh * g.OW + lane] = best;
+            if constexpr (FQ) Yq[plane * (int64_t)g.OH * g.OW + (int64_t)oh * g.OW + lane] = fq_apply(best, fqp);
+        }
     }
 }
 
@@ -554,26 +563,33 @@ void softmax_forward(const Tensor* input, Tensor* output, int axis) {
     st.finish();
 }
 
-void max_pool_forward(const Tensor* X, Tensor* Y, PoolParams* p) {
-    const char* name = "max_pool_forward";
-    if (!tensor_sane(X, name) || !tensor_sane(Y, name)) return;
-    if (!p || !p->pads || !p->strides || !p->dilations || !p->kernel_shape) { set_error("%s: NULL params", name); return; }
-    if (X->ndim != 4 || Y->ndim != 4) { set_error("%s: X and Y must be 4-D (NCHW)", name); return; }
+}  // extern "C"
+
+namespace {
+// max_pool_forward; with fq_kind 1 / 2 (uint8 / int8 codes, parameters fq_t =
+// {q scale, q zero point, d scale, d zero point} of one element each) the strip
+// kernel also writes Yq = fake quantization of Y.  Returns whether it did.
+bool maxpool_entry(const char* name, const Tensor* X, Tensor* Y, PoolParams* p, Tensor* Yq = nullptr, int fq_kind = 0,
+                   const Tensor* const* fq_t = nullptr) {
+    if (!tensor_sane(X, name) || !tensor_sane(Y, name)) return false;
+    if (!p || !p->pads || !p->strides || !p->dilations || !p->kernel_shape) { set_error("%s: NULL params", name); return false; }
+    if (X->ndim != 4 || Y->ndim != 4) { set_error("%s: X and Y must be 4-D (NCHW)", name); return false; }
     PoolGeom g;
     g.N = X->shape[0]; g.C = X->shape[1]; g.H = X->shape[2]; g.W = X->shape[3];
     g.OH = Y->shape[2]; g.OW = Y->shape[3];
     g.KH = p->kernel_shape[0]; g.KW = p->kernel_shape[1];
     g.pt = p->pads[0]; g.pl = p->pads[1]; g.sh = p->strides[0]; g.sw = p->strides[1];
     g.dh = p->dilations[0]; g.dw = p->dilations[1];
-    if (Y->shape[0] != g.N || Y->shape[1] != g.C) { set_error("%s: Y batch/channels differ from X", name); return; }
-    if (!ensure_device()) return;
+    if (Y->shape[0] != g.N || Y->shape[1] != g.C) { set_error("%s: Y batch/channels differ from X", name); return false; }
+    if (!ensure_device()) return false;
     const int64_t planes = (int64_t)g.N * g.C;
     const int64_t total = planes * g.OH * g.OW;
     Staging st;
     const void* x = st.in(X);
     void* y = st.out(Y, (size_t)total * dt_bytes((int)Y->dtype));
-    if (!x || !y) { st.finish(); return; }
+    if (!x || !y) { st.finish(); return false; }
     hipStream_t s = stream();
+    bool fq_done = false;
     if (total > 0) {
         const dim3 grid((unsigned)((g.OH + kPoolRows - 1) / kPoolRows), (unsigned)(planes < 65535 ? planes : 65535));
         const dim3 blk(256);
@@ -583,18 +599,56 @@ void max_pool_forward(const Tensor* X, Tensor* Y, PoolParams* p) {
                             g.pt == 1 && g.pl == 1 && g.W == 2 * g.OW && g.OW <= 64 && 2 * g.OH <= g.H + 2 &&
                             ((uintptr_t)x & 7) == 0;
         const int strip = (g.OH + kPoolStripWaves - 1) / kPoolStripWaves;
-        if (res3s2 && planes <= 0x7FFFFFFF && strip <= kPoolStrip)
-            hipLaunchKernelGGL(k_maxpool_3s2_strip, dim3((unsigned)planes), dim3(64 * kPoolStripWaves), 0, s,
-                               (const float*)x, (float*)y, g, strip);
+        const FakeQuant none{nullptr, nullptr, nullptr, nullptr, 0};
+        if (res3s2 && planes <= 0x7FFFFFFF && strip <= kPoolStrip && fq_kind) {
+            const void* fqd[4];
+            for (int k = 0; k < 4; k++) fqd[k] = st.in(fq_t[k]);
+            void* yq = st.out(Yq, (size_t)total * 4);
+            if (!fqd[0] || !fqd[1] || !fqd[2] || !fqd[3] || !yq) { st.finish(); return false; }
+            const FakeQuant fq{(const float*)fqd[0], fqd[1], (const float*)fqd[2], fqd[3], fq_kind};
+            hipLaunchKernelGGL(k_maxpool_3s2_strip<true>, dim3((unsigned)planes), dim3(64 * kPoolStripWaves), 0, s,
+                               (const float*)x, (float*)y, g, strip, (float*)yq, fq);
+            fq_done = true;
+        } else if (res3s2 && planes <= 0x7FFFFFFF && strip <= kPoolStrip)
+            hipLaunchKernelGGL(k_maxpool_3s2_strip<false>, dim3((unsigned)planes), dim3(64 * kPoolStripWaves), 0, s,
+                               (const float*)x, (float*)y, g, strip, nullptr, none);
         else if (res3s2)
             hipLaunchKernelGGL(k_maxpool_3s2, grid, blk, 0, s, (const float*)x, (float*)y, g, planes);
         else if (f32)
             hipLaunchKernelGGL((k_maxpool_rows<kF32, kF32>), grid, blk, 0, s, x, dtx, y, dty, g, planes);
         else
             hipLaunchKernelGGL((k_maxpool_rows<-1, -1>), grid, blk, 0, s, x, dtx, y, dty, g, planes);
-        if (!check_launch(name)) { st.finish(); return; }
+        if (!check_launch(name)) { st.finish(); return false; }
     }
     st.finish();
+    return fq_done;
+}
+}  // namespace
+
+extern "C" {
+void max_pool_forward(const Tensor* X, Tensor* Y, PoolParams* p) { maxpool_entry("max_pool_forward", X, Y, p); }
+
+// MaxPool with a second, fake-quantized output; see tensor_ops.h.  The strip
+// kernel writes both for the 3x3 / stride-2 case with uint8 / int8 codes and
+// one-element f32 scales and zero points of the code dtype; otherwise
+// max_pool_forward then quantize_dequantize_linear_forward(Y -> Yq).
+void max_pool_qdq_forward(const Tensor* X, Tensor* Y, PoolParams* p, const Tensor* QScale, const Tensor* QZeroPoint,
+                          const Tensor* DScale, const Tensor* DZeroPoint, int code_dtype, Tensor* Yq) {
+    const char* name = "max_pool_qdq_forward";
+    if (!tensor_sane(QScale, name) || !tensor_sane(QZeroPoint, name) || !tensor_sane(DScale, name) ||
+        !tensor_sane(DZeroPoint, name) || !tensor_sane(Y, name) || !tensor_sane(Yq, name))
+        return;
+    if (Yq->size != Y->size) { set_error("%s: Yq must have Y's size", name); return; }
+    const int kind = code_dtype == kU8 ? 1 : (code_dtype == kI8 ? 2 : 0);
+    const bool fq_ok = kind && Y->dtype == kF32 && Yq->dtype == kF32 && QScale->dtype == kF32 &&
+                       DScale->dtype == kF32 && QScale->size == 1 && DScale->size == 1 && QZeroPoint->size == 1 &&
+                       DZeroPoint->size == 1 && (int)QZeroPoint->dtype == code_dtype &&
+                       (int)DZeroPoint->dtype == code_dtype;
+    const Tensor* fq_t[4] = {QScale, QZeroPoint, DScale, DZeroPoint};
+    tensor_ops_hip_clear_error();
+    const bool done = maxpool_entry(name, X, Y, p, Yq, fq_ok ? kind : 0, fq_t);
+    if (!done && !tensor_ops_hip_last_error()[0])
+        quantize_dequantize_linear_forward(Y, QScale, QZeroPoint, DScale, DZeroPoint, Yq, code_dtype);
 }
 
 }  // extern "C"

@@ -368,6 +368,55 @@ class MaxPool(Ops):
         return _values(self, Tensor_(N, C, OH, OW, dtype=self.dtype))
 
 
+class MaxPoolQDQ(MaxPool):
+    """MaxPool with a second output in one call to ``max_pool_qdq_forward``:
+    outputs [y, yq] with y = MaxPool(x) and yq = DequantizeLinear(QuantizeLinear(y,
+    q_scale, q_zero_point), d_scale, d_zero_point); equal to the MaxPool ->
+    QuantizeLinear -> DequantizeLinear operators (nn/Operators.py:550-611,
+    :427-473) bit for bit, y read once.  ``inputs`` = [x, q_scale, q_zero_point,
+    d_scale, d_zero_point]; codes of dtype ``code_dtype``."""
+
+    def __init__(self, inputs, outputs, kernel_shape, pads, strides, dtype, code_dtype, dilations=[1, 1],
+                 version="17"):
+        super().__init__(inputs, outputs, kernel_shape, pads, strides, dtype, dilations, version)
+        self.code_dtype = code_dtype
+        self.lib.max_pool_qdq_forward.argtypes = [PT, PT, ctypes.POINTER(CPoolParams), PT, PT, PT, PT, ctypes.c_int,
+                                                  PT]
+        self.lib.max_pool_qdq_forward.restype = None
+
+    def forward(self, x: Tensor, q_scale: Tensor, q_zero_point: Tensor, d_scale: Tensor, d_zero_point: Tensor):
+        N, C, H, W = x.size
+        KH, KW = self.kernel_shape
+        OH, OW = _pool_out(H, W, self.pads, self.strides, self.dilations, KH, KW)
+        arrs = [_int_arr(self.pads), _int_arr(self.strides), _int_arr(self.dilations), _int_arr(self.kernel_shape)]
+        p = CPoolParams()
+        p.pads, p.strides, p.dilations, p.kernel_shape = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in arrs]
+        keep: list = []
+        dev = any(isinstance(t.data, DeviceArray) for t in (x, q_scale, q_zero_point, d_scale, d_zero_point))
+        outs = []
+        try:
+            cins = [self._in_ctensor(t, keep) for t in (x, q_scale, q_zero_point, d_scale, d_zero_point)]
+            for _ in range(2):
+                outs.append(((N, C, OH, OW), self.dtype) + self._out_ctensor((N, C, OH, OW), self.dtype, dev))
+            self._call("max_pool_qdq_forward", cins[0], outs[0][3], ctypes.byref(p), *cins[1:],
+                       ctypes.c_int(DTYPE_MAP[self.code_dtype]), outs[1][3])
+        except Exception:
+            for shape, dt, d, c in outs:
+                if d is None:
+                    self.lib.free_tensor(c)
+            for c in keep:
+                self.lib.free_tensor(c)
+            raise
+        tensors = [self._finish(shape, dt, d, c, []) for shape, dt, d, c in outs]
+        for c in keep:
+            self.lib.free_tensor(c)
+        return _values(self, tensors)
+
+    def forward_(self, x: Tensor_, *params):
+        y = super().forward_(x)["tensor"]
+        return _values(self, [y, Tensor_(*y.size, dtype=self.dtype)])
+
+
 class Gemm(Ops):
     """Y = alpha * A' B' + beta * C (nn/Operators.py:613-669 -> tensor_ops.c:1167-1228)."""
 

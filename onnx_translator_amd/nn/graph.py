@@ -159,17 +159,20 @@ class Graph:
     # -- fusion --------------------------------------------------------------------
     def fuse(self, elementwise: bool = True, dequantize_gemm: bool = True, conv_epilogue: bool = True,
              fold_constants: bool = True, dequantize_conv: bool = False,
-             quantize_dequantize: bool = True) -> "Graph":
+             quantize_dequantize: bool = True, pool_quantize_dequantize: bool = False) -> "Graph":
         """Request the graph passes; they are applied at the first ``forward`` (shapes needed).
         ``dequantize_conv`` folds activation DequantizeLinear nodes into their convolutions
-        and so takes precedence over ``quantize_dequantize`` for those pairs."""
+        and so takes precedence over ``quantize_dequantize`` for those pairs.
+        ``pool_quantize_dequantize`` lets a MaxPool write the fake-quantized copy of its
+        output as well (MaxPoolQDQ); off by default, as on the config-5 graph the pooling
+        kernel with two outputs is slower than the two separate passes."""
         self._fuse_pending = (elementwise, dequantize_gemm, conv_epilogue, fold_constants, dequantize_conv,
-                              quantize_dequantize)
+                              quantize_dequantize, pool_quantize_dequantize)
         return self
 
     def fuse_elementwise(self) -> "Graph":
         """Request elementwise fusion only."""
-        return self.fuse(True, False, False, False, False, False)
+        return self.fuse(True, False, False, False, False, False, False)
 
     def _edge_shapes(self, inputs) -> Dict[str, tuple]:
         shapes: Dict[str, tuple] = {k: (tuple(v.size), v.dtype) for k, v in self.initializers.items()}
@@ -186,7 +189,7 @@ class Graph:
         return shapes
 
     def _fuse(self, inputs):
-        elementwise, dq_gemm, conv_epi, fold, dq_conv, qdq = self._fuse_pending
+        elementwise, dq_gemm, conv_epi, fold, dq_conv, qdq, pool_qdq = self._fuse_pending
         self._fuse_pending = None
         shapes = self._edge_shapes(inputs)
         if dq_gemm:
@@ -201,6 +204,8 @@ class Graph:
             self._fuse_qdq(shapes, self._consumers())
             if conv_epi:
                 self._fuse_conv_qdq(shapes, self._consumers())
+            if pool_qdq:
+                self._fuse_pool_qdq(shapes)
         if elementwise:
             self._fuse_runs(shapes, self._consumers())
 
@@ -372,6 +377,30 @@ class Graph:
             replace[c.name] = fused
             drop.add(fq.name)
             self.fused_runs.append([c.name, fq.name])
+        out = [replace.get(o.name, o) for o in ops if o.name not in drop]
+        self.ops = OrderedDict((o.name, o) for o in out)
+
+    def _fuse_pool_qdq(self, shapes):
+        """MaxPool (f32) whose output a QuantizeDequantize with uint8 / int8 codes
+        reads: one MaxPoolQDQ in the MaxPool's place with both outputs (the pooled
+        tensor keeps its other readers, e.g. a residual Add), so the pooled
+        tensor is not read back for the fake quantization."""
+        ops = list(self.ops.values())
+        producer = {o: op for op in ops for o in op.outputs}
+        replace, drop = {}, set()
+        for fq in ops:
+            if type(fq) is not Op.QuantizeDequantize or fq.code_dtype not in ("uint8", "int8"):
+                continue
+            x = fq.inputs[0]
+            mp = producer.get(x)
+            if type(mp) is not Op.MaxPool or mp.dtype != "float32" or mp.name in replace or x in fq.inputs[1:]:
+                continue
+            fused = Op.MaxPoolQDQ([mp.inputs[0]] + list(fq.inputs[1:5]), [x, fq.outputs[0]], mp.kernel_shape,
+                                  mp.pads, mp.strides, mp.dtype, fq.code_dtype, mp.dilations)
+            fused.name = f"MaxPoolQDQ.{mp.name}+{fq.name}"
+            replace[mp.name] = fused
+            drop.add(fq.name)
+            self.fused_runs.append([mp.name, fq.name])
         out = [replace.get(o.name, o) for o in ops if o.name not in drop]
         self.ops = OrderedDict((o.name, o) for o in out)
 

@@ -188,6 +188,8 @@ class HipLib(O.CpuLib):
         lib.dequantize_gemm_forward.argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int, O.PT, O.PT, ctypes.c_float,
                                                 ctypes.c_float, ctypes.c_int, ctypes.c_int]
         lib.quantize_dequantize_linear_forward.argtypes = [O.PT] * 6 + [ctypes.c_int]
+        lib.max_pool_qdq_forward.argtypes = [O.PT, O.PT, ctypes.POINTER(O.CPoolParams), O.PT, O.PT, O.PT, O.PT,
+                                             ctypes.c_int, O.PT]
         lib.conv2d_fused_qdq_forward.argtypes = [O.PT, O.PT, O.PT, O.PT, ctypes.c_int, O.PT, O.PT, O.PT, O.PT,
                                                  ctypes.c_int, O.PT, ctypes.POINTER(O.CConvParams)]
 
@@ -282,6 +284,32 @@ class HipLib(O.CpuLib):
                 if t:
                     self.lib.free_tensor(t)
             self.lib.free_tensor(o)
+
+    def maxpool_qdq(self, x, kernel_shape, pads, strides, qs, qz, ds, dz, code_dt):
+        """max_pool_qdq_forward on host tensors: f32 x, f32 scales, zero points of
+        code_dt; returns (Y, Yq)."""
+        N, C, H, W = x.shape
+        KH, KW = kernel_shape
+        OH = (H + pads[0] + pads[2] - (KH - 1) - 1) // strides[0] + 1
+        OW = (W + pads[1] + pads[3] - (KW - 1) - 1) // strides[1] + 1
+        p = O.CPoolParams()
+        keep = [O._ints(pads), O._ints(strides), O._ints((1, 1)), O._ints(kernel_shape)]
+        p.pads, p.strides, p.dilations, p.kernel_shape = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep]
+        ins = [self.tensor(x, "float32"), self.tensor(np.atleast_1d(qs), "float32"),
+               self.tensor(np.atleast_1d(qz), code_dt), self.tensor(np.atleast_1d(ds), "float32"),
+               self.tensor(np.atleast_1d(dz), code_dt)]
+        outs = [self.empty((N, C, OH, OW), "float32") for _ in range(2)]
+        try:
+            self.lib.tensor_ops_hip_clear_error()
+            self.lib.max_pool_qdq_forward(ins[0], outs[0], ctypes.byref(p), *ins[1:], ctypes.c_int(O.NAMES[code_dt]),
+                                          outs[1])
+            err = self.last_error()
+            if err:
+                raise RuntimeError(err)
+            return self.read(outs[0], "float32"), self.read(outs[1], "float32")
+        finally:
+            for t in ins + outs:
+                self.lib.free_tensor(t)
 
     def conv_fused_qdq(self, x, w, b, skip, relu, qs, qz, ds, dz, code_dt, pads, strides, dilations=(1, 1),
                        group=1):

@@ -413,6 +413,41 @@ def test_conv_fused_qdq(hip, oracle_lib, case, exact):
         assert (diff > 0).mean() < 0.01, f"{tag}: {(diff > 0).mean():.4f} of the values differ"
 
 
+# max_pool_qdq_forward: Y = max_pool_forward(X) and Yq = quantize_dequantize_linear_forward(Y)
+# bit for bit (the strip kernel for 3x3 / stride 2, the sequence otherwise), and equal to
+# the oracle's MaxPool -> QuantizeLinear -> DequantizeLinear (all three are exact).
+POOL_QDQ = [
+    ("strip_u8_stem_shape", (2, 64, 112, 112), (3, 3), [1, 1, 1, 1], [2, 2], "uint8", 0, 8 / 255, 0, 8 / 255),
+    ("strip_i8_odd", (3, 5, 21, 22), (3, 3), [1, 1, 1, 1], [2, 2], "int8", -7, 0.02, 4, 0.03),
+    ("rows_fallback_u8", (2, 4, 17, 19), (2, 2), [0, 0, 0, 0], [2, 2], "uint8", 5, 0.05, 5, 0.05),
+    ("e5m2_fallback", (2, 4, 16, 16), (3, 3), [1, 1, 1, 1], [2, 2], "float8_e5m2", 0, 0.25, 0, 0.25),
+]
+
+
+@pytest.mark.parametrize("case", POOL_QDQ, ids=[c[0] for c in POOL_QDQ])
+def test_maxpool_qdq(hip, oracle_lib, case):
+    tag, xs, ks, pads, strides, cdt, qz, qs, dz, ds = case
+    rng = np.random.default_rng(len(tag) + xs[1])
+    x = rng.normal(0, 2, xs).astype(np.float32)
+    flat = x[0, 0].reshape(-1)
+    flat[:7] = [np.nan, np.inf, -np.inf, 0.0, -0.0, 1e30, -1e30]
+    # rint ties where they survive the max: whole plane 1 of image 0 at tie values
+    x[0, 1] = ((rng.integers(-40, 40, xs[2:]) + 0.5) * np.float32(qs)).astype(np.float32)
+    npz = {"int8": np.int8, "uint8": np.uint8}.get(cdt, np.uint8)
+    qsv, dsv = np.array([qs], np.float32), np.array([ds], np.float32)
+    zq, zd = np.array([qz], npz), np.array([dz], npz)
+    y, yq = hip.maxpool_qdq(x, ks, pads, strides, qsv, zq, dsv, zd, cdt)
+    y1 = hip.maxpool(x, O.F32, O.F32, ks, pads, strides)
+    assert np.array_equal(y.view(np.uint32), y1.view(np.uint32)), f"{tag}: Y differs from max_pool_forward"
+    seq = hip.qdq_fused(y1, qsv, zq, dsv, zd, cdt)
+    assert np.array_equal(yq.view(np.uint32), seq.view(np.uint32)), f"{tag}: Yq differs from the sequence"
+    ry = oracle_lib.maxpool(x, O.F32, O.F32, ks, pads, strides)
+    codes = oracle_lib.qdq("quantize", ry, O.F32, qsv, O.F32, zq, cdt, cdt)
+    ref = oracle_lib.qdq("dequantize", codes, cdt, dsv, O.F32, zd, cdt, O.F32)
+    assert_bitexact(y, ry, O.F32, what=f"maxpool qdq {tag} Y")
+    assert_bitexact(yq, ref, O.F32, what=f"maxpool qdq {tag} Yq")
+
+
 # dequantize_conv2d_fused_forward = dequantize_linear_forward -> conv2d_fused_forward
 # bit for bit: uint8 / int8 codes read by the gather (zero points that make the
 # padding taps differ from (0 - zp) * s), the direct 1x1 path, the split-k path,

@@ -199,6 +199,14 @@ def test_conv_qdq_pass(monkeypatch):
     g._fuse_conv_qdq(shapes, g._consumers())
     names = [type(o).__name__ for o in g.ops.values()]
     assert names.count("QuantizeDequantize") == 1 and names.count("FusedConvQDQ") == 3
+    # block 1's pair reads the MaxPool output, which block 1's residual also reads:
+    # the MaxPool writes both tensors
+    g._fuse_pool_qdq(shapes)
+    names = [type(o).__name__ for o in g.ops.values()]
+    assert "QuantizeDequantize" not in names and names.count("MaxPoolQDQ") == 1
+    mp = next(o for o in g.ops.values() if type(o).__name__ == "MaxPoolQDQ")
+    assert mp.inputs == ["stem.relu", "act.scale", "act.zp", "act.scale", "act.zp"]
+    assert mp.outputs == ["pool", "block1.xd"] and mp.code_dtype == "uint8"
     fc = [o for o in g.ops.values() if type(o).__name__ == "FusedConvQDQ"]
     assert fc[0].inputs[3] == "pool" and fc[0].relu == 1 and fc[0].code_dtype == "uint8"
     assert fc[0].inputs[4:] == ["act.scale", "act.zp", "act.scale", "act.zp"]
@@ -299,6 +307,14 @@ def test_resnet_qdq_graph(hip, oracle_lib, exact):
     assert sum(type(o).__name__ == "QuantizeDequantize" for o in g.ops.values()) == 1
     assert sum(type(o).__name__ == "FusedConvQDQ" for o in g.ops.values()) == 3
     assert np.array_equal(probs.view(np.uint32), unfused.view(np.uint32))
+    gp = load_graph(m, fuse=False).fuse(pool_quantize_dequantize=True)
+    hip.set_exact(exact)
+    try:
+        with_pool = gp.forward(x).numpy()
+    finally:
+        hip.set_exact(False)
+    assert sum(type(o).__name__ == "MaxPoolQDQ" for o in gp.ops.values()) == 1 and len(gp.fused_runs) == 13
+    assert np.array_equal(with_pool.view(np.uint32), unfused.view(np.uint32))
     gq = load_graph(m, fuse=False).fuse(dequantize_conv=True)
     hip.set_exact(exact)
     try:
