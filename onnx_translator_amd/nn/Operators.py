@@ -588,17 +588,23 @@ class GlobalAveragePool(Ops):
     """Mean over the two trailing (spatial) dims: NCHW -> NC11
     (nn/Operators.py:2997-3021 -> tensor_ops.c:2844-2868)."""
 
-    def __init__(self, inputs, outputs, dtype="float32", version="17"):
+    def __init__(self, inputs, outputs, dtype="float32", version="17", flatten=False):
         super().__init__(inputs, outputs)
         self.dtype = dtype
         self.version = version
+        # flatten: write the [N, C] result of a following Flatten(axis=1) directly (the
+        # same values in the same order; global_average_pool_forward takes any output
+        # of N*C elements)
+        self.flatten = flatten
+
+    def _out_shape(self, size):
+        return (int(size[0]), int(np.prod(size[1:-2], dtype=np.int64))) if self.flatten else tuple(size[:-2]) + (1, 1)
 
     def forward(self, x: Tensor):
-        out_shape = tuple(x.size[:-2]) + (1, 1)
-        return _values(self, self._run("global_average_pool_forward", [x], out_shape, self.dtype))
+        return _values(self, self._run("global_average_pool_forward", [x], self._out_shape(x.size), self.dtype))
 
     def forward_(self, x: Tensor_):
-        return _values(self, Tensor_(*(tuple(x.size[:-2]) + (1, 1)), dtype=self.dtype))
+        return _values(self, Tensor_(*self._out_shape(x.size), dtype=self.dtype))
 
 
 class DynamicQuantizeLinear(Ops):

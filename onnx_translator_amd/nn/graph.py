@@ -207,6 +207,7 @@ class Graph:
             if pool_qdq:
                 self._fuse_pool_qdq(shapes)
         if elementwise:
+            self._fuse_gap_flatten(shapes, self._consumers())
             self._fuse_runs(shapes, self._consumers())
 
     def _fold_constants(self):
@@ -377,6 +378,32 @@ class Graph:
             replace[c.name] = fused
             drop.add(fq.name)
             self.fused_runs.append([c.name, fq.name])
+        out = [replace.get(o.name, o) for o in ops if o.name not in drop]
+        self.ops = OrderedDict((o.name, o) for o in out)
+
+    def _fuse_gap_flatten(self, shapes, consumers):
+        """GlobalAveragePool -> Flatten(axis 1) with the pooled [N, C, 1, 1] tensor
+        read by the Flatten only: the pool writes the [N, C] output itself (same
+        bytes), and the Flatten's copy goes."""
+        ops = list(self.ops.values())
+        producer = {o: op for op in ops for o in op.outputs}
+        replace, drop = {}, set()
+        for fl in ops:
+            if type(fl) is not Op.Flatten or fl.axis not in (1, -3):
+                continue
+            x = fl.inputs[0]
+            gp = producer.get(x)
+            if type(gp) is not Op.GlobalAveragePool or gp.flatten or gp.name in replace:
+                continue
+            if consumers.get(x, 0) != 1 or x in self.output_name or len(shapes.get(x, ((),))[0]) != 4:
+                continue
+            if shapes[x][1] != shapes[fl.outputs[0]][1]:
+                continue
+            fused = Op.GlobalAveragePool(list(gp.inputs), list(fl.outputs), gp.dtype, gp.version, flatten=True)
+            fused.name = f"GlobalAveragePool.{gp.name}+{fl.name}"
+            replace[gp.name] = fused
+            drop.add(fl.name)
+            self.fused_runs.append([gp.name, fl.name])
         out = [replace.get(o.name, o) for o in ops if o.name not in drop]
         self.ops = OrderedDict((o.name, o) for o in out)
 

@@ -106,7 +106,7 @@ def test_importer_mapping_and_shapes():
     out = g.forward_(Tensor_(2, 3, 64, 64, dtype="float32"))
     assert out.size == (2, 1000) and out.dtype == "float32"
     g.fuse_elementwise()._fuse([Tensor_(2, 3, 64, 64, dtype="float32")])
-    assert g.fused_runs == [["RELU.1", "ADD.0"]]
+    assert g.fused_runs == [["GlobalAveragePool.0", "Flatten.0"], ["RELU.1", "ADD.0"]]
 
 
 def test_conv_epilogue_and_fold_passes(monkeypatch):
@@ -219,6 +219,23 @@ def test_conv_qdq_pass(monkeypatch):
         seen.update(o.outputs)
 
 
+def test_gap_flatten_pass():
+    """Placeholder-shape run: GlobalAveragePool -> Flatten(axis 1) becomes one
+    GlobalAveragePool writing the [N, C] tensor under the Flatten's name."""
+    from onnx_translator_amd.nn import Graph, Tensor_
+    from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
+    m = resnet_qdq_model(batch=3, image=32)
+    g = Graph(ONNXImport(m), ["input"], ["output"], initializers=initializers(m))
+    shapes = g._edge_shapes([Tensor_(3, 3, 32, 32, dtype="float32")])
+    g._fuse_gap_flatten(shapes, g._consumers())
+    names = [type(o).__name__ for o in g.ops.values()]
+    assert "Flatten" not in names
+    gap = next(o for o in g.ops.values() if type(o).__name__ == "GlobalAveragePool")
+    assert gap.flatten and gap.outputs == ["flat"] and gap.inputs == ["block4.out"]
+    assert tuple(gap.forward_(Tensor_(3, 512, 1, 1, dtype="float32"))["tensor"].size) == (3, 512)
+    assert g.fused_runs == [["GlobalAveragePool.0", "Flatten.0"]]
+
+
 def test_toy_graph_oracle_closed_form(oracle_lib):
     rng = np.random.default_rng(0)
     x = rng.normal(0, 1, (1, 3, 32, 32)).astype(np.float32)
@@ -303,7 +320,8 @@ def test_resnet_qdq_graph(hip, oracle_lib, exact):
     # the activation QuantizeLinear -> DequantizeLinear pairs in one pass, and on
     # request the activation dequantisation folded into the convolutions) keeps
     # the node-by-node bits
-    assert len(g.fused_runs) == 12 and len(g.folded) == 7
+    assert len(g.fused_runs) == 13 and len(g.folded) == 7
+    assert not any(type(o).__name__ == "Flatten" for o in g.ops.values())
     assert sum(type(o).__name__ == "QuantizeDequantize" for o in g.ops.values()) == 1
     assert sum(type(o).__name__ == "FusedConvQDQ" for o in g.ops.values()) == 3
     assert np.array_equal(probs.view(np.uint32), unfused.view(np.uint32))
@@ -313,7 +331,7 @@ def test_resnet_qdq_graph(hip, oracle_lib, exact):
         with_pool = gp.forward(x).numpy()
     finally:
         hip.set_exact(False)
-    assert sum(type(o).__name__ == "MaxPoolQDQ" for o in gp.ops.values()) == 1 and len(gp.fused_runs) == 13
+    assert sum(type(o).__name__ == "MaxPoolQDQ" for o in gp.ops.values()) == 1 and len(gp.fused_runs) == 14
     assert np.array_equal(with_pool.view(np.uint32), unfused.view(np.uint32))
     gq = load_graph(m, fuse=False).fuse(dequantize_conv=True)
     hip.set_exact(exact)
@@ -321,7 +339,7 @@ def test_resnet_qdq_graph(hip, oracle_lib, exact):
         with_dq = gq.forward(x).numpy()
     finally:
         hip.set_exact(False)
-    assert len(gq.fused_runs) == 12
+    assert len(gq.fused_runs) == 13
     assert np.array_equal(with_dq.view(np.uint32), unfused.view(np.uint32))
     env = run_model(oracle_lib, m, {"input": (x, "float32")})
     ref = env["output"][0]
