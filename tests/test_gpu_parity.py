@@ -413,6 +413,33 @@ def test_conv_fused_qdq(hip, oracle_lib, case, exact):
         assert (diff > 0).mean() < 0.01, f"{tag}: {(diff > 0).mean():.4f} of the values differ"
 
 
+# Config-5 sizes (batch 64): block 1's 3x3 conv (full grid of 64x128 tap-blocked tiles)
+# and block 3's strided 3x3 conv (5 k-slices and the 16-byte reduction) with the Relu,
+# residual and fake quantization of the graph; fused == sequence bit for bit.
+CONV_QDQ_FULL = [("block1", (64, 64, 56, 56), (64, 64, 3, 3), [1, 1]),
+                 ("block3", (64, 128, 28, 28), (256, 128, 3, 3), [2, 2])]
+
+
+@pytest.mark.parametrize("case", CONV_QDQ_FULL, ids=[c[0] for c in CONV_QDQ_FULL])
+def test_conv_fused_qdq_config5_size(hip, case):
+    tag, xs, ws, strides = case
+    rng = np.random.default_rng(xs[1] + ws[0])
+    x = np.maximum(rng.normal(0, 1, xs), 0).astype(np.float32)
+    w = rng.normal(0, np.sqrt(2 / (ws[1] * 9)), ws).astype(np.float32)
+    b = rng.normal(0, 1 / 64, (ws[0],)).astype(np.float32)
+    OH = (xs[2] + 2 - 3) // strides[0] + 1
+    skip = rng.normal(0, 1, (xs[0], ws[0], OH, OH)).astype(np.float32)
+    qs, zp = np.array([8 / 255], np.float32), np.array([0], np.uint8)
+    got = hip.conv_fused_qdq(x, w, b, skip, True, qs, zp, qs, zp, "uint8", [1, 1, 1, 1], strides)
+    y = hip.conv_fused(x, w, b, skip, True, "float32", [1, 1, 1, 1], strides)
+    seq = hip.qdq_fused(y, qs, zp, qs, zp, "uint8")
+    assert np.array_equal(got.view(np.uint32), seq.view(np.uint32)), f"{tag}: fused differs from the sequence"
+    # the fake-quantized values are multiples of the scale in [0, 255 * scale]
+    codes = got / np.float32(8 / 255)
+    assert np.all(np.abs(codes - np.rint(codes)) < 1e-3) and got.min() >= 0 and got.max() <= 8.0 + 1e-6
+    assert (got > 0).mean() > 0.3
+
+
 # max_pool_qdq_forward: Y = max_pool_forward(X) and Yq = quantize_dequantize_linear_forward(Y)
 # bit for bit (the strip kernel for 3x3 / stride 2, the sequence otherwise), and equal to
 # the oracle's MaxPool -> QuantizeLinear -> DequantizeLinear (all three are exact).
