@@ -1354,6 +1354,7 @@ extern "C" void dequantize_conv2d_fused_forward(const Tensor* Xq, const Tensor* 
     if (!tensor_sane(Xq, name) || !tensor_sane(XScale, name) || !tensor_sane(W, name) || !tensor_sane(Y, name)) return;
     const bool has_z = XZero && XZero->data;
     if (has_z && !tensor_sane(XZero, name)) return;
+    if (Xq->ndim != 4) { set_error("%s: X must be 4-D (NCHW), got rank %d", name, Xq->ndim); return; }
     if (!ensure_device()) return;
     if (conv_xq_fast(Xq, XScale, has_z ? XZero : nullptr, W, B, Skip, Y, params)) {
         tensor_ops_hip_clear_error();
@@ -1362,9 +1363,9 @@ extern "C" void dequantize_conv2d_fused_forward(const Tensor* Xq, const Tensor* 
         return;
     }
     // the unfused sequence: DequantizeLinear into an f32 tensor, then the convolution
-    int shp[8];
-    for (int i = 0; i < Xq->ndim && i < 8; i++) shp[i] = Xq->shape[i];
-    Tensor* Xd = create_tensor_device_empty(shp, Xq->ndim, DTYPE_FLOAT32);
+    int shp[4];
+    for (int i = 0; i < 4; i++) shp[i] = Xq->shape[i];
+    Tensor* Xd = create_tensor_device_empty(shp, 4, DTYPE_FLOAT32);
     if (!Xd) return;
     tensor_ops_hip_clear_error();
     if (has_z) {

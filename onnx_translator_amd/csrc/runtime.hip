@@ -45,8 +45,16 @@ struct State {
     std::atomic<hipStream_t> user{nullptr};
     std::atomic<int> exact{0};
 
-    std::mutex mu;                                        // registry + pools
-    std::unordered_map<const void*, Mem> reg;
+    std::mutex mu;                                        // registries + pools
+    // Residency of data pointers (for classify): kind and the number of live
+    // headers over the pointer, so two headers over one buffer (a wrapper over
+    // a library tensor's data, or two wrappers) keep it classified until the
+    // last one is freed.
+    struct Res { Mem m; int refs; };
+    std::unordered_map<const void*, Res> reg;
+    // Ownership per header: how free_tensor releases the data of each header
+    // this library returned (kDevBorrowed: the caller owns the data).
+    std::unordered_map<const Tensor*, Mem> owners;
     std::multimap<size_t, void*> dev_free;
     std::unordered_map<void*, size_t> dev_size;
     size_t dev_cached = 0;
@@ -116,17 +124,30 @@ bool exact_mode() { return S().exact.load() != 0; }
 int num_cus() { return S().cus > 0 ? S().cus : 256; }
 
 // ---- memory -------------------------------------------------------------------------
-static void reg_put(const void* p, Mem m) {
+// Records a new header t over data p.  An owning kind (library allocation)
+// takes precedence over a borrowed one for the residency entry.
+static void reg_put(const Tensor* t, const void* p, Mem m) {
     std::lock_guard<std::mutex> g(S().mu);
-    S().reg[p] = m;
+    S().owners[t] = m;
+    auto it = S().reg.find(p);
+    if (it == S().reg.end()) {
+        S().reg.emplace(p, State::Res{m, 1});
+    } else {
+        it->second.refs++;
+        if (m != Mem::kDevBorrowed) it->second.m = m;
+    }
 }
 
-static bool reg_take(const void* p, Mem* m) {
+// Forgets header t; returns false for a header this library did not create.
+// *m is how t's data must be released.
+static bool reg_take(const Tensor* t, Mem* m) {
     std::lock_guard<std::mutex> g(S().mu);
-    auto it = S().reg.find(p);
-    if (it == S().reg.end()) return false;
-    *m = it->second;
-    S().reg.erase(it);
+    auto ot = S().owners.find(t);
+    if (ot == S().owners.end()) return false;
+    *m = ot->second;
+    S().owners.erase(ot);
+    auto it = S().reg.find(t->data);
+    if (it != S().reg.end() && --it->second.refs <= 0) S().reg.erase(it);
     return true;
 }
 
@@ -134,7 +155,7 @@ Mem classify(const void* p) {
     {
         std::lock_guard<std::mutex> g(S().mu);
         auto it = S().reg.find(p);
-        if (it != S().reg.end()) return it->second;
+        if (it != S().reg.end()) return it->second.m;
     }
     if (!S().ok) return Mem::kHostForeign;
     hipPointerAttribute_t a;
@@ -466,7 +487,7 @@ Tensor* create_tensor(int* shape, int ndim, DataType dtype) {
     }
     if (!p) { free(t->shape); free(t); return nullptr; }
     t->data = p;
-    reg_put(p, kind);
+    reg_put(t, p, kind);
     return t;
 }
 
@@ -484,7 +505,7 @@ static Tensor* device_tensor(int* shape, int ndim, DataType dtype, bool zero) {
         return nullptr;
     }
     t->data = p;
-    reg_put(p, Mem::kDevOwned);
+    reg_put(t, p, Mem::kDevOwned);
     return t;
 }
 
@@ -497,17 +518,24 @@ Tensor* tensor_wrap_device(void* device_ptr, int* shape, int ndim, DataType dtyp
     Tensor* t = new_header(shape, ndim, dtype);
     if (!t) return nullptr;
     t->data = device_ptr;
-    reg_put(device_ptr, Mem::kDevBorrowed);
+    reg_put(t, device_ptr, Mem::kDevBorrowed);
     return t;
 }
 
-// tensor_ops.c:440-450
+// tensor_ops.c:440-450.  Data is released according to how this header was
+// created (create_tensor: host memory; create_tensor_device*: HBM pool;
+// tensor_wrap_device: left to the caller), whatever other headers share it.
+// A header this library did not create is not touched (its memory cannot be
+// attributed to an allocator) and an error is recorded.
 void free_tensor(Tensor* t) {
     if (!t) return;
-    Mem m = Mem::kHostMalloc;
-    const bool known = t->data && reg_take(t->data, &m);
+    Mem m;
+    if (!reg_take(t, &m)) {
+        set_error("free_tensor: tensor was not created by this library");
+        return;
+    }
     if (t->data) {
-        if (!known || m == Mem::kHostMalloc) free(t->data);
+        if (m == Mem::kHostMalloc) free(t->data);
         else if (m == Mem::kHostPinned) pinned_free(t->data);
         else if (m == Mem::kDevOwned) pool_free(t->data);
         // kDevBorrowed: caller owns the memory.

@@ -115,8 +115,10 @@ class Graph:
         return args
 
     def _run(self, inputs, method: str):
-        buf: Dict[str, object] = dict(self.initializers) if method == "forward" else {
-            k: Tensor_(*v.size, dtype=v.dtype) for k, v in self.initializers.items()}
+        # Shape propagation also sees the initializers themselves: they carry size
+        # and dtype like a placeholder, and operators whose output shape depends
+        # on a value (Reshape's shape input) read it.
+        buf: Dict[str, object] = dict(self.initializers)
         for na, t in zip(self.input_name, inputs):
             buf[na] = t
         pending = self._consumers()
@@ -176,7 +178,7 @@ class Graph:
 
     def _edge_shapes(self, inputs) -> Dict[str, tuple]:
         shapes: Dict[str, tuple] = {k: (tuple(v.size), v.dtype) for k, v in self.initializers.items()}
-        buf = {k: Tensor_(*v.size, dtype=v.dtype) for k, v in self.initializers.items()}
+        buf: Dict[str, object] = dict(self.initializers)     # value-dependent shapes (Reshape) read them
         for na, t in zip(self.input_name, inputs):
             buf[na] = Tensor_(*t.size, dtype=t.dtype)
             shapes[na] = (tuple(t.size), t.dtype)
@@ -352,6 +354,17 @@ class Graph:
         out = [replace.get(o.name, o) for o in ops if o.name not in drop]
         self.ops = OrderedDict((o.name, o) for o in out)
 
+    def _ready_before(self, ops, name, edges) -> bool:
+        """True when every edge is a graph input, an initializer, or an output of an
+        operator placed before ``name`` in ``ops`` (so a fused operator put at
+        ``name``'s position can read it)."""
+        before = set(self.input_name) | set(self.initializers)
+        for op in ops:
+            if op.name == name:
+                break
+            before.update(op.outputs)
+        return all(not e or e in before for e in edges)
+
     def _fuse_conv_qdq(self, shapes, consumers):
         """Conv / FusedConv (f32) whose output is read only by a QuantizeDequantize
         with uint8 / int8 codes: one FusedConvQDQ in the convolution's place that
@@ -369,6 +382,8 @@ class Graph:
                 continue
             if consumers.get(x, 0) != 1 or x in self.output_name or x in fq.inputs[1:]:
                 continue
+            if not self._ready_before(ops, c.name, fq.inputs[1:5]):
+                continue                       # a scale / zero point is produced after the conv
             b = c.inputs[2] if len(c.inputs) > 2 else ""
             skip = c.inputs[3] if type(c) is Op.FusedConv and len(c.inputs) > 3 else ""
             relu = c.relu if type(c) is Op.FusedConv else 0
@@ -422,6 +437,8 @@ class Graph:
             mp = producer.get(x)
             if type(mp) is not Op.MaxPool or mp.dtype != "float32" or mp.name in replace or x in fq.inputs[1:]:
                 continue
+            if not self._ready_before(ops, mp.name, fq.inputs[1:5]):
+                continue                       # a scale / zero point is produced after the pool
             fused = Op.MaxPoolQDQ([mp.inputs[0]] + list(fq.inputs[1:5]), [x, fq.outputs[0]], mp.kernel_shape,
                                   mp.pads, mp.strides, mp.dtype, fq.code_dtype, mp.dilations)
             fused.name = f"MaxPoolQDQ.{mp.name}+{fq.name}"

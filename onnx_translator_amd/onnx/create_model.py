@@ -25,7 +25,7 @@ import argparse
 
 import numpy as np
 
-from .proto import (FLOAT, INT8, UINT8, GraphProto, ModelProto, NodeProto, TensorProto, ValueInfoProto,
+from .proto import (FLOAT, INT8, INT64, UINT8, GraphProto, ModelProto, NodeProto, TensorProto, ValueInfoProto,
                     make_attribute, save)
 
 
@@ -55,6 +55,19 @@ def comprehensive_model() -> ModelProto:
     g = GraphProto("main_graph", b.nodes, [], [ValueInfoProto("input_x", FLOAT, [1, 3, 32, 32]),
                                                ValueInfoProto("input_y", FLOAT, [1, 1, 1, 32])],
                    [ValueInfoProto("output", FLOAT, [1, 3, 32, 32])])
+    return ModelProto(g, producer_name="onnx_translator_amd")
+
+
+def reshape_model(batch: int = 2) -> ModelProto:
+    """``y = Reshape(Relu(x), [batch, -1])`` then ``Cos``: x f32 [batch, 4, 6, 6], the
+    target shape an int64 initializer (exercises value-dependent shapes in the graph)."""
+    b = _Builder()
+    b.init("target", np.array([batch, -1], np.int64), INT64)
+    b.node("Relu", ["x"], ["r"])
+    b.node("Reshape", ["r", "target"], ["flat"])
+    b.node("Cos", ["flat"], ["y"])
+    g = GraphProto("reshape_graph", b.nodes, b.inits, [ValueInfoProto("x", FLOAT, [batch, 4, 6, 6])],
+                   [ValueInfoProto("y", FLOAT, [batch, 144])])
     return ModelProto(g, producer_name="onnx_translator_amd")
 
 

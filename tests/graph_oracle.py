@@ -57,6 +57,11 @@ def run_model(o, model, feeds: dict):
             axis = n.attr("axis", 1)
             shape = (int(np.prod(x.shape[:axis])), int(np.prod(x.shape[axis:])))
             out = (o.flatten(x, xdt, shape), xdt)
+        elif t == "Reshape":
+            target = [int(v) for v in env[n.inputs[1]][0].reshape(-1)]
+            known = int(np.prod([v for v in target if v != -1]))
+            shape = tuple(x.size // known if v == -1 else v for v in target)
+            out = (o.flatten(x, xdt, shape, name="reshape"), xdt)
         elif t == "Gemm":
             w, wdt = env[n.inputs[1]]
             c, cdt = env[n.inputs[2]] if len(n.inputs) > 2 else (None, "float32")

@@ -109,3 +109,51 @@ def test_no_gpu_fails_loudly(lib):
     x = Tensor(2, 2, dtype="float32", data=np.ones((2, 2), np.float32))
     with pytest.raises(RuntimeError):
         ADD([], [], "float32").forward(x, x)
+
+
+def test_free_tensor_ownership_per_header(lib):
+    """Each header releases only what it owns: two wrappers over one buffer, and a
+    wrapper over a library tensor's data, can be freed in either order."""
+    L = lib.lib
+    L.tensor_wrap_device.restype = O.PT
+    L.tensor_wrap_device.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int]
+    L.tensor_ops_hip_clear_error.argtypes = []
+    buf = np.arange(16, dtype=np.float32)
+    shp = (ctypes.c_int * 1)(16)
+    w1 = L.tensor_wrap_device(buf.ctypes.data, shp, 1, O.F32)
+    w2 = L.tensor_wrap_device(buf.ctypes.data, shp, 1, O.F32)
+    L.free_tensor(w1)
+    L.free_tensor(w2)                     # must not free() the caller's buffer
+    assert np.array_equal(buf, np.arange(16, dtype=np.float32))
+    for owner_first in (True, False):
+        t = lib.tensor(np.ones(16, np.float32), O.F32)
+        w = L.tensor_wrap_device(t.contents.data, shp, 1, O.F32)
+        if owner_first:
+            L.free_tensor(t)
+            L.free_tensor(w)
+        else:
+            L.free_tensor(w)
+            assert np.array_equal(lib.read(t, O.F32), np.ones(16, np.float32))
+            L.free_tensor(t)
+    # a header the library did not create is left alone, with an error
+    foreign = O.CTensor(ctypes.c_void_p(buf.ctypes.data), ctypes.cast(shp, ctypes.POINTER(ctypes.c_int)), 1, 16, O.F32)
+    L.tensor_ops_hip_clear_error()
+    L.free_tensor(ctypes.byref(foreign))
+    assert "not created by this library" in lib.last_error()
+    L.tensor_ops_hip_clear_error()
+
+
+def test_dequantize_conv_rejects_non_4d_input(lib):
+    """A rank other than 4 is an error before any allocation (ranks above 8 once
+    overran a fixed shape buffer on the unfused path)."""
+    L = lib.lib
+    xq = lib.tensor(np.zeros((1,) * 9, np.uint8), O.U8)
+    s = lib.tensor(np.ones(1, np.float32), O.F32)
+    w = lib.tensor(np.ones((1, 1, 1, 1), np.float32), O.F32)
+    y = lib.empty((1, 1, 1, 1), O.F32)
+    L.tensor_ops_hip_clear_error()
+    L.dequantize_conv2d_fused_forward(xq, s, O.PT(), w, O.PT(), O.PT(), 0, y, ctypes.POINTER(O.CConvParams)())
+    assert "must be 4-D" in lib.last_error()
+    L.tensor_ops_hip_clear_error()
+    for t in (xq, s, w, y):
+        L.free_tensor(t)

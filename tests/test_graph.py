@@ -12,7 +12,7 @@ import pytest
 
 from oracle import oracle as O
 from onnx_translator_amd.onnx import proto as P
-from onnx_translator_amd.onnx.create_model import comprehensive_model, resnet_qdq_model, woq_gemm_model
+from onnx_translator_amd.onnx.create_model import comprehensive_model, reshape_model, resnet_qdq_model, woq_gemm_model
 from tests.graph_oracle import run_model
 from tests.helpers import assert_bitexact, assert_close
 
@@ -219,6 +219,36 @@ def test_conv_qdq_pass(monkeypatch):
         seen.update(o.outputs)
 
 
+def test_conv_qdq_pass_needs_parameters_before_the_conv(monkeypatch):
+    """A QuantizeLinear scale produced by a node after the Conv cannot be read at
+    the Conv's position, so that Conv -> Q -> DQ is left unfused."""
+    from onnx_translator_amd.nn import Graph, Tensor_
+    from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
+    from onnx_translator_amd.onnx.create_model import _Builder
+    from onnx_translator_amd.onnx.proto import FLOAT, UINT8, GraphProto, ModelProto, ValueInfoProto
+    b = _Builder()
+    b.init("w", np.ones((4, 2, 3, 3), np.float32), FLOAT)
+    b.init("s0", np.array([0.05], np.float32), FLOAT)
+    b.init("zp", np.zeros(1, np.uint8), UINT8)
+    b.node("Conv", ["x", "w"], ["c"], pads=[1, 1, 1, 1])
+    b.node("Abs", ["s0"], ["s"])                       # the scale edge appears after the conv
+    b.node("QuantizeLinear", ["c", "s", "zp"], ["q"])
+    b.node("DequantizeLinear", ["q", "s", "zp"], ["y"])
+    m = ModelProto(GraphProto("late_scale", b.nodes, b.inits, [ValueInfoProto("x", FLOAT, [1, 2, 8, 8])],
+                              [ValueInfoProto("y", FLOAT, [1, 4, 8, 8])]))
+    g = Graph(ONNXImport(m), ["x"], ["y"], initializers=initializers(m))
+    shapes = g._edge_shapes([Tensor_(1, 2, 8, 8, dtype="float32")])
+    g._fuse_qdq(shapes, g._consumers())
+    assert "QuantizeDequantize" in [type(o).__name__ for o in g.ops.values()]
+    g._fuse_conv_qdq(shapes, g._consumers())
+    names = [type(o).__name__ for o in g.ops.values()]
+    assert "FusedConvQDQ" not in names and "CONV" in [n.upper() for n in names]
+    seen = {"x"} | set(g.initializers)
+    for o in g.ops.values():
+        assert all((not na) or na in seen for na in o.inputs), o.name
+        seen.update(o.outputs)
+
+
 def test_gap_flatten_pass():
     """Placeholder-shape run: GlobalAveragePool -> Flatten(axis 1) becomes one
     GlobalAveragePool writing the [N, C] tensor under the Flatten's name."""
@@ -234,6 +264,37 @@ def test_gap_flatten_pass():
     assert gap.flatten and gap.outputs == ["flat"] and gap.inputs == ["block4.out"]
     assert tuple(gap.forward_(Tensor_(3, 512, 1, 1, dtype="float32"))["tensor"].size) == (3, 512)
     assert g.fused_runs == [["GlobalAveragePool.0", "Flatten.0"]]
+
+
+def test_reshape_shapes_from_initializer():
+    """Shape propagation (used by the graph passes at the first forward) reads the
+    Reshape target from its initializer."""
+    from onnx_translator_amd.nn import Graph, Tensor_
+    from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
+    m = reshape_model(batch=3)
+    g = Graph(ONNXImport(m), ["x"], ["y"], initializers=initializers(m))
+    shapes = g._edge_shapes([Tensor_(3, 4, 6, 6, dtype="float32")])
+    assert shapes["flat"] == ((3, 144), "float32") and shapes["y"] == ((3, 144), "float32")
+    assert tuple(g.forward_(Tensor_(3, 4, 6, 6, dtype="float32")).size) == (3, 144)
+
+
+def test_reshape_graph_oracle(oracle_lib):
+    x = np.random.default_rng(0).normal(0, 2, (2, 4, 6, 6)).astype(np.float32)
+    env = run_model(oracle_lib, reshape_model(), {"x": (x, "float32")})
+    want = np.cos(np.maximum(x, 0).reshape(2, -1))
+    np.testing.assert_allclose(env["y"][0], want, atol=4e-7)
+
+
+@pytest.mark.gpu
+def test_reshape_graph_on_device(hip, oracle_lib):
+    """An imported model with a Reshape runs with the default graph passes on."""
+    from onnx_translator_amd.nn.ONNXImport import load_graph
+    m = reshape_model()
+    x = np.random.default_rng(1).normal(0, 2, (2, 4, 6, 6)).astype(np.float32)
+    out = load_graph(m).forward(x)
+    env = run_model(oracle_lib, m, {"x": (x, "float32")})
+    assert tuple(out.size) == (2, 144)
+    assert_bitexact(out.numpy(), env["y"][0], O.F32, what="reshape graph")
 
 
 def test_toy_graph_oracle_closed_form(oracle_lib):
