@@ -233,89 +233,133 @@ def bench_loop(torch, fn, iters, warm=3, warm_ms=50.0):
     return a.elapsed_time(b) / iters
 
 
-def run_suite(lib, torch):
-    """Other configs: one line per operator, achieved vs roofline."""
+SUITE = ("add_f32_bcast", "mul_f32_bcast", "sub_f32_bcast", "div_f32_bcast", "relu_f32", "abs_f32", "cos_f32",
+         "chain7_f32_fused", "add_i32_f32_to_f64", "gemm_f32_4096", "gemm_f16_4096", "gemm_woq_int8_fused",
+         "gemm_woq_int8_unfused", "conv_stem7x7s2", "conv_3x3", "conv_1x1", "maxpool_3x3s2", "softmax_64x32000",
+         "global_avg_pool", "dynamic_quantize_linear", "graph_resnet_qdq_b64")
+
+
+def run_suite(lib, torch, only=None, cpu=None):
+    """Other configs: one line per operator, achieved vs roofline; with `cpu` (a
+    CpuLeg) each line also carries the reference on this host's cores."""
     L = lib.lib
     out = []
-    rng = np.random.default_rng(0)
+
+    def want(*names):
+        return only is None or any(n in only for n in names)
+
+    def emit(line, cpu_fn=None):
+        if cpu is not None and cpu_fn is not None:
+            line.update(cpu.measure(cpu_fn, line))
+        out.append(line)
+        print(f"bench: {line['op']} done", file=sys.stderr, flush=True)
+
     # Config 1: f32 elementwise on [8,64,56,56] (+ B [64,1,1]); 40 rotating sets (> 512 MB).
+    rng = np.random.default_rng(0)
     A = rng.uniform(-4, 4, (8, 64, 56, 56)).astype(np.float32)
     B = rng.uniform(-4, 4, (64, 1, 1)).astype(np.float32)
     Bd = (np.sign(B) * np.maximum(np.abs(B), 0.1)).astype(np.float32)
-    R = 40
-    As = [lib.dev(A, F32) for _ in range(R)]
-    Os = [lib.empty(list(A.shape), F32) for _ in range(R)]
-    tb, tbd = lib.dev(B, F32), lib.dev(Bd, F32)
     nb = A.size * 8
-    for name, fn in (("add", L.add_forward), ("mul", L.mul_forward), ("sub", L.sub_forward),
-                     ("div", L.div_forward)):
-        b = tbd if name == "div" else tb
-        ms = bench_loop(torch, lambda i: fn(As[i % R], b, Os[i % R]), 200)
-        out.append(op_line(f"{name}_f32_bcast", "config1 [8,64,56,56] (+) [64,1,1]", nb, ms, "hbm"))
-    for name, fn in (("relu", L.relu_forward), ("abs", L.abs_forward), ("cos", L.cos_forward)):
-        ms = bench_loop(torch, lambda i: fn(As[i % R], Os[i % R]), 200)
-        out.append(op_line(f"{name}_f32", "config1 [8,64,56,56]", nb, ms, "hbm"))
-    # The same chain fused into one kernel (bit-identical to the op-by-op chain):
-    # 4 B in + 4 B out per element, plus the two [64,1,1] operands.
-    steps = (CStep * 7)(CStep(0, 0, 0), CStep(2, 0, 0), CStep(1, 0, 0), CStep(3, 1, 0), CStep(4, 0, 0),
-                        CStep(5, 0, 0), CStep(6, 0, 0))
-    opnds = (PT * 2)(tb, tbd)
-    ms = bench_loop(torch, lambda i: L.elementwise_chain_forward(As[i % R], opnds, 2, steps, 7, Os[i % R]), 200)
-    out.append(op_line("chain7_f32_fused", "config1 Add>Mul>Sub>Div>Relu>Abs>Cos, one pass", nb, ms, "hbm"))
-    I = rng.integers(-(2 ** 31), 2 ** 31 - 1, A.shape, dtype=np.int64).astype(np.int32)
-    Is = [lib.dev(I, I32) for _ in range(20)]
-    O64 = [lib.empty(list(A.shape), F64) for _ in range(20)]
-    ms = bench_loop(torch, lambda i: L.add_forward(Is[i % 20], tb, O64[i % 20]), 100)
-    out.append(op_line("add_i32_f32_to_f64", "config1 int32 [8,64,56,56] + f32 [64,1,1]", A.size * 12, ms, "hbm"))
-    lib.check("config1")
-    for t in As + Os + Is + O64 + [tb, tbd]:
-        L.free_tensor(t)
+    c1 = [n for n in SUITE[:9]]
+    if want(*c1):
+        R = 40
+        As = [lib.dev(A, F32) for _ in range(R)]
+        Os = [lib.empty(list(A.shape), F32) for _ in range(R)]
+        tb, tbd = lib.dev(B, F32), lib.dev(Bd, F32)
+        for name, fn in (("add", L.add_forward), ("mul", L.mul_forward), ("sub", L.sub_forward),
+                         ("div", L.div_forward)):
+            if not want(f"{name}_f32_bcast"):
+                continue
+            b = tbd if name == "div" else tb
+            ms = bench_loop(torch, lambda i: fn(As[i % R], b, Os[i % R]), 200)
+            emit(op_line(f"{name}_f32_bcast", "config1 [8,64,56,56] (+) [64,1,1]", nb, ms, "hbm"),
+                 CpuLeg.binary(name, A, Bd if name == "div" else B))
+        for name, fn in (("relu", L.relu_forward), ("abs", L.abs_forward), ("cos", L.cos_forward)):
+            if not want(f"{name}_f32"):
+                continue
+            ms = bench_loop(torch, lambda i: fn(As[i % R], Os[i % R]), 200)
+            emit(op_line(f"{name}_f32", "config1 [8,64,56,56]", nb, ms, "hbm"), CpuLeg.unary(name, A))
+        if want("chain7_f32_fused"):
+            # The same chain fused into one kernel (bit-identical to the op-by-op chain):
+            # 4 B in + 4 B out per element, plus the two [64,1,1] operands.  The CPU
+            # figure is the reference's op-by-op chain (7 calls) over the same bytes.
+            steps = (CStep * 7)(CStep(0, 0, 0), CStep(2, 0, 0), CStep(1, 0, 0), CStep(3, 1, 0), CStep(4, 0, 0),
+                                CStep(5, 0, 0), CStep(6, 0, 0))
+            opnds = (PT * 2)(tb, tbd)
+            ms = bench_loop(torch, lambda i: L.elementwise_chain_forward(As[i % R], opnds, 2, steps, 7, Os[i % R]),
+                            200)
+            emit(op_line("chain7_f32_fused", "config1 Add>Mul>Sub>Div>Relu>Abs>Cos, one pass", nb, ms, "hbm"),
+                 CpuLeg.chain(A, B, Bd))
+        for t in As + Os:
+            L.free_tensor(t)
+        if want("add_i32_f32_to_f64"):
+            I = rng.integers(-(2 ** 31), 2 ** 31 - 1, A.shape, dtype=np.int64).astype(np.int32)
+            Is = [lib.dev(I, I32) for _ in range(20)]
+            O64 = [lib.empty(list(A.shape), F64) for _ in range(20)]
+            ms = bench_loop(torch, lambda i: L.add_forward(Is[i % 20], tb, O64[i % 20]), 100)
+            emit(op_line("add_i32_f32_to_f64", "config1 int32 [8,64,56,56] + f32 [64,1,1]", A.size * 12, ms, "hbm"),
+                 CpuLeg.binary("add", I, B, I32, F64))
+            for t in Is + O64:
+                L.free_tensor(t)
+        lib.check("config1")
+        for t in (tb, tbd):
+            L.free_tensor(t)
 
     # Config 3: Gemm 4096^3 transB=1 with bias, f32 and f16.
     rng = np.random.default_rng(2)
     K = 4096
-    a = rng.normal(0, 1 / 64, (4096, K)).astype(np.float32)
-    b = rng.normal(0, 1 / 64, (4096, K)).astype(np.float32)
-    c = rng.normal(0, 1 / 64, (4096,)).astype(np.float32)
     flops = 2 * 4096 ** 3
-    tc = lib.dev(c, F32)
-    for dt, peak in ((F32, MFMA_F32), (F16, MFMA_F16)):
-        aa = a if dt == F32 else a.astype(np.float16)
-        bb = b if dt == F32 else b.astype(np.float16)
-        ta, tbb = lib.dev(aa, dt), lib.dev(bb, dt)
-        ty = lib.empty([4096, 4096], dt)
-        ms = bench_loop(torch, lambda i: L.gemm_forward(ta, tbb, tc, ty, 1.0, 1.0, 0, 1), 20, 1)
-        out.append(op_line(f"gemm_{'f32' if dt == F32 else 'f16'}_4096", "config3 4096x4096x4096 transB=1 +bias",
-                           flops, ms, "mfma", peak))
-        for t in (ta, tbb, ty):
-            L.free_tensor(t)
-    lib.check("config3")
-    # Config 3 weight-only-quant variant: B int8 [4096,4096] with per-row (axis 0)
-    # scales, DequantizeLinear -> Gemm on A [256,4096]; fused (codes read in the
-    # Gemm) and unfused (f32 weight written, then read).
-    bw = rng.normal(0, 1 / 64, (4096, K))
-    sw = (np.abs(bw).max(axis=1) / 127).astype(np.float32)
-    bq = np.clip(np.rint(bw / sw[:, None]), -127, 127).astype(np.int8)
-    a = rng.normal(0, 1 / 64, (256, K)).astype(np.float32)
-    ta, tq, tbd = lib.dev(a, F32), lib.dev(bq, I8), lib.empty([4096, K], F32)
-    ts1, tz1 = lib.dev(sw, F32), lib.dev(np.zeros(4096, np.int8), I8)
-    ts2, tz2 = lib.dev(sw.reshape(-1, 1), F32), lib.dev(np.zeros((4096, 1), np.int8), I8)
-    ty = lib.empty([256, 4096], F32)
-    wflops = 2 * 256 * 4096 * K
-    ms = bench_loop(torch, lambda i: L.dequantize_gemm_forward(ta, tq, ts1, tz1, 0, tc, ty, 1.0, 1.0, 0, 1), 20, 2)
-    out.append(op_line("gemm_woq_int8_fused", "config3 WOQ A[256,4096] x int8 B[4096,4096]^T, axis-0 scales, +bias",
-                       wflops, ms, "mfma", MFMA_F32))
+    if want("gemm_f32_4096", "gemm_f16_4096", "gemm_woq_int8_fused", "gemm_woq_int8_unfused"):
+        a = rng.normal(0, 1 / 64, (4096, K)).astype(np.float32)
+        b = rng.normal(0, 1 / 64, (4096, K)).astype(np.float32)
+        c = rng.normal(0, 1 / 64, (4096,)).astype(np.float32)
+        tc = lib.dev(c, F32)
+        for dt, peak in ((F32, MFMA_F32), (F16, MFMA_F16)):
+            name = f"gemm_{'f32' if dt == F32 else 'f16'}_4096"
+            if not want(name):
+                continue
+            aa = a if dt == F32 else a.astype(np.float16)
+            bb = b if dt == F32 else b.astype(np.float16)
+            ta, tbb = lib.dev(aa, dt), lib.dev(bb, dt)
+            ty = lib.empty([4096, 4096], dt)
+            ms = bench_loop(torch, lambda i: L.gemm_forward(ta, tbb, tc, ty, 1.0, 1.0, 0, 1), 20, 1)
+            emit(op_line(name, "config3 4096x4096x4096 transB=1 +bias", flops, ms, "mfma", peak),
+                 CpuLeg.gemm(aa, bb, c, dt))
+            for t in (ta, tbb, ty):
+                L.free_tensor(t)
+        lib.check("config3")
+        # Config 3 weight-only-quant variant: B int8 [4096,4096] with per-row (axis 0)
+        # scales, DequantizeLinear -> Gemm on A [256,4096]; fused (codes read in the
+        # Gemm) and unfused (f32 weight written, then read).
+        bw = rng.normal(0, 1 / 64, (4096, K))
+        sw = (np.abs(bw).max(axis=1) / 127).astype(np.float32)
+        bq = np.clip(np.rint(bw / sw[:, None]), -127, 127).astype(np.int8)
+        a = rng.normal(0, 1 / 64, (256, K)).astype(np.float32)
+        wflops = 2 * 256 * 4096 * K
+        if want("gemm_woq_int8_fused", "gemm_woq_int8_unfused"):
+            ta, tq, tbd = lib.dev(a, F32), lib.dev(bq, I8), lib.empty([4096, K], F32)
+            ts1, tz1 = lib.dev(sw, F32), lib.dev(np.zeros(4096, np.int8), I8)
+            ts2, tz2 = lib.dev(sw.reshape(-1, 1), F32), lib.dev(np.zeros((4096, 1), np.int8), I8)
+            ty = lib.empty([256, 4096], F32)
+            woq_cpu = CpuLeg.woq(a, bq, sw, c)
+            if want("gemm_woq_int8_fused"):
+                ms = bench_loop(torch, lambda i: L.dequantize_gemm_forward(ta, tq, ts1, tz1, 0, tc, ty, 1.0, 1.0, 0, 1),
+                                20, 2)
+                emit(op_line("gemm_woq_int8_fused",
+                             "config3 WOQ A[256,4096] x int8 B[4096,4096]^T, axis-0 scales, +bias",
+                             wflops, ms, "mfma", MFMA_F32), woq_cpu)
 
-    def unfused(i):
-        L.dequantize_linear_forward(tq, ts2, tz2, tbd)
-        L.gemm_forward(ta, tbd, tc, ty, 1.0, 1.0, 0, 1)
-    ms = bench_loop(torch, unfused, 20, 2)
-    out.append(op_line("gemm_woq_int8_unfused", "config3 WOQ DequantizeLinear -> Gemm (f32 weight in HBM)",
-                       wflops, ms, "mfma", MFMA_F32))
-    lib.check("config3 woq")
-    for t in (ta, tq, tbd, ts1, tz1, ts2, tz2, ty):
-        L.free_tensor(t)
-    L.free_tensor(tc)
+            def unfused(i):
+                L.dequantize_linear_forward(tq, ts2, tz2, tbd)
+                L.gemm_forward(ta, tbd, tc, ty, 1.0, 1.0, 0, 1)
+            if want("gemm_woq_int8_unfused"):
+                ms = bench_loop(torch, unfused, 20, 2)
+                emit(op_line("gemm_woq_int8_unfused", "config3 WOQ DequantizeLinear -> Gemm (f32 weight in HBM)",
+                             wflops, ms, "mfma", MFMA_F32), woq_cpu)
+            lib.check("config3 woq")
+            for t in (ta, tq, tbd, ts1, tz1, ts2, tz2, ty):
+                L.free_tensor(t)
+        L.free_tensor(tc)
 
     # Config 4: conv layers + maxpool.
     rng = np.random.default_rng(3)
@@ -325,6 +369,8 @@ def run_suite(lib, torch):
         x = rng.normal(0, 1, xs).astype(np.float32)
         w = rng.normal(0, np.sqrt(2 / (ws[1] * ws[2] * ws[3])), ws).astype(np.float32)
         bias = rng.normal(0, 1 / 64, (ws[0],)).astype(np.float32)
+        if not want(f"conv_{tag}"):
+            continue
         OH = (xs[2] + pads[0] + pads[2] - ws[2]) // strides[0] + 1
         OW = (xs[3] + pads[1] + pads[3] - ws[3]) // strides[1] + 1
         tx, tw, tbias = lib.dev(x, F32), lib.dev(w, F32), lib.dev(bias, F32)
@@ -334,52 +380,61 @@ def run_suite(lib, torch):
                   ctypes.cast(keep[2], ctypes.POINTER(ctypes.c_int)), 1)
         fl = 2 * xs[0] * ws[0] * OH * OW * ws[1] * ws[2] * ws[3]
         ms = bench_loop(torch, lambda i: L.conv2d_forward(tx, tw, tbias, ty, ctypes.byref(p)), 5, 1)
-        out.append(op_line(f"conv_{tag}", f"config4 x{list(xs)} w{list(ws)}", fl, ms, "mfma", MFMA_F32))
+        emit(op_line(f"conv_{tag}", f"config4 x{list(xs)} w{list(ws)}", fl, ms, "mfma", MFMA_F32),
+             CpuLeg.conv(x, w, bias, pads, strides))
         for t in (tx, tw, tbias, ty):
             L.free_tensor(t)
-    x = rng.normal(0, 1, (32, 64, 112, 112)).astype(np.float32)
-    txs = [lib.dev(x, F32) for _ in range(4)]
-    tys = [lib.empty([32, 64, 56, 56], F32) for _ in range(4)]
-    keep = [ints([1, 1, 1, 1]), ints([2, 2]), ints([1, 1]), ints([3, 3])]
-    pp = Params(*[ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep])
-    ms = bench_loop(torch, lambda i: L.max_pool_forward(txs[i % 4], tys[i % 4], ctypes.byref(pp)), 40)
-    out.append(op_line("maxpool_3x3s2", "config4 [32,64,112,112] -> [32,64,56,56]", x.size * 4 + x.size, ms, "hbm"))
-    for t in txs + tys:
-        L.free_tensor(t)
+    if want("maxpool_3x3s2"):
+        x = rng.normal(0, 1, (32, 64, 112, 112)).astype(np.float32)
+        txs = [lib.dev(x, F32) for _ in range(4)]
+        tys = [lib.empty([32, 64, 56, 56], F32) for _ in range(4)]
+        keep = [ints([1, 1, 1, 1]), ints([2, 2]), ints([1, 1]), ints([3, 3])]
+        pp = Params(*[ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep])
+        ms = bench_loop(torch, lambda i: L.max_pool_forward(txs[i % 4], tys[i % 4], ctypes.byref(pp)), 40)
+        emit(op_line("maxpool_3x3s2", "config4 [32,64,112,112] -> [32,64,56,56]", x.size * 4 + x.size, ms, "hbm"),
+             CpuLeg.maxpool(x))
+        for t in txs + tys:
+            L.free_tensor(t)
     lib.check("config4")
 
     # Config 5: softmax [64,32000] axis 1 (rotating 20 sets > 320 MB).
-    rng = np.random.default_rng(4)
-    s = rng.normal(0, 3, (64, 32000)).astype(np.float32)
-    ts = [lib.dev(s, F32) for _ in range(20)]
-    to = [lib.empty([64, 32000], F32) for _ in range(20)]
-    ms = bench_loop(torch, lambda i: L.softmax_forward(ts[i % 20], to[i % 20], 1), 200)
-    out.append(op_line("softmax_64x32000", "config5 [64,32000] axis=1", s.size * 8, ms, "hbm"))
-    for t in ts + to:
-        L.free_tensor(t)
-    lib.check("config5")
+    if want("softmax_64x32000"):
+        rng = np.random.default_rng(4)
+        s = rng.normal(0, 3, (64, 32000)).astype(np.float32)
+        ts = [lib.dev(s, F32) for _ in range(20)]
+        to = [lib.empty([64, 32000], F32) for _ in range(20)]
+        ms = bench_loop(torch, lambda i: L.softmax_forward(ts[i % 20], to[i % 20], 1), 200)
+        emit(op_line("softmax_64x32000", "config5 [64,32000] axis=1", s.size * 8, ms, "hbm"), CpuLeg.softmax(s))
+        for t in ts + to:
+            L.free_tensor(t)
+        lib.check("config5")
 
     # Next rows: GlobalAveragePool at the config-5 classifier input and
     # DynamicQuantizeLinear over the config-2 activation tensor.
-    rng = np.random.default_rng(5)
-    g = rng.normal(0, 1, (64, 512, 7, 7)).astype(np.float32)
-    tg = [lib.dev(g, F32) for _ in range(20)]
-    to = [lib.empty([64, 512, 1, 1], F32) for _ in range(20)]
-    ms = bench_loop(torch, lambda i: L.global_average_pool_forward(tg[i % 20], to[i % 20]), 200)
-    out.append(op_line("global_avg_pool", "[64,512,7,7] -> [64,512,1,1]", g.size * 4 + 64 * 512 * 4, ms, "hbm"))
-    for t in tg + to:
-        L.free_tensor(t)
-    x = config2_input(np.random.default_rng(1))
-    tx = [lib.dev(x, F32) for _ in range(4)]
-    ty = [lib.empty(list(x.shape), U8) for _ in range(4)]
-    ts, tz = lib.empty([1], F32), lib.empty([1], U8)
-    ms = bench_loop(torch, lambda i: L.dynamic_quantize_linear_forward(tx[i % 4], ty[i % 4], ts, tz), 50)
-    # two reads of x (min / max, then quantize) and one write of the codes
-    out.append(op_line("dynamic_quantize_linear", "x f32 [32,512,1024] -> u8", x.size * 9, ms, "hbm"))
-    for t in tx + ty + [ts, tz]:
-        L.free_tensor(t)
+    if want("global_avg_pool"):
+        rng = np.random.default_rng(5)
+        g = rng.normal(0, 1, (64, 512, 7, 7)).astype(np.float32)
+        tg = [lib.dev(g, F32) for _ in range(20)]
+        to = [lib.empty([64, 512, 1, 1], F32) for _ in range(20)]
+        ms = bench_loop(torch, lambda i: L.global_average_pool_forward(tg[i % 20], to[i % 20]), 200)
+        emit(op_line("global_avg_pool", "[64,512,7,7] -> [64,512,1,1]", g.size * 4 + 64 * 512 * 4, ms, "hbm"),
+             CpuLeg.gap(g))
+        for t in tg + to:
+            L.free_tensor(t)
+    if want("dynamic_quantize_linear"):
+        x = config2_input(np.random.default_rng(1))
+        tx = [lib.dev(x, F32) for _ in range(4)]
+        ty = [lib.empty(list(x.shape), U8) for _ in range(4)]
+        ts, tz = lib.empty([1], F32), lib.empty([1], U8)
+        ms = bench_loop(torch, lambda i: L.dynamic_quantize_linear_forward(tx[i % 4], ty[i % 4], ts, tz), 50)
+        # two reads of x (min / max, then quantize) and one write of the codes
+        emit(op_line("dynamic_quantize_linear", "x f32 [32,512,1024] -> u8", x.size * 9, ms, "hbm"),
+             CpuLeg.dql(x))
+        for t in tx + ty + [ts, tz]:
+            L.free_tensor(t)
     lib.check("next rows")
-    out.append(run_graph(torch))
+    if want("graph_resnet_qdq_b64"):
+        emit(run_graph(torch), CpuLeg.graph())
     return out
 
 
@@ -421,9 +476,214 @@ def op_line(name, shape, work, ms, bound, peak=HBM_PEAK):
     rate = work / (ms * 1e-3)
     if bound == "hbm":
         return {"op": name, "shape": shape, "ms": round(ms, 5), "GB/s": round(rate / 1e9, 1),
-                "frac_hbm": round(rate / peak, 4)}
+                "frac_hbm": round(rate / peak, 4), "work": work}
     return {"op": name, "shape": shape, "ms": round(ms, 4), "TFLOP/s": round(rate / 1e12, 2),
-            "frac_mfma": round(rate / peak, 4)}
+            "frac_mfma": round(rate / peak, 4), "work": work}
+
+
+# ---------------------------------------------------------------- CPU leg ---
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    return int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+
+
+class CpuLeg:
+    """The reference tensor_ops.c (oracle/_ref, compiled from its source; the
+    restatement where it was never built) on this host's cores, timed on a bounded
+    sample of each suite line's workload, operands prepared as the reference's
+    Python layer passes them (broadcast to full size).  Each sample function
+    returns (fraction of the line's work it covers, seconds, description)."""
+
+    def __init__(self, budget_s=1.0):
+        from oracle import oracle as O
+        self.O = O
+        ref = O.reference()
+        self.lib, self.kind = (ref, "reference") if ref is not None else (O.oracle(), "port")
+        self.budget = budget_s
+        self.cores = cpu_threads()
+        self.model = cpu_model()
+
+    def timed(self, fn, max_runs=5):
+        """Median of repeated calls after one untimed call (first-touch faults)."""
+        fn()
+        ts, t_end = [], time.perf_counter() + self.budget
+        while len(ts) < max_runs and (not ts or time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)), len(ts)
+
+    def measure(self, sample_fn, line):
+        frac, secs, desc = sample_fn(self)
+        work = line.get("work")
+        if "images/s" in line:
+            value, unit = frac / secs, "images/s"
+        elif "GB/s" in line:
+            value, unit = work * frac / secs / 1e9, "GB/s"
+        else:
+            value, unit = work * frac / secs / 1e12, "TFLOP/s"
+        return {"cpu": {"value": float(f"{value:.4g}"), "unit": unit, "cores": self.cores, "kind": self.kind,
+                        "cpu_model": self.model, "sample": desc}}
+
+    # -- tensors on the CPU library -------------------------------------------------
+    def _t(self, arr, dt):
+        return self.lib.tensor(arr, dt)
+
+    def _free(self, *ts):
+        for t in ts:
+            if t:
+                self.lib.lib.free_tensor(t)
+
+    # -- samples (static constructors return closures over the inputs) ---------------
+    @staticmethod
+    def binary(name, a, b, dta=F32, dto=F32):
+        def run(leg):
+            bb = np.ascontiguousarray(np.broadcast_to(b, a.shape))
+            ta, tb = leg._t(a, dta), leg._t(bb, F32)
+            to = leg.lib.empty(a.shape, dto)
+            fn = getattr(leg.lib.lib, f"{name}_forward")
+            secs, n = leg.timed(lambda: fn(ta, tb, to))
+            leg._free(ta, tb, to)
+            return 1.0, secs, f"full size, B pre-broadcast, median of {n}"
+        return run
+
+    @staticmethod
+    def unary(name, a):
+        def run(leg):
+            ta, to = leg._t(a, F32), leg.lib.empty(a.shape, F32)
+            fn = getattr(leg.lib.lib, f"{name}_forward")
+            secs, n = leg.timed(lambda: fn(ta, to))
+            leg._free(ta, to)
+            return 1.0, secs, f"full size, median of {n}"
+        return run
+
+    @staticmethod
+    def chain(a, b, bd):
+        def run(leg):
+            L = leg.lib.lib
+            tb = leg._t(np.ascontiguousarray(np.broadcast_to(b, a.shape)), F32)
+            tbd = leg._t(np.ascontiguousarray(np.broadcast_to(bd, a.shape)), F32)
+            t0, t1 = leg._t(a, F32), leg.lib.empty(a.shape, F32)
+
+            def chain():
+                L.add_forward(t0, tb, t1)
+                L.mul_forward(t1, tb, t1)
+                L.sub_forward(t1, tb, t1)
+                L.div_forward(t1, tbd, t1)
+                L.relu_forward(t1, t1)
+                L.abs_forward(t1, t1)
+                L.cos_forward(t1, t1)
+            secs, n = leg.timed(chain)
+            leg._free(tb, tbd, t0, t1)
+            return 1.0, secs, f"the 7 reference calls op by op, full size, median of {n}"
+        return run
+
+    @staticmethod
+    def gemm(a, b, c, dt, rows=64):
+        def run(leg):
+            ta, tb = leg._t(a[:rows], dt), leg._t(b, dt)
+            tc = leg._t(c.reshape(1, -1), F32)
+            ty = leg.lib.empty((rows, b.shape[0]), dt)
+            secs, n = leg.timed(lambda: leg.lib.lib.gemm_forward(ta, tb, tc, ty, 1.0, 1.0, 0, 1), max_runs=3)
+            leg._free(ta, tb, tc, ty)
+            return rows / a.shape[0], secs, f"{rows} of {a.shape[0]} rows of A (same N, K), median of {n}"
+        return run
+
+    @staticmethod
+    def woq(a, bq, sw, c, rows=16):
+        def run(leg):
+            L = leg.lib.lib
+            tq = leg._t(bq, I8)
+            ts = leg._t(np.ascontiguousarray(np.broadcast_to(sw.reshape(-1, 1), bq.shape)), F32)
+            tz = leg._t(np.zeros(bq.shape, np.int8), I8)
+            tw = leg.lib.empty(bq.shape, F32)
+            t_dq, n1 = leg.timed(lambda: L.dequantize_linear_forward(tq, ts, tz, tw), max_runs=3)
+            ta, tc, ty = leg._t(a[:rows], F32), leg._t(c.reshape(1, -1), F32), leg.lib.empty((rows, bq.shape[0]), F32)
+            t_mm, n2 = leg.timed(lambda: L.gemm_forward(ta, tw, tc, ty, 1.0, 1.0, 0, 1), max_runs=3)
+            leg._free(tq, ts, tz, tw, ta, tc, ty)
+            full = t_dq + t_mm * a.shape[0] / rows
+            return 1.0, full, (f"DequantizeLinear of the full weight ({t_dq * 1e3:.0f} ms) + Gemm on {rows} of "
+                               f"{a.shape[0]} rows scaled to all rows")
+        return run
+
+    @staticmethod
+    def conv(x, w, bias, pads, strides, images=1):
+        def run(leg):
+            OH = (x.shape[2] + pads[0] + pads[2] - w.shape[2]) // strides[0] + 1
+            OW = (x.shape[3] + pads[1] + pads[3] - w.shape[3]) // strides[1] + 1
+            tx, tw, tb = leg._t(x[:images], F32), leg._t(w, F32), leg._t(bias, F32)
+            ty = leg.lib.empty((images, w.shape[0], OH, OW), F32)
+            p = leg.O.CConvParams()
+            keep = [leg.O._ints(pads), leg.O._ints(strides), leg.O._ints([1, 1])]
+            p.pads, p.strides, p.dilations = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep]
+            p.group = 1
+            secs, n = leg.timed(lambda: leg.lib.lib.conv2d_forward(tx, tw, tb, ty, ctypes.byref(p)), max_runs=3)
+            leg._free(tx, tw, tb, ty)
+            return images / x.shape[0], secs, f"{images} of {x.shape[0]} images, median of {n}"
+        return run
+
+    @staticmethod
+    def maxpool(x, images=4):
+        def run(leg):
+            tx, ty = leg._t(x[:images], F32), leg.lib.empty((images, x.shape[1], 56, 56), F32)
+            p = leg.O.CPoolParams()
+            keep = [leg.O._ints([1, 1, 1, 1]), leg.O._ints([2, 2]), leg.O._ints([1, 1]), leg.O._ints([3, 3])]
+            p.pads, p.strides, p.dilations, p.kernel_shape = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int))
+                                                              for k in keep]
+            secs, n = leg.timed(lambda: leg.lib.lib.max_pool_forward(tx, ty, ctypes.byref(p)))
+            leg._free(tx, ty)
+            return images / x.shape[0], secs, f"{images} of {x.shape[0]} images, median of {n}"
+        return run
+
+    @staticmethod
+    def softmax(s):
+        def run(leg):
+            ts, to = leg._t(s, F32), leg.lib.empty(s.shape, F32)
+            secs, n = leg.timed(lambda: leg.lib.lib.softmax_forward(ts, to, 1))
+            leg._free(ts, to)
+            return 1.0, secs, f"full size, median of {n}"
+        return run
+
+    @staticmethod
+    def gap(g):
+        def run(leg):
+            tg, to = leg._t(g, F32), leg.lib.empty(g.shape[:2] + (1, 1), F32)
+            secs, n = leg.timed(lambda: leg.lib.lib.global_average_pool_forward(tg, to))
+            leg._free(tg, to)
+            return 1.0, secs, f"full size, median of {n}"
+        return run
+
+    @staticmethod
+    def dql(x):
+        def run(leg):
+            tx, ty = leg._t(x, F32), leg.lib.empty(x.shape, U8)
+            ts, tz = leg.lib.empty((1,), F32), leg.lib.empty((1,), U8)
+            secs, n = leg.timed(lambda: leg.lib.lib.dynamic_quantize_linear_forward(tx, ty, ts, tz), max_runs=3)
+            leg._free(tx, ty, ts, tz)
+            return 1.0, secs, f"full size, median of {n}"
+        return run
+
+    @staticmethod
+    def graph(images=1):
+        def run(leg):
+            from onnx_translator_amd.onnx.create_model import resnet_qdq_model
+            from tests.graph_oracle import run_model
+            m = resnet_qdq_model(batch=images)
+            x = np.random.default_rng(4).normal(0, 1, (images, 3, 224, 224)).astype(np.float32)
+            secs, n = leg.timed(lambda: run_model(leg.lib, m, {"input": (x, "float32")}), max_runs=2)
+            return images, secs, (f"{images} image(s) node by node through the C ABI (the reference's per-op "
+                                  f"path, host copies included), median of {n}")
+        return run
 
 
 # ---------------------------------------------------------------- CPU leg ---
@@ -460,8 +720,9 @@ def cpu_baseline(budget_s=10.0):
         for t in group:
             L.free_tensor(t)
     L.free_tensor(tx)
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    threads = cpu_threads()
     return {"value": round(total_bytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "cpu_model": cpu_model(),
             "sample": f"{rounds} full round trips of the 4 Q/DQ variants on x f32 [32,512,1024] "
                       f"({elapsed:.1f} s of C calls, OpenMP threads={threads}, scale/zp pre-broadcast)"}
 
@@ -474,6 +735,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--only", default=None,
+                    help="comma-separated suite lines to run instead of the full run (no headline, no CPU leg), "
+                         f"e.g. for per-kernel profiles; names: {', '.join(SUITE)}")
+    ap.add_argument("--cpu-line-budget", type=float, default=1.0,
+                    help="seconds of reference calls per suite line in the CPU leg")
     ap.add_argument("--graph-only", action="store_true",
                     help="only run the config-5 ONNX graph (batch 64, 10 timed forwards) and print its line "
                          "(for per-kernel profiles of the graph)")
@@ -510,6 +776,15 @@ def main():
     if args.graph_only:
         print(json.dumps(run_graph(torch)), flush=True)
         return
+    if args.only:
+        only = [n.strip() for n in args.only.split(",") if n.strip()]
+        unknown = [n for n in only if n not in SUITE]
+        if unknown:
+            print(f"bench.py: unknown suite line(s) {unknown}; names: {', '.join(SUITE)}", file=sys.stderr)
+            sys.exit(2)
+        for line in run_suite(lib, torch, only=set(only)):
+            print(json.dumps(line), flush=True)
+        return
     print("bench: headline Q/DQ round trips ...", file=sys.stderr, flush=True)
     h = run_headline(lib, torch, args.steps, args.warmup)
     value = h["bytes_per_step"] / (h["ms_per_step"] * 1e-3) / 1e9
@@ -522,7 +797,7 @@ def main():
     ops = []
     if not args.no_suite:
         print("bench: per-op suite ...", file=sys.stderr, flush=True)
-        ops = run_suite(lib, torch)
+        ops = run_suite(lib, torch, cpu=None if args.no_cpu else CpuLeg(args.cpu_line_budget))
     cpu = None
     if not args.no_cpu:
         print("bench: CPU baseline ...", file=sys.stderr, flush=True)

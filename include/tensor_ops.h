@@ -165,9 +165,12 @@ const char* tensor_ops_hip_last_error(void);
 void tensor_ops_hip_clear_error(void);
 /* Library version string. */
 const char* tensor_ops_hip_version(void);
-/* Gemm/Conv precision mode: 0 = MFMA fp32/fp16 accumulate (default, tolerance class);
- * 1 = exact replica of the reference (double accumulate, sequential k, bit-identical). */
+/* Gemm/Conv precision mode of the calling thread: 0 = MFMA fp32/fp16 accumulate
+ * (default, tolerance class); 1 = exact replica of the reference (double accumulate,
+ * sequential k, bit-identical).  Each thread starts from TENSOR_OPS_HIP_EXACT
+ * (unset: 0); setting it affects only calls made by the same thread. */
 void tensor_ops_hip_set_exact(int exact);
+int tensor_ops_hip_get_exact(void);
 /* Fused elementwise chain: one pass over X that applies the steps in order to the
  * running value v; binary steps take operands[operand] broadcast to X's shape and
  * compute v op b (b op v when reversed).  Every step rounds to float32 as the

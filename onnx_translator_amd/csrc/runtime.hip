@@ -43,7 +43,6 @@ struct State {
     int ndev = 0, dev = 0, cus = 0;
     hipStream_t own = nullptr;
     std::atomic<hipStream_t> user{nullptr};
-    std::atomic<int> exact{0};
 
     std::mutex mu;                                        // registries + pools
     // Residency of data pointers (for classify): kind and the number of live
@@ -96,8 +95,6 @@ static void do_init() {
     }
     if (hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, s.dev) != hipSuccess)
         s.cus = 256;
-    const char* ex = getenv("TENSOR_OPS_HIP_EXACT");
-    if (ex && *ex == '1') s.exact = 1;
     s.ok = true;
 }
 
@@ -120,7 +117,18 @@ hipStream_t stream() {
     return u ? u : s.own;
 }
 
-bool exact_mode() { return S().exact.load() != 0; }
+// Precision mode per calling thread (-1: not set yet, take the process default).
+static thread_local int t_exact = -1;
+
+static int default_exact() {
+    const char* ex = getenv("TENSOR_OPS_HIP_EXACT");
+    return (ex && *ex == '1') ? 1 : 0;
+}
+
+bool exact_mode() {
+    if (t_exact < 0) t_exact = default_exact();
+    return t_exact != 0;
+}
 int num_cus() { return S().cus > 0 ? S().cus : 256; }
 
 // ---- memory -------------------------------------------------------------------------
@@ -617,7 +625,9 @@ void tensor_ops_hip_clear_error(void) { t_err.clear(); }
 
 const char* tensor_ops_hip_version(void) { return "libtensor_ops_hip 0.1 (gfx950)"; }
 
-void tensor_ops_hip_set_exact(int exact) { S().exact.store(exact ? 1 : 0); }
+void tensor_ops_hip_set_exact(int exact) { t_exact = exact ? 1 : 0; }
+
+int tensor_ops_hip_get_exact(void) { return exact_mode() ? 1 : 0; }
 
 // tensor_ops.c:763-807 — builds the table once and uploads it when a GPU is present.
 void init_cos_lut(void) {

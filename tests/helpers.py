@@ -211,6 +211,20 @@ class HipLib(O.CpuLib):
             raise RuntimeError(err)
         return out
 
+    def binary_raw(self, name, a, dta, b, dtb, dto):
+        """add/sub/mul/div_forward with the operands passed un-broadcast (the
+        library broadcasts in-kernel); the output has the broadcast shape."""
+        a, b = np.asarray(a), np.asarray(b)
+        shape = np.broadcast_shapes(a.shape, b.shape)
+        return self._run(getattr(self.lib, name + "_forward"), [(a, dta), (b, dtb)], shape, dto)
+
+    def qdq_axis(self, name, x, dtx, s, z, dtz, dty, axis):
+        """quantize / dequantize_linear_axis_forward with 1-D Scale / ZeroPoint."""
+        x = np.asarray(x)
+        return self._run(getattr(self.lib, name + "_linear_axis_forward"),
+                         [(x, dtx), (np.atleast_1d(s), O.F32), (np.atleast_1d(z), dtz)], x.shape, dty,
+                         ctypes.c_int(axis))
+
     def qdq1(self, name, x, dtx, s, z, dtz, dty):
         """quantize / dequantize_linear_forward with Scale and ZeroPoint passed as
         given (not broadcast to X's shape: one-element tensors stay per-tensor)."""

@@ -49,6 +49,29 @@ def test_config1_int32_promotion(hip, oracle_lib, wide):
                         dt, what=f"int32+f32 -> {dt}")
 
 
+# The calls bench.py times pass the [64,1,1] operand un-broadcast, so the library
+# broadcasts it in-kernel (k_bin_f32_v4 / k_bin_typed over a collapsed stride
+# descriptor); the oracle gets it pre-broadcast, as the reference's Python layer
+# passes it (nn/__init__.py:210-279, tensor_ops.c:864-997).
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+def test_config1_binary_unbroadcast_full_size(hip, oracle_lib, op):
+    A, B, Bd = config1_inputs()
+    b = Bd if op == "div" else B
+    got = hip.binary_raw(op, A, O.F32, b, O.F32, O.F32)
+    assert_bitexact(got, oracle_lib.binary(op, A, O.F32, b, O.F32, O.F32), O.F32, what=f"{op} [64,1,1] in-kernel")
+
+
+@pytest.mark.parametrize("wide", [True, False], ids=["full_range", "pm2e20"])
+@pytest.mark.parametrize("dt", [O.F64, O.F32], ids=["to_f64", "to_f32"])
+def test_config1_int32_promotion_unbroadcast(hip, oracle_lib, wide, dt):
+    rng = np.random.default_rng(0)
+    _, B, _ = config1_inputs()
+    lo, hi = (-(2 ** 31), 2 ** 31 - 1) if wide else (-(2 ** 20), 2 ** 20)
+    I = rng.integers(lo, hi, (8, 64, 56, 56), dtype=np.int64).astype(np.int32)
+    got = hip.binary_raw("add", I, O.I32, B, O.F32, dt)
+    assert_bitexact(got, oracle_lib.binary("add", I, O.I32, B, O.F32, dt), dt, what="int32 + f32[64,1,1]")
+
+
 def config2_input():
     rng = np.random.default_rng(1)
     x = rng.normal(0, 1.5, (32, 512, 1024))
@@ -92,6 +115,26 @@ def test_config2_qdq_full_size(hip, oracle_lib, x2, idx):
         ok = (y > lo) & (y < hi)
         step = np.broadcast_to(sv, x2.shape)[ok].astype(np.float64)
         assert np.all(np.abs(xr[ok].astype(np.float64) - x2[ok]) <= step * 0.5 * (1 + 1e-6))
+
+
+@pytest.mark.parametrize("idx", range(6), ids=["u8", "i8axis", "e4m3", "e5m2", "e4m3_stress", "e5m2_stress"])
+def test_config2_qdq_unbroadcast_full_size(hip, oracle_lib, x2, idx):
+    """The calls bench.py times: one-element scale / zero point (per-tensor kernels)
+    or a [1,512,1] scale and zero point (per-axis kernels), passed as they are;
+    the oracle gets them broadcast to x's shape (tensor_ops.c:999-1034)."""
+    tag, s, z, ydt, axis = config2_variants(x2)[idx]
+    sv, zv = (s.reshape(1, -1, 1), z.reshape(1, -1, 1)) if axis is not None else (s, z)
+    y_ref = oracle_lib.qdq("quantize", x2, O.F32, sv, O.F32, zv, ydt, ydt)
+    y = hip.qdq1("quantize", x2, O.F32, sv, zv, ydt, ydt)
+    assert_bitexact(y, y_ref, ydt, what=f"Q {tag} un-broadcast")
+    xr = hip.qdq1("dequantize", y_ref, ydt, sv, zv, ydt, O.F32)
+    assert_bitexact(xr, oracle_lib.qdq("dequantize", y_ref, ydt, sv, O.F32, zv, ydt, O.F32), O.F32,
+                    what=f"DQ {tag} un-broadcast")
+    if axis is not None:
+        # the axis entry points with 1-D parameters reach the same kernels
+        assert_bitexact(hip.qdq_axis("quantize", x2, O.F32, s, z, ydt, ydt, axis), y_ref, ydt, what="Q axis 1-D")
+        assert_bitexact(hip.qdq_axis("dequantize", y_ref, ydt, s, z, ydt, O.F32, axis), xr, O.F32,
+                        what="DQ axis 1-D")
 
 
 def test_config2_per_axis_entry_point(hip, oracle_lib, x2):

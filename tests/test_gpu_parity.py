@@ -624,11 +624,19 @@ def test_zero_size_tensors(hip):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("against", ["reference", "oracle"])
 @pytest.mark.parametrize("exact", [False, True], ids=["mfma", "exact"])
-def test_verifier_plans(hip, oracle_lib, exact):
+def test_verifier_plans(hip, oracle_lib, exact, against):
     """The verifier harness (tests/verify.py) over all 45 reference plans with
-    fresh seeded inputs: every iteration inside its parity class."""
+    fresh seeded inputs: every iteration inside its parity class, against the
+    reference's own tensor_ops.c (oracle/_ref, compiled from its source) and
+    against the restatement."""
     from tests.verify import verify
-    failures, stats = verify(hip, oracle_lib, iterations=3, seed=7, exact=exact, log=lambda *a: None)
+    truth = oracle_lib
+    if against == "reference":
+        truth = O.reference()
+        if truth is None:
+            pytest.skip("oracle/_ref/tensor_ops.so not built (the reference source was absent at build time)")
+    failures, stats = verify(hip, truth, iterations=3, seed=7, exact=exact, log=lambda *a: None)
     assert not failures, failures[:3]
     assert sum(len(s["abs"]) for s in stats.values()) == 45 * 3

@@ -1,7 +1,10 @@
 """HIP verifier harness: the flow of the reference's ``numerical_correctness.py``
 (``verify_op`` over its test plans, ``numerical_correctness.py:257-425, 431-635``)
-with libtensor_ops_hip.so as the implementation under test and the CPU oracle
-(``oracle/``) as the ground truth, instead of the CUDA ``verify_*`` programs.
+with libtensor_ops_hip.so as the implementation under test, instead of the CUDA
+``verify_*`` programs.  The ground truth is the reference's own ``tensor_ops.c``
+(``oracle/_ref/tensor_ops.so``, compiled from the reference source by
+``oracle/Makefile``) wherever that library is present, else the restatement
+(``oracle/liboracle.so``); ``--against`` picks one explicitly.
 
 For each of the 45 plans (``tests/golden/make_golden.py`` PLANS, the dtype
 combinations of ``numerical_correctness.py:432-567``) it draws ``--iterations``
@@ -23,6 +26,7 @@ and exits non-zero if any iteration falls outside its class.  Test
 infrastructure: it needs a GPU and runs only here and in the GPU tests.
 
     python tests/verify.py [--iterations 20] [--seed 0] [--exact] [--plans 0,5,12]
+                           [--against reference|oracle]
 """
 from __future__ import annotations
 
@@ -119,7 +123,17 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--exact", action="store_true", help="fp64 Gemm / Conv mode: Gemm and Conv2d bit-exact as well")
     ap.add_argument("--plans", default=None, help="comma-separated plan indices (default: all)")
+    ap.add_argument("--against", choices=("reference", "oracle"), default=None,
+                    help="ground truth: the compiled reference tensor_ops.c (default where built) or the "
+                         "restatement")
     args = ap.parse_args()
+    ref = O.reference()
+    against = args.against or ("reference" if ref is not None else "oracle")
+    if against == "reference" and ref is None:
+        print("verify.py: oracle/_ref/tensor_ops.so is not built (run make -C oracle where the reference "
+              "source is present)", file=sys.stderr)
+        return 2
+    truth = ref if against == "reference" else O.oracle()
     try:
         import torch
         torch.cuda.init()
@@ -131,7 +145,8 @@ def main():
         print("verify.py: libtensor_ops_hip.so reports no GPU", file=sys.stderr)
         return 2
     plans = {int(p) for p in args.plans.split(",")} if args.plans else None
-    failures, stats = verify(hip, O.oracle(), args.iterations, args.seed, args.exact, plans)
+    print(f"ground truth: {against} ({truth.path})")
+    failures, stats = verify(hip, truth, args.iterations, args.seed, args.exact, plans)
     print()
     summary(stats)
     for f in failures[:20]:
