@@ -155,7 +155,15 @@ class Timer:
         return self.torch.cuda.Event(enable_timing=True)
 
 
-def run_headline(lib, torch, steps, warmup):
+def capture(torch, fn):
+    """fn's launches on the current (library) stream, captured into a graph."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=torch.cuda.current_stream()):
+        fn()
+    return g
+
+
+def run_headline(lib, torch, steps, warmup, use_graph=False):
     rng = np.random.default_rng(1)
     x = config2_input(rng)
     variants = config2_variants(x)
@@ -183,11 +191,23 @@ def run_headline(lib, torch, steps, warmup):
     lib.check("warmup")
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    w0 = time.perf_counter()
-    t0.record()
-    for k in range(steps):
-        step(warmup + k)
-    t1.record()
+    if use_graph:
+        # The K timed steps (8 launches each, the same rotation of buffers) are
+        # captured once into a HIP graph on the library's stream; one untimed
+        # replay, then one timed replay of exactly K steps.
+        g = capture(torch, lambda: [step(warmup + k) for k in range(steps)])
+        g.replay()
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        t0.record()
+        g.replay()
+        t1.record()
+    else:
+        w0 = time.perf_counter()
+        t0.record()
+        for k in range(steps):
+            step(warmup + k)
+        t1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     lib.check("timed steps")
@@ -203,8 +223,8 @@ def run_headline(lib, torch, steps, warmup):
 
         def dq_fn(i, v=v):
             L.dequantize_linear_forward(Y[v][i % R], S[v], Z[v], XR[i % R])
-        kern[f"quantize_f32_to_{var[0]}"] = bench_loop(torch, q_fn, steps, warm=4)
-        kern[f"dequantize_{var[0]}_to_f32"] = bench_loop(torch, dq_fn, steps, warm=4)
+        kern[f"quantize_f32_to_{var[0]}"] = bench_loop(torch, q_fn, steps, warm=4, graph=use_graph)
+        kern[f"dequantize_{var[0]}_to_f32"] = bench_loop(torch, dq_fn, steps, warm=4, graph=use_graph)
     lib.check("per-kernel pass")
     dom = max(kern, key=kern.get)
     for t in X + [t for ys in Y for t in ys] + XR + S + Z:
@@ -214,10 +234,12 @@ def run_headline(lib, torch, steps, warmup):
             "dominant": dom, "bytes_per_launch": bytes_per_launch, "n": n}
 
 
-def bench_loop(torch, fn, iters, warm=3, warm_ms=50.0):
+def bench_loop(torch, fn, iters, warm=3, warm_ms=50.0, graph=False):
     """Mean time of `iters` back-to-back calls.  The warm-up runs at least `warm`
     calls and `warm_ms` of wall time, so the GPU clocks have ramped up (a cold
-    4096^3 Gemm runs ~20% slower for its first few milliseconds)."""
+    4096^3 Gemm runs ~20% slower for its first few milliseconds).  graph: the
+    `iters` calls are captured into a HIP graph and timed as one replay (for
+    calls that launch kernels only: no host staging, no workspace allocation)."""
     t0, i = time.perf_counter(), 0
     while i < warm or (time.perf_counter() - t0) * 1e3 < warm_ms:
         fn(i)
@@ -225,10 +247,18 @@ def bench_loop(torch, fn, iters, warm=3, warm_ms=50.0):
         i += 1
     warm = i
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for i in range(iters):
-        fn(warm + i)
-    b.record()
+    if graph:
+        g = capture(torch, lambda: [fn(warm + k) for k in range(iters)])
+        g.replay()
+        torch.cuda.synchronize()
+        a.record()
+        g.replay()
+        b.record()
+    else:
+        a.record()
+        for i in range(iters):
+            fn(warm + i)
+        b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) / iters
 
@@ -271,13 +301,13 @@ def run_suite(lib, torch, only=None, cpu=None):
             if not want(f"{name}_f32_bcast"):
                 continue
             b = tbd if name == "div" else tb
-            ms = bench_loop(torch, lambda i: fn(As[i % R], b, Os[i % R]), 200)
+            ms = bench_loop(torch, lambda i: fn(As[i % R], b, Os[i % R]), 200, graph=True)
             emit(op_line(f"{name}_f32_bcast", "config1 [8,64,56,56] (+) [64,1,1]", nb, ms, "hbm"),
                  CpuLeg.binary(name, A, Bd if name == "div" else B))
         for name, fn in (("relu", L.relu_forward), ("abs", L.abs_forward), ("cos", L.cos_forward)):
             if not want(f"{name}_f32"):
                 continue
-            ms = bench_loop(torch, lambda i: fn(As[i % R], Os[i % R]), 200)
+            ms = bench_loop(torch, lambda i: fn(As[i % R], Os[i % R]), 200, graph=True)
             emit(op_line(f"{name}_f32", "config1 [8,64,56,56]", nb, ms, "hbm"), CpuLeg.unary(name, A))
         if want("chain7_f32_fused"):
             # The same chain fused into one kernel (bit-identical to the op-by-op chain):
@@ -287,7 +317,7 @@ def run_suite(lib, torch, only=None, cpu=None):
                                 CStep(5, 0, 0), CStep(6, 0, 0))
             opnds = (PT * 2)(tb, tbd)
             ms = bench_loop(torch, lambda i: L.elementwise_chain_forward(As[i % R], opnds, 2, steps, 7, Os[i % R]),
-                            200)
+                            200, graph=True)
             emit(op_line("chain7_f32_fused", "config1 Add>Mul>Sub>Div>Relu>Abs>Cos, one pass", nb, ms, "hbm"),
                  CpuLeg.chain(A, B, Bd))
         for t in As + Os:
@@ -296,7 +326,7 @@ def run_suite(lib, torch, only=None, cpu=None):
             I = rng.integers(-(2 ** 31), 2 ** 31 - 1, A.shape, dtype=np.int64).astype(np.int32)
             Is = [lib.dev(I, I32) for _ in range(20)]
             O64 = [lib.empty(list(A.shape), F64) for _ in range(20)]
-            ms = bench_loop(torch, lambda i: L.add_forward(Is[i % 20], tb, O64[i % 20]), 100)
+            ms = bench_loop(torch, lambda i: L.add_forward(Is[i % 20], tb, O64[i % 20]), 100, graph=True)
             emit(op_line("add_i32_f32_to_f64", "config1 int32 [8,64,56,56] + f32 [64,1,1]", A.size * 12, ms, "hbm"),
                  CpuLeg.binary("add", I, B, I32, F64))
             for t in Is + O64:
@@ -390,7 +420,7 @@ def run_suite(lib, torch, only=None, cpu=None):
         tys = [lib.empty([32, 64, 56, 56], F32) for _ in range(4)]
         keep = [ints([1, 1, 1, 1]), ints([2, 2]), ints([1, 1]), ints([3, 3])]
         pp = Params(*[ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep])
-        ms = bench_loop(torch, lambda i: L.max_pool_forward(txs[i % 4], tys[i % 4], ctypes.byref(pp)), 40)
+        ms = bench_loop(torch, lambda i: L.max_pool_forward(txs[i % 4], tys[i % 4], ctypes.byref(pp)), 40, graph=True)
         emit(op_line("maxpool_3x3s2", "config4 [32,64,112,112] -> [32,64,56,56]", x.size * 4 + x.size, ms, "hbm"),
              CpuLeg.maxpool(x))
         for t in txs + tys:
@@ -733,6 +763,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the headline steps as one HIP graph replay instead of eager back-to-back launches "
+                         "(measured slower for these 84 MB launches on MI355X)")
     ap.add_argument("--no-suite", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--only", default=None,
@@ -786,7 +819,7 @@ def main():
             print(json.dumps(line), flush=True)
         return
     print("bench: headline Q/DQ round trips ...", file=sys.stderr, flush=True)
-    h = run_headline(lib, torch, args.steps, args.warmup)
+    h = run_headline(lib, torch, args.steps, args.warmup, use_graph=args.graph)
     value = h["bytes_per_step"] / (h["ms_per_step"] * 1e-3) / 1e9
     dom_ms = h["kernel_ms"][h["dominant"]]
     achieved = h["bytes_per_launch"] / (dom_ms * 1e-3) / 1e9
@@ -809,7 +842,8 @@ def main():
         "vs_baseline": None, "dtype": "f32->u8/i8/e4m3/e5m2->f32 (fp64 quotient)", "data": "synthetic",
         "config": {"workload": "configs[1]: QuantizeLinear->DequantizeLinear round trip, x f32 [32,512,1024] "
                                "N(0,1.5)+0.1% x20 outliers, seed 1; u8 per-tensor, i8 per-axis(1), e4m3, e5m2",
-                   "elements": h["n"], "bytes_per_step": h["bytes_per_step"], "rotating_sets": 8},
+                   "elements": h["n"], "bytes_per_step": h["bytes_per_step"], "rotating_sets": 8,
+                   "timing": "one HIP graph replay of the K steps" if args.graph else "eager launches"},
         "frac_hbm": round(value * 1e9 / HBM_PEAK, 4),
         "roofline": {"bound": "hbm", "kernel": h["dominant"], "achieved": round(achieved, 1), "peak": 8000.0,
                      "unit": "GB/s", "frac": round(achieved / 8000.0, 4), "traffic": traffic,

@@ -46,31 +46,128 @@ template <int OP> __device__ __forceinline__ int64_t iop(int64_t a, int64_t b) {
     }
 }
 
-// fmod(a, 2pi) for a = |x|, exactly.  Below 2^30 the quotient q = trunc(a / 2pi)
-// is found from a * (1 / 2pi) to within one, and fma(-q, 2pi, a) is exact
-// for the right q (the remainder of fmod is representable and the fma rounds
-// the exact value a - q * 2pi once); an off-by-one q shows as r < 0 or
-// r >= 2pi and is corrected the same way.  Larger (or non-finite) a uses fmod.
-__device__ __forceinline__ double fmod_two_pi(double a) {
-    const double two_pi = 2.0 * 3.141592653589793238462643383279502884197;
-    if (!(a < 0x1p30)) return fmod(a, two_pi);
-    const double q = __builtin_trunc(a * (1.0 / two_pi));
-    double r = __builtin_fma(-q, two_pi, a);
-    if (r < 0.0) r = __builtin_fma(-(q - 1.0), two_pi, a);
-    else if (r >= two_pi) r = __builtin_fma(-(q + 1.0), two_pi, a);
+constexpr double kTwoPi = 2.0 * 3.141592653589793238462643383279502884197;
+constexpr int kLutN = 4097;   // table entries (tensor_ops.c:763-807)
+
+// fmod(a, 2pi) for 0 <= a < 2^30, exactly.  The quotient q = trunc(a / 2pi)
+// is found from a * (1 / 2pi) to within one, and fma(-q, 2pi, a) is exact for
+// the right q (the remainder of fmod is representable and the fma rounds the
+// exact value a - q * 2pi once); an off-by-one q shows as r < 0 or r >= 2pi
+// and is corrected the same way.
+__device__ __forceinline__ double fmod_two_pi_small(double a) {
+    const double q = __builtin_trunc(a * (1.0 / kTwoPi));
+    double r = __builtin_fma(-q, kTwoPi, a);
+    if (r < 0.0) r = __builtin_fma(-(q - 1.0), kTwoPi, a);
+    else if (r >= kTwoPi) r = __builtin_fma(-(q + 1.0), kTwoPi, a);
     return r;
 }
 
-// tensor_ops.c:815-833: r = fmod(|x|, 2pi); pos = r * 4096 / 2pi; lerp.
+// fmod(a, 2pi) for a = |x| of any double: larger (or non-finite) a uses fmod.
+__device__ __forceinline__ double fmod_two_pi(double a) {
+    if (!(a < 0x1p30)) return fmod(a, kTwoPi);
+    return fmod_two_pi_small(a);
+}
+
+// tensor_ops.c:815-833: r = fmod(|x|, 2pi); pos = r * 4096 / 2pi; lerp.  The
+// reference's arithmetic for any input (f64 inputs reach every double r).
 __device__ __forceinline__ double lut_cos(double x, const double* __restrict__ T) {
-    const double two_pi = 2.0 * 3.141592653589793238462643383279502884197;
     const double r = fmod_two_pi(fabs(x));
     if (r != r) return r;                              // NaN / inf input
-    const double pos = r * 4096.0 / two_pi;
+    const double pos = r * 4096.0 / kTwoPi;
     int k = (int)pos;
     double w = pos - (double)k;
     if (k >= 4096) { k = 4095; w = 0.0; }
     return T[k] * (1.0 - w) + T[k + 1] * w;
+}
+
+// pos = RN(r * 4096 / 2pi) without a division, for the r an f32 input reaches:
+// q0 = RN(a * y) with y = RN(1 / 2pi) is within an ulp of a / 2pi, so the
+// residual e = a - q0 * 2pi is exact in one fma and q0 + e * y rounds to the
+// correctly rounded quotient (Markstein's correction step).  r * 4096 is exact.
+// Every f32 input is checked against the division on the GPU
+// (test_cos_f32_fast_path_every_input: all 2^32 patterns).
+__device__ __forceinline__ double cos_pos_f32(double r) {
+    const double a = r * 4096.0;
+    const double y = 1.0 / kTwoPi;
+    const double q0 = a * y;
+    const double e = __builtin_fma(-q0, kTwoPi, a);
+    return __builtin_fma(e, y, q0);
+}
+
+// cos_forward's value for W f32 inputs, the table in LDS.  The index
+// arithmetic of all W values comes first, then their table reads, then the
+// interpolations, so the W lookups overlap.  The remainder r = fmod(|x|, 2pi)
+// takes one fma from the estimated quotient; the lanes where that estimate is
+// off by one (r < 0 or r >= 2pi, both exact values, so one exact add fixes
+// them: the true remainder is representable and within 2^-19 of 0 or of 2pi),
+// and inputs of magnitude >= 2^30 or NaN / inf (fmod), go through one branch
+// for the W values.  The read index min(k, 4095) with w = pos - k reproduces
+// the reference's clamp (k >= 4096 -> k = 4095, w = 0: pos <= 4096, so k = 4096
+// only with w = 0).  A NaN input gives a NaN through the arithmetic.
+// Bit-identical to (float)lut_cos((double)x, T) for every f32 x.
+template <int W>
+__device__ __forceinline__ void cos_lds(float (&v)[W], const double* __restrict__ sT) {
+    double r[W];
+    bool slow = false;
+#pragma unroll
+    for (int e = 0; e < W; e++) {
+        const double a = __builtin_fabs((double)v[e]);
+        const double q = __builtin_trunc(a * (1.0 / kTwoPi));
+        r[e] = __builtin_fma(-q, kTwoPi, a);
+        slow = slow || !(a < 0x1p30) || !(r[e] >= 0.0 && r[e] < kTwoPi);
+    }
+    if (slow) {
+#pragma unroll
+        for (int e = 0; e < W; e++) {
+            const double a = __builtin_fabs((double)v[e]);
+            if (!(a < 0x1p30)) r[e] = fmod(a, kTwoPi);
+            else if (r[e] < 0.0) r[e] = r[e] + kTwoPi;
+            else if (r[e] >= kTwoPi) r[e] = r[e] - kTwoPi;
+        }
+    }
+    uint32_t k[W];
+    double w[W];
+#pragma unroll
+    for (int e = 0; e < W; e++) {
+        const double pos = cos_pos_f32(r[e]);
+        // pos lies in [0, 4096]; fmin also maps a NaN pos to an in-bounds index
+        const int ki = (int)__builtin_fmin(pos, 4096.0);
+        w[e] = pos - (double)ki;
+        k[e] = min((uint32_t)ki, 4095u);
+    }
+    double t0[W], t1[W];
+#pragma unroll
+    for (int e = 0; e < W; e++) {
+        t0[e] = sT[k[e]];
+        t1[e] = sT[k[e] + 1];
+    }
+#pragma unroll
+    for (int e = 0; e < W; e++) v[e] = (float)(t0[e] * (1.0 - w[e]) + t1[e] * w[e]);
+}
+
+// Copies the table into LDS (every thread of the block takes part): 16-byte
+// loads, all issued before the first LDS store, so the copy costs one
+// round trip to L2 rather than one per element a thread moves.
+template <int BLOCK>
+__device__ __forceinline__ void load_table(double* __restrict__ sT, const double* __restrict__ T) {
+    constexpr int kPairs = (kLutN - 1) / 2;                // 2048 double2; entry 4096 separately
+    constexpr int kPer = (kPairs + BLOCK - 1) / BLOCK;
+    const double2* T2 = reinterpret_cast<const double2*>(T);
+    double2* S2 = reinterpret_cast<double2*>(sT);
+    double2 t[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; j++) {
+        const int i = threadIdx.x + j * BLOCK;
+        if (kPairs % BLOCK == 0 || i < kPairs) t[j] = T2[i];
+    }
+    const double last = T[kLutN - 1];
+#pragma unroll
+    for (int j = 0; j < kPer; j++) {
+        const int i = threadIdx.x + j * BLOCK;
+        if (kPairs % BLOCK == 0 || i < kPairs) S2[i] = t[j];
+    }
+    if (threadIdx.x == 0) sT[kLutN - 1] = last;
+    __syncthreads();
 }
 
 __device__ __forceinline__ float abs_f32(float v) {
@@ -104,6 +201,60 @@ __global__ __launch_bounds__(kBlock) void k_unary_f32(const float* __restrict__ 
         const size_t i = nv * 4 + threadIdx.x;
         Y[i] = unary_f32<U>(X[i], T);
     }
+}
+
+// Cos of f32 -> f32 with the table in LDS.  Blocks of kLutBlock threads, at
+// most kLutBlocksPerCU per CU (each block copies the 32 KB table once, so the
+// grid is capped and strides over the tensor); U float4 units per thread per
+// tile.  The first tile's loads are issued before the table copy, so the two
+// latencies overlap.
+constexpr int kLutBlock = 512;
+constexpr int kLutBlocksPerCU = 3;
+constexpr int kCosUnits = 1;        // float4 units per thread of k_cos_f32
+
+template <int U>
+__global__ __launch_bounds__(kLutBlock) void k_cos_f32(const float* __restrict__ X, float* __restrict__ Y,
+                                                       uint32_t nv, uint32_t n, const double* __restrict__ T) {
+    __shared__ __attribute__((aligned(16))) double sT[kLutN];
+    const float4* X4 = reinterpret_cast<const float4*>(X);
+    float4* Y4 = reinterpret_cast<float4*>(Y);
+    const uint32_t tile = kLutBlock * U, stride = gridDim.x * tile;
+    uint32_t base = blockIdx.x * tile;
+    float4 x[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const uint32_t i = base + u * kLutBlock + threadIdx.x;
+        x[u] = i < nv ? ld_stream(X4 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    load_table<kLutBlock>(sT, T);
+    for (; base < nv; base += stride) {
+        float v[4 * U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            v[4 * u] = x[u].x; v[4 * u + 1] = x[u].y; v[4 * u + 2] = x[u].z; v[4 * u + 3] = x[u].w;
+        }
+        const uint32_t next = base + stride;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t i = next + u * kLutBlock + threadIdx.x;
+            x[u] = i < nv ? ld_stream(X4 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        cos_lds<4 * U>(v, sT);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t i = base + u * kLutBlock + threadIdx.x;
+            if (i < nv) st_stream(Y4 + i, make_float4(v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]));
+        }
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+        float t[1] = {X[nv * 4 + threadIdx.x]};
+        cos_lds<1>(t, sT);
+        Y[nv * 4 + threadIdx.x] = t[0];
+    }
+}
+
+inline unsigned lut_grid(size_t tiles, int per_cu = kLutBlocksPerCU) {
+    return grid_for(tiles, 1, (unsigned)(per_cu * num_cus()));
 }
 
 // Any dtypes: tensor_ops.c:708-757 (int input -> int64 path), :840-854 (cos, double path).
@@ -289,7 +440,13 @@ void unary_entry(const char* name, const Tensor* X, Tensor* Y) {
     const size_t n = X->size;
     hipStream_t s = stream();
     if (n) {
-        if (X->dtype == DTYPE_FLOAT32 && Y->dtype == DTYPE_FLOAT32 && aligned16(x) && aligned16(y)) {
+        const bool f32 = X->dtype == DTYPE_FLOAT32 && Y->dtype == DTYPE_FLOAT32 && aligned16(x) && aligned16(y);
+        if (U == U_COS && f32 && n < (size_t(1) << 31)) {
+            const uint32_t nv = (uint32_t)(n / 4);
+            hipLaunchKernelGGL((k_cos_f32<kCosUnits>), dim3(lut_grid((nv + kLutBlock * kCosUnits - 1) /
+                                                                     (kLutBlock * kCosUnits))),
+                               dim3(kLutBlock), 0, s, (const float*)x, (float*)y, nv, (uint32_t)n, T);
+        } else if (f32) {
             hipLaunchKernelGGL((k_unary_f32<U>), dim3(grid_for(n / 4 + 1, kBlock)), dim3(kBlock), 0, s,
                                (const float*)x, (float*)y, n, T);
         } else {
@@ -313,95 +470,188 @@ void unary_entry(const char* name, const Tensor* X, Tensor* Y) {
 // into two 64-bit words held in scalar registers, so the unrolled step loop
 // decodes it with shifts instead of indexing the kernel argument memory.
 constexpr int kChainMaxSteps = 16, kChainMaxOperands = kMaxOperands - 1;
+constexpr int kChainW = 8;          // elements per thread of the vectorised chain kernel
+constexpr int kChainLutBlock = 256; // threads per block of the chain kernel with a Cos step
+constexpr int kChainLutPerCU = 4;   // its blocks per CU (LDS: one 32 KB table each)
 struct ChainProg {
     int n;
     uint64_t code[2];
 };
 
-// One step on the W values of a thread: one (uniform) dispatch per step.
 template <int W>
-__device__ __forceinline__ void chain_step(int op, float (&v)[W], const float (&b)[W], int rev, const double* T) {
-    switch (op) {
-    case TENSOR_OPS_CHAIN_ADD:
+__device__ __forceinline__ void binary_step(int op, int rev, float (&v)[W], const float (&b)[W]) {
+    switch (op * 2 + rev) {
+    case TENSOR_OPS_CHAIN_ADD * 2:
 #pragma unroll
-        for (int e = 0; e < W; e++) v[e] = rev ? b[e] + v[e] : v[e] + b[e];
+        for (int e = 0; e < W; e++) v[e] = v[e] + b[e];
         break;
-    case TENSOR_OPS_CHAIN_SUB:
+    case TENSOR_OPS_CHAIN_ADD * 2 + 1:
 #pragma unroll
-        for (int e = 0; e < W; e++) v[e] = rev ? b[e] - v[e] : v[e] - b[e];
+        for (int e = 0; e < W; e++) v[e] = b[e] + v[e];
         break;
-    case TENSOR_OPS_CHAIN_MUL:
+    case TENSOR_OPS_CHAIN_SUB * 2:
 #pragma unroll
-        for (int e = 0; e < W; e++) v[e] = rev ? b[e] * v[e] : v[e] * b[e];
+        for (int e = 0; e < W; e++) v[e] = v[e] - b[e];
         break;
-    case TENSOR_OPS_CHAIN_DIV:
+    case TENSOR_OPS_CHAIN_SUB * 2 + 1:
 #pragma unroll
-        for (int e = 0; e < W; e++) v[e] = rev ? b[e] / v[e] : v[e] / b[e];
+        for (int e = 0; e < W; e++) v[e] = b[e] - v[e];
         break;
-    case TENSOR_OPS_CHAIN_RELU:
+    case TENSOR_OPS_CHAIN_MUL * 2:
 #pragma unroll
-        for (int e = 0; e < W; e++) v[e] = unary_f32<U_RELU>(v[e], T);
+        for (int e = 0; e < W; e++) v[e] = v[e] * b[e];
         break;
-    case TENSOR_OPS_CHAIN_ABS:
+    case TENSOR_OPS_CHAIN_MUL * 2 + 1:
 #pragma unroll
-        for (int e = 0; e < W; e++) v[e] = unary_f32<U_ABS>(v[e], T);
+        for (int e = 0; e < W; e++) v[e] = b[e] * v[e];
+        break;
+    case TENSOR_OPS_CHAIN_DIV * 2:
+#pragma unroll
+        for (int e = 0; e < W; e++) v[e] = v[e] / b[e];
         break;
     default:
 #pragma unroll
-        for (int e = 0; e < W; e++) v[e] = unary_f32<U_COS>(v[e], T);
+        for (int e = 0; e < W; e++) v[e] = b[e] / v[e];
         break;
     }
 }
 
-// V4: eight consecutive elements per thread as two float4 (inner dim % 8 == 0,
-// 16-byte aligned), which amortises the per-step dispatch; else one element.
-template <int ND, bool V4>
-__global__ __launch_bounds__(kBlock) void k_chain_f32(const float* __restrict__ X, const float* __restrict__ B0,
-                                                      const float* __restrict__ B1, const float* __restrict__ B2,
-                                                      float* __restrict__ Y, BDesc d, ChainProg prog, uint32_t nitems,
-                                                      int stream_x, const double* __restrict__ T) {
-    constexpr int W = V4 ? 8 : 1;
-    const float* Bp[3] = {B0, B1, B2};
-    const uint32_t stride = gridDim.x * kBlock;
-    for (uint32_t it = blockIdx.x * kBlock + threadIdx.x; it < nitems; it += stride) {
-        int64_t off[kMaxOperands];
-        bd_offsets32<kMaxOperands, ND>(d, it * W, off);
-        float v[W], b[kChainMaxOperands][W];
-        if constexpr (V4) {
-            const int64_t sx = d.st[0][d.nd - 1];
+// Operands of the fused chain with their access kind, chosen on the host from
+// the descriptor (uniform across the grid):
+//   kOpItem   one value per item of W elements (innermost stride 0): one load;
+//   kOpVec    contiguous along the item (innermost stride 1, 16-byte aligned,
+//             innermost dim a multiple of 4): float4 loads;
+//   kOpGather anything else: W loads.
+enum { kOpItem = 0, kOpVec = 1, kOpGather = 2 };
+struct ChainOperands {
+    const float* p[kChainMaxOperands];
+    int kind[kChainMaxOperands];
+    int n;
+};
+
+// Offsets (elements, 32-bit) of operands 1..NOP of d for output index i.
+template <int NOP, int ND>
+__device__ __forceinline__ void operand_offsets(const BDesc& d, uint32_t i, uint32_t (&off)[NOP]) {
+    const int nd = ND > 0 ? ND : d.nd;
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const float4 x = load4(X, off[0] + 4 * h * sx, sx, stream_x != 0);
-                v[4 * h] = x.x; v[4 * h + 1] = x.y; v[4 * h + 2] = x.z; v[4 * h + 3] = x.w;
+    for (int k = 0; k < NOP; k++) off[k] = 0;
+#pragma unroll
+    for (int a = (ND > 0 ? ND : kMaxDims) - 1; a > 0; a--) {
+        if (ND == 0 && a >= nd) continue;
+        const uint32_t q = d.fd[a].div(i);
+        const uint32_t c = i - q * d.dim[a];
+#pragma unroll
+        for (int k = 0; k < NOP; k++) off[k] += c * (uint32_t)d.st[k + 1][a];
+        i = q;
+    }
+#pragma unroll
+    for (int k = 0; k < NOP; k++) off[k] += i * (uint32_t)d.st[k + 1][0];
+}
+
+// The fused chain over Y->size elements, W consecutive elements per thread
+// (W = 4 or 8: X and Y 16-byte aligned, innermost dim a multiple of W; else 1).
+// X has Y's size and is read flat; operands go through the descriptor.  The
+// program is packed 8 bits per step (op | operand << 3 | reversed << 5) in
+// scalar registers; each step is one uniform dispatch (op, operand and order
+// select code paths, not per-element values).  LUT (the program has a Cos
+// step): blocks copy the cosine table into LDS first and the grid is capped
+// (see k_cos_f32), so the loop strides.
+template <int ND, int W, bool LUT, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void k_chain_f32(const float* __restrict__ X, ChainOperands B,
+                                                     float* __restrict__ Y, BDesc d, ChainProg prog, uint32_t nitems,
+                                                     const double* __restrict__ Tg) {
+    constexpr int H = W >= 4 ? W / 4 : 1;      // float4 per thread
+    __shared__ __attribute__((aligned(16))) double sT[LUT ? kLutN : 2];
+    const uint32_t stride = gridDim.x * BLOCK;
+    uint32_t it = blockIdx.x * BLOCK + threadIdx.x;
+    // X of this thread's first item is requested before the table copy, so
+    // the two latencies overlap; later items load at the top of the loop
+    float4 xf[H];
+#pragma unroll
+    for (int h = 0; h < H; h++) {
+        if constexpr (W >= 4) {
+            xf[h] = it < nitems ? ld_stream(reinterpret_cast<const float4*>(X) + H * it + h)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            xf[h].x = it < nitems ? X[it] : 0.f;
+        }
+    }
+    const double* T = Tg;
+    if constexpr (LUT) {
+        load_table<BLOCK>(sT, Tg);
+        T = sT;
+    }
+    for (bool first = true; it < nitems; it += stride, first = false) {
+        float v[W], b[kChainMaxOperands][W];
+        if (!first) {
+#pragma unroll
+            for (int h = 0; h < H; h++) {
+                if constexpr (W >= 4) xf[h] = ld_stream(reinterpret_cast<const float4*>(X) + H * it + h);
+                else xf[h].x = X[it];
+            }
+        }
+        if constexpr (W >= 4) {
+#pragma unroll
+            for (int h = 0; h < H; h++) {
+                v[4 * h] = xf[h].x; v[4 * h + 1] = xf[h].y; v[4 * h + 2] = xf[h].z; v[4 * h + 3] = xf[h].w;
             }
         } else {
-            v[0] = X[off[0]];
+            v[0] = xf[0].x;
         }
+        uint32_t off[kChainMaxOperands];
+        operand_offsets<kChainMaxOperands, ND>(d, it * W, off);
 #pragma unroll
         for (int k = 0; k < kChainMaxOperands; k++) {
-            if (!Bp[k]) continue;
-            if constexpr (V4) {
-                const int64_t sb = d.st[k + 1][d.nd - 1];
+            if (k >= B.n) break;
+            const float* P = B.p[k];
+            if (W == 1 || B.kind[k] == kOpItem) {
+                const float t = P[off[k]];
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const float4 t = load4(Bp[k], off[k + 1] + 4 * h * sb, sb, false);
+                for (int e = 0; e < W; e++) b[k][e] = t;
+            } else if (B.kind[k] == kOpVec) {
+#pragma unroll
+                for (int h = 0; h < H; h++) {
+                    const float4 t = *reinterpret_cast<const float4*>(P + off[k] + 4 * h);
                     b[k][4 * h] = t.x; b[k][4 * h + 1] = t.y; b[k][4 * h + 2] = t.z; b[k][4 * h + 3] = t.w;
                 }
             } else {
-                b[k][0] = Bp[k][off[k + 1]];
+                const uint32_t sb = (uint32_t)d.st[k + 1][d.nd - 1];
+#pragma unroll
+                for (int e = 0; e < W; e++) b[k][e] = P[off[k] + e * sb];
             }
         }
         for (int sidx = 0; sidx < prog.n; sidx++) {
             const uint32_t c = (uint32_t)(prog.code[sidx >> 3] >> (8 * (sidx & 7))) & 0xFFu;
-            const int a = (c >> 3) & 3;
-            float bb[W];
+            const int op = (int)(c & 7u), a = (int)((c >> 3) & 3u), rev = (int)((c >> 5) & 1u);
+            if (W > 1 && op == TENSOR_OPS_CHAIN_DIV && !rev && B.kind[a] == kOpItem) {
+                // v / b for one b per item: RN32((double)v * RN64(1 / b)).  The
+                // double product is within 2^-52 (relative) of v / b, and the
+                // quotient of two f32 values is never a rounding midpoint of f32
+                // nor within 2^-49 (relative) of one, so the product rounds to the
+                // same f32 as the correctly rounded division (zeros, infinities,
+                // NaN and subnormal results included).
+                const double rb = 1.0 / (double)(a == 0 ? b[0][0] : (a == 1 ? b[1][0] : b[2][0]));
 #pragma unroll
-            for (int e = 0; e < W; e++) bb[e] = a == 0 ? b[0][e] : (a == 1 ? b[1][e] : b[2][e]);
-            chain_step<W>((int)(c & 7u), v, bb, (int)((c >> 5) & 1u), T);
+                for (int e = 0; e < W; e++) v[e] = (float)((double)v[e] * rb);
+            } else if (op <= TENSOR_OPS_CHAIN_DIV) {
+                if (a == 0) binary_step<W>(op, rev, v, b[0]);
+                else if (a == 1) binary_step<W>(op, rev, v, b[1]);
+                else binary_step<W>(op, rev, v, b[2]);
+            } else if (op == TENSOR_OPS_CHAIN_RELU) {
+#pragma unroll
+                for (int e = 0; e < W; e++) v[e] = unary_f32<U_RELU>(v[e], T);
+            } else if (op == TENSOR_OPS_CHAIN_ABS) {
+#pragma unroll
+                for (int e = 0; e < W; e++) v[e] = unary_f32<U_ABS>(v[e], T);
+            } else if constexpr (LUT) {
+                cos_lds<W>(v, T);
+            }
         }
-        if constexpr (V4) {
-            st_stream(reinterpret_cast<float4*>(Y) + 2 * it, make_float4(v[0], v[1], v[2], v[3]));
-            st_stream(reinterpret_cast<float4*>(Y) + 2 * it + 1, make_float4(v[4], v[5], v[6], v[7]));
+        if constexpr (W >= 4) {
+#pragma unroll
+            for (int h = 0; h < H; h++)
+                st_stream(reinterpret_cast<float4*>(Y) + H * it + h,
+                          make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]));
         } else {
             Y[it] = v[0];
         }
@@ -454,17 +704,34 @@ void chain_entry(const Tensor* X, const Tensor* const* operands, int noperands, 
     const size_t n = Y->size;
     if (n) {
         if (n >= ((size_t)1 << 31)) { set_error("%s: more than 2^31 elements", name); st.finish(); return; }
-        bool v4 = d.dim[d.nd - 1] % 8u == 0 && aligned16(x) && aligned16(y);
-        for (int k = 0; k < noperands; k++) v4 = v4 && aligned16(b[k]);
-        hipStream_t s = stream();
-        if (v4) {
-            const uint32_t nv = (uint32_t)(n / 8);
-            ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, true>), dim3(grid_for(nv, kBlock)), dim3(kBlock), 0, s,
-                                               x, b[0], b[1], b[2], y, d, prog, nv, 1, T));
-        } else {
-            ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, false>), dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s,
-                                               x, b[0], b[1], b[2], y, d, prog, (uint32_t)n, 0, T));
+        bool al = aligned16(x) && aligned16(y);
+        const uint32_t inner = d.dim[d.nd - 1];
+        // elements per thread: kChainW where the layout allows, else 4, else 1
+        const int w = (al && inner % kChainW == 0) ? kChainW : ((al && inner % 4 == 0) ? 4 : 1);
+        ChainOperands B{};
+        B.n = noperands;
+        for (int k = 0; k < noperands; k++) {
+            B.p[k] = b[k];
+            const int64_t sb = d.st[k + 1][d.nd - 1];
+            B.kind[k] = sb == 0 ? kOpItem : ((sb == 1 && aligned16(b[k])) ? kOpVec : kOpGather);
         }
+        const uint32_t items = (uint32_t)(n / w);
+        hipStream_t s = stream();
+        const dim3 bl(cos ? kChainLutBlock : kBlock);
+        const dim3 gr(cos ? lut_grid((items + kChainLutBlock - 1) / kChainLutBlock, kChainLutPerCU)
+                          : grid_for(items, kBlock));
+#define CHAIN_K(WV)                                                                                              \
+    if (cos) {                                                                                                   \
+        ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, WV, true, kChainLutBlock>), gr, bl, 0, s, x, B, y, d,\
+                                           prog, items, T));                                                     \
+    } else {                                                                                                     \
+        ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, WV, false, kBlock>), gr, bl, 0, s, x, B, y, d, prog, \
+                                           items, T));                                                           \
+    }
+        if (w == kChainW) { CHAIN_K(kChainW) }
+        else if (w == 4) { CHAIN_K(4) }
+        else { CHAIN_K(1) }
+#undef CHAIN_K
         if (!check_launch(name)) { st.finish(); return; }
     }
     st.finish();

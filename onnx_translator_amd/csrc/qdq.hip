@@ -95,10 +95,11 @@ __device__ __forceinline__ uint8_t qslow1(float x, float s, double zd) {
 // code word) with the scale / zero-point values they need, loaded together so
 // that the parameter loads overlap the data loads.  MODE 0: one pair for the
 // tensor (not stored per unit); 1: one pair per unit; 2: one pair per element;
-// 3: one pair per wave — the 64 units of a wave are 256 consecutive elements
-// starting at a multiple of 256 and the parameters change only every `inner`
-// elements, a multiple of 256, so the wave shares one pair, located from its
-// first unit's index (uniform: its address math and loads go to the scalar unit).
+// 3: one pair per wave — a wave's units are one run of consecutive elements
+// (256 for dequantize, 256 * kQU per tile for quantize) starting at a multiple
+// of the run, and the parameters change only every `inner` elements, a
+// multiple of the run, so the wave shares one pair, located from its first
+// unit's index (uniform: its address math and loads go to the scalar unit).
 template <int ZDT> using zraw_t = typename std::conditional<ZDT == kF32, float, uint8_t>::type;
 
 template <int ZDT, int MODE>
@@ -182,12 +183,29 @@ __device__ __forceinline__ uint32_t quant_unit(const float4 xv, const Params<ZDT
     return w;
 }
 
-// One tile: kQU float4 units per thread, unit u of a block is one contiguous span.
+// One tile: kQU float4 units per thread.  Unit u of thread (wave, lane):
+//   MODE 3: t * kBlock * kQU + wave * 64 * kQU + u * 64 + lane — each wave
+//           covers one contiguous run of 64 * kQU units (4 * 64 * kQU
+//           elements), which the host guarantees lies inside one channel, so
+//           the wave loads one scale / zero point and forms its quantization
+//           parameters once per tile;
+//   else:   t * kBlock * kQU + u * kBlock + threadIdx.x (unit u of the block
+//           is one contiguous span).
+// Either way a wave's 64 lanes read 64 consecutive units (1 KB).
 template <int ZDT, int MODE>
 struct QTile {
+    static constexpr int kP = MODE == 3 ? 1 : kQU;
     float4 x[kQU];
-    Params<ZDT, MODE> p[kQU];
+    Params<ZDT, MODE> p[kP];
 };
+
+template <int MODE>
+__device__ __forceinline__ uint32_t qunit(uint32_t t, int u) {
+    if constexpr (MODE == 3)
+        return t * (kBlock * kQU) + (threadIdx.x >> 6) * (64 * kQU) + u * 64 + (threadIdx.x & 63u);
+    else
+        return t * (kBlock * kQU) + u * kBlock + threadIdx.x;
+}
 
 // Loads tile t.  X goes through the buffer resource (units at or beyond nv
 // read as zero without touching memory); parameter indices are clamped to the
@@ -195,25 +213,40 @@ struct QTile {
 template <int ZDT, int MODE, int ND>
 __device__ __forceinline__ void qload(QTile<ZDT, MODE>& q, __amdgpu_buffer_rsrc_t xr, const float* S, const void* Z,
                                       const BDesc& d, const AxisDesc& ax, uint32_t vbase, uint32_t nv, uint32_t t) {
-    // first thread of this wave, as a uniform value (MODE 3 indexes parameters per wave)
-    const uint32_t wbase = __builtin_amdgcn_readfirstlane(threadIdx.x) & ~63u;
 #pragma unroll
-    for (int u = 0; u < kQU; u++) {
-        const uint32_t v = t * (kBlock * kQU) + u * kBlock + threadIdx.x;
-        q.x[u] = ld_buf_stream(xr, v * 16u);
-        const uint32_t vp = MODE == 3 ? t * (kBlock * kQU) + u * kBlock + wbase : v;
-        load_params<ZDT, MODE, ND>(q.p[u], S, Z, d, ax, vbase + min(vp, nv - 1));
+    for (int u = 0; u < kQU; u++) q.x[u] = ld_buf_stream(xr, qunit<MODE>(t, u) * 16u);
+    if constexpr (MODE == 3) {
+        // the wave's first unit, as a uniform value: address math and loads go to the scalar unit
+        const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x) >> 6;
+        const uint32_t vp = t * (kBlock * kQU) + wave * (64 * kQU);
+        load_params<ZDT, MODE, ND>(q.p[0], S, Z, d, ax, vbase + min(vp, nv - 1));
+    } else {
+#pragma unroll
+        for (int u = 0; u < kQU; u++)
+            load_params<ZDT, MODE, ND>(q.p[u], S, Z, d, ax, vbase + min(qunit<MODE>(t, u), nv - 1));
     }
 }
 
 template <int YDT, int ZDT, int MODE>
 __device__ __forceinline__ void qstore(const QTile<ZDT, MODE>& q, uint32_t* Y4, const QParm& pu, uint32_t nv,
                                        uint32_t t) {
+    if constexpr (MODE == 3) {
+        // one channel per wave and tile: the per-tensor arithmetic with this channel's parameters
+        const QParm pc = qparm<YDT>(q.p[0].s[0], ld_d<ZDT>(&q.p[0].z[0], 0));
+        const Params<ZDT, 0> none{};
 #pragma unroll
-    for (int u = 0; u < kQU; u++) {
-        const uint32_t v = t * (kBlock * kQU) + u * kBlock + threadIdx.x;
-        const uint32_t w = quant_unit<YDT, ZDT, MODE>(q.x[u], q.p[u], pu);
-        if (v < nv) Y4[v] = w;
+        for (int u = 0; u < kQU; u++) {
+            const uint32_t v = qunit<MODE>(t, u);
+            const uint32_t w = quant_unit<YDT, ZDT, 0>(q.x[u], none, pc);
+            if (v < nv) Y4[v] = w;
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kQU; u++) {
+            const uint32_t v = qunit<MODE>(t, u);
+            const uint32_t w = quant_unit<YDT, ZDT, MODE>(q.x[u], q.p[u], pu);
+            if (v < nv) Y4[v] = w;
+        }
     }
 }
 
@@ -425,10 +458,13 @@ void qdq_entry(const char* name, const Tensor* X, const Tensor* S, const Tensor*
                 ax.inner = make_fastdiv((uint32_t)inner);
                 ax.c = make_fastdiv(d.dim[axis]);
                 ax.zs = zs;
-                // kBlock is a multiple of 64 and each wave's 64 units start at a multiple of
-                // 64 units, so inner % 256 == 0 keeps a wave inside one channel.
+                // A wave's units stay inside one channel when the channel's run of
+                // elements is a multiple of the wave's run: dequantize — 64 units of
+                // 4 elements at a multiple of 64 units; quantize — 64 * kQU units
+                // at a multiple of that (see QTile).
+                const uint64_t wave_run = QUANT ? 4u * 64u * kQU : 4u * 64u;
                 const bool zword = dtz == kF32 || (tensor_bytes(Z) % 4 == 0 && ((uintptr_t)z % 4) == 0);
-                mode = (inner % 256 == 0 && zword && ((uintptr_t)s % 4) == 0) ? 3 : 1;
+                mode = (inner % wave_run == 0 && zword && ((uintptr_t)s % 4) == 0) ? 3 : 1;
             }
 #define QDQ_MODES(LAUNCH_K)                                          \
     if (mode == 0) { LAUNCH_K(0, 1); }                               \

@@ -475,3 +475,34 @@ def test_cos_near_multiples_of_two_pi(hip, oracle_lib):
     xd = np.concatenate([k * 2 * np.pi, np.nextafter(k * 2 * np.pi, 0), rng.uniform(0, 2.0 ** 31, 5000)])
     assert_bitexact(hip.unary("cos", xd, O.F64, O.F64), oracle_lib.unary("cos", xd, O.F64, O.F64), O.F64,
                     what="cos f64 near 2pi multiples")
+
+
+@pytest.mark.parametrize("shape,axis", [((3, 40, 1024), 1), ((2, 7, 2048), 1), ((130, 1024), 0), ((1, 3, 4096), 1),
+                                        ((5, 6, 768), 1), ((4, 9, 256), 1), ((3, 5, 12), 1), ((6, 3, 4, 1024), 2)],
+                         ids=["inner1024", "inner2048", "axis0", "inner4096", "inner768", "inner256", "inner12",
+                              "rank4"])
+@pytest.mark.parametrize("ydt", [O.I8, O.U8], ids=["i8", "u8"])
+def test_per_axis_qdq_layouts(hip, oracle_lib, shape, axis, ydt):
+    """Per-axis QuantizeLinear / DequantizeLinear over channel runs that take the
+    per-wave parameter kernels (runs a multiple of 1024 elements for quantize,
+    256 for dequantize) and the per-unit ones (shorter runs), with per-channel
+    zero points, rounding ties and saturation, against the oracle
+    (tensor_ops.c:999-1034)."""
+    rng = np.random.default_rng(hash((shape, axis, ydt)) % 2 ** 32)
+    C = shape[axis]
+    s = rng.uniform(0.01, 0.2, C).astype(np.float32)
+    lo, hi = (-6, 6) if ydt == O.I8 else (0, 12)
+    z = rng.integers(lo, hi, C).astype(np.int8 if ydt == O.I8 else np.uint8)
+    x = rng.normal(0, 8, shape).astype(np.float32)
+    on = [1] * len(shape)
+    on[axis] = C
+    sb, zb = np.broadcast_to(s.reshape(on), shape), np.broadcast_to(z.reshape(on), shape)
+    x.reshape(-1)[::7] = ((np.rint(x.reshape(-1)[::7] / sb.reshape(-1)[::7]) + 0.5) * sb.reshape(-1)[::7])
+    want = oracle_lib.qdq("quantize", x, O.F32, s.reshape(on), O.F32, z.reshape(on), ydt, ydt)
+    assert_bitexact(hip.qdq1("quantize", x, O.F32, s.reshape(on), z.reshape(on), ydt, ydt), want, ydt,
+                    what=f"Q {shape} axis {axis}")
+    assert_bitexact(hip.qdq_axis("quantize", x, O.F32, s, z, ydt, ydt, axis), want, ydt, what="Q axis entry")
+    back = oracle_lib.qdq("dequantize", want, ydt, s.reshape(on), O.F32, z.reshape(on), ydt, O.F32)
+    assert_bitexact(hip.qdq1("dequantize", want, ydt, s.reshape(on), z.reshape(on), ydt, O.F32), back, O.F32,
+                    what=f"DQ {shape} axis {axis}")
+    assert_bitexact(hip.qdq_axis("dequantize", want, ydt, s, z, ydt, O.F32, axis), back, O.F32, what="DQ axis entry")

@@ -1,0 +1,105 @@
+"""Library calls captured into a HIP graph (as bench.py times the headline).
+
+The calls of one headline step (per-tensor u8 and per-axis i8 QuantizeLinear,
+their DequantizeLinear, the fused config-1 chain) are captured on the
+library's stream; the graph is replayed several times with the program's own
+eager work and synchronisations between replays, the outputs overwritten
+before each replay, and every replay must reproduce the eager results bit for
+bit.  None of these calls records a memset or allocates inside the capture.
+torch provides device memory and the graph object only.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import assert_bitexact
+
+pytestmark = pytest.mark.gpu
+
+
+class Step(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_int), ("operand", ctypes.c_int), ("reversed", ctypes.c_int)]
+
+
+def test_graph_replays_match_eager(hip):
+    import torch
+    torch.cuda.init()
+    side = torch.cuda.Stream()
+    L = hip.lib
+    L.tensor_ops_hip_set_stream(ctypes.c_void_p(side.cuda_stream))
+    keep = []
+
+    def wrap(t, shape, dt):
+        arr = (ctypes.c_int * len(shape))(*shape)
+        p = L.tensor_wrap_device(ctypes.c_void_p(t.data_ptr()), arr, len(shape), dt)
+        assert p
+        keep.append(p)
+        return p
+
+    try:
+        with torch.cuda.stream(side):
+            rng = np.random.default_rng(11)
+            xs = rng.normal(0, 1.5, (8, 512, 1024)).astype(np.float32)
+            shp = list(xs.shape)
+            x = torch.from_numpy(xs).cuda()
+            s_u8 = torch.tensor([np.abs(xs).max() / 127], dtype=torch.float32, device="cuda")
+            z_u8 = torch.tensor([128], dtype=torch.uint8, device="cuda")
+            s_ax = torch.from_numpy((np.abs(xs).max(axis=(0, 2)) / 127).astype(np.float32).reshape(1, 512, 1)).cuda()
+            z_ax = torch.zeros((1, 512, 1), dtype=torch.int8, device="cuda")
+            a = torch.from_numpy(rng.uniform(-4, 4, (8, 64, 56, 56)).astype(np.float32)).cuda()
+            bb = torch.from_numpy(rng.uniform(0.5, 4, (64, 1, 1)).astype(np.float32)).cuda()
+            outs = {"q_u8": torch.empty(shp, dtype=torch.uint8, device="cuda"),
+                    "q_i8": torch.empty(shp, dtype=torch.int8, device="cuda"),
+                    "dq_u8": torch.empty(shp, dtype=torch.float32, device="cuda"),
+                    "dq_i8": torch.empty(shp, dtype=torch.float32, device="cuda"),
+                    "chain": torch.empty_like(a)}
+            tx, ta, tb = wrap(x, shp, O.F32), wrap(a, list(a.shape), O.F32), wrap(bb, [64, 1, 1], O.F32)
+            ts_u8, tz_u8 = wrap(s_u8, [1], O.F32), wrap(z_u8, [1], O.U8)
+            ts_ax, tz_ax = wrap(s_ax, [1, 512, 1], O.F32), wrap(z_ax, [1, 512, 1], O.I8)
+            t = {"q_u8": wrap(outs["q_u8"], shp, O.U8), "q_i8": wrap(outs["q_i8"], shp, O.I8),
+                 "dq_u8": wrap(outs["dq_u8"], shp, O.F32), "dq_i8": wrap(outs["dq_i8"], shp, O.F32),
+                 "chain": wrap(outs["chain"], list(a.shape), O.F32)}
+            steps = (Step * 7)(Step(0, 0, 0), Step(2, 0, 0), Step(1, 0, 0), Step(3, 0, 0), Step(4, 0, 0),
+                               Step(5, 0, 0), Step(6, 0, 0))
+            opnds = (O.PT * 1)(tb)
+            L.elementwise_chain_forward.argtypes = [O.PT, ctypes.POINTER(O.PT), ctypes.c_int, ctypes.POINTER(Step),
+                                                    ctypes.c_int, O.PT]
+
+            def step():
+                L.quantize_linear_forward(tx, ts_u8, tz_u8, t["q_u8"])
+                L.quantize_linear_forward(tx, ts_ax, tz_ax, t["q_i8"])
+                L.dequantize_linear_forward(t["q_u8"], ts_u8, tz_u8, t["dq_u8"])
+                L.dequantize_linear_forward(t["q_i8"], ts_ax, tz_ax, t["dq_i8"])
+                L.elementwise_chain_forward(ta, opnds, 1, steps, 7, t["chain"])
+
+            hip.lib.tensor_ops_hip_clear_error()
+            step()
+            torch.cuda.synchronize()
+            assert not hip.last_error(), hip.last_error()
+            eager = {k: v.cpu().numpy() for k, v in outs.items()}
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                step()
+            assert not hip.last_error(), hip.last_error()
+            for r in range(3):
+                for v in outs.values():
+                    v.view(torch.uint8).fill_(0xA5)
+                torch.cuda.synchronize()
+                g.replay()
+                torch.cuda.synchronize()
+                for k, v in outs.items():
+                    dt = {"q_u8": O.U8, "q_i8": O.I8, "chain": O.F32}.get(k, O.F32)
+                    assert_bitexact(v.cpu().numpy(), eager[k], dt, what=f"replay {r} {k}")
+                # eager library work between replays
+                L.add_forward(ta, tb, t["chain"])
+                torch.cuda.synchronize()
+        # the captured Q / DQ results are the oracle's too
+        o = O.oracle()
+        want = o.qdq("quantize", xs, O.F32, s_u8.cpu().numpy(), O.F32, z_u8.cpu().numpy(), O.U8, O.U8)
+        assert_bitexact(eager["q_u8"], want, O.U8, what="eager q_u8 vs oracle")
+    finally:
+        for p in keep:
+            L.free_tensor(p)
+        L.tensor_ops_hip_set_stream(None)
