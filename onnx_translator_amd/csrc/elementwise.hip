@@ -170,11 +170,11 @@ __device__ __forceinline__ void load_table(double* __restrict__ sT, const double
     __syncthreads();
 }
 
-__device__ __forceinline__ float abs_f32(float v) {
-    uint32_t u = f2u(v) & 0x7FFFFFFFu;
-    if (u > 0x7F800000u) u |= 0x00400000u;            // fabs through double quiets NaN
-    return u2f(u);
-}
+// fabs through double, as the reference computes it: exact for every
+// non-NaN value; a NaN comes back quiet with its sign cleared and its payload
+// kept (the f32 -> f64 -> f32 round trip).  Canonicalisation (IEEE mode:
+// denormals kept, signalling NaNs quieted) of |v| is that, in one instruction.
+__device__ __forceinline__ float abs_f32(float v) { return __builtin_canonicalizef(__builtin_fabsf(v)); }
 
 template <int U> __device__ __forceinline__ float unary_f32(float v, const double* T) {
     if constexpr (U == U_RELU) return v > 0.0f ? v : 0.0f;
@@ -208,8 +208,8 @@ __global__ __launch_bounds__(kBlock) void k_unary_f32(const float* __restrict__ 
 // grid is capped and strides over the tensor); U float4 units per thread per
 // tile.  The first tile's loads are issued before the table copy, so the two
 // latencies overlap.
-constexpr int kLutBlock = 512;
-constexpr int kLutBlocksPerCU = 3;
+constexpr int kLutBlock = 1024;
+constexpr int kLutBlocksPerCU = 1;
 constexpr int kCosUnits = 1;        // float4 units per thread of k_cos_f32
 
 template <int U>
@@ -471,8 +471,8 @@ void unary_entry(const char* name, const Tensor* X, Tensor* Y) {
 // decodes it with shifts instead of indexing the kernel argument memory.
 constexpr int kChainMaxSteps = 16, kChainMaxOperands = kMaxOperands - 1;
 constexpr int kChainW = 8;          // elements per thread of the vectorised chain kernel
-constexpr int kChainLutBlock = 256; // threads per block of the chain kernel with a Cos step
-constexpr int kChainLutPerCU = 4;   // its blocks per CU (LDS: one 32 KB table each)
+constexpr int kChainLutBlock = 512; // threads per block of the chain kernel with a Cos step
+constexpr int kChainLutPerCU = 2;   // its blocks per CU (LDS: one 32 KB table each)
 struct ChainProg {
     int n;
     uint64_t code[2];
