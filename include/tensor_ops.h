@@ -248,6 +248,15 @@ void conv2d_fused_qdq_forward(const Tensor* X, const Tensor* W, const Tensor* B,
 void dequantize_conv2d_fused_forward(const Tensor* Xq, const Tensor* XScale, const Tensor* XZero,
                                      const Tensor* W, const Tensor* B, const Tensor* Skip, int relu,
                                      Tensor* Y, ConvParams* params);
+/* DynamicQuantizeLinear that allocates nothing.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments and the same bits as
+ * dynamic_quantize_linear_forward; every tensor must be device-resident (an error
+ * otherwise: host tensors would need staging buffers).  Its min / max partials live in a
+ * fixed 32,784-byte device array per GPU (at most 2048 partials, whatever the input size),
+ * held until the process ends and shared by every call on that GPU: calls that overlap on
+ * one GPU race. */
+void dynamic_quantize_linear_forward_noalloc(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp);
 
 #ifdef __cplusplus
 }

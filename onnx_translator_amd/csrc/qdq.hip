@@ -43,6 +43,7 @@
 // 256-thread blocks, 8 blocks per CU; dequantize — one 4-byte code load and
 // one 16-byte nontemporal store per thread, 256-thread blocks, full grid.
 #include <algorithm>
+#include <mutex>
 #include <cfloat>
 
 #include "quant.h"
@@ -671,20 +672,68 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(const void* __restric
     }
 }
 
-void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp) {
-    const char* name = "dynamic_quantize_linear_forward";
+// Scratch of dynamic_quantize_linear_forward_noalloc: the min / max partials of
+// k_dql_minmax and the (scale, zero point) pair of k_dql_params, in a
+// file-scope device array (each GPU holds its own copy until the process
+// ends).  In host code `scratch` names a host-side stand-in, not device
+// memory: host code uses only the address hipGetSymbolAddress returns for the
+// library's device (dql_scratch).  Every call on one GPU shares the array, so
+// calls that overlap on one GPU (different streams or threads) race.  Nothing
+// in it needs to start at zero: k_dql_minmax writes every partial it launches
+// and k_dql_params the pair before any kernel reads them.
+constexpr int kDqlScratch = 2 * kDqlMaxParts + 2;             // 32,784 bytes
+static __device__ __align__(256) double scratch[kDqlScratch];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+double* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the library's device, resolved once per device
+// (with that device current) and kept; nullptr with the error set on failure.
+double* dql_scratch() {
+    const int dev = device_id();
+    if (dev < 0 || dev >= kMaxScratchDevices) { set_error("no-allocation scratch: device %d out of range", dev); return nullptr; }
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        int cur = 0;
+        if (!check_hip(hipGetDevice(&cur), "hipGetDevice")) return nullptr;
+        if (cur != dev && !check_hip(hipSetDevice(dev), "hipSetDevice")) return nullptr;
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (!check_hip(e, "hipGetSymbolAddress(scratch)")) return nullptr;
+        g_scratch_ptr[dev] = (double*)p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+// noalloc: the partials live in `scratch` instead of the HBM pool, and every
+// tensor must already be device-resident (host tensors would need staging
+// buffers); nothing is allocated.
+void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp, bool noalloc = false) {
+    const char* name = noalloc ? "dynamic_quantize_linear_forward_noalloc" : "dynamic_quantize_linear_forward";
     if (!tensor_sane(x, name) || !tensor_sane(y, name) || !tensor_sane(y_scale, name) || !tensor_sane(y_zp, name))
         return;
     if (y->size < x->size || y_scale->size < 1 || y_zp->size < 1) { set_error("%s: output too small", name); return; }
     if (!ensure_device()) return;
+    double* part = nullptr;
+    if (noalloc) {
+        const Tensor* all[4] = {x, y, y_scale, y_zp};
+        for (const Tensor* t : all)
+            if (t->size && !is_dev(classify(t->data))) {
+                set_error("%s: every tensor must be device-resident (host tensors need staging buffers)", name);
+                return;
+            }
+        if (!(part = dql_scratch())) return;
+    }
     const int64_t n = (int64_t)x->size;
     Staging st;
     const void* xd = st.in(x);
     void* yd = st.out(y, (size_t)n * dt_bytes((int)y->dtype));
     void* sd = st.out(y_scale, dt_bytes((int)y_scale->dtype));
     void* zd = st.out(y_zp, dt_bytes((int)y_zp->dtype));
-    double* part = (double*)pool_alloc(sizeof(double) * (2 * kDqlMaxParts + 2));
-    if (!xd || !yd || !sd || !zd || !part) { if (part) pool_free(part); st.finish(); return; }
+    if (!noalloc) part = (double*)pool_alloc(sizeof(double) * kDqlScratch);
+    if (!xd || !yd || !sd || !zd || !part) { if (part && !noalloc) pool_free(part); st.finish(); return; }
     double* params = part + 2 * kDqlMaxParts;
     const int dtx = (int)x->dtype, dty = (int)y->dtype;
     const bool v4 = dtx == kF32 && ((uintptr_t)xd & 15) == 0;
@@ -704,7 +753,7 @@ void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp) {
     else
         hipLaunchKernelGGL((k_dql_quant<-1, -1>), dim3(qblocks), dim3(kDqlThreads), 0, s, xd, dtx, n, params, yd, dty);
     const bool ok = check_launch(name);
-    pool_free(part);      // pool buffers are reused in stream order
+    if (!noalloc) pool_free(part);      // pool buffers are reused in stream order
     if (!ok) { st.finish(); return; }
     st.finish();
 }
@@ -785,6 +834,9 @@ void quantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Te
 }
 void dynamic_quantize_linear_forward(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp) {
     dql_entry(x, y, y_scale, y_zp);
+}
+void dynamic_quantize_linear_forward_noalloc(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp) {
+    dql_entry(x, y, y_scale, y_zp, true);
 }
 void dequantize_linear_axis_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint, Tensor* Y,
                                     int axis) {

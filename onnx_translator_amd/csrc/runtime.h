@@ -28,6 +28,7 @@ int device_count();
 bool exact_mode();
 const double* device_cos_lut();  // 4097 doubles in device memory (after init_cos_lut)
 int num_cus();
+int device_id();                 // the device the library stream belongs to (after ensure_device)
 
 // ---- memory -----------------------------------------------------------------
 enum class Mem { kHostPinned, kHostMalloc, kDevOwned, kDevBorrowed, kHostForeign, kDevForeign };

@@ -130,6 +130,7 @@ bool exact_mode() {
     return t_exact != 0;
 }
 int num_cus() { return S().cus > 0 ? S().cus : 256; }
+int device_id() { return S().dev; }
 
 // ---- memory -------------------------------------------------------------------------
 // Records a new header t over data p.  An owning kind (library allocation)
