@@ -144,6 +144,29 @@ __global__ __launch_bounds__(kRowThreads) void k_softmax_row_rt(const void* __re
 constexpr int kSplitThreads = 256;
 constexpr int kSplitWaves = kSplitThreads / 64;
 
+// The IPT values of this thread in the block's chunk [j0, j1) of a row
+// (element j0 + threadIdx.x + t * 256 for t < IPT; 0 past j1).  f32 goes
+// through a buffer resource over the chunk, so the loads are unconditional and
+// issue back to back (lanes past the end read 0 without touching memory).
+template <int DIN, int IPT>
+__device__ __forceinline__ void load_chunk(double (&v)[IPT], const void* __restrict__ X, int dtx, int64_t base,
+                                           int64_t j0, int64_t j1) {
+    if constexpr (DIN == kF32) {
+        const int64_t n = j1 > j0 ? j1 - j0 : 0;
+        const __amdgpu_buffer_rsrc_t xr = buffer_rsrc((const float*)X + base + j0, (uint32_t)(n * 4));
+#pragma unroll
+        for (int t = 0; t < IPT; t++)
+            v[t] = (double)__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                         xr, (uint32_t)((threadIdx.x + t * kSplitThreads) * 4), 0, 0));
+    } else {
+#pragma unroll
+        for (int t = 0; t < IPT; t++) {
+            const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
+            v[t] = j < j1 ? ldx<DIN>(X, base + j, dtx) : 0.0;
+        }
+    }
+}
+
 template <int DIN, int IPT>
 __global__ __launch_bounds__(kSplitThreads) void k_sm_part(const void* __restrict__ X, int dtx, int64_t L, int G,
                                                            double* __restrict__ part) {
@@ -154,10 +177,11 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_part(const void* __restric
     double mx = -DBL_MAX, sum = 0.0;
     if constexpr (IPT > 0) {
         double v[IPT];
+        load_chunk<DIN, IPT>(v, X, dtx, base, j0, j1);
 #pragma unroll
         for (int t = 0; t < IPT; t++) {
             const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
-            v[t] = j < j1 ? ldx<DIN>(X, base + j, dtx) : -DBL_MAX;
+            v[t] = j < j1 ? v[t] : -DBL_MAX;
             mx = v[t] > mx ? v[t] : mx;
         }
         mx = block_reduce<true, kSplitWaves>(mx, lds);
@@ -192,6 +216,9 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_out(const void* __restrict
     const int64_t base = row * L;
     const double* pm = part + row * G;
     const double* ps = part + rows * G + row * G;
+    // X first (independent of the partials), so its latency overlaps the fold
+    double v[IPT > 0 ? IPT : 1];
+    if constexpr (IPT > 0) load_chunk<DIN, IPT>(v, X, dtx, base, j0, j1);
     // Lane g folds partial g (G <= 64); every wave of every block of the row
     // runs the same butterfly on the same values, so all agree on M and S.
     const int lane = threadIdx.x & 63;
@@ -200,12 +227,6 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_out(const void* __restrict
     const double S = wave_sum(lane < G ? ps[lane] * sm_exp(m_l - M) : 0.0);
     const double rs = 1.0 / S;
     if constexpr (IPT > 0) {
-        double v[IPT];
-#pragma unroll
-        for (int t = 0; t < IPT; t++) {
-            const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
-            v[t] = j < j1 ? ldx<DIN>(X, base + j, dtx) : 0.0;
-        }
 #pragma unroll
         for (int t = 0; t < IPT; t++) {
             const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
