@@ -83,6 +83,7 @@ class Lib:
         L.tensor_from_host.restype = ctypes.c_int
         L.tensor_ops_hip_last_error.restype = ctypes.c_char_p
         L.tensor_ops_hip_set_stream.argtypes = [ctypes.c_void_p]
+        L.tensor_ops_hip_set_thread_stream.argtypes = [ctypes.c_void_p]
         L.free_tensor.argtypes = [PT]
         for n in ("quantize_linear_forward", "dequantize_linear_forward"):
             getattr(L, n).argtypes = [PT, PT, PT, PT]
@@ -163,7 +164,7 @@ def capture(torch, fn):
     return g
 
 
-def run_headline(lib, torch, steps, warmup, use_graph=False):
+def run_headline(lib, torch, steps, warmup, use_graph=False, nstreams=1):
     rng = np.random.default_rng(1)
     x = config2_input(rng)
     variants = config2_variants(x)
@@ -177,21 +178,45 @@ def run_headline(lib, torch, steps, warmup, use_graph=False):
     Z = [lib.dev(v[2], v[3]) for v in variants]
     L = lib.lib
     bytes_per_launch = 5 * n
+    # The four variants are independent: variant v runs on stream v % nstreams
+    # (default priority), so one variant's launch gap and tail overlap another's
+    # kernel.  Every buffer is written by one stream only (Y[v][*] by variant v;
+    # XR[q % R] with q = 4k + v is XR[v] or XR[v + 4]).
+    main = torch.cuda.current_stream()
+    streams = [torch.cuda.Stream() for _ in range(nstreams)] if nstreams > 1 else []
 
     def step(k):
         # launch q reads input set q % R; the dequantize of variant v reads the
         # codes its quantize wrote one step earlier (4 launches, > 600 MB ago)
         for v in range(4):
             q = 4 * k + v
+            if streams:
+                L.tensor_ops_hip_set_thread_stream(ctypes.c_void_p(streams[v % nstreams].cuda_stream))
             L.quantize_linear_forward(X[q % R], S[v], Z[v], Y[v][k % R])
             L.dequantize_linear_forward(Y[v][(k - 1) % R], S[v], Z[v], XR[q % R])
+        if streams:
+            L.tensor_ops_hip_set_thread_stream(None)
 
+    def fork():
+        e = torch.cuda.Event()
+        e.record(main)
+        for st in streams:
+            st.wait_event(e)
+
+    def join():
+        for st in streams:
+            e = torch.cuda.Event()
+            e.record(st)
+            main.wait_event(e)
+
+    fork()
     for k in range(warmup):
         step(k)
+    join()
     lib.check("warmup")
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    if use_graph:
+    if use_graph and not streams:
         # The K timed steps (8 launches each, the same rotation of buffers) are
         # captured once into a HIP graph on the library's stream; one untimed
         # replay, then one timed replay of exactly K steps.
@@ -204,10 +229,12 @@ def run_headline(lib, torch, steps, warmup, use_graph=False):
         t1.record()
     else:
         w0 = time.perf_counter()
-        t0.record()
+        t0.record(main)
+        fork()
         for k in range(steps):
             step(warmup + k)
-        t1.record()
+        join()
+        t1.record(main)
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     lib.check("timed steps")
@@ -763,6 +790,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--streams", type=int, default=1,
+                    help="HIP streams the four headline variants are spread over (1: one stream, in order; "
+                         "2 and 4 measured no faster on MI355X: the step is bandwidth-bound)")
     ap.add_argument("--graph", action="store_true",
                     help="time the headline steps as one HIP graph replay instead of eager back-to-back launches "
                          "(measured slower for these 84 MB launches on MI355X)")
@@ -819,7 +849,7 @@ def main():
             print(json.dumps(line), flush=True)
         return
     print("bench: headline Q/DQ round trips ...", file=sys.stderr, flush=True)
-    h = run_headline(lib, torch, args.steps, args.warmup, use_graph=args.graph)
+    h = run_headline(lib, torch, args.steps, args.warmup, use_graph=args.graph, nstreams=args.streams)
     value = h["bytes_per_step"] / (h["ms_per_step"] * 1e-3) / 1e9
     dom_ms = h["kernel_ms"][h["dominant"]]
     achieved = h["bytes_per_launch"] / (dom_ms * 1e-3) / 1e9
@@ -843,7 +873,8 @@ def main():
         "config": {"workload": "configs[1]: QuantizeLinear->DequantizeLinear round trip, x f32 [32,512,1024] "
                                "N(0,1.5)+0.1% x20 outliers, seed 1; u8 per-tensor, i8 per-axis(1), e4m3, e5m2",
                    "elements": h["n"], "bytes_per_step": h["bytes_per_step"], "rotating_sets": 8,
-                   "timing": "one HIP graph replay of the K steps" if args.graph else "eager launches"},
+                   "timing": ("one HIP graph replay of the K steps" if args.graph and args.streams <= 1 else
+                              f"eager launches, the 4 variants over {max(1, args.streams)} HIP stream(s)")},
         "frac_hbm": round(value * 1e9 / HBM_PEAK, 4),
         "roofline": {"bound": "hbm", "kernel": h["dominant"], "achieved": round(achieved, 1), "peak": 8000.0,
                      "unit": "GB/s", "frac": round(achieved / 8000.0, 4), "traffic": traffic,

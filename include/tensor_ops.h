@@ -157,6 +157,11 @@ int tensor_from_host(Tensor* t, const void* host_src);
 int tensor_ops_hip_sync(void);
 /* Use a caller-provided hipStream_t (NULL restores the library's own stream). */
 void tensor_ops_hip_set_stream(void* stream);
+/* Stream for the calling thread's subsequent calls only, overriding the one above (NULL
+ * clears the override).  Nothing is drained: the caller orders work across its streams.
+ * Library workspace buffers are reused only on the stream they were released on; a
+ * tensor used on several streams must be freed once the caller has ordered them. */
+void tensor_ops_hip_set_thread_stream(void* stream);
 void* tensor_ops_hip_get_stream(void);
 /* Number of usable GPUs (0 on a machine without one). */
 int tensor_ops_hip_device_count(void);

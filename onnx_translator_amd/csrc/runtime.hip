@@ -54,7 +54,9 @@ struct State {
     // Ownership per header: how free_tensor releases the data of each header
     // this library returned (kDevBorrowed: the caller owns the data).
     std::unordered_map<const Tensor*, Mem> owners;
-    std::multimap<size_t, void*> dev_free;
+    // Cached HBM buffers per stream: a buffer freed while stream S was current
+    // is handed out again only to work on S, so reuse follows S's order.
+    std::map<hipStream_t, std::multimap<size_t, void*>> dev_free;
     std::unordered_map<void*, size_t> dev_size;
     size_t dev_cached = 0;
     std::multimap<size_t, void*> pin_free;
@@ -111,7 +113,11 @@ int device_count() {
     return s.ok ? s.ndev : 0;
 }
 
+// Stream of the calling thread (tensor_ops_hip_set_thread_stream), if set.
+static thread_local hipStream_t t_stream = nullptr;
+
 hipStream_t stream() {
+    if (t_stream) return t_stream;
     State& s = S();
     hipStream_t u = s.user.load();
     return u ? u : s.own;
@@ -201,17 +207,20 @@ void* pool_alloc(size_t bytes) {
     const size_t need = round_bytes(bytes);
     {
         std::lock_guard<std::mutex> g(s.mu);
-        if (void* p = take_cached(s.dev_free, need, s.dev_cached)) return p;
+        auto fl = s.dev_free.find(stream());
+        if (fl != s.dev_free.end())
+            if (void* p = take_cached(fl->second, need, s.dev_cached)) return p;
     }
     void* p = nullptr;
     if (hipMalloc(&p, need) != hipSuccess) {
         (void)hipGetLastError();
         // Release the cache and retry once.
         std::lock_guard<std::mutex> g(s.mu);
-        for (auto& kv : s.dev_free) {
-            (void)hipFree(kv.second);
-            s.dev_size.erase(kv.second);
-        }
+        for (auto& per_stream : s.dev_free)
+            for (auto& kv : per_stream.second) {
+                (void)hipFree(kv.second);
+                s.dev_size.erase(kv.second);
+            }
         s.dev_free.clear();
         s.dev_cached = 0;
         if (hipMalloc(&p, need) != hipSuccess) {
@@ -237,7 +246,7 @@ void pool_free(void* p) {
         return;
     }
     s.dev_cached += it->second;
-    s.dev_free.emplace(it->second, p);
+    s.dev_free[stream()].emplace(it->second, p);
 }
 
 static void* pinned_alloc(size_t bytes) {
@@ -611,9 +620,24 @@ int tensor_ops_hip_sync(void) {
 
 void tensor_ops_hip_set_stream(void* s) {
     if (!ensure_device()) return;
-    // Drain the previous stream so pool buffers freed on it are safe to reuse.
-    (void)hipStreamSynchronize(stream());
-    S().user.store((hipStream_t)s);
+    State& st = S();
+    // Drain the previous stream, then its cached buffers may serve the new one.
+    const hipStream_t old_s = st.user.load() ? st.user.load() : st.own;
+    (void)hipStreamSynchronize(old_s);
+    st.user.store((hipStream_t)s);
+    const hipStream_t new_s = s ? (hipStream_t)s : st.own;
+    std::lock_guard<std::mutex> g(st.mu);
+    auto it = st.dev_free.find(old_s);
+    if (it != st.dev_free.end() && old_s != new_s) {
+        auto& dst = st.dev_free[new_s];
+        for (auto& kv : it->second) dst.emplace(kv.first, kv.second);
+        st.dev_free.erase(old_s);
+    }
+}
+
+void tensor_ops_hip_set_thread_stream(void* s) {
+    if (!ensure_device()) return;
+    t_stream = (hipStream_t)s;
 }
 
 void* tensor_ops_hip_get_stream(void) { return ensure_device() ? (void*)stream() : nullptr; }

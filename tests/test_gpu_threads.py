@@ -4,9 +4,10 @@ ctypes releases the GIL around every foreign call, so threads really do enter
 the library at the same time, as callers of the reference can
 (tensor_ops.c:21-25,763-807: the reference is re-entrant, its one-time cosine
 table set-up is mutex-guarded).  Each thread runs host-tensor calls (staged,
-synchronous), device-tensor calls (asynchronous on the library stream) and
-its own precision mode, and every result must equal the oracle's to its
-parity class; the precision mode one thread sets must not reach another.
+synchronous), device-tensor calls (asynchronous on the library stream, or on
+a stream of the thread's own for half of them) and its own precision mode,
+and every result must equal the oracle's to its parity class; the precision
+mode one thread sets must not reach another.
 """
 import ctypes
 import threading
@@ -52,11 +53,19 @@ def test_concurrent_calls_match_the_oracle(hip, oracle_lib):
     errors = []
     start = threading.Barrier(THREADS)
 
+    import torch
+    torch.cuda.init()
+    L.tensor_ops_hip_set_thread_stream.argtypes = [ctypes.c_void_p]
+    # threads 2, 3, 6, 7 launch on a stream of their own (tensor_ops_hip_set_thread_stream)
+    own = {t: torch.cuda.Stream() for t in range(THREADS) if t % 4 >= 2}
+
     def work(t):
         c = cases[t]
         exact = t % 2 == 1
         try:
             hip.set_exact(exact)
+            if t in own:
+                L.tensor_ops_hip_set_thread_stream(ctypes.c_void_p(own[t].cuda_stream))
             start.wait(timeout=120)
             for r in range(ROUNDS):
                 # host tensors: staged through HBM, synchronous
@@ -88,6 +97,7 @@ def test_concurrent_calls_match_the_oracle(hip, oracle_lib):
             errors.append(f"thread {t}: {e!r}"[:600])
         finally:
             hip.set_exact(False)
+            L.tensor_ops_hip_set_thread_stream(None)
 
     print(f"threads: {THREADS} x {ROUNDS} rounds of add / quantize / gemm / device add+cos", flush=True)
     threads = [threading.Thread(target=work, args=(t,)) for t in range(THREADS)]

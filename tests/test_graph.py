@@ -423,7 +423,7 @@ def test_resnet_qdq_graph_batch64(hip, oracle_lib, exact):
     independent, so the oracle runs the two images as a batch of 2 of the same
     model (same seeded weights).  Exact mode: logits bit for bit, probabilities in
     the Softmax tolerance class.  MFMA mode: fp32 accumulation flips a few uint8
-    activation codes at rounding ties; bounds below (measured error x ~3)."""
+    activation codes at rounding ties; bounds below (measured error x ~7)."""
     from onnx_translator_amd.nn.graph import Graph
     from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
     m = resnet_qdq_model(batch=64)
@@ -451,6 +451,8 @@ def test_resnet_qdq_graph_batch64(hip, oracle_lib, exact):
 
 
 # MFMA-mode bounds of the batch-64 check, relative to the largest reference
-# logit / probability (set from the measured errors on MI355X with margin).
-LOGIT_BOUND = 5e-3
-PROB_BOUND = 5e-3
+# logit / probability.  Measured on MI355X over image pairs (0, 63), (1, 2),
+# (30, 31): logits 3.6e-5 .. 6.5e-5, probabilities 0.8e-4 .. 1.5e-4 (a few
+# flipped uint8 activation codes at rounding ties); the bounds keep ~7x margin.
+LOGIT_BOUND = 1e-3
+PROB_BOUND = 1e-3
