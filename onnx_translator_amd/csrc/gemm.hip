@@ -388,9 +388,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm_mfma_f16(GemmArgs g, int vec)
 // A [M, K] and B [N, K] row-major (transA = 0, transB = 1: the layout of the
 // ONNX Gemm with transB = 1).  Block tile BM x BN x BK over NT = 64 * WGM * WGN
 // threads; wave tile (BM / WGM) x (BN / WGN) of 32x32 MFMA tiles.
-// Pipeline per k-tile: issue the global loads of tile k + 1 into registers,
-// run the MFMAs of tile k from LDS, write the registers to the other LDS
-// buffer, one barrier.  LDS rows are BK + 8 halves (16 bytes of padding), so
+// Pipeline per k-tile (below): the next tile's registers go to the other LDS
+// buffer, the tile after it is requested, the MFMAs of tile k run from LDS,
+// one barrier.  LDS rows are BK + 8 halves (16 bytes of padding), so
 // the 16-byte fragment reads of 8 consecutive rows cover all banks once.
 // Tile order: consecutive workgroups are spread over the 8 XCDs by the
 // dispatcher, so the block index is remapped to give each XCD a contiguous
@@ -432,7 +432,54 @@ __device__ __forceinline__ void epilogue_fast(const GemmArgs& g, int m, int n, d
     }
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int YDT, int NBUF = 2, int IGLP = -1, bool PIN = false>
+// The 16 accumulators a lane holds for one 32x32 MFMA tile: column n, rows
+// mb + 8 * (r >> 2) + (r & 3).  Same arithmetic as epilogue_fast, specialised
+// on the bias (BIAS 0: none, 1: scalar / per column, loaded and multiplied once
+// per column, 3: per row) and on whether the tile lies wholly inside Y (FULL:
+// no per-element checks), so the stores need no divergent branches.
+template <int YDT, int BIAS, bool FULL>
+__device__ __forceinline__ void epilogue_col_f(const GemmArgs& g, int mb, int n, const floatx16& a) {
+    const gfloat* c = (const gfloat*)g.c.p;
+    double cn = 0.0;
+    if constexpr (BIAS == 1) cn = g.beta * (double)c[g.c.mode == 1 ? 0 : n];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int m = mb + 8 * (r >> 2) + (r & 3);
+        if (!FULL && (m >= g.M || n >= g.N)) continue;
+        double v = g.alpha * (double)a[r];
+        if constexpr (BIAS == 1) v += cn;
+        if constexpr (BIAS == 3) v += g.beta * (double)c[m];
+        const int64_t i = (int64_t)m * g.N + n;
+        if constexpr (YDT == kF16) ((gu16*)g.Y)[i] = enc_f16((float)v);
+        else ((gfloat*)g.Y)[i] = (float)v;
+    }
+}
+
+template <int YDT, int BIAS>
+__device__ __forceinline__ void epilogue_col_b(const GemmArgs& g, bool full, int mb, int n, const floatx16& a) {
+    if (full) epilogue_col_f<YDT, BIAS, true>(g, mb, n, a);
+    else epilogue_col_f<YDT, BIAS, false>(g, mb, n, a);
+}
+
+// mt, nt: the MFMA tile's first row and column (uniform over the wave).
+template <int YDT>
+__device__ __forceinline__ void epilogue_col(const GemmArgs& g, int mt, int mb, int nt, int n, const floatx16& a) {
+    if constexpr (YDT == kF16 || YDT == kF32) {
+        const bool full = mt + 32 <= g.M && nt + 32 <= g.N;
+        if (g.c.mode == 0) epilogue_col_b<YDT, 0>(g, full, mb, n, a);
+        else if (g.c.mode == 3) epilogue_col_b<YDT, 3>(g, full, mb, n, a);
+        else epilogue_col_b<YDT, 1>(g, full, mb, n, a);
+    } else {
+        if (n >= g.N) return;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = mb + 8 * (r >> 2) + (r & 3);
+            if (m < g.M) store_rt(g, m, n, (double)a[r]);
+        }
+    }
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, int YDT, int IGLP = -1>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_f16_nt(GemmArgs g) {
     constexpr int NT = 64 * WGM * WGN;
     constexpr int LDK = BK + 8;
@@ -441,7 +488,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_f16_nt(GemmArgs g) {
     constexpr int CPR = BK / 8;                   // 16-byte chunks per tile row
     constexpr int CA = BM * CPR / NT, CB = BN * CPR / NT;
     static_assert(CA * NT == BM * CPR && CB * NT == BN * CPR, "tile / thread mismatch");
-    __shared__ _Float16 lds[NBUF][(BM + BN) * LDK];
+    __shared__ _Float16 lds[2][(BM + BN) * LDK];
 
     const int nbm = (g.M + BM - 1) / BM, nbn = (g.N + BN - 1) / BN;
     int tm, tn;
@@ -514,41 +561,38 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_f16_nt(GemmArgs g) {
         }
     };
 
+    // Pipeline: tile k + 1 sits in registers while tile k is multiplied.  At
+    // the top of iteration k it goes to the other LDS buffer (its loads were
+    // issued one whole iteration earlier, so their latency is hidden), then
+    // the loads of tile k + 2 are issued into the same registers, then tile
+    // k's MFMAs run, then one barrier.  The buffer written in iteration k was
+    // last read in iteration k - 1, before that iteration's barrier.
     const int nk = (g.K + BK - 1) / BK;
     load_tile(0);
     if (BK > g.K) mask_tile(0);
     store_tile(0);
+    if (nk > 1) load_tile(BK);
     __syncthreads();
-    // All k-tiles but the last: one basic block per iteration (loads of the
-    // next tile, MFMAs of this one, LDS writes of the next), so the scheduler
-    // can interleave the three streams.
-    int kt = 0;
-    for (; kt + 1 < nk; kt++) {
-        const int cur = NBUF == 2 ? (kt & 1) : 0;
-        const int k1 = (kt + 1) * BK;
-        load_tile(k1);
-        // PIN: keep the next tile's loads at the top of the iteration, ahead of
-        // this tile's MFMAs (the scheduler otherwise sinks them next to their
-        // use, exposing the global latency).
-        if constexpr (PIN) __builtin_amdgcn_sched_barrier(0);
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) {
+            const int k1 = (kt + 1) * BK;
+            if (k1 + BK > g.K) mask_tile(k1);
+            store_tile(cur ^ 1);
+            if (kt + 2 < nk) load_tile(k1 + BK);
+        }
+        // keep the stores and the next loads ahead of this tile's MFMAs
+        __builtin_amdgcn_sched_barrier(0);
         compute(cur);
         if constexpr (IGLP >= 0) __builtin_amdgcn_iglp_opt(IGLP);
-        if (k1 + BK > g.K) mask_tile(k1);
-        if constexpr (NBUF == 1) __syncthreads();
-        store_tile(NBUF == 2 ? (cur ^ 1) : 0);
         __syncthreads();
     }
-    compute(NBUF == 2 ? (kt & 1) : 0);
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + (lk >> 1) + (r & 3);
-                const int n = n0 + wn * WTN + j * 32 + lr;
-                if (m < g.M && n < g.N) epilogue_fast<YDT>(g, m, n, (double)acc[i][j][r]);
-            }
+            epilogue_col<YDT>(g, m0 + wm * WTM + i * 32, m0 + wm * WTM + i * 32 + (lk >> 1), n0 + wn * WTN + j * 32,
+                              n0 + wn * WTN + j * 32 + lr, acc[i][j]);
 }
 
 // ------------------------------------------------------------- f32 NT tiled ---
@@ -772,30 +816,29 @@ void launch_f16_y(const GemmArgs& g, dim3 grid, int vec, hipStream_t s) {
 
 // f16 x f16 with both operands K-major (A [M, K], B [N, K]) and 16-byte
 // aligned rows: the tiled kernel.  256x256 tiles (16 waves of 64x64) when the
-// grid still covers the 256 CUs, else 128x128 tiles (4 waves of 64x64); the
-// next tile's loads pinned ahead of the MFMAs.  Sweeps on MI355X: 16 waves of
-// 64x64 beat 8 waves of 128x64 (0.37-0.39 vs 0.30-0.34 of the fp16 peak at
-// 4096^3) once the loads are pinned.
+// grid still covers the 256 CUs, else 128x128 tiles (4 waves of 64x64).
+// Sweeps on MI355X: 16 waves of 64x64 beat 8 waves of 128x64 or 64x128 and a
+// two-group ping-pong of 8 waves at 4096^3.
 // Returns false when the operands exceed the 2 GB reach of a buffer resource.
-template <int BM, int BN, int BK, int WGM, int WGN, int NBUF, int IGLP>
+template <int BM, int BN, int BK, int WGM, int WGN, int IGLP>
 void launch_f16_nt_cfg(const GemmArgs& g, hipStream_t s) {
     const int nb = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
     const bool fast_bias = g.c.mode == 0 || (g.c.dt == kF32 && g.c.mode <= 3);
     const dim3 grid(nb), block(64 * WGM * WGN);
     if (fast_bias && g.dty == kF16)
-        hipLaunchKernelGGL((k_gemm_f16_nt<BM, BN, BK, WGM, WGN, kF16, NBUF, IGLP, true>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((k_gemm_f16_nt<BM, BN, BK, WGM, WGN, kF16, IGLP>), grid, block, 0, s, g);
     else if (fast_bias && g.dty == kF32)
-        hipLaunchKernelGGL((k_gemm_f16_nt<BM, BN, BK, WGM, WGN, kF32, NBUF, IGLP, true>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((k_gemm_f16_nt<BM, BN, BK, WGM, WGN, kF32, IGLP>), grid, block, 0, s, g);
     else
-        hipLaunchKernelGGL((k_gemm_f16_nt<BM, BN, BK, WGM, WGN, -1, NBUF, IGLP, true>), grid, block, 0, s, g);
+        hipLaunchKernelGGL((k_gemm_f16_nt<BM, BN, BK, WGM, WGN, -1, IGLP>), grid, block, 0, s, g);
 }
 
 bool launch_f16_nt(const GemmArgs& g, hipStream_t s) {
     const int64_t reach = (int64_t)1 << 31;
     if ((int64_t)(g.M + 256) * g.lda * 2 >= reach || (int64_t)(g.N + 256) * g.ldb * 2 >= reach) return false;
     const int64_t big_tiles = (int64_t)((g.M + 255) / 256) * ((g.N + 255) / 256);
-    if (big_tiles >= 192) launch_f16_nt_cfg<256, 256, 64, 4, 4, 2, 0>(g, s);
-    else launch_f16_nt_cfg<128, 128, 64, 2, 2, 2, 0>(g, s);
+    if (big_tiles >= 192) launch_f16_nt_cfg<256, 256, 64, 4, 4, 1>(g, s);
+    else launch_f16_nt_cfg<128, 128, 64, 2, 2, 1>(g, s);
     return true;
 }
 
