@@ -25,6 +25,7 @@
 // gives -inf, the first of +-0 wins.  General windows: one wave per output
 // row, one lane per output column.  The ResNet 3x3 / stride 2 / pad 1 f32
 // window has a block-per-plane strip kernel that loads each input row once.
+#include <atomic>
 #include <cfloat>
 
 #include "quant.h"
@@ -238,19 +239,195 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_out(const void* __restrict
     }
 }
 
+// Split rows in one launch (IPT > 0): block b of a row computes its chunk's
+// partial (m_b, s_b) exactly as k_sm_part does, publishes it, waits for the
+// row's other G - 1 partials, folds them exactly as k_sm_out does and writes
+// its chunk from registers: X is read once and there is no second launch.
+// Publication: four 64-bit words per block, (tag, high / low half of m_b),
+// (tag, high / low half of s_b), written and polled with
+// relaxed device-scope atomics (single-copy atomic words, coherent across the
+// XCDs' L2s).  The tag is unique to the call, so a word is current exactly
+// when it carries the call's tag: no fence, no zeroing, no reset of the
+// workspace (stale words from earlier calls carry other tags).
+// The wait is bounded (`spin` polls): if a partial has not appeared by then
+// (the row's blocks are not all resident, e.g. other work fills the GPU), the
+// whole block recomputes that chunk's partial from X with the same thread
+// mapping and reduction order, which gives the same bits, so every block ends
+// with the same (M, S) either way and every wave exits.
+constexpr int kSmSpinDefault = 1 << 14;   // polls of ~64 cycles each (about 0.5 ms)
+std::atomic<int> g_sm_spin{kSmSpinDefault};   // tensor_ops_hip_set_softmax_spin
+
+__device__ __forceinline__ void sm_pub(unsigned long long* p, uint32_t tag, uint32_t v) {
+    __hip_atomic_store(p, ((unsigned long long)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool sm_get(const unsigned long long* p, uint32_t tag, uint32_t& v) {
+    const unsigned long long w = __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    v = (uint32_t)w;
+    return (uint32_t)(w >> 32) == tag;
+}
+
+// (m, s) of chunk c of a row, the whole block participating; v receives the
+// chunk's values (as k_sm_part holds them).
+template <int DIN, int IPT>
+__device__ __forceinline__ void sm_chunk_partial(double (&v)[IPT], const void* __restrict__ X, int dtx, int64_t base,
+                                                 int64_t L, int64_t chunk, int c, double* lds, double& mx, double& sum) {
+    const int64_t j0 = c * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
+    load_chunk<DIN, IPT>(v, X, dtx, base, j0, j1);
+    mx = -DBL_MAX;
+#pragma unroll
+    for (int t = 0; t < IPT; t++) {
+        const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
+        v[t] = j < j1 ? v[t] : -DBL_MAX;
+        mx = v[t] > mx ? v[t] : mx;
+    }
+    mx = block_reduce<true, kSplitWaves>(mx, lds);
+    sum = 0.0;
+#pragma unroll
+    for (int t = 0; t < IPT; t++) {
+        const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
+        if (j < j1) sum += sm_exp(v[t] - mx);
+    }
+    sum = block_reduce<false, kSplitWaves>(sum, lds);
+}
+
 template <int DIN, int DOUT, int IPT>
-void launch_split_ipt(const void* x, int dtx, void* y, int dty, int64_t L, int G, double* part, dim3 g, hipStream_t s) {
-    hipLaunchKernelGGL((k_sm_part<DIN, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, L, G, part);
-    hipLaunchKernelGGL((k_sm_out<DIN, DOUT, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, y, dty, L, G, part);
+__global__ __launch_bounds__(kSplitThreads) void k_sm_one(const void* __restrict__ X, int dtx, void* __restrict__ Y,
+                                                          int dty, int64_t L, int G,
+                                                          unsigned long long* __restrict__ slots, uint32_t tag,
+                                                          int spin) {
+    __shared__ double lds[kSplitWaves];
+    __shared__ double fm[64], fs[64];          // partials recomputed by this block
+    __shared__ unsigned long long s_missing;
+    __shared__ double sM, sS;
+    const int64_t row = blockIdx.y, chunk = (L + G - 1) / G;
+    const int64_t base = row * L;
+    const int64_t j0 = blockIdx.x * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
+    double v[IPT];
+    double mx, sum;
+    sm_chunk_partial<DIN, IPT>(v, X, dtx, base, L, chunk, (int)blockIdx.x, lds, mx, sum);
+    unsigned long long* rs = slots + (size_t)row * G * 4;
+    if (threadIdx.x == 0) {
+        const unsigned long long mb = __builtin_bit_cast(unsigned long long, mx);
+        const unsigned long long sb = __builtin_bit_cast(unsigned long long, sum);
+        sm_pub(rs + blockIdx.x * 4 + 0, tag, (uint32_t)(mb >> 32));
+        sm_pub(rs + blockIdx.x * 4 + 1, tag, (uint32_t)mb);
+        sm_pub(rs + blockIdx.x * 4 + 2, tag, (uint32_t)(sb >> 32));
+        sm_pub(rs + blockIdx.x * 4 + 3, tag, (uint32_t)sb);
+    }
+    // Wave 0, lane g: wait for partial g (its own block's included).
+    const int lane = threadIdx.x & 63;
+    uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
+    bool have = false;
+    if (threadIdx.x < 64) {
+        if (lane < G) {
+            if (lane == (int)blockIdx.x) {
+                const unsigned long long mb = __builtin_bit_cast(unsigned long long, mx);
+                const unsigned long long sb = __builtin_bit_cast(unsigned long long, sum);
+                w0 = (uint32_t)(mb >> 32);
+                w1 = (uint32_t)mb;
+                w2 = (uint32_t)(sb >> 32);
+                w3 = (uint32_t)sb;
+                have = true;
+            }
+            for (int it = 0; !have && it < spin; it++) {
+                have = sm_get(rs + lane * 4 + 0, tag, w0) && sm_get(rs + lane * 4 + 1, tag, w1) &&
+                       sm_get(rs + lane * 4 + 2, tag, w2) && sm_get(rs + lane * 4 + 3, tag, w3);
+                if (!have) __builtin_amdgcn_s_sleep(1);
+            }
+        } else {
+            have = true;
+        }
+        const unsigned long long miss = __ballot(!have);
+        if (lane == 0) s_missing = miss;
+    }
+    __syncthreads();
+    // Partials that did not arrive in time: recompute them here (uniform loop).
+    for (unsigned long long miss = s_missing; miss; miss &= miss - 1) {
+        const int c = __builtin_ctzll(miss);
+        double w[IPT], m_c, s_c;
+        sm_chunk_partial<DIN, IPT>(w, X, dtx, base, L, chunk, c, lds, m_c, s_c);
+        if (threadIdx.x == 0) { fm[c] = m_c; fs[c] = s_c; }
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        double m_l = -DBL_MAX, s_l = 0.0;
+        if (lane < G) {
+            if (have) {
+                m_l = __builtin_bit_cast(double, ((unsigned long long)w0 << 32) | w1);
+                s_l = __builtin_bit_cast(double, ((unsigned long long)w2 << 32) | w3);
+            } else {
+                m_l = fm[lane];
+                s_l = fs[lane];
+            }
+        }
+        // the fold of k_sm_out
+        const double M = wave_max(m_l);
+        const double S = wave_sum(lane < G ? s_l * sm_exp(m_l - M) : 0.0);
+        if (lane == 0) { sM = M; sS = S; }
+    }
+    __syncthreads();
+    const double M = sM, r = 1.0 / sS;
+#pragma unroll
+    for (int t = 0; t < IPT; t++) {
+        const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
+        if (j < j1) stx<DOUT>(Y, base + j, sm_exp(v[t] - M) * r, dty);
+    }
+}
+
+// Tags of the one-launch split kernel: unique per call in this process (0 is
+// never used, so zeroed memory never matches).
+std::atomic<uint32_t> g_sm_tag{0};
+uint32_t next_sm_tag() {
+    uint32_t t;
+    do t = g_sm_tag.fetch_add(1, std::memory_order_relaxed) + 1; while (t == 0);
+    return t;
+}
+
+// Whether s is being captured into a graph: a captured launch would replay
+// with the tag of its capture, so the next replay could take the previous
+// replay's partials for current ones; captured calls use the two launches.
+bool stream_capturing(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return cs != hipStreamCaptureStatusNone;
+}
+
+// Returns false when the workspace cannot be allocated (error set).
+template <int DIN, int DOUT, int IPT>
+bool launch_split_ipt(const void* x, int dtx, void* y, int dty, int64_t L, int G, dim3 g, hipStream_t s) {
+    if (IPT > 0 && !stream_capturing(s)) {
+        unsigned long long* slots =
+            (unsigned long long*)pool_alloc(sizeof(unsigned long long) * 4 * (size_t)g.y * (size_t)G);
+        if (!slots) return false;
+        if constexpr (IPT > 0)
+            hipLaunchKernelGGL((k_sm_one<DIN, DOUT, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, y, dty, L, G, slots,
+                               next_sm_tag(), g_sm_spin.load(std::memory_order_relaxed));
+        pool_free(slots);   // stream-ordered reuse: later work on this stream runs after the kernel
+        return true;
+    } else {
+        // sized as the one-launch workspace, so a call captured into a graph
+        // after an eager call of the same shape reuses that call's cached
+        // buffer instead of allocating inside the capture
+        double* part = (double*)pool_alloc(sizeof(double) * 4 * (size_t)g.y * (size_t)G);
+        if (!part) return false;
+        hipLaunchKernelGGL((k_sm_part<DIN, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, L, G, part);
+        hipLaunchKernelGGL((k_sm_out<DIN, DOUT, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, y, dty, L, G, part);
+        pool_free(part);
+    }
+    return true;
 }
 
 template <int DIN, int DOUT>
-void launch_split(const void* x, int dtx, void* y, int dty, int64_t L, int G, double* part, dim3 g, hipStream_t s) {
+bool launch_split(const void* x, int dtx, void* y, int dty, int64_t L, int G, dim3 g, hipStream_t s) {
     const int64_t ipt = ((L + G - 1) / G + kSplitThreads - 1) / kSplitThreads;
-    if (ipt <= 4) launch_split_ipt<DIN, DOUT, 4>(x, dtx, y, dty, L, G, part, g, s);
-    else if (ipt <= 8) launch_split_ipt<DIN, DOUT, 8>(x, dtx, y, dty, L, G, part, g, s);
-    else if (ipt <= 16) launch_split_ipt<DIN, DOUT, 16>(x, dtx, y, dty, L, G, part, g, s);
-    else launch_split_ipt<DIN, DOUT, 0>(x, dtx, y, dty, L, G, part, g, s);
+    if (ipt <= 4) return launch_split_ipt<DIN, DOUT, 4>(x, dtx, y, dty, L, G, g, s);
+    if (ipt <= 8) return launch_split_ipt<DIN, DOUT, 8>(x, dtx, y, dty, L, G, g, s);
+    if (ipt <= 16) return launch_split_ipt<DIN, DOUT, 16>(x, dtx, y, dty, L, G, g, s);
+    return launch_split_ipt<DIN, DOUT, 0>(x, dtx, y, dty, L, G, g, s);
 }
 
 // inner > 1: one thread per (outer, r) column; rows of the axis are coalesced across threads.
@@ -529,6 +706,10 @@ void global_average_pool_forward(const Tensor* input, Tensor* output) {
 }
 
 
+int tensor_ops_hip_set_softmax_spin(int polls) {
+    return g_sm_spin.exchange(polls < 0 ? kSmSpinDefault : polls);
+}
+
 void softmax_forward(const Tensor* input, Tensor* output, int axis) {
     const char* name = "softmax_forward";
     if (!tensor_sane(input, name) || !tensor_sane(output, name)) return;
@@ -556,16 +737,12 @@ void softmax_forward(const Tensor* input, Tensor* output, int axis) {
             if (G > 64) G = 64;
         }
         if (inner == 1 && G > 1) {
-            double* part = (double*)pool_alloc(sizeof(double) * 2 * (size_t)outer * G);
-            if (!part) { st.finish(); return; }
             const dim3 g((unsigned)G, (unsigned)outer);
-            if (dtx == kF32 && dty == kF32) launch_split<kF32, kF32>(x, dtx, y, dty, L, G, part, g, s);
-            else if (dtx == kF32) launch_split<kF32, -1>(x, dtx, y, dty, L, G, part, g, s);
-            else launch_split<-1, -1>(x, dtx, y, dty, L, G, part, g, s);
-            const bool ok = check_launch(name);
-            // Pool buffers are reused in stream order, so the partials can go back now.
-            pool_free(part);
-            if (!ok) { st.finish(); return; }
+            bool ok;
+            if (dtx == kF32 && dty == kF32) ok = launch_split<kF32, kF32>(x, dtx, y, dty, L, G, g, s);
+            else if (dtx == kF32) ok = launch_split<kF32, -1>(x, dtx, y, dty, L, G, g, s);
+            else ok = launch_split<-1, -1>(x, dtx, y, dty, L, G, g, s);
+            if (!ok || !check_launch(name)) { st.finish(); return; }
         } else if (inner == 1) {
             bool done = false;
             if (outer <= 0x7FFFFFFF && L <= 0x7FFFFFFF) {

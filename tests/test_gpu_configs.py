@@ -249,6 +249,32 @@ def test_config5_softmax(hip, oracle_lib):
     assert_close(hip.softmax(x2, O.F32, O.F32, -1), oracle_lib.softmax(x2, O.F32, O.F32, -1), O.F32)
 
 
+# Few long rows run the one-launch split kernel (each row over G blocks that
+# exchange partial (max, sum) pairs); chunks over 4096 elements run the
+# two-launch form.  spin = 0 makes every block recompute every other block's
+# pair from X instead of waiting for it: the result must not change by a bit.
+SOFTMAX_SPLIT = [((64, 32000), "float32", O.F32, O.F32), ((8, 20000), "float32", O.F32, O.F32),
+                 ((3, 31999), "float32", O.F32, O.F32), ((5, 6000), "float64", O.F64, O.F64),
+                 ((4, 9000), "float16", O.F16, O.F32), ((2, 70001), "float32", O.F32, O.F32),
+                 ((2, 300000), "float32", O.F32, O.F32)]
+
+
+@pytest.mark.parametrize("shape,npdt,dtx,dty", SOFTMAX_SPLIT,
+                         ids=[f"{s[0]}x{s[1]}-{n}" for s, n, _, _ in SOFTMAX_SPLIT])
+def test_softmax_split_rows(hip, oracle_lib, shape, npdt, dtx, dty):
+    rng = np.random.default_rng(shape[1])
+    x = rng.normal(0, 3, shape).astype(npdt)
+    x.reshape(-1)[rng.choice(x.size, 7, replace=False)] = 40.0    # a few clear maxima per tensor
+    y = hip.softmax(x, dtx, dty, 1)
+    assert_close(y, oracle_lib.softmax(x, dtx, dty, 1), dty, what=f"softmax {shape}")
+    old = hip.lib.tensor_ops_hip_set_softmax_spin(0)
+    try:
+        y0 = hip.softmax(x, dtx, dty, 1)
+    finally:
+        hip.lib.tensor_ops_hip_set_softmax_spin(old)
+    assert np.array_equal(y0.view(np.uint8), y.view(np.uint8)), f"recomputed partials changed softmax {shape}"
+
+
 @pytest.mark.parametrize("ydt,zdt", [(O.U8, O.U8), (O.I8, O.I8), (O.E4M3, O.E4M3), (O.E5M2, O.E5M2),
                                      (O.I8, O.F32), (O.U8, O.F32), (O.E4M3, O.F32), (O.E5M2, O.F32)])
 def test_quantize_fast_path_boundaries(hip, oracle_lib, ydt, zdt):

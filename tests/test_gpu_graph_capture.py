@@ -1,5 +1,9 @@
 """Library calls captured into a HIP graph (as bench.py times the headline).
 
+A second test captures Softmax over few long rows, whose eager form is one
+launch whose blocks exchange per-call tagged partials: under capture it must
+take the two-launch form, so replays on changed inputs stay correct.
+
 The calls of one headline step (per-tensor u8 and per-axis i8 QuantizeLinear,
 their DequantizeLinear, the fused config-1 chain) are captured on the
 library's stream; the graph is replayed several times with the program's own
@@ -99,6 +103,57 @@ def test_graph_replays_match_eager(hip):
         o = O.oracle()
         want = o.qdq("quantize", xs, O.F32, s_u8.cpu().numpy(), O.F32, z_u8.cpu().numpy(), O.U8, O.U8)
         assert_bitexact(eager["q_u8"], want, O.U8, what="eager q_u8 vs oracle")
+    finally:
+        for p in keep:
+            L.free_tensor(p)
+        L.tensor_ops_hip_set_stream(None)
+
+
+def test_softmax_split_rows_under_capture(hip):
+    """Softmax [64, 32000] captured after an eager call on the same stream;
+    the input is rewritten before every replay and each replay must equal an
+    eager call on that input bit for bit (a replayed one-launch kernel would
+    find the previous replay's partials under its capture-time tag)."""
+    import torch
+    torch.cuda.init()
+    side = torch.cuda.Stream()
+    L = hip.lib
+    L.tensor_ops_hip_set_stream(ctypes.c_void_p(side.cuda_stream))
+    keep = []
+
+    def wrap(t, shape, dt):
+        arr = (ctypes.c_int * len(shape))(*shape)
+        p = L.tensor_wrap_device(ctypes.c_void_p(t.data_ptr()), arr, len(shape), dt)
+        assert p
+        keep.append(p)
+        return p
+
+    try:
+        with torch.cuda.stream(side):
+            rng = np.random.default_rng(21)
+            inputs = [rng.normal(0, 3, (64, 32000)).astype(np.float32) for _ in range(4)]
+            x = torch.from_numpy(inputs[0]).cuda()
+            y = torch.empty_like(x)
+            ye = torch.empty_like(x)
+            tx, ty, tye = wrap(x, [64, 32000], O.F32), wrap(y, [64, 32000], O.F32), wrap(ye, [64, 32000], O.F32)
+            hip.lib.tensor_ops_hip_clear_error()
+            L.softmax_forward(tx, ty, 1)
+            torch.cuda.synchronize()
+            assert not hip.last_error(), hip.last_error()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                L.softmax_forward(tx, ty, 1)
+            assert not hip.last_error(), hip.last_error()
+            for r in range(1, 4):
+                x.copy_(torch.from_numpy(inputs[r]))
+                y.fill_(0)
+                torch.cuda.synchronize()
+                g.replay()
+                torch.cuda.synchronize()
+                L.softmax_forward(tx, tye, 1)
+                torch.cuda.synchronize()
+                assert not hip.last_error(), hip.last_error()
+                assert_bitexact(y.cpu().numpy(), ye.cpu().numpy(), O.F32, what=f"softmax replay {r}")
     finally:
         for p in keep:
             L.free_tensor(p)
