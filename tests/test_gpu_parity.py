@@ -272,6 +272,10 @@ CONV_TILED = [
     # channel tile; asymmetric padding without bias
     ("stem_plan_m80", (2, 3, 20, 180), (80, 3, 7, 7), [3, 3, 3, 3], [2, 2], [1, 1], 1, True, "float32"),
     ("stem_plan_asym_nobias", (1, 3, 17, 224), (64, 3, 7, 7), [2, 3, 4, 1], [2, 2], [1, 1], 1, False, "float32"),
+    # direct 1x1 layers of the config-4 shape class (64 input channels, 256 and 512
+    # output channels)
+    ("direct_m256", (2, 64, 16, 16), (256, 64, 1, 1), [0, 0, 0, 0], [1, 1], [1, 1], 1, True, "float32"),
+    ("direct_m512_nobias", (3, 64, 14, 16), (512, 64, 1, 1), [0, 0, 0, 0], [1, 1], [1, 1], 1, False, "float32"),
 ]
 
 
@@ -305,6 +309,8 @@ CONV_FUSED = [
     ("tap_m128_relu_skip", (4, 64, 30, 30), (128, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, "full", "float32"),
     ("tap_small_img_relu_skip", (2, 64, 14, 14), (192, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, "full", "float32"),
     ("stem_plan_relu_skip", (2, 3, 20, 180), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2], 1, True, True, "full", "float32"),
+    ("direct_m256_relu_skip", (2, 64, 16, 16), (256, 64, 1, 1), [0, 0, 0, 0], [1, 1], 1, True, True, "full", "float32"),
+    ("direct_m512_skip_nobias", (1, 64, 8, 32), (512, 64, 1, 1), [0, 0, 0, 0], [1, 1], 1, False, False, "full", "float32"),
 ]
 
 
@@ -360,6 +366,7 @@ CONV_QDQ = [
     ("split_scalar_i8", (1, 256, 9, 9), (129, 256, 3, 3), [1, 1, 1, 1], [2, 2], "int8", 0, 0.05, 0, 0.05),
     ("gather_u8", (2, 12, 13, 11), (24, 12, 3, 3), [1, 1, 1, 1], [1, 1], "uint8", 9, 0.02, 9, 0.02),
     ("direct_1x1_u8", (2, 40, 12, 12), (96, 40, 1, 1), [0, 0, 0, 0], [1, 1], "uint8", 0, 0.04, 0, 0.04),
+    ("direct_m256_i8", (2, 64, 16, 16), (256, 64, 1, 1), [0, 0, 0, 0], [1, 1], "int8", 2, 0.04, 2, 0.04),
     ("tail_rows_m200_i8", (1, 30, 9, 9), (200, 30, 3, 3), [1, 1, 1, 1], [1, 1], "int8", 1, 0.03, 1, 0.03),
     ("stem_u8", (2, 3, 20, 180), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2], "uint8", 0, 8 / 255, 0, 8 / 255),
     ("e4m3_fallback", (2, 64, 12, 12), (64, 64, 3, 3), [1, 1, 1, 1], [1, 1], "float8_e4m3", 0, 0.01, 0, 0.01),
