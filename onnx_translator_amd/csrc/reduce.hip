@@ -624,47 +624,49 @@ __global__ __launch_bounds__(kGapPlanes) void k_gap(const void* __restrict__ X, 
     if (t < np) stx<DOUT>(Y, p0 + t, sum / hw, dty);
 }
 
-// f32 planes of at most 128 values: a wave's 64 planes are one contiguous
-// region, copied into LDS with fully coalesced loads, then lane l sums plane
-// l from LDS in index order (the same exact sequential sum).
-constexpr int kGapSmallHW = 128;
+// f32 planes of at most 128 values: a block's 64 planes are one contiguous
+// region, copied into LDS by its four waves with coalesced loads (up to 16 per
+// thread in flight, so a region of up to 64 x 64 values arrives in one round
+// trip), then lane l of the first wave sums plane l from LDS in index order
+// (the same exact sequential sum).
+constexpr int kGapSmallHW = 128, kGapSmallThreads = 256;
 
 template <int DOUT>
-__global__ __launch_bounds__(64) void k_gap_small_f32(const float* __restrict__ X, void* __restrict__ Y, int dty,
-                                                      int64_t planes, int hw) {
+__global__ __launch_bounds__(kGapSmallThreads) void k_gap_small_f32(const float* __restrict__ X, void* __restrict__ Y,
+                                                                    int dty, int64_t planes, int hw) {
     __shared__ float tile[64 * kGapSmallHW];
-    const int lane = threadIdx.x;
+    const int t = threadIdx.x;
     const int64_t p0 = (int64_t)blockIdx.x * 64;
     const int np = planes - p0 < 64 ? (int)(planes - p0) : 64;
     const int cnt = np * hw;
-    // 16 loads in flight per lane before the LDS stores (buffer loads: reads
-    // past the region return 0 without touching memory)
+    // buffer loads: reads past the region return 0 without touching memory
     const __amdgpu_buffer_rsrc_t r = buffer_rsrc(X + p0 * hw, (uint32_t)cnt * 4u);
-    for (int base = 0; base < cnt; base += 64 * 16) {
+    for (int base = 0; base < cnt; base += kGapSmallThreads * 16) {
         float v[16];
 #pragma unroll
         for (int j = 0; j < 16; j++)
-            v[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (uint32_t)(base + lane + 64 * j) * 4u, 0, 0));
+            v[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                 r, (uint32_t)(base + t + kGapSmallThreads * j) * 4u, 0, 0));
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            const int i = base + lane + 64 * j;
+            const int i = base + t + kGapSmallThreads * j;
             if (i < cnt) tile[i] = v[j];
         }
     }
     __syncthreads();
-    if (lane < np) {
-        const float* t = tile + lane * hw;
+    if (t < np) {
+        const float* tp = tile + t * hw;
         double sum = 0.0;
         int k = 0;
         for (; k + 4 <= hw; k += 4) {
-            const float a = t[k], b = t[k + 1], c = t[k + 2], d = t[k + 3];
+            const float a = tp[k], b = tp[k + 1], c = tp[k + 2], d = tp[k + 3];
             sum += (double)a;
             sum += (double)b;
             sum += (double)c;
             sum += (double)d;
         }
-        for (; k < hw; k++) sum += (double)t[k];
-        stx<DOUT>(Y, p0 + lane, sum / hw, dty);
+        for (; k < hw; k++) sum += (double)tp[k];
+        stx<DOUT>(Y, p0 + t, sum / hw, dty);
     }
 }
 
@@ -691,7 +693,7 @@ void global_average_pool_forward(const Tensor* input, Tensor* output) {
         const dim3 g((unsigned)((planes + kGapPlanes - 1) / kGapPlanes)), b(kGapPlanes);
         const int dtx = (int)input->dtype, dty = (int)output->dtype;
         hipStream_t s = stream();
-        const dim3 gs((unsigned)((planes + 63) / 64)), bs(64);
+        const dim3 gs((unsigned)((planes + 63) / 64)), bs(kGapSmallThreads);
         if (dtx == kF32 && hw <= kGapSmallHW && dty == kF32)
             hipLaunchKernelGGL((k_gap_small_f32<kF32>), gs, bs, 0, s, (const float*)x, y, dty, planes, hw);
         else if (dtx == kF32 && hw <= kGapSmallHW)

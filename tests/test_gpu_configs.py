@@ -392,7 +392,7 @@ def test_dynamic_quantize_linear_full_size(hip, oracle_lib, x2):
     assert_bitexact(y, ry, O.U8, what="dql codes")
 
 
-@pytest.mark.parametrize("shape", [(64, 512, 7, 7), (8, 64, 56, 56), (3, 5, 1, 1), (1, 300, 3, 3)])
+@pytest.mark.parametrize("shape", [(64, 512, 7, 7), (8, 64, 56, 56), (3, 5, 1, 1), (1, 300, 3, 3), (2, 70, 10, 11)])
 def test_global_average_pool_sizes(hip, oracle_lib, shape):
     rng = np.random.default_rng(sum(shape))
     x = rng.normal(0, 1, shape).astype(np.float32)
