@@ -216,7 +216,9 @@ POOLS = [("3x3s2p1", (2, 3, 30, 28), [3, 3], [1, 1, 1, 1], [2, 2], [1, 1]),
          ("2x2s2", (2, 4, 16, 12), [2, 2], [0, 0, 0, 0], [2, 2], [1, 1]),
          ("3x3s1p1_dil2", (1, 5, 20, 24), [3, 3], [1, 1, 1, 1], [1, 1], [2, 2]),
          ("7x7_asym", (1, 3, 36, 40), [7, 5], [3, 2, 1, 0], [2, 3], [1, 1]),
-         ("allpad_window", (1, 2, 8, 8), [2, 2], [3, 3, 3, 3], [4, 4], [1, 1])]
+         ("allpad_window", (1, 2, 8, 8), [2, 2], [3, 3, 3, 3], [4, 4], [1, 1]),
+         # the strip kernel's resident blocks walking 1500 planes (one or two each)
+         ("3x3s2p1_1500_planes", (3, 500, 14, 12), [3, 3], [1, 1, 1, 1], [2, 2], [1, 1])]
 
 
 @pytest.mark.parametrize("case", POOLS, ids=[c[0] for c in POOLS])
