@@ -240,7 +240,8 @@ template <int XQ> __device__ __forceinline__ float xq_value(uint32_t code, float
     return (float)(c - z) * s;
 }
 
-// SPLIT: blockIdx.z = slice * groups + group; slice s covers k in
+// SPLIT: gridDim.z = slices * groups, a block's z = slice * groups + group
+// (from its work index, below); slice s covers k in
 // [s * kchunk, (s + 1) * kchunk) (kchunk a multiple of BK) and stores its raw
 // fp32 sums, without bias, to Y + s * N * M * OH * OW (Y is then the f32
 // workspace); k_conv_splitk_reduce adds the slices in order with the bias.
@@ -282,20 +283,23 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
-    const int grp = SPLIT ? (int)blockIdx.z % groups : (int)blockIdx.z;
-    const int slice = SPLIT ? (int)blockIdx.z / groups : 0;
-    // Tile order: the dispatcher deals consecutive workgroups to the 8 XCDs in
-    // turn (each with its own L2), so the block index L becomes a tile index
-    // that gives XCD class L % 8 a contiguous run of tiles, and within it the
-    // channel tile varies fastest: the channel tiles of one pixel tile share
-    // their input through one L2 (config-5 block 4: its 4 channel tiles had
-    // fetched the input 4x past L2).  A bijection on [0, tiles) for any count.
-    int m0, p0;
+    // Tile order: the dispatcher deals consecutive workgroups (linear index L
+    // over x, y, z) to the 8 XCDs in turn, each with its own L2, so L becomes a
+    // work index w that gives XCD class L % 8 a contiguous run of the whole
+    // grid, ordered (z, pixel tile, channel tile) with the channel tile
+    // fastest: the channel tiles of one pixel tile share their input through
+    // one L2, and an XCD's run spans one or two k-slices of a split layer, so
+    // it fetches only those slices' weights (per-z runs had every XCD fetch
+    // every slice's weights).  A bijection on [0, blocks) for any count.
+    int grp, slice, m0, p0;
     {
-        const int ntm = (int)gridDim.y, tiles = (int)gridDim.x * ntm;
-        const int L = (int)blockIdx.x + (int)blockIdx.y * (int)gridDim.x;
-        const int cls = L & 7, q = tiles >> 3, rem = tiles & 7;
-        const int tid = cls * q + min(cls, rem) + (L >> 3);
+        const int ntm = (int)gridDim.y, tiles = (int)gridDim.x * ntm, total = tiles * (int)gridDim.z;
+        const int L = (int)blockIdx.x + ((int)blockIdx.y + (int)blockIdx.z * ntm) * (int)gridDim.x;
+        const int cls = L & 7, q = total >> 3, rem = total & 7;
+        const int w = cls * q + min(cls, rem) + (L >> 3);
+        const int z = w / tiles, tid = w - z * tiles;
+        grp = SPLIT ? z % groups : z;
+        slice = SPLIT ? z / groups : 0;
         const int tp = tid / ntm;
         m0 = (tid - tp * ntm) * BM;
         p0 = tp * BP;
