@@ -202,9 +202,12 @@ def test_quantize_dequantize_fused(hip, oracle_lib, case):
 # K tail masked in registers): 128x128 tiles for small grids, 256x256 tiles when
 # the grid has >= 192 of them.  Ragged M / N and K % 64 != 0 exercise the edges;
 # the bias modes cover the inline epilogue (none / scalar / per row / per
-# column) and the out-of-line one (2-D bias).
+# column) and the out-of-line one (2-D bias).  Grids of >= 192 256x256 tiles
+# with K % 64 == 0 and an inline epilogue run the direct-to-LDS kernel (the
+# last four cases: ragged M / N load as zeros past the operands' ends).
 F16_NT = [(300, 200, 136, "col"), (130, 1000, 8, "none"), (257, 129, 64, "scalar"), (96, 72, 520, "row"),
-          (3600, 3500, 72, "col"), (3584, 3584, 200, "2d")]
+          (3600, 3500, 72, "col"), (3584, 3584, 200, "2d"),
+          (3600, 3500, 128, "col"), (3584, 3712, 64, "row"), (3300, 3850, 192, "scalar"), (4000, 3000, 256, "none")]
 
 
 @pytest.mark.parametrize("M,N,K,bias", F16_NT, ids=[f"{m}x{n}x{k}-{b}" for m, n, k, b in F16_NT])
