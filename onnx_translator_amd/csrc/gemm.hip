@@ -982,7 +982,7 @@ bool launch_f16_nt(const GemmArgs& g, hipStream_t s) {
     const int64_t big_tiles = (int64_t)((g.M + 255) / 256) * ((g.N + 255) / 256);
     const bool fast_bias = g.c.mode == 0 || (g.c.dt == kF32 && g.c.mode <= 3);
     if (big_tiles >= 192 && g.K > 0 && g.K % 64 == 0 && fast_bias && (g.dty == kF16 || g.dty == kF32)) {
-        // 4096^3 on MI355X: 124 -> 118 us against the 16-wave kernel
+        // 4096^3 on MI355X: 132.9 -> 124.0 us against the 16-wave kernel on one box
         const dim3 grid((unsigned)big_tiles), block(512);
         if (g.dty == kF16) hipLaunchKernelGGL((k_gemm_f16_dl<kF16>), grid, block, 0, s, g);
         else hipLaunchKernelGGL((k_gemm_f16_dl<kF32>), grid, block, 0, s, g);
