@@ -254,7 +254,14 @@ template <int XQ> __device__ __forceinline__ float xq_value(uint32_t code, float
 // with a wave-uniform scalar offset (c * H * W).  Its LDS tiles keep k
 // contiguous ([row][k]), and lane half h feeds MFMA step s with k = h*BK/2 + s,
 // so each operand is read as 16-byte vectors covering four steps.  DEPTH 2
-// (MODE 2 only) keeps a second loaded tile in registers.
+// (MODE 2 only) keeps a second loaded tile in registers.  DEPTH 3 (MODE 2
+// only) is the store-first pipeline: at the top of k-tile k the registers of
+// tile k + 1 (loaded one whole k-tile earlier) go to the idle LDS buffer and the
+// loads of tile k + 2 are issued, interleaved with the MFMAs; each 4-step
+// sub-step's fragments are read one sub-step ahead; the barrier sits between
+// the two halves of the last sub-step, and the next tile's first fragments are
+// read right after it, under the second half's MFMAs.  Same k order and MFMA
+// sequence as DEPTH 1 / 2, so the same bits.
 template <int BM, int BP, int BK, int WGM, int WGN, int MODE, int YDT, bool SPLIT = false, int XQ = 0, int DEPTH = 1>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __restrict__ X, const float* __restrict__ Wt,
                                                                const float* __restrict__ Bv, void* __restrict__ Y,
@@ -275,7 +282,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
     static_assert(EA >= 1 && BK % EA == 0 && EB >= 1, "tile / thread mismatch");
     constexpr bool TAP = MODE == 2;
     static_assert(!TAP || BK % 8 == 0, "MODE 2 reads four k per lane half and vector");
-    static_assert(DEPTH == 1 || (TAP && DEPTH == 2), "two register sets are a MODE 2 option");
+    static_assert(DEPTH == 1 || (TAP && (DEPTH == 2 || DEPTH == 3)), "DEPTH 2 / 3 are MODE 2 options");
     // MODE 0 / 1: [k][row]; MODE 2: [row][k] (rows of BK + 4 floats: 16-byte
     // reads and writes of consecutive rows fall in distinct bank groups)
     __shared__ float As[2][TAP ? BM : BK][TAP ? BK + 4 : BM + 4];
@@ -514,8 +521,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
             else
                 db[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, voff, soff, 0));
         }
-        // keep the loads ahead of the MFMA steps that follow
-        __builtin_amdgcn_sched_barrier(0);
+        // keep the loads ahead of the MFMA steps that follow (DEPTH 3
+        // interleaves them with the MFMAs instead)
+        if constexpr (DEPTH != 3) __builtin_amdgcn_sched_barrier(0);
     };
     auto tap_store = [&](int buf, const float (&sa)[EA], const float (&sb)[EB]) {
 #pragma unroll
@@ -551,7 +559,66 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
     };
 
     int kt = 0;
-    if constexpr (TAP) {
+    if constexpr (TAP && DEPTH == 3) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        constexpr int NS = BK / 8;                  // 4-step sub-steps per k-tile
+        constexpr int NM = 4 * TM * TP;             // MFMAs per sub-step
+        constexpr int NLD = EA + KPT, NWR = EA + KPT / 4, NRD = TM + TP;
+        constexpr int PRE = 2;                      // steps of the last sub-step ahead of the barrier
+        f32x4 fa[2][TM], fb[2][TP];
+        auto fread = [&](int buf, int j, int f) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                fa[f][i] = *reinterpret_cast<const f32x4*>(&As[buf][wm * WTM + i * 32 + lr][lk * (BK / 2) + 4 * j]);
+#pragma unroll
+            for (int jj = 0; jj < TP; jj++)
+                fb[f][jj] = *reinterpret_cast<const f32x4*>(&Bs[buf][wn * WTP + jj * 32 + lr][lk * (BK / 2) + 4 * j]);
+        };
+        auto mf = [&](int f, int qlo, int qhi) {
+#pragma unroll
+            for (int q = qlo; q < qhi; q++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int jj = 0; jj < TP; jj++)
+                        acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[f][i][q], fb[f][jj][q], acc[i][jj], 0, 0, 0);
+        };
+        tap_load(kbeg, ra, rb);
+        tap_store(0, ra, rb);
+        tap_load(kbeg + BK, ra, rb);                // past the end: the last tile again (unused)
+        __syncthreads();
+        fread(0, 0, 0);
+        for (; kt < nk; kt++) {
+            const int cur = kt & 1;
+#pragma unroll
+            for (int s = 0; s < NS - 1; s++) {
+                fread(cur, s + 1, (s + 1) & 1);
+                if (s == 0) {
+                    tap_store(cur ^ 1, ra, rb);     // tile k + 1 (past the end: an unused copy)
+                    tap_load(kbeg + (kt + 2) * BK, ra, rb);
+                }
+                mf(s & 1, 0, 4);
+                // sched_group_barrier masks: MFMA 0x008, DS read 0x100, DS write
+                // 0x200, VMEM read 0x020
+#pragma unroll
+                for (int q = 0; q < NM; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (q < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    if (s == 0) {
+                        __builtin_amdgcn_sched_group_barrier(0x200, (NWR + NM - 1) / NM, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x020, (NLD + NM - 1) / NM, 0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            mf((NS - 1) & 1, 0, PRE);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+            fread(cur ^ 1, 0, 0);
+            mf((NS - 1) & 1, PRE, 4);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else if constexpr (TAP) {
         // Two tiles per trip with fixed LDS buffers: tile kt (even) sits in
         // buffer 0 at the top of each trip.  DEPTH 2 keeps tile kt + 1 in a
         // second register set, loaded one trip earlier.
@@ -1139,9 +1206,11 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
     else if (plan == kT128x128)
         launch_conv_tiled_cfg<128, 128, 16, 4, 4, 2, XQ, 2>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else if (plan == kT128x256)
-        launch_conv_tiled_cfg<128, 256, 16, 2, 8, 2, XQ, 2>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
+        // store-first pipeline (DEPTH 3): config-5 block 2 89.3 -> 86.8 us (best of 3, same bits)
+        launch_conv_tiled_cfg<128, 256, 16, 2, 8, 2, XQ, 3>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else if (plan == kT64x256)
-        launch_conv_tiled_cfg<64, 256, 16, 2, 4, 2, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
+        // store-first pipeline (DEPTH 3): the config-4 3x3 layer 85.7 -> 84.3 us (best of 3, same bits)
+        launch_conv_tiled_cfg<64, 256, 16, 2, 4, 2, XQ, 3>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else if (g.Kg <= 256)
         launch_conv_tiled_cfg<64, 256, 8, 2, 4, 0, XQ>(xf, wf, b, dtb, y, dty, g, cg.group, ux, uw, uy, epi, xq, s);
     else if (balance(((P + 127) / 128) * ((g.Mg + 63) / 64) * cg.group) > 1.05 * balance(blocks))
