@@ -208,11 +208,15 @@ def test_quantize_dequantize_fused(hip, oracle_lib, case):
 F16_NT = [(300, 200, 136, "col"), (130, 1000, 8, "none"), (257, 129, 64, "scalar"), (96, 72, 520, "row"),
           (3600, 3500, 72, "col"), (3584, 3584, 200, "2d"),
           (3600, 3500, 128, "col"), (3584, 3712, 64, "row"), (3300, 3850, 192, "scalar"), (4000, 3000, 256, "none")]
+# alpha = 1 takes the direct-to-LDS kernel's lean epilogue on whole blocks (the
+# ragged edge blocks keep the general one): no bias, scalar and per-column bias.
+F16_NT_A1 = [(3584, 3584, 128, "none"), (3600, 3500, 64, "scalar"), (3584, 3712, 192, "col")]
 
 
-@pytest.mark.parametrize("M,N,K,bias", F16_NT, ids=[f"{m}x{n}x{k}-{b}" for m, n, k, b in F16_NT])
+@pytest.mark.parametrize("M,N,K,bias,alpha", [c + (0.75,) for c in F16_NT] + [c + (1.0,) for c in F16_NT_A1],
+                         ids=[f"{m}x{n}x{k}-{b}" for m, n, k, b in F16_NT] + [f"{m}x{n}x{k}-{b}-a1" for m, n, k, b in F16_NT_A1])
 @pytest.mark.parametrize("ydt", ["float16", "float32"])
-def test_gemm_f16_tiled_kernel(hip, M, N, K, bias, ydt):
+def test_gemm_f16_tiled_kernel(hip, M, N, K, bias, alpha, ydt):
     from tests.helpers import assert_close
     rng = np.random.default_rng(M + 3 * N + 7 * K)
     a = rng.normal(0, 1, (M, K)).astype(np.float16)
@@ -221,7 +225,7 @@ def test_gemm_f16_tiled_kernel(hip, M, N, K, bias, ydt):
          "col": rng.normal(0, 1, (N,)), "2d": rng.normal(0, 1, (M, N))}[bias]
     if c is not None:
         c = c.astype(np.float32)
-    alpha, beta = 0.75, 1.5
+    beta = 1.5
     y = hip.gemm(a, O.F16, b, O.F16, c, O.F32, ydt, alpha, beta, 0, 1)
     rows = np.arange(M) if M * N <= 1 << 20 else np.unique(np.r_[rng.choice(M, 40, replace=False), 0, M - 1])
     ref = alpha * (a[rows].astype(np.float64) @ b.astype(np.float64).T)
