@@ -72,6 +72,30 @@ def test_config1_int32_promotion_unbroadcast(hip, oracle_lib, wide, dt):
     assert_bitexact(got, oracle_lib.binary("add", I, O.I32, B, O.F32, dt), dt, what="int32 + f32[64,1,1]")
 
 
+# int32 x f32 -> f64 / f32 runs four elements per thread when the last
+# dimension is a multiple of 4 (k_bin_i32f32_v4), one otherwise (k_bin_typed):
+# the int32 operand broadcast, the f32 operand broadcast along the last
+# dimension, and a ragged last dimension, over the four operators.
+I32_LAYOUTS = {"i32_bcast_channel": ((64, 1, 1), (4, 64, 56, 56)), "f32_last_dim": ((4, 64, 56, 56), (56,)),
+               "ragged_last_dim": ((4, 64, 56, 55), (4, 64, 56, 55))}
+
+
+@pytest.mark.parametrize("layout", list(I32_LAYOUTS))
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+@pytest.mark.parametrize("dt", [O.F64, O.F32], ids=["to_f64", "to_f32"])
+def test_int32_f32_promotion_layouts(hip, oracle_lib, layout, op, dt):
+    rng = np.random.default_rng(5)
+    sa, sb = I32_LAYOUTS[layout]
+    I = rng.integers(-(2 ** 31), 2 ** 31 - 1, sa, dtype=np.int64).astype(np.int32)
+    F = rng.uniform(-4, 4, sb).astype(np.float32)
+    if op == "div":
+        F = np.where(np.abs(F) < 0.1, np.float32(0.5), F).astype(np.float32)
+    got = hip.binary_raw(op, I, O.I32, F, O.F32, dt)
+    shape = np.broadcast_shapes(I.shape, F.shape)
+    want = oracle_lib.binary(op, np.broadcast_to(I, shape).copy(), O.I32, np.broadcast_to(F, shape).copy(), O.F32, dt)
+    assert_bitexact(got, want, dt, what=f"int32 {sa} {op} f32 {sb} -> {dt}")
+
+
 def config2_input():
     rng = np.random.default_rng(1)
     x = rng.normal(0, 1.5, (32, 512, 1024))
