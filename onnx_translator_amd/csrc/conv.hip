@@ -1159,9 +1159,10 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
                 1.05 * balance(((P + 255) / 256) * ((g.Mg + 63) / 64) * cg.group))
             plan = kT64x128;
     }
-    // 64-row tiles instead of a k split when they alone cover >= 3/4 of the
-    // CUs: no slices to write and reduce (config-5 block 3: 98 128x256 tiles
-    // -> 196 64x256 tiles, 97.4 -> 92.8 us with the slice reduction counted)
+    // 64-row tiles when 128-row ones leave CUs idle and the 64-row grid alone
+    // covers >= 3/4 of them: no k split, so no slices to write and reduce
+    // (config-5 block 3: 98 128x256 tiles -> 196 64x256 tiles, 97.4 -> 92.8 us
+    // with the slice reduction counted; block 2, 196 -> 392 tiles, unchanged)
     bool no_split = false;
     if (plan == kT128x256 && ((P + 255) / 256) * ((g.Mg + 127) / 128) * cg.group < num_cus() &&
         4 * ((P + 255) / 256) * ((g.Mg + 63) / 64) * cg.group >= 3 * (int64_t)num_cus()) {
