@@ -10,7 +10,8 @@
 //     blocks so the fp64 exp / divide work covers the chip: pass 1 writes each
 //     block's (max m_b, sum_b exp(v - m_b)); pass 2 folds them into the row's
 //     max M and sum S = sum_b s_b * exp(m_b - M) (fixed order) and writes
-//     exp(v - M) / S;
+//     exp(v - m_b) * (exp(m_b - M) / S); the one-launch form keeps exp(v - m_b)
+//     in registers from its partial pass, so each value is exponentiated once;
 //   * inner > 1: one thread per column, coalesced along the inner dimension.
 // Max, sums and the final scaling are in double (the sums are trees instead of the
 // reference's sequential loop); exp is sm_exp below (fp64 range reduction,
@@ -206,9 +207,10 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_part(const void* __restric
     }
 }
 
-// Split rows: pass 2.  Output exp(v - M) * (1 / S): a tolerance-class
-// operator, so the reciprocal (one division per thread, within one double ulp
-// of a division per element) replaces the fp64 divide per element.
+// Split rows: pass 2.  Output exp(v - M) / S computed per chunk b as
+// exp(v - m_b) * (exp(m_b - M) / S): a tolerance-class operator (~2e-7
+// relative to the reference's double result), with one division per thread
+// instead of an fp64 divide per element.
 template <int DIN, int DOUT, int IPT>
 __global__ __launch_bounds__(kSplitThreads) void k_sm_out(const void* __restrict__ X, int dtx, void* __restrict__ Y,
                                                           int dty, int64_t L, int G, const double* __restrict__ part) {
@@ -226,16 +228,20 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_out(const void* __restrict
     const double m_l = lane < G ? pm[lane] : -DBL_MAX;
     const double M = wave_max(m_l);
     const double S = wave_sum(lane < G ? ps[lane] * sm_exp(m_l - M) : 0.0);
-    const double rs = 1.0 / S;
+    // exp(v - M) / S as exp(v - m_b) * (exp(m_b - M) / S), m_b this chunk's
+    // max: the one-launch kernel keeps exp(v - m_b) from its partial pass and
+    // applies the same per-chunk factor, so the two forms return the same bits
+    const double mb = pm[blockIdx.x];
+    const double scale = sm_exp(mb - M) / S;
     if constexpr (IPT > 0) {
 #pragma unroll
         for (int t = 0; t < IPT; t++) {
             const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
-            if (j < j1) stx<DOUT>(Y, base + j, sm_exp(v[t] - M) * rs, dty);
+            if (j < j1) stx<DOUT>(Y, base + j, sm_exp(v[t] - mb) * scale, dty);
         }
     } else {
         for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads)
-            stx<DOUT>(Y, base + j, sm_exp(ldx<DIN>(X, base + j, dtx) - M) * rs, dty);
+            stx<DOUT>(Y, base + j, sm_exp(ldx<DIN>(X, base + j, dtx) - mb) * scale, dty);
     }
 }
 
@@ -286,7 +292,8 @@ __device__ __forceinline__ void sm_chunk_partial(double (&v)[IPT], const void* _
 #pragma unroll
     for (int t = 0; t < IPT; t++) {
         const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
-        if (j < j1) sum += sm_exp(v[t] - mx);
+        v[t] = j < j1 ? sm_exp(v[t] - mx) : 0.0;     // kept for the output: exp(v - m_b)
+        sum += v[t];
     }
     sum = block_reduce<false, kSplitWaves>(sum, lds);
 }
@@ -367,11 +374,12 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_one(const void* __restrict
         if (lane == 0) { sM = M; sS = S; }
     }
     __syncthreads();
-    const double M = sM, r = 1.0 / sS;
+    // v holds exp(v - m_b) from the partial pass (k_sm_out's per-chunk form)
+    const double scale = sm_exp(mx - sM) / sS;
 #pragma unroll
     for (int t = 0; t < IPT; t++) {
         const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
-        if (j < j1) stx<DOUT>(Y, base + j, sm_exp(v[t] - M) * r, dty);
+        if (j < j1) stx<DOUT>(Y, base + j, v[t] * scale, dty);
     }
 }
 
