@@ -451,8 +451,10 @@ __device__ __forceinline__ void epilogue_col_f(const GemmArgs& g, int mb, int n,
         if constexpr (BIAS == 1) v += cn;
         if constexpr (BIAS == 3) v += g.beta * (double)c[m];
         const int64_t i = (int64_t)m * g.N + n;
-        if constexpr (YDT == kF16) ((gu16*)g.Y)[i] = enc_f16((float)v);
-        else ((gfloat*)g.Y)[i] = (float)v;
+        // nontemporal: Y is written once and not read back here (4096^3 f16:
+        // 118.0 -> 116.5 us, same bits)
+        if constexpr (YDT == kF16) __builtin_nontemporal_store(enc_f16((float)v), &((gu16*)g.Y)[i]);
+        else __builtin_nontemporal_store((float)v, &((gfloat*)g.Y)[i]);
     }
 }
 
