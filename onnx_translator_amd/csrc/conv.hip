@@ -759,7 +759,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
                             if (epi.skip)
                                 v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(zr, vo, so, 0));
                             if (epi.fq.kind) v = fq_apply(v, fqp);
-                            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, vo, so, 0);
+                            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, vo, so,
+                                                                  MODE == 1 ? 2 /* nt */ : 0);
                         }
                 }
             }
