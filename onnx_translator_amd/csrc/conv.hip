@@ -759,6 +759,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
                             if (epi.skip)
                                 v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(zr, vo, so, 0));
                             if (epi.fq.kind) v = fq_apply(v, fqp);
+                            // MODE 1: nontemporal (config-4 1x1 46.5 -> 43.5 us).  The MODE 2
+                            // and stem epilogues keep cached stores: with nontemporal ones the
+                            // config-5 graph, whose next layer re-reads each output, ran 1.6%
+                            // slower (0.740 -> 0.752 ms) for 1-2% on the standalone layers.
                             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, vo, so,
                                                                   MODE == 1 ? 2 /* nt */ : 0);
                         }
