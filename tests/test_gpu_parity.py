@@ -555,6 +555,38 @@ def test_dequantize_conv_fused(hip, oracle_lib, case, mode):
     assert_close(got, ref, O.F32, what=f"dq conv {tag}")
 
 
+# Grids of >= 256 tiles take the store-first MODE 2 pipeline without a k
+# split: 64x256 tiles for 64 output channels, 128x256 for >= 128; f32 input and
+# uint8 / int8 codes dequantised in the gather.
+D3_PLANS = [("f32_m256_128x256", (8, 16, 64, 64), (256, 16, 3, 3), None),
+            ("u8_m64_64x256", (16, 16, 64, 64), (64, 16, 3, 3), "uint8"),
+            ("i8_m256_128x256", (8, 16, 64, 64), (256, 16, 3, 3), "int8")]
+
+
+@pytest.mark.parametrize("case", D3_PLANS, ids=[c[0] for c in D3_PLANS])
+def test_conv_store_first_plans(hip, oracle_lib, case):
+    from tests.helpers import assert_close
+    tag, xs, ws, xdt = case
+    rng = np.random.default_rng(len(tag) + xs[0])
+    w = rng.normal(0, np.sqrt(2 / (ws[1] * 9)), ws).astype(np.float32)
+    b = rng.normal(0, 1, (ws[0],)).astype(np.float32)
+    pads, strides = [1, 1, 1, 1], [1, 1]
+    if xdt is None:
+        x = rng.normal(0, 1, xs).astype(np.float32)
+        got = hip.conv(x, O.F32, w, O.F32, b, O.F32, "float32", pads, strides, [1, 1], 1)
+    else:
+        lo, hi = (0, 256) if xdt == "uint8" else (-128, 128)
+        xq = rng.integers(lo, hi, xs).astype(np.uint8 if xdt == "uint8" else np.int8)
+        sc, z = np.array([0.029], np.float32), np.array([3 if xdt == "uint8" else -2], xq.dtype)
+        x = oracle_lib.qdq("dequantize", xq, xdt, sc, O.F32, z, xdt, O.F32)
+        got = hip.dq_conv_fused(xq, xdt, sc, z, w, b, None, False, pads, strides, [1, 1], 1)
+        seq = hip.conv_fused(hip.qdq("dequantize", xq, xdt, sc, O.F32, z, xdt, O.F32), w, b, None, False, O.F32,
+                             pads, strides, [1, 1], 1)
+        assert np.array_equal(got.view(np.uint32), seq.view(np.uint32)), f"{tag}: fused differs from the sequence"
+    ref = oracle_lib.conv(x, O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], 1)
+    assert_close(got, ref, O.F32, what=f"conv {tag}")
+
+
 def test_device_path_matches_host_path(hip):
     """Config-1 chain with device-resident tensors (no host round trips between ops)."""
     from onnx_translator_amd.nn import Tensor
