@@ -236,7 +236,11 @@ def test_config4_maxpool_full_size(hip, oracle_lib):
     assert_bitexact(y, oracle_lib.maxpool(x, O.F32, O.F32, [3, 3], [1, 1, 1, 1], [2, 2]), O.F32, what="maxpool")
 
 
+# 3x3 / stride 2 / pad 1 runs the strip kernel (odd input and output heights,
+# W % 4 == 0 and == 2 included).
 POOLS = [("3x3s2p1", (2, 3, 30, 28), [3, 3], [1, 1, 1, 1], [2, 2], [1, 1]),
+         ("3x3s2p1_odd_h", (2, 3, 29, 28), [3, 3], [1, 1, 1, 1], [2, 2], [1, 1]),
+         ("3x3s2p1_w26_strip", (2, 3, 30, 26), [3, 3], [1, 1, 1, 1], [2, 2], [1, 1]),
          ("2x2s2", (2, 4, 16, 12), [2, 2], [0, 0, 0, 0], [2, 2], [1, 1]),
          ("3x3s1p1_dil2", (1, 5, 20, 24), [3, 3], [1, 1, 1, 1], [1, 1], [2, 2]),
          ("7x7_asym", (1, 3, 36, 40), [7, 5], [3, 2, 1, 0], [2, 3], [1, 1]),
