@@ -261,17 +261,19 @@ def run_headline(lib, torch, steps, warmup, use_graph=False, nstreams=1):
             "dominant": dom, "bytes_per_launch": bytes_per_launch, "n": n}
 
 
-def bench_loop(torch, fn, iters, warm=3, warm_ms=50.0, graph=False):
+def bench_loop(torch, fn, iters, warm=3, warm_ms=100.0, graph=False):
     """Mean time of `iters` back-to-back calls.  The warm-up runs at least `warm`
-    calls and `warm_ms` of wall time, so the GPU clocks have ramped up (a cold
+    calls and `warm_ms` of wall time, in batches of up to 8 calls with no host
+    wait inside a batch, so the GPU stays busy while its clocks ramp up (a cold
     4096^3 Gemm runs ~20% slower for its first few milliseconds).  graph: the
     `iters` calls are captured into a HIP graph and timed as one replay (for
     calls that launch kernels only: no host staging, no workspace allocation)."""
     t0, i = time.perf_counter(), 0
     while i < warm or (time.perf_counter() - t0) * 1e3 < warm_ms:
-        fn(i)
+        for _ in range(min(8, warm - i) if i < warm else 8):
+            fn(i)
+            i += 1
         torch.cuda.synchronize()
-        i += 1
     warm = i
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if graph:
@@ -436,7 +438,7 @@ def run_suite(lib, torch, only=None, cpu=None):
         p = ConvP(ctypes.cast(keep[0], ctypes.POINTER(ctypes.c_int)), ctypes.cast(keep[1], ctypes.POINTER(ctypes.c_int)),
                   ctypes.cast(keep[2], ctypes.POINTER(ctypes.c_int)), 1)
         fl = 2 * xs[0] * ws[0] * OH * OW * ws[1] * ws[2] * ws[3]
-        ms = bench_loop(torch, lambda i: L.conv2d_forward(tx, tw, tbias, ty, ctypes.byref(p)), 5, 1)
+        ms = bench_loop(torch, lambda i: L.conv2d_forward(tx, tw, tbias, ty, ctypes.byref(p)), 20, 1)
         emit(op_line(f"conv_{tag}", f"config4 x{list(xs)} w{list(ws)}", fl, ms, "mfma", MFMA_F32),
              CpuLeg.conv(x, w, bias, pads, strides))
         for t in (tx, tw, tbias, ty):
