@@ -37,34 +37,66 @@ namespace {
 
 // exp(x) for x <= 0 (x = v - max), NaN propagated.  Range reduction in fp64
 // (t = x * log2 e, n = rint(t), f = t - n exactly, |f| <= 1/2), the core 2^f
-// on the fp32 exp2 unit, scaled back with ldexp in fp64: ~1e-7 relative to
-// the reference's libm exp in double, at a fraction of the cost of a full
-// fp64 exp (which made this operator ALU-bound).  Below 2^-1080 the double
-// result underflows to 0, as exp() does.
+// on the fp32 exp2 unit (v_exp_f32: no range handling is needed for |f| <= 1/2),
+// scaled back with ldexp in fp64: ~1e-7 relative to the reference's libm exp
+// in double, at a fraction of the cost of a full fp64 exp (which made this
+// operator ALU-bound).  Branch-free: t below -1100 (-inf included) is clamped
+// there, where ldexp underflows to +0 as exp() does (anything below 2^-1075
+// rounds to 0); a NaN fails the compare, passes through rint, the subtraction
+// and the exp unchanged and comes out NaN.
 __device__ __forceinline__ double sm_exp(double x) {
-    const double t = x * 1.4426950408889634;
-    if (!(t > -1080.0)) return t != t ? t : 0.0;
+    double t = x * 1.4426950408889634;
+    t = t < -1100.0 ? -1100.0 : t;
     const double n = __builtin_rint(t);
-    const float r = exp2f((float)(t - n));
+    const float r = __builtin_amdgcn_exp2f((float)(t - n));
     return __builtin_ldexp((double)r, (int)n);
 }
 
 constexpr int kRowThreads = 1024;
 constexpr int kWaves = kRowThreads / 64;
 
-__device__ __forceinline__ double wave_max(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const double t = __shfl_xor(v, o, 64);
-        v = t > v ? t : v;
-    }
-    return v;
+// A 64-bit value of another lane, moved as two 32-bit DPP moves (CTRL: a DPP
+// pattern whose source lanes all exist, e.g. a quad permutation or a mirror).
+template <int CTRL> __device__ __forceinline__ double dpp_d(double v) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)u, CTRL, 0xF, 0xF, false);
+    const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
 }
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// The gfx950 permlane swaps, on a value held in two registers: a receives
+// the value of the even partner (row 2k of a row pair for 16, the low half of
+// the wave for 32) and b that of the odd partner, in every lane of the pair.
+template <int W> __device__ __forceinline__ void swap_d(double v, double& a, double& b) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const unsigned lo = (unsigned)u, hi = (unsigned)(u >> 32);
+    const auto l = W == 16 ? __builtin_amdgcn_permlane16_swap(lo, lo, false, false)
+                           : __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto h = W == 16 ? __builtin_amdgcn_permlane16_swap(hi, hi, false, false)
+                           : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    a = __builtin_bit_cast(double, ((unsigned long long)h[0] << 32) | l[0]);
+    b = __builtin_bit_cast(double, ((unsigned long long)h[1] << 32) | l[1]);
 }
+
+// Max (strict >) or sum over the wave's 64 lanes, the same result in every lane
+// (all 64 lanes must be active).  Lanes pair up as quad neighbours, quad
+// halves, 8-lane halves (row_half_mirror) and 16-lane halves (row_mirror) with
+// DPP moves, then rows 0 / 1 and 2 / 3 and the two wave halves with permlane
+// swaps: no LDS traffic.  The sum's association order is fixed, so every call
+// on the same values returns the same bits.
+template <bool MAX> __device__ __forceinline__ double wave_reduce(double v) {
+    const auto op = [](double x, double y) { return MAX ? (y > x ? y : x) : x + y; };
+    v = op(v, dpp_d<0xB1>(v));     // quad_perm [1, 0, 3, 2]
+    v = op(v, dpp_d<0x4E>(v));     // quad_perm [2, 3, 0, 1]
+    v = op(v, dpp_d<0x141>(v));    // row_half_mirror
+    v = op(v, dpp_d<0x140>(v));    // row_mirror
+    double a, b;
+    swap_d<16>(v, a, b);
+    v = op(a, b);
+    swap_d<32>(v, a, b);
+    return op(a, b);
+}
+__device__ __forceinline__ double wave_max(double v) { return wave_reduce<true>(v); }
+__device__ __forceinline__ double wave_sum(double v) { return wave_reduce<false>(v); }
 
 // Block-wide reduction across the NW waves of a block (NW * 64 threads).
 template <bool MAX, int NW> __device__ __forceinline__ double block_reduce(double v, double* lds) {
@@ -169,38 +201,100 @@ __device__ __forceinline__ void load_chunk(double (&v)[IPT], const void* __restr
     }
 }
 
+// Writes o[t] to element j0 + threadIdx.x + t * 256 of the row for the lanes
+// inside the chunk of n elements.  f32 output goes through a buffer resource
+// over the chunk: the stores are unconditional and the hardware drops the
+// lanes past its end.
+template <int DOUT, int IPT>
+__device__ __forceinline__ void store_chunk(void* __restrict__ Y, int dty, int64_t base, int64_t j0, int n,
+                                            const double (&o)[IPT]) {
+    const int tid = (int)threadIdx.x;
+    if constexpr (DOUT == kF32) {
+        const __amdgpu_buffer_rsrc_t yr = buffer_rsrc((float*)Y + base + j0, (uint32_t)n * 4u);
+#pragma unroll
+        for (int t = 0; t < IPT; t++)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, (float)o[t]), yr,
+                                                  (uint32_t)((tid + t * kSplitThreads) * 4), 0, 0);
+    } else {
+#pragma unroll
+        for (int t = 0; t < IPT; t++)
+            if (tid + t * kSplitThreads < n) stx<DOUT>(Y, base + j0 + tid + t * kSplitThreads, o[t], dty);
+    }
+}
+
+// (m, s) of chunk c of a row, the whole block participating: m is the chunk's
+// max, s = sum exp(v - m), and v receives exp(v - m) per element, kept for the
+// output.  Lanes past the chunk's end hold -inf, which never wins the max and
+// whose exp is +0 whatever m is (-inf - m is -inf), so every lane runs the
+// same straight-line code.  Lane indices are 32-bit (a chunk holds at most
+// IPT * 256 elements).  f32 input: the max is taken on the floats themselves,
+// the same comparisons on the same (exactly converted) values, so the same
+// max; the f32 -inf start stands for the -DBL_MAX start (neither -inf nor NaN
+// ever beats either).
+template <int DIN, int IPT>
+__device__ __forceinline__ void sm_chunk_partial(double (&v)[IPT], const void* __restrict__ X, int dtx, int64_t base,
+                                                 int64_t L, int64_t chunk, int c, double* lds, double& mx, double& sum) {
+    const int64_t j0 = c * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
+    const int n = j1 > j0 ? (int)(j1 - j0) : 0;
+    const int tid = (int)threadIdx.x;
+    if constexpr (DIN == kF32) {
+        const __amdgpu_buffer_rsrc_t xr = buffer_rsrc((const float*)X + base + j0, (uint32_t)n * 4u);
+        float f[IPT];
+#pragma unroll
+        for (int t = 0; t < IPT; t++) {
+            const float x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                          xr, (uint32_t)((tid + t * kSplitThreads) * 4), 0, 0));
+            f[t] = tid + t * kSplitThreads < n ? x : -__builtin_inff();
+        }
+        float mf = -__builtin_inff();
+#pragma unroll
+        for (int t = 0; t < IPT; t++) mf = f[t] > mf ? f[t] : mf;
+        mx = block_reduce<true, kSplitWaves>(mf == -__builtin_inff() ? -DBL_MAX : (double)mf, lds);
+        sum = 0.0;
+#pragma unroll
+        for (int t = 0; t < IPT; t++) {
+            v[t] = sm_exp((double)f[t] - mx);
+            sum += v[t];
+        }
+    } else {
+        load_chunk<DIN, IPT>(v, X, dtx, base, j0, j1);
+        mx = -DBL_MAX;
+#pragma unroll
+        for (int t = 0; t < IPT; t++) {
+            v[t] = tid + t * kSplitThreads < n ? v[t] : -__builtin_inf();
+            mx = v[t] > mx ? v[t] : mx;
+        }
+        mx = block_reduce<true, kSplitWaves>(mx, lds);
+        sum = 0.0;
+#pragma unroll
+        for (int t = 0; t < IPT; t++) {
+            v[t] = sm_exp(v[t] - mx);
+            sum += v[t];
+        }
+    }
+    sum = block_reduce<false, kSplitWaves>(sum, lds);
+}
+
 template <int DIN, int IPT>
 __global__ __launch_bounds__(kSplitThreads) void k_sm_part(const void* __restrict__ X, int dtx, int64_t L, int G,
                                                            double* __restrict__ part) {
     __shared__ double lds[kSplitWaves];
     const int64_t row = blockIdx.y, rows = gridDim.y, chunk = (L + G - 1) / G;
-    const int64_t j0 = blockIdx.x * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
     const int64_t base = row * L;
     double mx = -DBL_MAX, sum = 0.0;
     if constexpr (IPT > 0) {
         double v[IPT];
-        load_chunk<DIN, IPT>(v, X, dtx, base, j0, j1);
-#pragma unroll
-        for (int t = 0; t < IPT; t++) {
-            const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
-            v[t] = j < j1 ? v[t] : -DBL_MAX;
-            mx = v[t] > mx ? v[t] : mx;
-        }
-        mx = block_reduce<true, kSplitWaves>(mx, lds);
-#pragma unroll
-        for (int t = 0; t < IPT; t++) {
-            const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
-            if (j < j1) sum += sm_exp(v[t] - mx);
-        }
+        sm_chunk_partial<DIN, IPT>(v, X, dtx, base, L, chunk, (int)blockIdx.x, lds, mx, sum);
     } else {
+        const int64_t j0 = blockIdx.x * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
         for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) {
             const double v = ldx<DIN>(X, base + j, dtx);
             mx = v > mx ? v : mx;
         }
         mx = block_reduce<true, kSplitWaves>(mx, lds);
         for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads) sum += sm_exp(ldx<DIN>(X, base + j, dtx) - mx);
+        sum = block_reduce<false, kSplitWaves>(sum, lds);
     }
-    sum = block_reduce<false, kSplitWaves>(sum, lds);
     if (threadIdx.x == 0) {
         part[row * G + blockIdx.x] = mx;
         part[rows * G + row * G + blockIdx.x] = sum;
@@ -235,10 +329,8 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_out(const void* __restrict
     const double scale = sm_exp(mb - M) / S;
     if constexpr (IPT > 0) {
 #pragma unroll
-        for (int t = 0; t < IPT; t++) {
-            const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
-            if (j < j1) stx<DOUT>(Y, base + j, sm_exp(v[t] - mb) * scale, dty);
-        }
+        for (int t = 0; t < IPT; t++) v[t] = sm_exp(v[t] - mb) * scale;
+        store_chunk<DOUT, IPT>(Y, dty, base, j0, j1 > j0 ? (int)(j1 - j0) : 0, v);
     } else {
         for (int64_t j = j0 + threadIdx.x; j < j1; j += kSplitThreads)
             stx<DOUT>(Y, base + j, sm_exp(ldx<DIN>(X, base + j, dtx) - mb) * scale, dty);
@@ -271,31 +363,6 @@ __device__ __forceinline__ bool sm_get(const unsigned long long* p, uint32_t tag
                                                    __HIP_MEMORY_SCOPE_AGENT);
     v = (uint32_t)w;
     return (uint32_t)(w >> 32) == tag;
-}
-
-// (m, s) of chunk c of a row, the whole block participating; v receives the
-// chunk's values (as k_sm_part holds them).
-template <int DIN, int IPT>
-__device__ __forceinline__ void sm_chunk_partial(double (&v)[IPT], const void* __restrict__ X, int dtx, int64_t base,
-                                                 int64_t L, int64_t chunk, int c, double* lds, double& mx, double& sum) {
-    const int64_t j0 = c * chunk, j1 = j0 + chunk < L ? j0 + chunk : L;
-    load_chunk<DIN, IPT>(v, X, dtx, base, j0, j1);
-    mx = -DBL_MAX;
-#pragma unroll
-    for (int t = 0; t < IPT; t++) {
-        const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
-        v[t] = j < j1 ? v[t] : -DBL_MAX;
-        mx = v[t] > mx ? v[t] : mx;
-    }
-    mx = block_reduce<true, kSplitWaves>(mx, lds);
-    sum = 0.0;
-#pragma unroll
-    for (int t = 0; t < IPT; t++) {
-        const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
-        v[t] = j < j1 ? sm_exp(v[t] - mx) : 0.0;     // kept for the output: exp(v - m_b)
-        sum += v[t];
-    }
-    sum = block_reduce<false, kSplitWaves>(sum, lds);
 }
 
 template <int DIN, int DOUT, int IPT>
@@ -338,8 +405,10 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_one(const void* __restrict
                 have = true;
             }
             for (int it = 0; !have && it < spin; it++) {
-                have = sm_get(rs + lane * 4 + 0, tag, w0) && sm_get(rs + lane * 4 + 1, tag, w1) &&
-                       sm_get(rs + lane * 4 + 2, tag, w2) && sm_get(rs + lane * 4 + 3, tag, w3);
+                // four independent loads per poll (one round trip, not four in a row)
+                const bool h0 = sm_get(rs + lane * 4 + 0, tag, w0), h1 = sm_get(rs + lane * 4 + 1, tag, w1);
+                const bool h2 = sm_get(rs + lane * 4 + 2, tag, w2), h3 = sm_get(rs + lane * 4 + 3, tag, w3);
+                have = h0 & h1 & h2 & h3;
                 if (!have) __builtin_amdgcn_s_sleep(1);
             }
         } else {
@@ -377,10 +446,8 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_one(const void* __restrict
     // v holds exp(v - m_b) from the partial pass (k_sm_out's per-chunk form)
     const double scale = sm_exp(mx - sM) / sS;
 #pragma unroll
-    for (int t = 0; t < IPT; t++) {
-        const int64_t j = j0 + threadIdx.x + t * kSplitThreads;
-        if (j < j1) stx<DOUT>(Y, base + j, v[t] * scale, dty);
-    }
+    for (int t = 0; t < IPT; t++) v[t] *= scale;
+    store_chunk<DOUT, IPT>(Y, dty, base, j0, j1 > j0 ? (int)(j1 - j0) : 0, v);
 }
 
 // Tags of the one-launch split kernel: unique per call in this process (0 is
