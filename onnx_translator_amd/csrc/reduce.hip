@@ -393,6 +393,20 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_one(const void* __restrict
     }
     // Wave 0, lane g: wait for partial g (its own block's included).
     const int lane = threadIdx.x & 63;
+    // lane g's partial: the published words, or the recomputed pair; lanes
+    // past G hold the fold's neutral values
+    const auto m_of = [&](uint32_t hi, uint32_t lo, const double* f, int l, bool h) {
+        return l >= G ? -DBL_MAX : h ? __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo) : f[l];
+    };
+    const auto s_of = [&](uint32_t hi, uint32_t lo, const double* f, int l, bool h) {
+        return l >= G ? 0.0 : h ? __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo) : f[l];
+    };
+    // the fold of k_sm_out, by wave 0 (all 64 lanes)
+    const auto fold = [&](double m_l, double s_l) {
+        const double M = wave_max(m_l);
+        const double S = wave_sum(lane < G ? s_l * sm_exp(m_l - M) : 0.0);
+        if (lane == 0) { sM = M; sS = S; }
+    };
     uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
     bool have = false;
     if (threadIdx.x < 64) {
@@ -417,34 +431,24 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_one(const void* __restrict
             have = true;
         }
         const unsigned long long miss = __ballot(!have);
+        // all partials here (the usual case): fold them now, so the block
+        // needs a single barrier before the output
+        if (miss == 0) fold(m_of(w0, w1, fm, lane, true), s_of(w2, w3, fs, lane, true));
         if (lane == 0) s_missing = miss;
     }
     __syncthreads();
-    // Partials that did not arrive in time: recompute them here (uniform loop).
-    for (unsigned long long miss = s_missing; miss; miss &= miss - 1) {
-        const int c = __builtin_ctzll(miss);
-        double w[IPT], m_c, s_c;
-        sm_chunk_partial<DIN, IPT>(w, X, dtx, base, L, chunk, c, lds, m_c, s_c);
-        if (threadIdx.x == 0) { fm[c] = m_c; fs[c] = s_c; }
-    }
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        double m_l = -DBL_MAX, s_l = 0.0;
-        if (lane < G) {
-            if (have) {
-                m_l = __builtin_bit_cast(double, ((unsigned long long)w0 << 32) | w1);
-                s_l = __builtin_bit_cast(double, ((unsigned long long)w2 << 32) | w3);
-            } else {
-                m_l = fm[lane];
-                s_l = fs[lane];
-            }
+    if (s_missing) {     // uniform over the block
+        // Partials that did not arrive in time: recompute them here (uniform loop).
+        for (unsigned long long miss = s_missing; miss; miss &= miss - 1) {
+            const int c = __builtin_ctzll(miss);
+            double w[IPT], m_c, s_c;
+            sm_chunk_partial<DIN, IPT>(w, X, dtx, base, L, chunk, c, lds, m_c, s_c);
+            if (threadIdx.x == 0) { fm[c] = m_c; fs[c] = s_c; }
         }
-        // the fold of k_sm_out
-        const double M = wave_max(m_l);
-        const double S = wave_sum(lane < G ? s_l * sm_exp(m_l - M) : 0.0);
-        if (lane == 0) { sM = M; sS = S; }
+        __syncthreads();
+        if (threadIdx.x < 64) fold(m_of(w0, w1, fm, lane, have), s_of(w2, w3, fs, lane, have));
+        __syncthreads();
     }
-    __syncthreads();
     // v holds exp(v - m_b) from the partial pass (k_sm_out's per-chunk form)
     const double scale = sm_exp(mx - sM) / sS;
 #pragma unroll
