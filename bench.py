@@ -486,8 +486,8 @@ def run_suite(lib, torch, only=None, cpu=None):
         ty = [lib.empty(list(x.shape), U8) for _ in range(4)]
         ts, tz = lib.empty([1], F32), lib.empty([1], U8)
         ms = bench_loop(torch, lambda i: L.dynamic_quantize_linear_forward(tx[i % 4], ty[i % 4], ts, tz), 50)
-        # two reads of x (min / max, then quantize) and one write of the codes
-        emit(op_line("dynamic_quantize_linear", "x f32 [32,512,1024] -> u8", x.size * 9, ms, "hbm"),
+        # algorithmic bytes: x read once (4 B) and the codes written once (1 B)
+        emit(op_line("dynamic_quantize_linear", "x f32 [32,512,1024] -> u8", x.size * 5, ms, "hbm"),
              CpuLeg.dql(x))
         for t in tx + ty + [ts, tz]:
             L.free_tensor(t)

@@ -176,11 +176,12 @@ const char* tensor_ops_hip_version(void);
  * (unset: 0); setting it affects only calls made by the same thread. */
 void tensor_ops_hip_set_exact(int exact);
 int tensor_ops_hip_get_exact(void);
-/* Softmax over few long rows runs one launch in which the blocks of a row exchange
- * partial (max, sum) pairs and wait for each other's with a bounded poll; a block whose
- * wait runs out recomputes the missing pairs from X (same bits).  Sets that bound
- * (polls of ~64 cycles; 0 makes every block recompute, < 0 restores the default) and
- * returns the previous value.  For tests of the recompute path; process-wide. */
+/* Softmax over few long rows and f32 -> uint8 DynamicQuantizeLinear run one launch in
+ * which blocks exchange partial results (a row's (max, sum) pairs; every block's
+ * (min, max)) and wait for each other's with a bounded poll; a block whose wait runs out
+ * recomputes the missing partials from X (same bits).  Sets that bound for both (polls
+ * of ~64 cycles; 0 makes every block recompute, < 0 restores the default) and returns
+ * the previous value.  For tests of the recompute path; process-wide. */
 int tensor_ops_hip_set_softmax_spin(int polls);
 /* Fused elementwise chain: one pass over X that applies the steps in order to the
  * running value v; binary steps take operands[operand] broadcast to X's shape and

@@ -334,4 +334,70 @@ template <int NOP> TO_HD void bd_offsets64(const BDesc& d, int64_t i, int64_t (&
     for (int k = 0; k < NOP; k++) off[k] += i * d.st[k][0];
 }
 
+// One-launch exchanges: a 64-bit word holds (tag, 32-bit payload), written and
+// read with relaxed device-scope atomics (single-copy atomic words, coherent
+// across the XCDs' L2s).  A word is current exactly when it carries the call's
+// tag, so no fence, zeroing or reset of the slots is needed.
+__device__ __forceinline__ void xchg_pub(unsigned long long* p, uint32_t tag, uint32_t v) {
+    __hip_atomic_store(p, ((unsigned long long)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool xchg_get(const unsigned long long* p, uint32_t tag, uint32_t& v) {
+    const unsigned long long w = __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    v = (uint32_t)w;
+    return (uint32_t)(w >> 32) == tag;
+}
+
+// ---- wave-wide reductions without LDS --------------------------------------------
+// Another lane's value (float or double) by DPP moves (CTRL: a pattern whose
+// source lanes all exist, e.g. a quad permutation or a row mirror).
+template <int CTRL, class T> __device__ __forceinline__ T dpp_mov(T v) {
+    if constexpr (sizeof(T) == 8) {
+        const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+        const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)u, CTRL, 0xF, 0xF, false);
+        const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), CTRL, 0xF, 0xF, false);
+        return __builtin_bit_cast(T, ((unsigned long long)hi << 32) | lo);
+    } else {
+        return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+    }
+}
+// The gfx950 permlane swaps: a receives the value of the even partner (row 2k
+// of a row pair for W = 16, the low half of the wave for W = 32) and b that of
+// the odd partner, in every lane of the pair.
+template <int W, class T> __device__ __forceinline__ void permlane_pair(T v, T& a, T& b) {
+    if constexpr (sizeof(T) == 8) {
+        const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+        const unsigned lo = (unsigned)u, hi = (unsigned)(u >> 32);
+        const auto l = W == 16 ? __builtin_amdgcn_permlane16_swap(lo, lo, false, false)
+                               : __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+        const auto h = W == 16 ? __builtin_amdgcn_permlane16_swap(hi, hi, false, false)
+                               : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+        a = __builtin_bit_cast(T, ((unsigned long long)h[0] << 32) | l[0]);
+        b = __builtin_bit_cast(T, ((unsigned long long)h[1] << 32) | l[1]);
+    } else {
+        const unsigned u = __builtin_bit_cast(unsigned, v);
+        const auto l = W == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                               : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        a = __builtin_bit_cast(T, (unsigned)l[0]);
+        b = __builtin_bit_cast(T, (unsigned)l[1]);
+    }
+}
+// op over the wave's 64 lanes, the result in every lane (all 64 lanes must be
+// active).  Lanes pair up as quad neighbours, quad halves, 8-lane halves
+// (row_half_mirror) and 16-lane halves (row_mirror) with DPP moves, then rows
+// 0 / 1 and 2 / 3 and the two wave halves with permlane swaps: no LDS traffic.
+// The association order is fixed, so a sum over the same values always returns
+// the same bits.
+template <class T, class OP> __device__ __forceinline__ T wave_allreduce(T v, OP op) {
+    v = op(v, dpp_mov<0xB1>(v));     // quad_perm [1, 0, 3, 2]
+    v = op(v, dpp_mov<0x4E>(v));     // quad_perm [2, 3, 0, 1]
+    v = op(v, dpp_mov<0x141>(v));    // row_half_mirror
+    v = op(v, dpp_mov<0x140>(v));    // row_mirror
+    T a, b;
+    permlane_pair<16>(v, a, b);
+    v = op(a, b);
+    permlane_pair<32>(v, a, b);
+    return op(a, b);
+}
+
 }  // namespace tohip

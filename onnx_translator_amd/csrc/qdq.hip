@@ -539,7 +539,9 @@ void qdq_axis_entry(const char* name, const Tensor* X, const Tensor* S, const Te
 }
 
 // ------------------------------------------------------- DynamicQuantizeLinear ---
-// tensor_ops.c:3760-3809.  Three launches:
+// tensor_ops.c:3760-3809.  f32 -> uint8 runs one launch that reads x once
+// (k_dql_one, below); other dtypes, graph capture, the no-allocation entry
+// point and tensors too large for its grid take three launches:
 //  * k_dql_minmax: each block reduces min / max of its grid-stride share with
 //    the reference's compares (v < lo, v > hi: NaN never enters), so the
 //    result does not depend on the order; f32 input is read as float4;
@@ -605,6 +607,19 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const void* __restri
     if (threadIdx.x == 0) { part[2 * blockIdx.x] = lo; part[2 * blockIdx.x + 1] = hi; }
 }
 
+// Scale and zero point from the tensor's min / max, in double exactly as the
+// reference (tensor_ops.c:3760-3809).
+__device__ __forceinline__ void dql_params(double lo, double hi, double& scale, double& zpd) {
+    // fmin(lo, 0.0) / fmax(hi, 0.0) as x86 libm returns them (a zero gives +0)
+    lo = lo < 0.0 ? lo : 0.0;
+    hi = hi > 0.0 ? hi : 0.0;
+    scale = (hi - lo) / 255.0;
+    if (scale == 0.0) scale = 1.0;
+    zpd = round(0.0 - lo / scale);
+    if (zpd < 0.0) zpd = 0.0;
+    if (zpd > 255.0) zpd = 255.0;
+}
+
 // params[0] = scale, params[1] = zero point (an integer in [0, 255]).
 __global__ __launch_bounds__(kDqlThreads) void k_dql_params(const double* __restrict__ part, int nparts,
                                                             double* __restrict__ params, void* __restrict__ ys,
@@ -617,14 +632,8 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_params(const double* __rest
     }
     dql_fold(lo, hi, lds);
     if (threadIdx.x != 0) return;
-    // fmin(lo, 0.0) / fmax(hi, 0.0) as x86 libm returns them (a zero gives +0)
-    lo = lo < 0.0 ? lo : 0.0;
-    hi = hi > 0.0 ? hi : 0.0;
-    double scale = (hi - lo) / 255.0;
-    if (scale == 0.0) scale = 1.0;
-    double zpd = round(0.0 - lo / scale);
-    if (zpd < 0.0) zpd = 0.0;
-    if (zpd > 255.0) zpd = 255.0;
+    double scale, zpd;
+    dql_params(lo, hi, scale, zpd);
     params[0] = scale;
     params[1] = zpd;
     st_d_rt(dts, ys, 0, scale);
@@ -669,6 +678,196 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(const void* __restric
         const double q = dql_q(dql_ld<DIN>(X, i, dtx), scale, inv, zpd);
         if constexpr (DY >= 0) st_d<DY>(Y, i, q);
         else st_d_rt(dty, Y, i, q);
+    }
+}
+
+// One launch, x read once (f32 x, uint8 y, x 16-byte and y 4-byte aligned,
+// n % 4 == 0, at most one block per CU (256 blocks) x 1024 threads x 16
+// float4s): block b holds its chunk of cv float4s in registers (thread t:
+// float4s t + 1024 k), reduces its min / max
+// (on the floats: the same compares on the same exactly converted values as the
+// double fold, a +inf / -inf result standing for the DBL_MAX / -DBL_MAX start
+// that nothing beat), publishes them as two tagged words (xchg_pub), waits for
+// every other block's pair with a bounded poll (recomputing from x, with the
+// same min / max, any pair that does not arrive), derives scale and zero point
+// as k_dql_params does and writes the codes of its chunk from registers.  The
+// min / max of a set does not depend on the fold order (the sign of a zero
+// aside, which dql_params maps to +0), so every block derives the same scale
+// and zero point, equal to the three-launch path's.
+constexpr int kDqlOneThreads = 1024, kDqlOneMaxEpt4 = 16, kDqlOneMaxBlocks = 256;
+
+// This thread's (min, max) over its float4s t + 1024 k (k < EPT4) of the n4
+// float4s at p; KEEP: the float4s are also kept in x (else loaded one at a time).
+template <int EPT4, bool KEEP>
+__device__ __forceinline__ void dql_thread_minmax(const float* __restrict__ p, int n4, float4 (&x)[EPT4], float& lo,
+                                                  float& hi) {
+    const int tid = (int)threadIdx.x;
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p, (uint32_t)n4 * 16u);
+    typedef unsigned int u32x4_t __attribute__((__vector_size__(16)));
+    lo = __builtin_inff();
+    hi = -__builtin_inff();
+    const auto load = [&](int k) {
+        return __builtin_bit_cast(float4, (u32x4_t)__builtin_amdgcn_raw_buffer_load_b128(
+                                              xr, (uint32_t)((tid + k * kDqlOneThreads) * 16), 0, 0));
+    };
+    const auto fold = [&](float e) {
+        lo = e < lo ? e : lo;
+        hi = e > hi ? e : hi;
+    };
+    if constexpr (KEEP) {
+#pragma unroll
+        for (int k = 0; k < EPT4; k++) x[k] = load(k);
+    }
+#pragma unroll
+    for (int k = 0; k < EPT4; k++) {
+        const float4 v = KEEP ? x[k] : load(k);
+        if (tid + k * kDqlOneThreads < n4) { fold(v.x); fold(v.y); fold(v.z); fold(v.w); }
+    }
+}
+
+// Block-wide (min, max) of the n4 float4s at p (see dql_thread_minmax); every
+// thread returns the block's pair.
+template <int EPT4, bool KEEP>
+__device__ __forceinline__ void dql_chunk_minmax(const float* __restrict__ p, int n4, float4 (&x)[EPT4], float& lo,
+                                                 float& hi, float* lds) {
+    const int tid = (int)threadIdx.x;
+    dql_thread_minmax<EPT4, KEEP>(p, n4, x, lo, hi);
+    lo = wave_allreduce(lo, [](float a, float b) { return b < a ? b : a; });
+    hi = wave_allreduce(hi, [](float a, float b) { return b > a ? b : a; });
+    const int w = tid >> 6;
+    if ((tid & 63) == 0) { lds[2 * w] = lo; lds[2 * w + 1] = hi; }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kDqlOneThreads / 64; i++) {
+        lo = lds[2 * i] < lo ? lds[2 * i] : lo;
+        hi = lds[2 * i + 1] > hi ? lds[2 * i + 1] : hi;
+    }
+    __syncthreads();
+}
+
+// The code of v: rint(v / scale) + zp clamped to [0, 255].  With an f32
+// reciprocal (fast: 2^-120 < scale < 2^120, so 1 / scale is a normal float and
+// |v / scale| <= 255 + |zp| cannot overflow) p = RN(v * RN(1 / scale)) lies
+// within 2^-22.8 |p| of the exact quotient, and of its double rounding, which
+// is what the reference rounds; rint(p) is that quotient's rint unless p is
+// within 2^-21 |p| of a half-integer.  Those lanes (and NaN / inf, whose
+// compares fail) take dql_q, the double path.
+__device__ __forceinline__ uint32_t dql_code(float v, bool fast, float invf, float zpf, double scale, double inv,
+                                             double zpd) {
+    if (fast) {
+        const float p = v * invf;
+        const float r = __builtin_rintf(p);
+        if (__builtin_fabsf(__builtin_fabsf(p - r) - 0.5f) > 0x1p-21f * __builtin_fabsf(p))
+            return (uint32_t)__builtin_amdgcn_fmed3f(r + zpf, 0.0f, 255.0f);
+    }
+    return (uint32_t)dql_q((double)v, scale, inv, zpd);
+}
+
+// (1024, 4): at most 128 registers per lane (4 waves per SIMD), so a block fits
+// on every CU and the whole grid (one block per CU) is resident at once.
+template <int EPT4>
+__global__ __launch_bounds__(kDqlOneThreads, 4) void k_dql_one(const float* __restrict__ X, int64_t nv, int64_t cv,
+                                                            unsigned char* __restrict__ Y,
+                                                            unsigned long long* __restrict__ slots, uint32_t tag,
+                                                            int spin, void* __restrict__ ys, int dts,
+                                                            void* __restrict__ yz, int dtz) {
+    __shared__ float lds[2 * kDqlOneThreads / 64];
+    __shared__ unsigned long long s_miss[kDqlOneMaxBlocks / 64];
+    __shared__ int s_any;
+    __shared__ float s_lo, s_hi;
+    __shared__ double s_scale, s_zp;
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int nblk = (int)gridDim.x;
+    const auto chunk_n4 = [&](int b) { return (int)max<int64_t>(0, min<int64_t>(cv, nv - (int64_t)b * cv)); };
+    const int n4 = chunk_n4((int)blockIdx.x);
+    float4 x[EPT4];
+    float lo, hi;
+    dql_chunk_minmax<EPT4, true>(X + 4 * (int64_t)blockIdx.x * cv, n4, x, lo, hi, lds);
+    if (tid == 0) {
+        xchg_pub(slots + 2 * blockIdx.x, tag, __builtin_bit_cast(uint32_t, lo));
+        xchg_pub(slots + 2 * blockIdx.x + 1, tag, __builtin_bit_cast(uint32_t, hi));
+    }
+    // Wave 0, lane l: the pairs of blocks l + 64 i (i < 16), polled together.
+    const auto params = [&](float flo, float fhi) {
+        double scale, zpd;
+        dql_params(flo == __builtin_inff() ? DBL_MAX : (double)flo, fhi == -__builtin_inff() ? -DBL_MAX : (double)fhi,
+                   scale, zpd);
+        s_scale = scale;
+        s_zp = zpd;
+        if (blockIdx.x == 0) {
+            st_d_rt(dts, ys, 0, scale);
+            st_d_rt(dtz, yz, 0, zpd);       // an integer in [0, 255]: the code is zpd itself
+        }
+    };
+    if (tid < 64) {
+        // fold each pair as it arrives (this block's own pair is already in)
+        float flo = lo, fhi = hi;
+        unsigned need = 0;
+#pragma unroll
+        for (int i = 0; i < kDqlOneMaxBlocks / 64; i++) {
+            const int b = lane + 64 * i;
+            if (b < nblk && b != (int)blockIdx.x) need |= 1u << i;
+        }
+        for (int it = 0; need && it < spin; it++) {
+#pragma unroll
+            for (int i = 0; i < kDqlOneMaxBlocks / 64; i++) {
+                if (need >> i & 1) {
+                    const int b = lane + 64 * i;
+                    uint32_t wl, wh;
+                    const bool a = xchg_get(slots + 2 * b, tag, wl), c = xchg_get(slots + 2 * b + 1, tag, wh);
+                    if (a & c) {
+                        need &= ~(1u << i);
+                        const float pl = __builtin_bit_cast(float, wl), ph = __builtin_bit_cast(float, wh);
+                        flo = pl < flo ? pl : flo;
+                        fhi = ph > fhi ? ph : fhi;
+                    }
+                }
+            }
+            if (need) __builtin_amdgcn_s_sleep(1);
+        }
+        flo = wave_allreduce(flo, [](float a, float b) { return b < a ? b : a; });
+        fhi = wave_allreduce(fhi, [](float a, float b) { return b > a ? b : a; });
+        int any = 0;
+#pragma unroll
+        for (int i = 0; i < kDqlOneMaxBlocks / 64; i++) {
+            const unsigned long long m = __ballot(need >> i & 1);
+            if (lane == 0) s_miss[i] = m;
+            any |= m != 0;
+        }
+        if (lane == 0) {
+            s_any = any;
+            s_lo = flo;
+            s_hi = fhi;
+            if (!any) params(flo, fhi);
+        }
+    }
+    __syncthreads();
+    if (s_any) {        // uniform over the block: recompute the pairs that did not arrive
+        for (int i = 0; i < kDqlOneMaxBlocks / 64; i++)
+            for (unsigned long long m = s_miss[i]; m; m &= m - 1) {
+                const int b = 64 * i + __builtin_ctzll(m);
+                float bl, bh;
+                dql_chunk_minmax<EPT4, false>(X + 4 * (int64_t)b * cv, chunk_n4(b), x, bl, bh, lds);
+                if (tid == 0) {
+                    s_lo = bl < s_lo ? bl : s_lo;
+                    s_hi = bh > s_hi ? bh : s_hi;
+                }
+            }
+        __syncthreads();
+        if (tid == 0) params(s_lo, s_hi);
+        __syncthreads();
+    }
+    const double scale = s_scale, zpd = s_zp, inv = 1.0 / scale;
+    const bool fast = scale > 0x1p-120 && scale < 0x1p120;
+    const float invf = (float)inv, zpf = (float)zpd;
+    const __amdgpu_buffer_rsrc_t yr = buffer_rsrc(Y + 4 * (int64_t)blockIdx.x * cv, (uint32_t)n4 * 4u);
+#pragma unroll
+    for (int k = 0; k < EPT4; k++) {
+        const uint32_t c = dql_code(x[k].x, fast, invf, zpf, scale, inv, zpd) |
+                           (dql_code(x[k].y, fast, invf, zpf, scale, inv, zpd) << 8) |
+                           (dql_code(x[k].z, fast, invf, zpf, scale, inv, zpd) << 16) |
+                           (dql_code(x[k].w, fast, invf, zpf, scale, inv, zpd) << 24);
+        __builtin_amdgcn_raw_buffer_store_b32(c, yr, (uint32_t)((tid + k * kDqlOneThreads) * 4), 0, 2 /* nt */);
     }
 }
 
@@ -732,6 +931,8 @@ void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp, bool n
     void* yd = st.out(y, (size_t)n * dt_bytes((int)y->dtype));
     void* sd = st.out(y_scale, dt_bytes((int)y_scale->dtype));
     void* zd = st.out(y_zp, dt_bytes((int)y_zp->dtype));
+    // (also taken by the one-launch path, which does not use it: a call captured into a
+    // graph after an eager call then reuses this cached buffer instead of allocating)
     if (!noalloc) part = (double*)pool_alloc(sizeof(double) * kDqlScratch);
     if (!xd || !yd || !sd || !zd || !part) { if (part && !noalloc) pool_free(part); st.finish(); return; }
     double* params = part + 2 * kDqlMaxParts;
@@ -742,6 +943,39 @@ void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp, bool n
                                                                                      (4 * kDqlThreads)));
     const unsigned qblocks = grid_for((size_t)std::max<int64_t>(items, 1), kDqlThreads, 8192);
     hipStream_t s = stream();
+    // f32 -> uint8 in one launch that reads x once (k_dql_one), unless captured
+    // into a graph (its exchange tags are per call) or too large for its grid
+    if (!noalloc && v4 && dty == kU8 && ((uintptr_t)yd & 3) == 0 && n % 4 == 0 && !stream_capturing(s)) {
+        const int64_t nv = n / 4, maxblk = std::min(num_cus(), kDqlOneMaxBlocks);
+        int ept4 = 0;
+        for (int e : {4, 8, kDqlOneMaxEpt4})
+            if (!ept4 && nv <= maxblk * kDqlOneThreads * (int64_t)e) ept4 = e;
+        if (ept4) {
+            const int64_t nblk = (nv + (int64_t)kDqlOneThreads * ept4 - 1) / ((int64_t)kDqlOneThreads * ept4);
+            const int64_t cv = (nv + nblk - 1) / nblk;
+            unsigned long long* slots = (unsigned long long*)pool_alloc(sizeof(unsigned long long) * 2 * nblk);
+            if (!slots) { pool_free(part); st.finish(); return; }
+            const uint32_t tag = next_exchange_tag();
+            const int spin = exchange_spin();
+            const int dts = (int)y_scale->dtype, dtz = (int)y_zp->dtype;
+            unsigned char* y8 = (unsigned char*)yd;
+            const float* xf = (const float*)xd;
+            if (ept4 == 4)
+                hipLaunchKernelGGL((k_dql_one<4>), dim3((unsigned)nblk), dim3(kDqlOneThreads), 0, s, xf, nv, cv, y8,
+                                   slots, tag, spin, sd, dts, zd, dtz);
+            else if (ept4 == 8)
+                hipLaunchKernelGGL((k_dql_one<8>), dim3((unsigned)nblk), dim3(kDqlOneThreads), 0, s, xf, nv, cv, y8,
+                                   slots, tag, spin, sd, dts, zd, dtz);
+            else
+                hipLaunchKernelGGL((k_dql_one<kDqlOneMaxEpt4>), dim3((unsigned)nblk), dim3(kDqlOneThreads), 0, s, xf,
+                                   nv, cv, y8, slots, tag, spin, sd, dts, zd, dtz);
+            check_launch(name);         // sets the error on failure; the buffers go back either way
+            pool_free(slots);
+            pool_free(part);
+            st.finish();
+            return;
+        }
+    }
     if (v4) hipLaunchKernelGGL((k_dql_minmax<kF32>), dim3(nparts), dim3(kDqlThreads), 0, s, xd, dtx, n, part);
     else hipLaunchKernelGGL((k_dql_minmax<-1>), dim3(nparts), dim3(kDqlThreads), 0, s, xd, dtx, n, part);
     hipLaunchKernelGGL(k_dql_params, dim3(1), dim3(kDqlThreads), 0, s, part, nparts, params, sd, (int)y_scale->dtype,

@@ -55,45 +55,10 @@ __device__ __forceinline__ double sm_exp(double x) {
 constexpr int kRowThreads = 1024;
 constexpr int kWaves = kRowThreads / 64;
 
-// A 64-bit value of another lane, moved as two 32-bit DPP moves (CTRL: a DPP
-// pattern whose source lanes all exist, e.g. a quad permutation or a mirror).
-template <int CTRL> __device__ __forceinline__ double dpp_d(double v) {
-    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
-    const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)u, CTRL, 0xF, 0xF, false);
-    const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), CTRL, 0xF, 0xF, false);
-    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
-}
-// The gfx950 permlane swaps, on a value held in two registers: a receives
-// the value of the even partner (row 2k of a row pair for 16, the low half of
-// the wave for 32) and b that of the odd partner, in every lane of the pair.
-template <int W> __device__ __forceinline__ void swap_d(double v, double& a, double& b) {
-    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
-    const unsigned lo = (unsigned)u, hi = (unsigned)(u >> 32);
-    const auto l = W == 16 ? __builtin_amdgcn_permlane16_swap(lo, lo, false, false)
-                           : __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
-    const auto h = W == 16 ? __builtin_amdgcn_permlane16_swap(hi, hi, false, false)
-                           : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
-    a = __builtin_bit_cast(double, ((unsigned long long)h[0] << 32) | l[0]);
-    b = __builtin_bit_cast(double, ((unsigned long long)h[1] << 32) | l[1]);
-}
-
-// Max (strict >) or sum over the wave's 64 lanes, the same result in every lane
-// (all 64 lanes must be active).  Lanes pair up as quad neighbours, quad
-// halves, 8-lane halves (row_half_mirror) and 16-lane halves (row_mirror) with
-// DPP moves, then rows 0 / 1 and 2 / 3 and the two wave halves with permlane
-// swaps: no LDS traffic.  The sum's association order is fixed, so every call
-// on the same values returns the same bits.
+// Max (strict >) or sum over the wave's 64 lanes, the same result in every
+// lane (wave_allreduce: DPP moves and permlane swaps, all 64 lanes active).
 template <bool MAX> __device__ __forceinline__ double wave_reduce(double v) {
-    const auto op = [](double x, double y) { return MAX ? (y > x ? y : x) : x + y; };
-    v = op(v, dpp_d<0xB1>(v));     // quad_perm [1, 0, 3, 2]
-    v = op(v, dpp_d<0x4E>(v));     // quad_perm [2, 3, 0, 1]
-    v = op(v, dpp_d<0x141>(v));    // row_half_mirror
-    v = op(v, dpp_d<0x140>(v));    // row_mirror
-    double a, b;
-    swap_d<16>(v, a, b);
-    v = op(a, b);
-    swap_d<32>(v, a, b);
-    return op(a, b);
+    return wave_allreduce(v, [](double x, double y) { return MAX ? (y > x ? y : x) : x + y; });
 }
 __device__ __forceinline__ double wave_max(double v) { return wave_reduce<true>(v); }
 __device__ __forceinline__ double wave_sum(double v) { return wave_reduce<false>(v); }
@@ -354,19 +319,6 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_out(const void* __restrict
 // whole block recomputes that chunk's partial from X with the same thread
 // mapping and reduction order, which gives the same bits, so every block ends
 // with the same (M, S) either way and every wave exits.
-constexpr int kSmSpinDefault = 1 << 14;   // polls of ~64 cycles each (about 0.5 ms)
-std::atomic<int> g_sm_spin{kSmSpinDefault};   // tensor_ops_hip_set_softmax_spin
-
-__device__ __forceinline__ void sm_pub(unsigned long long* p, uint32_t tag, uint32_t v) {
-    __hip_atomic_store(p, ((unsigned long long)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool sm_get(const unsigned long long* p, uint32_t tag, uint32_t& v) {
-    const unsigned long long w = __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-    v = (uint32_t)w;
-    return (uint32_t)(w >> 32) == tag;
-}
-
 template <int DIN, int DOUT, int IPT>
 __global__ __launch_bounds__(kSplitThreads) void k_sm_one(const void* __restrict__ X, int dtx, void* __restrict__ Y,
                                                           int dty, int64_t L, int G,
@@ -386,10 +338,10 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_one(const void* __restrict
     if (threadIdx.x == 0) {
         const unsigned long long mb = __builtin_bit_cast(unsigned long long, mx);
         const unsigned long long sb = __builtin_bit_cast(unsigned long long, sum);
-        sm_pub(rs + blockIdx.x * 4 + 0, tag, (uint32_t)(mb >> 32));
-        sm_pub(rs + blockIdx.x * 4 + 1, tag, (uint32_t)mb);
-        sm_pub(rs + blockIdx.x * 4 + 2, tag, (uint32_t)(sb >> 32));
-        sm_pub(rs + blockIdx.x * 4 + 3, tag, (uint32_t)sb);
+        xchg_pub(rs + blockIdx.x * 4 + 0, tag, (uint32_t)(mb >> 32));
+        xchg_pub(rs + blockIdx.x * 4 + 1, tag, (uint32_t)mb);
+        xchg_pub(rs + blockIdx.x * 4 + 2, tag, (uint32_t)(sb >> 32));
+        xchg_pub(rs + blockIdx.x * 4 + 3, tag, (uint32_t)sb);
     }
     // Wave 0, lane g: wait for partial g (its own block's included).
     const int lane = threadIdx.x & 63;
@@ -422,8 +374,8 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_one(const void* __restrict
             }
             for (int it = 0; !have && it < spin; it++) {
                 // four independent loads per poll (one round trip, not four in a row)
-                const bool h0 = sm_get(rs + lane * 4 + 0, tag, w0), h1 = sm_get(rs + lane * 4 + 1, tag, w1);
-                const bool h2 = sm_get(rs + lane * 4 + 2, tag, w2), h3 = sm_get(rs + lane * 4 + 3, tag, w3);
+                const bool h0 = xchg_get(rs + lane * 4 + 0, tag, w0), h1 = xchg_get(rs + lane * 4 + 1, tag, w1);
+                const bool h2 = xchg_get(rs + lane * 4 + 2, tag, w2), h3 = xchg_get(rs + lane * 4 + 3, tag, w3);
                 have = h0 & h1 & h2 & h3;
                 if (!have) __builtin_amdgcn_s_sleep(1);
             }
@@ -456,27 +408,6 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_one(const void* __restrict
     store_chunk<DOUT, IPT>(Y, dty, base, j0, j1 > j0 ? (int)(j1 - j0) : 0, v);
 }
 
-// Tags of the one-launch split kernel: unique per call in this process (0 is
-// never used, so zeroed memory never matches).
-std::atomic<uint32_t> g_sm_tag{0};
-uint32_t next_sm_tag() {
-    uint32_t t;
-    do t = g_sm_tag.fetch_add(1, std::memory_order_relaxed) + 1; while (t == 0);
-    return t;
-}
-
-// Whether s is being captured into a graph: a captured launch would replay
-// with the tag of its capture, so the next replay could take the previous
-// replay's partials for current ones; captured calls use the two launches.
-bool stream_capturing(hipStream_t s) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
-        (void)hipGetLastError();
-        return false;
-    }
-    return cs != hipStreamCaptureStatusNone;
-}
-
 // Returns false when the workspace cannot be allocated (error set).
 template <int DIN, int DOUT, int IPT>
 bool launch_split_ipt(const void* x, int dtx, void* y, int dty, int64_t L, int G, dim3 g, hipStream_t s) {
@@ -486,7 +417,7 @@ bool launch_split_ipt(const void* x, int dtx, void* y, int dty, int64_t L, int G
         if (!slots) return false;
         if constexpr (IPT > 0)
             hipLaunchKernelGGL((k_sm_one<DIN, DOUT, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, y, dty, L, G, slots,
-                               next_sm_tag(), g_sm_spin.load(std::memory_order_relaxed));
+                               next_exchange_tag(), exchange_spin());
         pool_free(slots);   // stream-ordered reuse: later work on this stream runs after the kernel
         return true;
     } else {
@@ -789,9 +720,6 @@ void global_average_pool_forward(const Tensor* input, Tensor* output) {
 }
 
 
-int tensor_ops_hip_set_softmax_spin(int polls) {
-    return g_sm_spin.exchange(polls < 0 ? kSmSpinDefault : polls);
-}
 
 void softmax_forward(const Tensor* input, Tensor* output, int axis) {
     const char* name = "softmax_forward";

@@ -30,6 +30,17 @@ const double* device_cos_lut();  // 4097 doubles in device memory (after init_co
 int num_cus();
 int device_id();                 // the device the library stream belongs to (after ensure_device)
 
+// ---- one-launch exchanges ----------------------------------------------------
+// Kernels whose blocks exchange partial results through device memory in one
+// launch (softmax over few long rows, DynamicQuantizeLinear) tag each published
+// word with a number unique to the call, wait for the other blocks' words with a
+// bounded poll and recompute what did not arrive.  A call captured into a graph
+// would replay with its capture-time tag, so captured calls take the
+// multi-launch forms.
+uint32_t next_exchange_tag();    // never 0, so zeroed memory never matches
+int exchange_spin();             // the poll bound (tensor_ops_hip_set_softmax_spin)
+bool stream_capturing(hipStream_t s);
+
 // ---- memory -----------------------------------------------------------------
 enum class Mem { kHostPinned, kHostMalloc, kDevOwned, kDevBorrowed, kHostForeign, kDevForeign };
 Mem classify(const void* p);     // registry first, then hipPointerGetAttributes

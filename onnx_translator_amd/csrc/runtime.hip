@@ -138,6 +138,30 @@ bool exact_mode() {
 int num_cus() { return S().cus > 0 ? S().cus : 256; }
 int device_id() { return S().dev; }
 
+// ---- one-launch exchanges ---------------------------------------------------------
+// Tags are unique per call in this process; 0 is skipped.
+std::atomic<uint32_t> g_xchg_tag{0};
+uint32_t next_exchange_tag() {
+    uint32_t t;
+    do t = g_xchg_tag.fetch_add(1, std::memory_order_relaxed) + 1; while (t == 0);
+    return t;
+}
+
+// Polls of ~64 cycles each before a block recomputes what has not arrived (about
+// 0.5 ms: far longer than any co-resident block takes to publish).
+constexpr int kXchgSpinDefault = 1 << 14;
+std::atomic<int> g_xchg_spin{kXchgSpinDefault};
+int exchange_spin() { return g_xchg_spin.load(std::memory_order_relaxed); }
+
+bool stream_capturing(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return cs != hipStreamCaptureStatusNone;
+}
+
 // ---- memory -------------------------------------------------------------------------
 // Records a new header t over data p.  An owning kind (library allocation)
 // takes precedence over a borrowed one for the residency entry.
@@ -651,6 +675,10 @@ void tensor_ops_hip_clear_error(void) { t_err.clear(); }
 const char* tensor_ops_hip_version(void) { return "libtensor_ops_hip 0.1 (gfx950)"; }
 
 void tensor_ops_hip_set_exact(int exact) { t_exact = exact ? 1 : 0; }
+
+int tensor_ops_hip_set_softmax_spin(int polls) {
+    return tohip::g_xchg_spin.exchange(polls < 0 ? tohip::kXchgSpinDefault : polls);
+}
 
 int tensor_ops_hip_get_exact(void) { return exact_mode() ? 1 : 0; }
 

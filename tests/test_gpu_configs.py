@@ -422,6 +422,56 @@ def test_dynamic_quantize_linear_full_size(hip, oracle_lib, x2):
     assert_bitexact(y, ry, O.U8, what="dql codes")
 
 
+def _dql_case(name):
+    rng = np.random.default_rng(len(name))
+    if name == "normal_1M":
+        return rng.normal(0, 3, 1 << 20).astype(np.float32)
+    if name == "nan_inf":
+        x = rng.normal(0, 2, 1 << 16).astype(np.float32)
+        x[rng.choice(x.size, 9, replace=False)] = np.nan
+        x[rng.choice(x.size, 3, replace=False)] = np.inf
+        x[rng.choice(x.size, 3, replace=False)] = -np.inf
+        return x
+    if name == "all_nan":
+        return np.full(4096, np.nan, np.float32)
+    if name == "zeros":
+        return np.zeros(1 << 14, np.float32)
+    if name == "negative":
+        return -np.abs(rng.normal(0, 5, 1 << 15)).astype(np.float32)
+    if name == "positive":
+        return np.abs(rng.normal(0, 5, 1 << 15)).astype(np.float32) + 1
+    if name == "tiny":     # scale below 2^-120: every code through the double path
+        return (rng.normal(0, 1, 1 << 14) * 1e-38).astype(np.float32)
+    if name == "huge":     # scale above 2^120
+        return (rng.uniform(-1, 1, 1 << 14) * 3e38).astype(np.float32)
+    if name == "odd_size":  # n % 4 != 0: the three-launch path
+        return rng.normal(0, 1, 100_003).astype(np.float32)
+    raise ValueError(name)
+
+
+DQL_CASES = ["normal_1M", "nan_inf", "all_nan", "zeros", "negative", "positive", "tiny", "huge", "odd_size"]
+
+
+@pytest.mark.parametrize("name", DQL_CASES)
+def test_dql_one_launch_cases(hip, oracle_lib, name):
+    """DynamicQuantizeLinear's one-launch kernel (x read once, blocks exchange
+    their min / max) against the oracle, bit for bit, on special values and
+    scales outside the f32 reciprocal's range; spin = 0 makes every block
+    recompute the other blocks' min / max from x instead of waiting."""
+    x = _dql_case(name)
+    ry, rs, rz = oracle_lib.dql(x, O.F32)
+    old = hip.lib.tensor_ops_hip_set_softmax_spin(-1)
+    try:
+        for spin in (-1, 0):
+            hip.lib.tensor_ops_hip_set_softmax_spin(spin)
+            y, s, z = hip.dql(x, O.F32)
+            assert_bitexact(s, rs, O.F32, what=f"dql scale {name} spin {spin}")
+            assert_bitexact(z, rz, O.U8, what=f"dql zero point {name} spin {spin}")
+            assert_bitexact(y, ry, O.U8, what=f"dql codes {name} spin {spin}")
+    finally:
+        hip.lib.tensor_ops_hip_set_softmax_spin(old)
+
+
 @pytest.mark.parametrize("shape", [(64, 512, 7, 7), (8, 64, 56, 56), (3, 5, 1, 1), (1, 300, 3, 3), (2, 70, 10, 11)])
 def test_global_average_pool_sizes(hip, oracle_lib, shape):
     rng = np.random.default_rng(sum(shape))

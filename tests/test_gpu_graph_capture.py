@@ -1,8 +1,9 @@
 """Library calls captured into a HIP graph (as bench.py times the headline).
 
-A second test captures Softmax over few long rows, whose eager form is one
-launch whose blocks exchange per-call tagged partials: under capture it must
-take the two-launch form, so replays on changed inputs stay correct.
+Two more tests capture Softmax over few long rows and f32 -> uint8
+DynamicQuantizeLinear, whose eager forms are one launch whose blocks exchange
+per-call tagged partials: under capture they must take their multi-launch
+forms, so replays on changed inputs stay correct.
 
 The calls of one headline step (per-tensor u8 and per-axis i8 QuantizeLinear,
 their DequantizeLinear, the fused config-1 chain) are captured on the
@@ -154,6 +155,67 @@ def test_softmax_split_rows_under_capture(hip):
                 torch.cuda.synchronize()
                 assert not hip.last_error(), hip.last_error()
                 assert_bitexact(y.cpu().numpy(), ye.cpu().numpy(), O.F32, what=f"softmax replay {r}")
+    finally:
+        for p in keep:
+            L.free_tensor(p)
+        L.tensor_ops_hip_set_stream(None)
+
+
+def test_dynamic_quantize_linear_under_capture(hip):
+    """f32 -> uint8 DynamicQuantizeLinear captured after an eager call (eager:
+    one launch whose blocks exchange call-tagged (min, max) pairs; captured: the
+    three-launch form).  The input is rewritten before every replay and each
+    replay must equal an eager call on that input bit for bit."""
+    import torch
+    torch.cuda.init()
+    side = torch.cuda.Stream()
+    L = hip.lib
+    L.tensor_ops_hip_set_stream(ctypes.c_void_p(side.cuda_stream))
+    keep = []
+
+    def wrap(t, shape, dt):
+        arr = (ctypes.c_int * len(shape))(*shape)
+        p = L.tensor_wrap_device(ctypes.c_void_p(t.data_ptr()), arr, len(shape), dt)
+        assert p
+        keep.append(p)
+        return p
+
+    try:
+        with torch.cuda.stream(side):
+            rng = np.random.default_rng(31)
+            shp = [8, 512, 1024]
+            inputs = [rng.normal(0, s, shp).astype(np.float32) for s in (1.0, 3.0, 0.5, 2.0)]
+            x = torch.from_numpy(inputs[0]).cuda()
+            y, ye = (torch.empty(shp, dtype=torch.uint8, device="cuda") for _ in range(2))
+            sc, sce = (torch.empty([1], dtype=torch.float32, device="cuda") for _ in range(2))
+            zp, zpe = (torch.empty([1], dtype=torch.uint8, device="cuda") for _ in range(2))
+            tx, ty, tye = wrap(x, shp, O.F32), wrap(y, shp, O.U8), wrap(ye, shp, O.U8)
+            ts, tse, tz, tze = wrap(sc, [1], O.F32), wrap(sce, [1], O.F32), wrap(zp, [1], O.U8), wrap(zpe, [1], O.U8)
+            hip.lib.tensor_ops_hip_clear_error()
+            L.dynamic_quantize_linear_forward(tx, ty, ts, tz)
+            torch.cuda.synchronize()
+            assert not hip.last_error(), hip.last_error()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                L.dynamic_quantize_linear_forward(tx, ty, ts, tz)
+            assert not hip.last_error(), hip.last_error()
+            for r in range(1, 4):
+                x.copy_(torch.from_numpy(inputs[r]))
+                y.fill_(0xA5)
+                sc.fill_(-1.0)
+                zp.fill_(7)
+                torch.cuda.synchronize()
+                g.replay()
+                torch.cuda.synchronize()
+                L.dynamic_quantize_linear_forward(tx, tye, tse, tze)
+                torch.cuda.synchronize()
+                assert not hip.last_error(), hip.last_error()
+                assert_bitexact(sc.cpu().numpy(), sce.cpu().numpy(), O.F32, what=f"dql scale replay {r}")
+                assert_bitexact(zp.cpu().numpy(), zpe.cpu().numpy(), O.U8, what=f"dql zero point replay {r}")
+                assert_bitexact(y.cpu().numpy(), ye.cpu().numpy(), O.U8, what=f"dql codes replay {r}")
+        ry, rs, rz = O.oracle().dql(inputs[3], O.F32)
+        assert_bitexact(ye.cpu().numpy(), ry, O.U8, what="eager dql vs oracle")
+        assert_bitexact(sce.cpu().numpy(), rs, O.F32, what="eager dql scale vs oracle")
     finally:
         for p in keep:
             L.free_tensor(p)
