@@ -382,6 +382,12 @@ template <int W, class T> __device__ __forceinline__ void permlane_pair(T v, T& 
         b = __builtin_bit_cast(T, (unsigned)l[1]);
     }
 }
+// The value of lane l - 1 in lane l (DPP wave_shr:1; lane 0 receives 0), all 64
+// lanes active: a VALU move instead of an LDS-pipe permute.
+__device__ __forceinline__ float lane_prev(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x138, 0xF, 0xF, false));
+}
+
 // op over the wave's 64 lanes, the result in every lane (all 64 lanes must be
 // active).  Lanes pair up as quad neighbours, quad halves, 8-lane halves
 // (row_half_mirror) and 16-lane halves (row_mirror) with DPP moves, then rows

@@ -529,7 +529,7 @@ __global__ __launch_bounds__(256) void k_maxpool_3s2(const float* __restrict__ X
             if (ih < 0 || ih >= g.H) continue;
             float2 v = make_float2(-__builtin_inff(), -__builtin_inff());
             if (live) v = *reinterpret_cast<const float2*>(xp + (int64_t)ih * g.W + 2 * lane);
-            const float left = __shfl_up(v.y, 1, 64);
+            const float left = lane_prev(v.y);
             if (lane > 0 && left > best) best = left;           // kw = 0: column 2l - 1
             if (v.x > best) best = v.x;                          // kw = 1: column 2l
             if (v.y > best) best = v.y;                          // kw = 2: column 2l + 1
@@ -571,7 +571,7 @@ __global__ __launch_bounds__(64 * kPoolStripWaves) void k_maxpool_3s2_strip(cons
     };
     // taps of one input row in the reference's kw order: 2l-1, 2l, 2l+1
     auto row_max = [&](float best, float2 v, bool valid) {
-        const float left = __shfl_up(v.y, 1, 64);
+        const float left = lane_prev(v.y);
         if (valid) {
             if (lane > 0 && left > best) best = left;
             if (v.x > best) best = v.x;
