@@ -696,19 +696,26 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(const void* __restric
 // and zero point, equal to the three-launch path's.
 constexpr int kDqlOneThreads = 1024, kDqlOneMaxEpt4 = 16, kDqlOneMaxBlocks = 256;
 
+// A buffer resource over the n units (of `unit` bytes) at p; none when n <= 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dql_rsrc(const void* p, int n, int unit) {
+    return buffer_rsrc(p, n > 0 ? (uint32_t)n * (uint32_t)unit : 0u);
+}
+
 // This thread's (min, max) over its float4s t + 1024 k (k < EPT4) of the n4
 // float4s at p; KEEP: the float4s are also kept in x (else loaded one at a time).
 template <int EPT4, bool KEEP>
 __device__ __forceinline__ void dql_thread_minmax(const float* __restrict__ p, int n4, float4 (&x)[EPT4], float& lo,
                                                   float& hi) {
     const int tid = (int)threadIdx.x;
-    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p, (uint32_t)n4 * 16u);
     typedef unsigned int u32x4_t __attribute__((__vector_size__(16)));
     lo = __builtin_inff();
     hi = -__builtin_inff();
+    // one buffer resource per k (scalar registers), over float4s k * 1024 ..,
+    // so every load takes the same per-lane offset tid * 16
     const auto load = [&](int k) {
         return __builtin_bit_cast(float4, (u32x4_t)__builtin_amdgcn_raw_buffer_load_b128(
-                                              xr, (uint32_t)((tid + k * kDqlOneThreads) * 16), 0, 0));
+                                              dql_rsrc(p + 4 * k * kDqlOneThreads, n4 - k * kDqlOneThreads, 16),
+                                              (uint32_t)(tid * 16), 0, 0));
     };
     const auto fold = [&](float e) {
         lo = e < lo ? e : lo;
@@ -860,14 +867,15 @@ __global__ __launch_bounds__(kDqlOneThreads, 4) void k_dql_one(const float* __re
     const double scale = s_scale, zpd = s_zp, inv = 1.0 / scale;
     const bool fast = scale > 0x1p-120 && scale < 0x1p120;
     const float invf = (float)inv, zpf = (float)zpd;
-    const __amdgpu_buffer_rsrc_t yr = buffer_rsrc(Y + 4 * (int64_t)blockIdx.x * cv, (uint32_t)n4 * 4u);
+    unsigned char* yb = Y + 4 * (int64_t)blockIdx.x * cv;
 #pragma unroll
     for (int k = 0; k < EPT4; k++) {
         const uint32_t c = dql_code(x[k].x, fast, invf, zpf, scale, inv, zpd) |
                            (dql_code(x[k].y, fast, invf, zpf, scale, inv, zpd) << 8) |
                            (dql_code(x[k].z, fast, invf, zpf, scale, inv, zpd) << 16) |
                            (dql_code(x[k].w, fast, invf, zpf, scale, inv, zpd) << 24);
-        __builtin_amdgcn_raw_buffer_store_b32(c, yr, (uint32_t)((tid + k * kDqlOneThreads) * 4), 0, 2 /* nt */);
+        __builtin_amdgcn_raw_buffer_store_b32(c, dql_rsrc(yb + 4 * k * kDqlOneThreads, n4 - k * kDqlOneThreads, 4),
+                                              (uint32_t)(tid * 4), 0, 2 /* nt */);
     }
 }
 
