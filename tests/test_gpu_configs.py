@@ -446,10 +446,15 @@ def _dql_case(name):
         return (rng.uniform(-1, 1, 1 << 14) * 3e38).astype(np.float32)
     if name == "odd_size":  # n % 4 != 0: the three-launch path
         return rng.normal(0, 1, 100_003).astype(np.float32)
+    if name == "ragged_62_blocks":  # 250,001 float4s: 62 blocks, the last one partial
+        return rng.normal(1, 2, 4 * 250_001).astype(np.float32)
+    if name == "full_minus_one_float4":  # 256 blocks of 16 float4s per thread, the last block one short
+        return rng.normal(0, 1, 32 * 512 * 1024 - 4).astype(np.float32)
     raise ValueError(name)
 
 
-DQL_CASES = ["normal_1M", "nan_inf", "all_nan", "zeros", "negative", "positive", "tiny", "huge", "odd_size"]
+DQL_CASES = ["normal_1M", "nan_inf", "all_nan", "zeros", "negative", "positive", "tiny", "huge", "odd_size",
+             "ragged_62_blocks", "full_minus_one_float4"]
 
 
 @pytest.mark.parametrize("name", DQL_CASES)
