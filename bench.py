@@ -824,7 +824,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
-              "(every hot op shards without exchange; see DESIGN.md)", file=sys.stderr)
+              "(every hot op shards along its outer dimension without exchange; run one process per GPU)",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():

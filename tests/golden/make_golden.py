@@ -205,7 +205,8 @@ PLANS = [
 
 
 def edge_cases(ref, w):
-    """SURVEY Appendix-A style known-answer inputs, answered by the reference."""
+    """Known-answer inputs at the codecs' rounding and saturation boundaries
+    (ties, the e4m3 / e5m2 extremes, NaN and infinities), answered by the reference."""
     f32 = np.float32
     xq = np.array([0.3, 0.5, 1.5, 2.5, -2.5, 3.5, 17, 18, 19, 448, 464, 480, 1000, 57344, 61439,
                    61440, 65536, np.inf, -np.inf, np.nan, -0.0], dtype=f32)
