@@ -339,7 +339,10 @@ __global__ __launch_bounds__(kBlock) void k_bin_i32f32_v4(const int* __restrict_
         bd_offsets32<2, ND>(d, v * 4u, off);
         int4 a;
         if (sa == 1) {
-            a = *reinterpret_cast<const int4*>(A + off[0]);
+            // read once: a streaming (nontemporal) load
+            typedef int i32x4_t __attribute__((ext_vector_type(4)));
+            const i32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const i32x4_t*>(A + off[0]));
+            a = make_int4(t.x, t.y, t.z, t.w);
         } else if (sa == 0) {
             const int t = A[off[0]];
             a = make_int4(t, t, t, t);
