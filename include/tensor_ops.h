@@ -22,6 +22,14 @@
  * data through device memory.  A Tensor made by create_tensor_device() or
  * tensor_wrap_device() holds device memory; operators whose operands are all
  * device-resident are enqueued on the library stream and return immediately.
+ *
+ * Graph capture: operators on device tensors may be captured into a HIP graph
+ * on the library stream.  Captured calls allocate nothing (no split-k slices;
+ * Softmax over few long rows and DynamicQuantizeLinear keep their partials in
+ * fixed per-GPU device arrays, so replays of such graphs that overlap on one
+ * GPU race).  Anything that would allocate or synchronise under capture (host
+ * tensors, create_tensor_device*, tensor_to_host / tensor_from_host, internal
+ * temporaries of the fallback paths) is refused with an error instead.
  */
 #ifndef TENSOR_OPS_HIP_H
 #define TENSOR_OPS_HIP_H
@@ -140,10 +148,12 @@ void dynamic_quantize_linear_forward(const Tensor* x, Tensor* y, Tensor* y_scale
  * Extensions (no counterpart in the reference)
  * ------------------------------------------------------------------------- */
 
-/* Zero-filled tensor in device memory (HBM).  NULL on failure. */
+/* Zero-filled tensor in device memory (HBM).  NULL on failure, and while the library
+ * stream is being captured into a graph (create device tensors before the capture). */
 Tensor* create_tensor_device(int* shape, int ndim, DataType dtype);
 /* Device tensor with undefined contents, for an operator output that the next
- * call writes in full (saves the fill of create_tensor_device).  NULL on failure. */
+ * call writes in full (saves the fill of create_tensor_device).  NULL on failure and
+ * under capture, as create_tensor_device. */
 Tensor* create_tensor_device_empty(int* shape, int ndim, DataType dtype);
 /* Tensor header over caller-owned device memory; free_tensor frees only the header. */
 Tensor* tensor_wrap_device(void* device_ptr, int* shape, int ndim, DataType dtype);
@@ -159,7 +169,9 @@ int tensor_ops_hip_sync(void);
 void tensor_ops_hip_set_stream(void* stream);
 /* Stream for the calling thread's subsequent calls only, overriding the one above (NULL
  * clears the override).  Nothing is drained: the caller orders work across its streams.
- * Library workspace buffers are reused only on the stream they were released on; a
+ * Library workspace buffers are reused only on the stream they were released on, and
+ * those cached under the stream a thread leaves go to other streams only once the work
+ * enqueued on it before the switch has completed (an event recorded at the switch); a
  * tensor used on several streams must be freed once the caller has ordered them. */
 void tensor_ops_hip_set_thread_stream(void* stream);
 void* tensor_ops_hip_get_stream(void);
@@ -183,6 +195,18 @@ int tensor_ops_hip_get_exact(void);
  * of ~64 cycles; 0 makes every block recompute, < 0 restores the default) and returns
  * the previous value.  For tests of the recompute path; process-wide. */
 int tensor_ops_hip_set_softmax_spin(int polls);
+/* Those exchanges tag their words with the low 32 bits of a per-process call count
+ * (the high bits are an epoch: buffers are zero-filled again when it changes).  Moves
+ * the count forward to at least `count` (never back, so tags stay unique within an
+ * epoch) and returns the count now in effect; 0 only reads it.  For tests of the tag
+ * wrap-around. */
+unsigned long long tensor_ops_hip_advance_exchange_count(unsigned long long count);
+/* Fills every device buffer that the library hands out with undefined contents
+ * (create_tensor_device_empty, the staging copy of a host output) with `byte` (e.g.
+ * 0xFF: NaN in every float format) before the operator writes it, so a test sees any
+ * element an operator failed to write; < 0 turns it off (the default).  Returns the
+ * previous setting.  Process-wide; for tests. */
+int tensor_ops_hip_set_poison(int byte);
 /* Fused elementwise chain: one pass over X that applies the steps in order to the
  * running value v; binary steps take operands[operand] broadcast to X's shape and
  * compute v op b (b op v when reversed).  Every step rounds to float32 as the
@@ -266,8 +290,8 @@ void dequantize_conv2d_fused_forward(const Tensor* Xq, const Tensor* XScale, con
  * dynamic_quantize_linear_forward; every tensor must be device-resident (an error
  * otherwise: host tensors would need staging buffers).  Its min / max partials live in a
  * fixed 32,784-byte device array per GPU (at most 2048 partials, whatever the input size),
- * held until the process ends and shared by every call on that GPU: calls that overlap on
- * one GPU race. */
+ * held until the process ends and shared by every call on that GPU (and by captured calls
+ * of dynamic_quantize_linear_forward): calls that overlap on one GPU race. */
 void dynamic_quantize_linear_forward_noalloc(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp);
 
 #ifdef __cplusplus

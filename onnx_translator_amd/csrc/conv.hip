@@ -1183,7 +1183,8 @@ bool launch_conv_tiled_xq(const void* x, const void* w, const void* b, int dtb, 
     // the output), and only if that beats the unsplit grid by 5%.
     // Config-5 block 4: 100 tiles -> 5 slices (0.98 of the CUs busy, not 0.39).
     int split = 1;
-    if (blocks < num_cus() && !no_split) {
+    // (not under graph capture: the slices' workspace would have to outlive the call)
+    if (blocks < num_cus() && !no_split && !stream_capturing(s)) {
         const int smax = (int)std::min<int64_t>(g.Kg / 128, 8);
         const double base = balance(blocks);
         double best = base;

@@ -1030,7 +1030,9 @@ int launch_f32_nt(const GemmArgs& g, const WoqB& q, hipStream_t s) {
     const bool fast_bias = g.c.mode == 0 || (g.c.dt == kF32 && g.c.mode <= 3);
     const int ydt = fast_bias && (g.dty == kF32 || g.dty == kF16) ? g.dty : -1;
     bool big = false;
-    const int split = nt_split_plan(g.M, g.N, g.K, big);
+    int split = nt_split_plan(g.M, g.N, g.K, big);
+    // (no k split under graph capture: the slices' workspace would have to outlive the call)
+    if (split > 1 && stream_capturing(s)) split = 1;
     if (big) {
         launch_nt_kernel<128, 256, 16, 2, 4, BQ, false>(g, q, 0, 1, ydt, s);
         return 1;

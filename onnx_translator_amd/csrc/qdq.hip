@@ -879,51 +879,43 @@ __global__ __launch_bounds__(kDqlOneThreads, 4) void k_dql_one(const float* __re
     }
 }
 
-// Scratch of dynamic_quantize_linear_forward_noalloc: the min / max partials of
+// Scratch of dynamic_quantize_linear_forward_noalloc and of calls captured into
+// a graph (whose workspace must outlive the call): the min / max partials of
 // k_dql_minmax and the (scale, zero point) pair of k_dql_params, in a
 // file-scope device array (each GPU holds its own copy until the process
 // ends).  In host code `scratch` names a host-side stand-in, not device
-// memory: host code uses only the address hipGetSymbolAddress returns for the
-// library's device (dql_scratch).  Every call on one GPU shares the array, so
-// calls that overlap on one GPU (different streams or threads) race.  Nothing
-// in it needs to start at zero: k_dql_minmax writes every partial it launches
-// and k_dql_params the pair before any kernel reads them.
+// memory: host code uses only the address that init_qdq_workspace resolves
+// with hipGetSymbolAddress, once per device with that device current, at
+// library initialisation (dql_scratch).  Every such call on one GPU shares the
+// array, so those that overlap on one GPU (different streams or threads, or
+// concurrent replays of captured graphs) race.  Nothing in it needs to start at
+// zero: k_dql_minmax writes every partial it launches and k_dql_params the
+// pair before any kernel reads them.
 constexpr int kDqlScratch = 2 * kDqlMaxParts + 2;             // 32,784 bytes
 static __device__ __align__(256) double scratch[kDqlScratch];
 
 constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mu;
 double* g_scratch_ptr[kMaxScratchDevices] = {};
 
-// Device address of `scratch` on the library's device, resolved once per device
-// (with that device current) and kept; nullptr with the error set on failure.
+// Device address of `scratch` on the library's device; nullptr with the error
+// set when initialisation could not resolve it.
 double* dql_scratch() {
     const int dev = device_id();
-    if (dev < 0 || dev >= kMaxScratchDevices) { set_error("no-allocation scratch: device %d out of range", dev); return nullptr; }
-    std::lock_guard<std::mutex> g(g_scratch_mu);
-    if (!g_scratch_ptr[dev]) {
-        int cur = 0;
-        if (!check_hip(hipGetDevice(&cur), "hipGetDevice")) return nullptr;
-        if (cur != dev && !check_hip(hipSetDevice(dev), "hipSetDevice")) return nullptr;
-        void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (cur != dev) (void)hipSetDevice(cur);
-        if (!check_hip(e, "hipGetSymbolAddress(scratch)")) return nullptr;
-        g_scratch_ptr[dev] = (double*)p;
-    }
-    return g_scratch_ptr[dev];
+    double* p = (dev >= 0 && dev < kMaxScratchDevices) ? g_scratch_ptr[dev] : nullptr;
+    if (!p) set_error("dynamic_quantize_linear: fixed scratch of device %d unavailable", dev);
+    return p;
 }
 
-// noalloc: the partials live in `scratch` instead of the HBM pool, and every
-// tensor must already be device-resident (host tensors would need staging
-// buffers); nothing is allocated.
+// Workspace of the three-launch path: `scratch` for noalloc and captured calls
+// (nothing is allocated), an HBM pool buffer otherwise.  The noalloc entry
+// point also requires device-resident tensors (host tensors would need staging
+// buffers).
 void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp, bool noalloc = false) {
     const char* name = noalloc ? "dynamic_quantize_linear_forward_noalloc" : "dynamic_quantize_linear_forward";
     if (!tensor_sane(x, name) || !tensor_sane(y, name) || !tensor_sane(y_scale, name) || !tensor_sane(y_zp, name))
         return;
     if (y->size < x->size || y_scale->size < 1 || y_zp->size < 1) { set_error("%s: output too small", name); return; }
     if (!ensure_device()) return;
-    double* part = nullptr;
     if (noalloc) {
         const Tensor* all[4] = {x, y, y_scale, y_zp};
         for (const Tensor* t : all)
@@ -931,7 +923,6 @@ void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp, bool n
                 set_error("%s: every tensor must be device-resident (host tensors need staging buffers)", name);
                 return;
             }
-        if (!(part = dql_scratch())) return;
     }
     const int64_t n = (int64_t)x->size;
     Staging st;
@@ -939,11 +930,7 @@ void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp, bool n
     void* yd = st.out(y, (size_t)n * dt_bytes((int)y->dtype));
     void* sd = st.out(y_scale, dt_bytes((int)y_scale->dtype));
     void* zd = st.out(y_zp, dt_bytes((int)y_zp->dtype));
-    // (also taken by the one-launch path, which does not use it: a call captured into a
-    // graph after an eager call then reuses this cached buffer instead of allocating)
-    if (!noalloc) part = (double*)pool_alloc(sizeof(double) * kDqlScratch);
-    if (!xd || !yd || !sd || !zd || !part) { if (part && !noalloc) pool_free(part); st.finish(); return; }
-    double* params = part + 2 * kDqlMaxParts;
+    if (!xd || !yd || !sd || !zd) { st.finish(); return; }
     const int dtx = (int)x->dtype, dty = (int)y->dtype;
     const bool v4 = dtx == kF32 && ((uintptr_t)xd & 15) == 0;
     const int64_t items = v4 ? n / 4 : n;
@@ -951,9 +938,10 @@ void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp, bool n
                                                                                      (4 * kDqlThreads)));
     const unsigned qblocks = grid_for((size_t)std::max<int64_t>(items, 1), kDqlThreads, 8192);
     hipStream_t s = stream();
+    const bool captured = stream_capturing(s);
     // f32 -> uint8 in one launch that reads x once (k_dql_one), unless captured
     // into a graph (its exchange tags are per call) or too large for its grid
-    if (!noalloc && v4 && dty == kU8 && ((uintptr_t)yd & 3) == 0 && n % 4 == 0 && !stream_capturing(s)) {
+    if (!noalloc && !captured && v4 && dty == kU8 && ((uintptr_t)yd & 3) == 0 && n % 4 == 0) {
         const int64_t nv = n / 4, maxblk = std::min(num_cus(), kDqlOneMaxBlocks);
         int ept4 = 0;
         for (int e : {4, 8, kDqlOneMaxEpt4})
@@ -961,9 +949,10 @@ void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp, bool n
         if (ept4) {
             const int64_t nblk = (nv + (int64_t)kDqlOneThreads * ept4 - 1) / ((int64_t)kDqlOneThreads * ept4);
             const int64_t cv = (nv + nblk - 1) / nblk;
-            unsigned long long* slots = (unsigned long long*)pool_alloc(sizeof(unsigned long long) * 2 * nblk);
-            if (!slots) { pool_free(part); st.finish(); return; }
-            const uint32_t tag = next_exchange_tag();
+            uint32_t tag = 0;
+            unsigned long long* slots =
+                (unsigned long long*)xchg_alloc(sizeof(unsigned long long) * 2 * nblk, &tag);
+            if (!slots) { st.finish(); return; }
             const int spin = exchange_spin();
             const int dts = (int)y_scale->dtype, dtz = (int)y_zp->dtype;
             unsigned char* y8 = (unsigned char*)yd;
@@ -977,13 +966,16 @@ void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp, bool n
             else
                 hipLaunchKernelGGL((k_dql_one<kDqlOneMaxEpt4>), dim3((unsigned)nblk), dim3(kDqlOneThreads), 0, s, xf,
                                    nv, cv, y8, slots, tag, spin, sd, dts, zd, dtz);
-            check_launch(name);         // sets the error on failure; the buffers go back either way
-            pool_free(slots);
-            pool_free(part);
+            check_launch(name);         // sets the error on failure; the buffer goes back either way
+            xchg_free(slots);
             st.finish();
             return;
         }
     }
+    const bool pooled = !noalloc && !captured;
+    double* part = pooled ? (double*)pool_alloc(sizeof(double) * kDqlScratch) : dql_scratch();
+    if (!part) { st.finish(); return; }
+    double* params = part + 2 * kDqlMaxParts;
     if (v4) hipLaunchKernelGGL((k_dql_minmax<kF32>), dim3(nparts), dim3(kDqlThreads), 0, s, xd, dtx, n, part);
     else hipLaunchKernelGGL((k_dql_minmax<-1>), dim3(nparts), dim3(kDqlThreads), 0, s, xd, dtx, n, part);
     hipLaunchKernelGGL(k_dql_params, dim3(1), dim3(kDqlThreads), 0, s, part, nparts, params, sd, (int)y_scale->dtype,
@@ -995,7 +987,7 @@ void dql_entry(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp, bool n
     else
         hipLaunchKernelGGL((k_dql_quant<-1, -1>), dim3(qblocks), dim3(kDqlThreads), 0, s, xd, dtx, n, params, yd, dty);
     const bool ok = check_launch(name);
-    if (!noalloc) pool_free(part);      // pool buffers are reused in stream order
+    if (pooled) pool_free(part);        // pool buffers are reused in stream order
     if (!ok) { st.finish(); return; }
     st.finish();
 }
@@ -1059,6 +1051,16 @@ void qdq_fused_entry(const Tensor* X, const Tensor* QS, const Tensor* QZ, const 
 }
 
 }  // namespace
+
+// Resolves `scratch` on the library's device (current during initialisation)
+// and keeps its address per device.
+void init_qdq_workspace() {
+    const int dev = device_id();
+    if (dev < 0 || dev >= kMaxScratchDevices) { set_error("no-allocation scratch: device %d out of range", dev); return; }
+    void* p = nullptr;
+    if (check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"))
+        g_scratch_ptr[dev] = (double*)p;
+}
 }  // namespace tohip
 
 using namespace tohip;

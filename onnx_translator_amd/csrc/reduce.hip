@@ -408,28 +408,43 @@ __global__ __launch_bounds__(kSplitThreads) void k_sm_one(const void* __restrict
     store_chunk<DOUT, IPT>(Y, dty, base, j0, j1 > j0 ? (int)(j1 - j0) : 0, v);
 }
 
-// Returns false when the workspace cannot be allocated (error set).
+// Workspace of split-row calls captured into a graph: the (m_b, s_b) partials
+// of k_sm_part / k_sm_out, in a file-scope device array (each GPU holds its own
+// copy until the process ends), since a captured call's workspace must outlive
+// the call.  Host code uses only the address resolved at initialisation
+// (g_sm_capture_ws); replays of captured split-row calls that overlap on one
+// GPU share it and race.  Nothing in it needs to start at zero: k_sm_part
+// writes every partial that k_sm_out reads.
+constexpr int kSmCaptureParts = 2 * 1024;                  // (m, s) pairs of up to 1024 row chunks
+static __device__ __align__(256) double sm_capture_ws[kSmCaptureParts];
+double* g_sm_capture_ws = nullptr;
+
+// Returns false when the workspace cannot be had (error set).
 template <int DIN, int DOUT, int IPT>
 bool launch_split_ipt(const void* x, int dtx, void* y, int dty, int64_t L, int G, dim3 g, hipStream_t s) {
-    if (IPT > 0 && !stream_capturing(s)) {
+    const bool captured = stream_capturing(s);
+    if (IPT > 0 && !captured) {
+        uint32_t tag = 0;
         unsigned long long* slots =
-            (unsigned long long*)pool_alloc(sizeof(unsigned long long) * 4 * (size_t)g.y * (size_t)G);
+            (unsigned long long*)xchg_alloc(sizeof(unsigned long long) * 4 * (size_t)g.y * (size_t)G, &tag);
         if (!slots) return false;
         if constexpr (IPT > 0)
             hipLaunchKernelGGL((k_sm_one<DIN, DOUT, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, y, dty, L, G, slots,
-                               next_exchange_tag(), exchange_spin());
-        pool_free(slots);   // stream-ordered reuse: later work on this stream runs after the kernel
+                               tag, exchange_spin());
+        xchg_free(slots);   // stream-ordered reuse: later work on this stream runs after the kernel
         return true;
-    } else {
-        // sized as the one-launch workspace, so a call captured into a graph
-        // after an eager call of the same shape reuses that call's cached
-        // buffer instead of allocating inside the capture
-        double* part = (double*)pool_alloc(sizeof(double) * 4 * (size_t)g.y * (size_t)G);
-        if (!part) return false;
-        hipLaunchKernelGGL((k_sm_part<DIN, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, L, G, part);
-        hipLaunchKernelGGL((k_sm_out<DIN, DOUT, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, y, dty, L, G, part);
-        pool_free(part);
     }
+    const size_t nparts = 2 * (size_t)g.y * (size_t)G;
+    double* part;
+    if (captured) {
+        if (nparts > (size_t)kSmCaptureParts) { set_error("softmax: %zu partials exceed the capture workspace", nparts); return false; }
+        if (!(part = g_sm_capture_ws)) { set_error("softmax: capture workspace unavailable"); return false; }
+    } else if (!(part = (double*)pool_alloc(sizeof(double) * nparts))) {
+        return false;
+    }
+    hipLaunchKernelGGL((k_sm_part<DIN, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, L, G, part);
+    hipLaunchKernelGGL((k_sm_out<DIN, DOUT, IPT>), g, dim3(kSplitThreads), 0, s, x, dtx, y, dty, L, G, part);
+    if (!captured) pool_free(part);
     return true;
 }
 
@@ -683,6 +698,13 @@ __global__ __launch_bounds__(kGapSmallThreads) void k_gap_small_f32(const float*
 }
 
 }  // namespace
+
+// Resolves sm_capture_ws on the library's device (current during initialisation).
+void init_reduce_workspace() {
+    void* p = nullptr;
+    if (check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(sm_capture_ws)), "hipGetSymbolAddress(sm_capture_ws)"))
+        g_sm_capture_ws = (double*)p;
+}
 }  // namespace tohip
 
 using namespace tohip;
@@ -749,6 +771,8 @@ void softmax_forward(const Tensor* input, Tensor* output, int axis) {
             if (G > gmax) G = (int)gmax;
             if (G > 64) G = 64;
         }
+        // (a captured call keeps its partials in the fixed capture workspace)
+        if (G > 1 && 2 * outer * G > kSmCaptureParts && stream_capturing(s)) G = 1;
         if (inner == 1 && G > 1) {
             const dim3 g((unsigned)G, (unsigned)outer);
             bool ok;

@@ -34,19 +34,42 @@ int device_id();                 // the device the library stream belongs to (af
 // Kernels whose blocks exchange partial results through device memory in one
 // launch (softmax over few long rows, DynamicQuantizeLinear) tag each published
 // word with a number unique to the call, wait for the other blocks' words with a
-// bounded poll and recompute what did not arrive.  A call captured into a graph
-// would replay with its capture-time tag, so captured calls take the
-// multi-launch forms.
-uint32_t next_exchange_tag();    // never 0, so zeroed memory never matches
+// bounded poll and recompute what did not arrive.  The words live in buffers
+// that hold nothing but exchange words: created zero-filled (0 is never a tag)
+// and zero-filled again before their first use after the 32-bit tag counter
+// wraps, so a word carries a call's tag only if that call wrote it.  A call
+// captured into a graph would replay with its capture-time tag, so captured
+// calls take the multi-launch forms (xchg_alloc refuses under capture).
+// xchg_alloc: a buffer of at least `bytes` for one call on the library stream,
+// and that call's tag in *tag; nullptr with the error set on failure.
+void* xchg_alloc(size_t bytes, uint32_t* tag);
+void xchg_free(void* p);         // back to the current stream's exchange list
 int exchange_spin();             // the poll bound (tensor_ops_hip_set_softmax_spin)
 bool stream_capturing(hipStream_t s);
+
+// ---- fixed workspaces ----------------------------------------------------------
+// Some paths keep their workspace in a file-scope __device__ array (each GPU
+// holds its own copy until the process ends): the no-allocation entry point and
+// calls captured into a graph, whose workspace must outlive the call.  In host
+// code such an array's name is a host-side stand-in, so each owning file
+// resolves the device address once, with hipGetSymbolAddress, in these hooks,
+// which the device initialisation calls with the library's device current (no
+// call under capture resolves one).  They record an error and leave the address
+// null on failure; the paths that need it then report that error.
+void init_qdq_workspace();
+void init_reduce_workspace();
 
 // ---- memory -----------------------------------------------------------------
 enum class Mem { kHostPinned, kHostMalloc, kDevOwned, kDevBorrowed, kHostForeign, kDevForeign };
 Mem classify(const void* p);     // registry first, then hipPointerGetAttributes
 inline bool is_dev(Mem m) { return m == Mem::kDevOwned || m == Mem::kDevBorrowed || m == Mem::kDevForeign; }
 
-void* pool_alloc(size_t bytes);  // device memory from the caching pool
+// Device memory from the caching pool, reused in the order of the stream it was
+// released on.  Refused (nullptr, error set) while the library stream is being
+// captured into a graph: a buffer taken inside a capture goes back to the pool
+// when the call returns while the graph goes on using it, and a fresh one would
+// need hipMalloc inside the capture.
+void* pool_alloc(size_t bytes);
 void pool_free(void* p);
 
 size_t tensor_bytes(const Tensor* t);
@@ -77,7 +100,8 @@ bool make_bdesc_for(BDesc& d, const Tensor* Y, const Tensor* const* ops, int nop
 // Resolves each operand to a device pointer.  Host inputs are copied to pool
 // buffers (H2D on the library stream); a host output gets a pool buffer that
 // finish() copies back.  finish() synchronises only if staging happened, so
-// calls on device-resident tensors stay asynchronous.
+// calls on device-resident tensors stay asynchronous.  Under graph capture a
+// host operand is an error (staging needs pool buffers and a synchronisation).
 class Staging {
   public:
     Staging() = default;

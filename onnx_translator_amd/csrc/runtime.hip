@@ -62,6 +62,16 @@ struct State {
     std::multimap<size_t, void*> pin_free;
     std::unordered_map<void*, size_t> pin_size;
     size_t pin_cached = 0;
+    // Exchange-word buffers (xchg_alloc), kept apart from the pool above so
+    // they never hold anything but exchange words: per-stream free lists, and
+    // per buffer its size and the tag epoch it was last zero-filled in.
+    struct XBuf { size_t bytes; uint32_t epoch; };
+    std::map<hipStream_t, std::multimap<size_t, void*>> xchg_free;
+    std::unordered_map<void*, XBuf> xchg_info;
+    // Cached buffers of a stream that a thread left (tensor_ops_hip_set_thread_stream):
+    // free for any stream once `ev`, recorded on the old stream at the switch, completes.
+    struct Parked { hipEvent_t ev; std::multimap<size_t, void*> dev, xchg; };
+    std::vector<Parked> parked;
 
     std::mutex lut_mu;
     std::atomic<int> lut_host_ready{0};
@@ -74,6 +84,8 @@ static State& S() {
     static State* s = new State;
     return *s;
 }
+
+static void reclaim_parked(State& s, hipStream_t st);
 
 static constexpr size_t kDevCacheLimit = size_t(32) << 30;   // 32 GiB of cached HBM buffers
 static constexpr size_t kPinCacheLimit = size_t(4) << 30;
@@ -98,6 +110,8 @@ static void do_init() {
     if (hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, s.dev) != hipSuccess)
         s.cus = 256;
     s.ok = true;
+    init_qdq_workspace();
+    init_reduce_workspace();
 }
 
 bool ensure_device() {
@@ -139,12 +153,66 @@ int num_cus() { return S().cus > 0 ? S().cus : 256; }
 int device_id() { return S().dev; }
 
 // ---- one-launch exchanges ---------------------------------------------------------
-// Tags are unique per call in this process; 0 is skipped.
-std::atomic<uint32_t> g_xchg_tag{0};
-uint32_t next_exchange_tag() {
-    uint32_t t;
-    do t = g_xchg_tag.fetch_add(1, std::memory_order_relaxed) + 1; while (t == 0);
-    return t;
+// One 64-bit count per call: its low 32 bits are the call's tag (0 skipped, so
+// zero-filled words never match), its high bits the epoch.  Tags are unique
+// within an epoch; a buffer handed out in an epoch other than the one it was
+// last zero-filled in is zero-filled first (on the stream, before the kernel),
+// so a word carrying a call's tag was written by that call.
+std::atomic<uint64_t> g_xchg_count{0};
+
+void* xchg_alloc(size_t bytes, uint32_t* tag) {
+    State& s = S();
+    const hipStream_t st = stream();
+    if (stream_capturing(st)) {
+        set_error("exchange workspace requested while the library stream is being captured");
+        return nullptr;
+    }
+    uint64_t c;
+    do c = g_xchg_count.fetch_add(1, std::memory_order_relaxed) + 1; while ((uint32_t)c == 0);
+    const uint32_t epoch = (uint32_t)(c >> 32);
+    const size_t need = bytes < 256 ? 256 : (bytes + 255) / 256 * 256;
+    void* p = nullptr;
+    size_t have = 0;
+    bool fill = true;
+    {
+        std::lock_guard<std::mutex> g(s.mu);
+        if (!s.parked.empty()) reclaim_parked(s, st);
+        auto fl = s.xchg_free.find(st);
+        if (fl != s.xchg_free.end()) {
+            auto it = fl->second.lower_bound(need);    // any larger one serves (they are a few KB)
+            if (it != fl->second.end()) {
+                p = it->second;
+                fl->second.erase(it);
+                State::XBuf& xb = s.xchg_info[p];
+                have = xb.bytes;
+                fill = xb.epoch != epoch;
+                xb.epoch = epoch;
+            }
+        }
+    }
+    if (!p) {
+        if (!check_hip(hipMalloc(&p, need), "exchange workspace")) return nullptr;
+        have = need;
+        std::lock_guard<std::mutex> g(s.mu);
+        s.xchg_info[p] = State::XBuf{need, epoch};
+    }
+    if (fill && !check_hip(hipMemsetAsync(p, 0, have, st), "exchange workspace fill")) {
+        std::lock_guard<std::mutex> g(s.mu);
+        s.xchg_info[p].epoch = epoch + 1;             // not filled: fill before its next use
+        s.xchg_free[st].emplace(have, p);
+        return nullptr;
+    }
+    *tag = (uint32_t)c;
+    return p;
+}
+
+void xchg_free(void* p) {
+    if (!p) return;
+    State& s = S();
+    std::lock_guard<std::mutex> g(s.mu);
+    auto it = s.xchg_info.find(p);
+    if (it == s.xchg_info.end()) return;
+    s.xchg_free[stream()].emplace(it->second.bytes, p);
 }
 
 // Polls of ~64 cycles each before a block recomputes what has not arrived (about
@@ -161,6 +229,10 @@ bool stream_capturing(hipStream_t s) {
     }
     return cs != hipStreamCaptureStatusNone;
 }
+
+// Test hook: byte that fills every buffer handed out with undefined contents
+// (create_tensor_device_empty, staged outputs), or -1 for none.
+std::atomic<int> g_poison{-1};
 
 // ---- memory -------------------------------------------------------------------------
 // Records a new header t over data p.  An owning kind (library allocation)
@@ -217,6 +289,18 @@ static size_t round_bytes(size_t b) {
     return (b + mb - 1) / mb * mb;
 }
 
+// Parked buffers whose event has completed join stream st's lists (s.mu held).
+static void reclaim_parked(State& s, hipStream_t st) {
+    for (size_t i = 0; i < s.parked.size();) {
+        State::Parked& pk = s.parked[i];
+        if (hipEventQuery(pk.ev) != hipSuccess) { (void)hipGetLastError(); i++; continue; }
+        (void)hipEventDestroy(pk.ev);
+        if (!pk.dev.empty()) s.dev_free[st].insert(pk.dev.begin(), pk.dev.end());
+        if (!pk.xchg.empty()) s.xchg_free[st].insert(pk.xchg.begin(), pk.xchg.end());
+        s.parked.erase(s.parked.begin() + (std::ptrdiff_t)i);
+    }
+}
+
 static void* take_cached(std::multimap<size_t, void*>& fl, size_t need, size_t& cached) {
     auto it = fl.lower_bound(need);
     if (it == fl.end() || it->first > need + need / 8) return nullptr;
@@ -228,9 +312,15 @@ static void* take_cached(std::multimap<size_t, void*>& fl, size_t need, size_t& 
 
 void* pool_alloc(size_t bytes) {
     State& s = S();
+    if (stream_capturing(stream())) {
+        set_error("device memory requested while the library stream is being captured into a graph "
+                  "(allocate before the capture; captured calls must not allocate)");
+        return nullptr;
+    }
     const size_t need = round_bytes(bytes);
     {
         std::lock_guard<std::mutex> g(s.mu);
+        if (!s.parked.empty()) reclaim_parked(s, stream());
         auto fl = s.dev_free.find(stream());
         if (fl != s.dev_free.end())
             if (void* p = take_cached(fl->second, need, s.dev_cached)) return p;
@@ -238,8 +328,18 @@ void* pool_alloc(size_t bytes) {
     void* p = nullptr;
     if (hipMalloc(&p, need) != hipSuccess) {
         (void)hipGetLastError();
-        // Release the cache and retry once.
+        // Release the cache and retry once (parked buffers after their event).
         std::lock_guard<std::mutex> g(s.mu);
+        for (State::Parked& pk : s.parked) {
+            (void)hipEventSynchronize(pk.ev);
+            (void)hipEventDestroy(pk.ev);
+            for (auto& kv : pk.dev) {
+                (void)hipFree(kv.second);
+                s.dev_size.erase(kv.second);
+            }
+            if (!pk.xchg.empty()) s.xchg_free[stream()].insert(pk.xchg.begin(), pk.xchg.end());
+        }
+        s.parked.clear();
         for (auto& per_stream : s.dev_free)
             for (auto& kv : per_stream.second) {
                 (void)hipFree(kv.second);
@@ -403,10 +503,19 @@ Staging::~Staging() {
     for (auto& b : bufs_) pool_free(b.dev);
 }
 
+// A host operand under graph capture: staging would allocate and synchronise.
+static bool refuse_host_under_capture() {
+    if (!stream_capturing(stream())) return false;
+    set_error("host tensor used while the library stream is being captured into a graph "
+              "(captured calls take device tensors only)");
+    return true;
+}
+
 const void* Staging::in(const Tensor* t) {
     if (!t->size) return t->data;
     const Mem m = classify(t->data);
     if (is_dev(m)) return t->data;
+    if (refuse_host_under_capture()) { failed_ = true; return nullptr; }
     const size_t b = tensor_bytes(t);
     void* d = pool_alloc(b);
     if (!d) { failed_ = true; return nullptr; }
@@ -423,8 +532,15 @@ void* Staging::out(Tensor* t, size_t bytes_written) {
     if (!t->size) return t->data;
     const Mem m = classify(t->data);
     if (is_dev(m)) return t->data;
+    if (refuse_host_under_capture()) { failed_ = true; return nullptr; }
     void* d = pool_alloc(tensor_bytes(t));
     if (!d) { failed_ = true; return nullptr; }
+    const int poison = g_poison.load(std::memory_order_relaxed);
+    if (poison >= 0 && !check_hip(hipMemsetAsync(d, poison, tensor_bytes(t), stream()), "poison fill")) {
+        pool_free(d);
+        failed_ = true;
+        return nullptr;
+    }
     bufs_.push_back({d, t->data, bytes_written, true});
     staged_ = true;
     return d;
@@ -533,14 +649,23 @@ Tensor* create_tensor(int* shape, int ndim, DataType dtype) {
     return t;
 }
 
+// Refused while the library stream is being captured into a graph: the pool
+// buffer would go back to the pool at free_tensor while the graph still holds
+// it, and the fill would record a memset node.
 static Tensor* device_tensor(int* shape, int ndim, DataType dtype, bool zero) {
     if (!ensure_device()) return nullptr;
+    if (stream_capturing(stream())) {
+        set_error("%s: device tensors cannot be created while the library stream is being captured into a graph "
+                  "(create them before the capture)", zero ? "create_tensor_device" : "create_tensor_device_empty");
+        return nullptr;
+    }
     Tensor* t = new_header(shape, ndim, dtype);
     if (!t) return nullptr;
     const size_t bytes = t->size * dt_bytes((int)dtype);
     void* p = pool_alloc(bytes ? bytes : 1);
     if (!p) { free(t->shape); free(t); return nullptr; }
-    if (zero && !check_hip(hipMemsetAsync(p, 0, bytes ? bytes : 1, stream()), "zero fill")) {
+    const int fill = zero ? 0 : g_poison.load(std::memory_order_relaxed);
+    if (fill >= 0 && !check_hip(hipMemsetAsync(p, fill, bytes ? bytes : 1, stream()), "fill")) {
         pool_free(p);
         free(t->shape);
         free(t);
@@ -588,11 +713,20 @@ void free_tensor(Tensor* t) {
 
 int tensor_is_device(const Tensor* t) { return (t && t->data && is_dev(classify(t->data))) ? 1 : 0; }
 
+// A copy that synchronises, refused under graph capture (a synchronisation
+// there would invalidate the capture).
+static bool sync_copy_under_capture(const char* name) {
+    if (!stream_capturing(stream())) return false;
+    set_error("%s: synchronous copy while the library stream is being captured into a graph", name);
+    return true;
+}
+
 int tensor_to_host(const Tensor* t, void* host_dst) {
     if (!tensor_sane(t, "tensor_to_host") || !host_dst) return -1;
     const size_t b = tensor_bytes(t);
     if (!b) return 0;
     if (is_dev(classify(t->data))) {
+        if (sync_copy_under_capture("tensor_to_host")) return -1;
         if (!check_hip(hipMemcpyAsync(host_dst, t->data, b, hipMemcpyDeviceToHost, stream()), "D2H copy") ||
             !check_hip(hipStreamSynchronize(stream()), "stream synchronize"))
             return -1;
@@ -607,6 +741,7 @@ int tensor_from_host(Tensor* t, const void* host_src) {
     const size_t b = tensor_bytes(t);
     if (!b) return 0;
     if (is_dev(classify(t->data))) {
+        if (sync_copy_under_capture("tensor_from_host")) return -1;
         if (!check_hip(hipMemcpyAsync(t->data, host_src, b, hipMemcpyHostToDevice, stream()), "H2D copy") ||
             !check_hip(hipStreamSynchronize(stream()), "stream synchronize"))
             return -1;
@@ -630,6 +765,7 @@ static void copy_tensor(const Tensor* in, Tensor* out, const char* name) {
     const bool di = is_dev(classify(in->data)), dout = is_dev(classify(out->data));
     if (!di && !dout) { memcpy(out->data, in->data, b); return; }
     if (!ensure_device()) return;
+    if (!(di && dout) && sync_copy_under_capture(name)) return;
     if (!check_hip(hipMemcpyAsync(out->data, in->data, b, hipMemcpyDefault, stream()), name)) return;
     if (!(di && dout)) (void)check_hip(hipStreamSynchronize(stream()), "stream synchronize");
 }
@@ -642,6 +778,42 @@ int tensor_ops_hip_sync(void) {
     return check_hip(hipStreamSynchronize(stream()), "stream synchronize") ? 0 : -1;
 }
 
+// Buffers cached under stream `from` (pool and exchange lists) now serve `to`.
+// The caller has drained `from`, so no work of it still uses them.
+static void move_cached(hipStream_t from, hipStream_t to) {
+    if (from == to) return;
+    State& st = S();
+    std::lock_guard<std::mutex> g(st.mu);
+    for (auto* lists : {&st.dev_free, &st.xchg_free}) {
+        auto it = lists->find(from);
+        if (it == lists->end()) continue;
+        auto& dst = (*lists)[to];
+        for (auto& kv : it->second) dst.emplace(kv.first, kv.second);
+        lists->erase(it);
+    }
+}
+
+// Buffers cached under stream `from`, which the calling thread leaves without
+// draining it: they wait behind an event recorded on `from` now, and any
+// stream may take them once that event has completed (reclaim_parked).
+static void park_cached(hipStream_t from) {
+    State& st = S();
+    std::lock_guard<std::mutex> g(st.mu);
+    auto d = st.dev_free.find(from);
+    auto x = st.xchg_free.find(from);
+    if (d == st.dev_free.end() && x == st.xchg_free.end()) return;
+    State::Parked pk{nullptr, {}, {}};
+    if (hipEventCreateWithFlags(&pk.ev, hipEventDisableTiming) != hipSuccess ||
+        hipEventRecord(pk.ev, from) != hipSuccess) {
+        (void)hipGetLastError();
+        if (pk.ev) (void)hipEventDestroy(pk.ev);
+        return;                       // left under `from` (used again if the thread comes back to it)
+    }
+    if (d != st.dev_free.end()) { pk.dev.swap(d->second); st.dev_free.erase(d); }
+    if (x != st.xchg_free.end()) { pk.xchg.swap(x->second); st.xchg_free.erase(x); }
+    st.parked.push_back(std::move(pk));
+}
+
 void tensor_ops_hip_set_stream(void* s) {
     if (!ensure_device()) return;
     State& st = S();
@@ -649,18 +821,17 @@ void tensor_ops_hip_set_stream(void* s) {
     const hipStream_t old_s = st.user.load() ? st.user.load() : st.own;
     (void)hipStreamSynchronize(old_s);
     st.user.store((hipStream_t)s);
-    const hipStream_t new_s = s ? (hipStream_t)s : st.own;
-    std::lock_guard<std::mutex> g(st.mu);
-    auto it = st.dev_free.find(old_s);
-    if (it != st.dev_free.end() && old_s != new_s) {
-        auto& dst = st.dev_free[new_s];
-        for (auto& kv : it->second) dst.emplace(kv.first, kv.second);
-        st.dev_free.erase(old_s);
-    }
+    move_cached(old_s, s ? (hipStream_t)s : st.own);
 }
 
+// A thread leaving its own stream (cleared or replaced) parks the buffers
+// cached under it behind an event on that stream, so nothing stays keyed by a
+// handle that the caller may destroy (and the runtime may give to a new stream
+// while the old one's work still uses them); nothing is drained.
 void tensor_ops_hip_set_thread_stream(void* s) {
     if (!ensure_device()) return;
+    const hipStream_t old_s = t_stream;
+    if (old_s && old_s != (hipStream_t)s && !stream_capturing(old_s)) park_cached(old_s);
     t_stream = (hipStream_t)s;
 }
 
@@ -681,6 +852,17 @@ int tensor_ops_hip_set_softmax_spin(int polls) {
 }
 
 int tensor_ops_hip_get_exact(void) { return exact_mode() ? 1 : 0; }
+
+int tensor_ops_hip_set_poison(int byte) {
+    return tohip::g_poison.exchange(byte < 0 ? -1 : (byte & 0xFF));
+}
+
+unsigned long long tensor_ops_hip_advance_exchange_count(unsigned long long count) {
+    uint64_t cur = tohip::g_xchg_count.load();
+    while (cur < count && !tohip::g_xchg_count.compare_exchange_weak(cur, count)) {
+    }
+    return tohip::g_xchg_count.load();
+}
 
 // tensor_ops.c:763-807 — builds the table once and uploads it when a GPU is present.
 void init_cos_lut(void) {

@@ -6,7 +6,8 @@ import this module.  It drives any library that exports the reference C ABI
 
 * ``oracle/liboracle.so``       — the restatement in ``tensor_ops_oracle.c``;
 * ``oracle/_ref/tensor_ops.so`` — the reference ``tensor_ops.c`` compiled from
-  its own source by ``oracle/Makefile`` (present only where it was built).
+  its own source by ``oracle/Makefile`` (present only where it was built), or
+  the build that ``TENSOR_OPS_REF_SO`` names.
 
 Arrays are passed in their storage form: float16 / bfloat16 as uint16 bits,
 fp8 as uint8 codes, int4 as int8.  Callers pre-broadcast binary / Q / DQ
@@ -260,5 +261,14 @@ def oracle() -> CpuLib:
 
 
 def reference():
-    """The compiled reference library, or None where it was never built."""
+    """The compiled reference library, or None where it was never built.
+
+    ``TENSOR_OPS_REF_SO`` names another build of the reference ``tensor_ops.c``
+    (the reference's own Python layer loads a hard-coded ``./tensor_ops.so``,
+    ``nn/__init__.py:150``); it must exist when set.  Unset: ``oracle/_ref``."""
+    path = os.environ.get("TENSOR_OPS_REF_SO")
+    if path:
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"TENSOR_OPS_REF_SO={path} does not exist")
+        return _get(os.path.abspath(path))
     return _get(REF_SO) if os.path.exists(REF_SO) else None

@@ -13,7 +13,7 @@
  * steps of an encoder must match, they produce the same bits by a formulation
  * of our own (checked by exhaustive sweeps against the compiled reference).
  *
- * Pinning (see tests/test_oracle_*.py):
+ * Pinning (see tests/test_oracle.py):
  *   codecs       exhaustive 2^32 / 2^16 / 2^8 sweeps vs oracle/_ref and golden digests
  *   elementwise  golden vectors from oracle/_ref + closed forms (IEEE fp32 ops)
  *   cos          golden vectors from oracle/_ref (bit-exact LUT replica)

@@ -13,6 +13,7 @@ Comparison rules (the parity bar):
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import json
 import os
@@ -195,6 +196,20 @@ class HipLib(O.CpuLib):
 
     def device_count(self):
         return int(self.lib.tensor_ops_hip_device_count())
+
+    @contextlib.contextmanager
+    def poisoned(self, byte=0xFF):
+        """Every device buffer the library hands out with undefined contents
+        (device outputs from create_tensor_device_empty, staged host outputs) is
+        filled with `byte` first (0xFF: NaN in every float format), so an
+        element an operator fails to write shows up."""
+        fn = self.lib.tensor_ops_hip_set_poison
+        fn.argtypes, fn.restype = [ctypes.c_int], ctypes.c_int
+        prev = fn(int(byte))
+        try:
+            yield
+        finally:
+            fn(prev)
 
     def last_error(self):
         e = self.lib.tensor_ops_hip_last_error()

@@ -171,7 +171,12 @@ def test_config2_per_axis_entry_point(hip, oracle_lib, x2):
 
 
 @pytest.mark.parametrize("dt", ["float32", "float16"])
-def test_config3_gemm_4096(hip, dt):
+def test_config3_gemm_4096(hip, oracle_lib, dt):
+    """Config-3 Gemm at full size.  Every element of the MFMA result (output
+    poisoned with NaN first, so an unwritten tile fails) is compared with the
+    exact-mode result of the same call (fp64 accumulation in the reference's
+    order); the exact mode is anchored bit for bit to the oracle on 16 rows,
+    and the MFMA result to a float64 product on 48 rows."""
     rng = np.random.default_rng(2)
     K = 4096
     a = rng.normal(0, 1 / np.sqrt(K), (4096, K)).astype(np.float32)
@@ -179,7 +184,14 @@ def test_config3_gemm_4096(hip, dt):
     c = rng.normal(0, 1 / 64, (4096,)).astype(np.float32)
     if dt == "float16":
         a, b = a.astype(np.float16), b.astype(np.float16)
-    y = hip.gemm(a, dt, b, dt, c, "float32", dt, 1.0, 1.0, 0, 1)
+    with hip.poisoned():
+        y = hip.gemm(a, dt, b, dt, c, "float32", dt, 1.0, 1.0, 0, 1)
+        hip.set_exact(True)
+        try:
+            ye = hip.gemm(a, dt, b, dt, c, "float32", dt, 1.0, 1.0, 0, 1)
+        finally:
+            hip.set_exact(False)
+    assert_close(y, ye, dt, what=f"gemm {dt} 4096: every element, MFMA vs exact mode")
     rows = rng.choice(4096, 48, replace=False)
     ref = a[rows].astype(np.float64) @ b.astype(np.float64).T + c.astype(np.float64)
     if dt == "float16":
@@ -187,6 +199,9 @@ def test_config3_gemm_4096(hip, dt):
         assert_close(y[rows], ref_codes, O.F16, what="gemm f16 4096")
     else:
         assert_close(y[rows], ref.astype(np.float32), O.F32, what="gemm f32 4096")
+    few = rows[:16]
+    want = oracle_lib.gemm(a[few], dt, b, dt, c, "float32", dt, 1.0, 1.0, 0, 1)
+    assert_bitexact(ye[few], want, dt, what=f"gemm {dt} 4096 exact mode vs oracle")
 
 
 def test_config3_woq(hip, oracle_lib):
@@ -212,21 +227,28 @@ CONVS = [("stem", (32, 3, 224, 224), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2]),
 
 @pytest.mark.parametrize("layer", CONVS, ids=[c[0] for c in CONVS])
 def test_config4_conv_full_size(hip, oracle_lib, layer):
+    """Config-4 convolution at full size.  Every element of the MFMA result
+    (output poisoned with NaN first) is compared with the exact-mode result of
+    the same call over the whole batch; the exact mode is anchored bit for bit
+    to the oracle on the first and last images, as is the MFMA mode within
+    tolerance."""
     tag, xs, ws, pads, strides = layer
     rng = np.random.default_rng(3)
     x = rng.normal(0, 1, xs).astype(np.float32)
     w = rng.normal(0, np.sqrt(2 / (ws[1] * ws[2] * ws[3])), ws).astype(np.float32)
     b = rng.normal(0, 1 / 64, (ws[0],)).astype(np.float32)
-    y = hip.conv(x, O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], 1)
+    with hip.poisoned():
+        y = hip.conv(x, O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], 1)
+        hip.set_exact(True)
+        try:
+            ye = hip.conv(x, O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], 1)
+        finally:
+            hip.set_exact(False)
+    assert_close(y, ye, O.F32, what=f"conv {tag}: every element, MFMA vs exact mode")
     imgs = [0, xs[0] - 1]
     ref = oracle_lib.conv(x[imgs], O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], 1)
     assert_close(y[imgs], ref, O.F32, what=f"conv {tag}")
-    hip.set_exact(True)
-    try:
-        ye = hip.conv(x[imgs], O.F32, w, O.F32, b, O.F32, O.F32, pads, strides, [1, 1], 1)
-    finally:
-        hip.set_exact(False)
-    assert_bitexact(ye, ref, O.F32, what=f"conv {tag} exact")
+    assert_bitexact(ye[imgs], ref, O.F32, what=f"conv {tag} exact")
 
 
 def test_config4_maxpool_full_size(hip, oracle_lib):

@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.helpers import assert_bitexact
+from tests.helpers import assert_bitexact, assert_close
 
 pytestmark = pytest.mark.gpu
 
@@ -216,6 +216,170 @@ def test_dynamic_quantize_linear_under_capture(hip):
         ry, rs, rz = O.oracle().dql(inputs[3], O.F32)
         assert_bitexact(ye.cpu().numpy(), ry, O.U8, what="eager dql vs oracle")
         assert_bitexact(sce.cpu().numpy(), rs, O.F32, what="eager dql scale vs oracle")
+    finally:
+        for p in keep:
+            L.free_tensor(p)
+        L.tensor_ops_hip_set_stream(None)
+
+
+def _wrapper(L, keep):
+    def wrap(t, shape, dt):
+        arr = (ctypes.c_int * len(shape))(*shape)
+        p = L.tensor_wrap_device(ctypes.c_void_p(t.data_ptr()), arr, len(shape), dt)
+        assert p
+        keep.append(p)
+        return p
+    return wrap
+
+
+def test_allocation_and_host_work_refused_under_capture(hip):
+    """Under capture, calls that would allocate or synchronise (device tensor
+    creation, host operands, tensor_to_host) return an error instead, the
+    device-only call captured beside them replays correctly, and the library
+    works as before once the capture has ended."""
+    import torch
+    torch.cuda.init()
+    side = torch.cuda.Stream()
+    L = hip.lib
+    L.tensor_ops_hip_set_stream(ctypes.c_void_p(side.cuda_stream))
+    L.create_tensor_device_empty.restype = O.PT
+    L.create_tensor_device_empty.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int]
+    keep = []
+    wrap = _wrapper(L, keep)
+    rng = np.random.default_rng(51)
+    xs = rng.normal(0, 1, (4, 1000)).astype(np.float32)
+    relu = np.where(xs > 0, xs, np.float32(0)).astype(np.float32)     # tensor_ops.c:708-728
+    hx, hy = hip.tensor(xs, O.F32), hip.empty(xs.shape, O.F32)
+    dt = hip.dev_from(xs, O.F32)
+    host = np.empty(xs.shape, np.float32)
+    try:
+        with torch.cuda.stream(side):
+            x = torch.from_numpy(xs).cuda()
+            y = torch.empty_like(x)
+            tx, ty = wrap(x, [4, 1000], O.F32), wrap(y, [4, 1000], O.F32)
+            torch.cuda.synchronize()
+            shape = (ctypes.c_int * 2)(4, 1000)
+            errors = {}
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                L.relu_forward(tx, ty)                          # device only: captured
+                L.tensor_ops_hip_clear_error()
+                errors["create_tensor_device"] = (L.create_tensor_device(shape, 2, O.F32), hip.last_error())
+                L.tensor_ops_hip_clear_error()
+                errors["create_tensor_device_empty"] = (L.create_tensor_device_empty(shape, 2, O.F32),
+                                                        hip.last_error())
+                L.tensor_ops_hip_clear_error()
+                L.relu_forward(hx, hy)
+                errors["host operands"] = (None, hip.last_error())
+                L.tensor_ops_hip_clear_error()
+                errors["tensor_to_host"] = (L.tensor_to_host(dt, host.ctypes.data), hip.last_error())
+                L.tensor_ops_hip_clear_error()
+            for what, (ret, err) in errors.items():
+                print(f"capture refusal: {what}: {err}", flush=True)
+                assert not ret or ret == -1, f"{what} returned {ret} under capture"
+                assert "captur" in err, f"{what}: no capture error ({err!r})"
+            y.fill_(-1)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert_bitexact(y.cpu().numpy(), relu, O.F32, what="captured relu")
+        # after the capture: the refused calls work again
+        L.tensor_ops_hip_clear_error()
+        t = L.create_tensor_device(shape, 2, O.F32)
+        assert t, hip.last_error()
+        L.free_tensor(t)
+        L.relu_forward(hx, hy)
+        assert not hip.last_error(), hip.last_error()
+        assert_bitexact(hip.read(hy, O.F32), relu, O.F32, what="host relu after capture")
+        assert L.tensor_to_host(dt, host.ctypes.data) == 0
+        assert_bitexact(host, xs, O.F32, what="tensor_to_host after capture")
+    finally:
+        for p in keep + [hx, hy, dt]:
+            L.free_tensor(p)
+        L.tensor_ops_hip_set_stream(None)
+
+
+def test_capture_first_on_fresh_stream(hip, oracle_lib):
+    """Calls captured on a stream the library has never used, with no eager call
+    before them: Softmax over few long rows and DynamicQuantizeLinear (partials
+    in the fixed capture workspaces), the no-allocation DynamicQuantizeLinear
+    and a Gemm whose eager plan splits k (captured unsplit).  Nothing may
+    allocate inside the capture; the graph is replayed on changed inputs and
+    every replay is compared with eager calls on the same inputs (bit for bit;
+    the Gemm against the oracle within tolerance, its eager plan differing)."""
+    import torch
+    torch.cuda.init()
+    side = torch.cuda.Stream()
+    L = hip.lib
+    L.dynamic_quantize_linear_forward_noalloc.argtypes = [O.PT, O.PT, O.PT, O.PT]
+    L.tensor_ops_hip_set_stream(ctypes.c_void_p(side.cuda_stream))
+    keep = []
+    wrap = _wrapper(L, keep)
+    rng = np.random.default_rng(53)
+    try:
+        with torch.cuda.stream(side):
+            sm_x = torch.empty((64, 32000), dtype=torch.float32, device="cuda")
+            dq_x = torch.empty((8, 512, 1024), dtype=torch.float32, device="cuda")
+            ga = torch.empty((64, 512), dtype=torch.float32, device="cuda")
+            gb = torch.from_numpy(rng.normal(0, 0.05, (1000, 512)).astype(np.float32)).cuda()
+            gc = torch.from_numpy(rng.normal(0, 1, (1, 1000)).astype(np.float32)).cuda()
+            outs = {"softmax": torch.empty_like(sm_x), "gemm": torch.empty((64, 1000), dtype=torch.float32, device="cuda")}
+            for k in ("dql", "dql_noalloc"):
+                outs[k] = torch.empty((8, 512, 1024), dtype=torch.uint8, device="cuda")
+                outs[k + "_scale"] = torch.empty([1], dtype=torch.float32, device="cuda")
+                outs[k + "_zp"] = torch.empty([1], dtype=torch.uint8, device="cuda")
+            t = {"sm_x": wrap(sm_x, [64, 32000], O.F32), "dq_x": wrap(dq_x, [8, 512, 1024], O.F32),
+                 "ga": wrap(ga, [64, 512], O.F32), "gb": wrap(gb, [1000, 512], O.F32), "gc": wrap(gc, [1, 1000], O.F32)}
+            dts = {"softmax": O.F32, "gemm": O.F32, "dql": O.U8, "dql_noalloc": O.U8}
+            for k, v in outs.items():
+                dt = dts.get(k, O.F32 if k.endswith("scale") else O.U8)
+                t[k] = wrap(v, list(v.shape), dt)
+
+            def calls(o):
+                L.softmax_forward(t["sm_x"], o["softmax"], 1)
+                L.dynamic_quantize_linear_forward(t["dq_x"], o["dql"], o["dql_scale"], o["dql_zp"])
+                L.dynamic_quantize_linear_forward_noalloc(t["dq_x"], o["dql_noalloc"], o["dql_noalloc_scale"],
+                                                          o["dql_noalloc_zp"])
+                L.gemm_forward(t["ga"], t["gb"], t["gc"], o["gemm"], 1.0, 1.0, 0, 1)
+
+            hip.lib.tensor_ops_hip_clear_error()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                calls({k: t[k] for k in outs})
+            assert not hip.last_error(), hip.last_error()
+        # eager results on the library's own stream, into separate outputs
+        L.tensor_ops_hip_set_stream(None)
+        eo = {k: torch.empty_like(v) for k, v in outs.items()}
+        et = {k: wrap(v, list(v.shape), dts.get(k, O.F32 if k.endswith("scale") else O.U8)) for k, v in eo.items()}
+        for r in range(3):
+            sm_np = rng.normal(0, 3 + r, (64, 32000)).astype(np.float32)
+            dq_np = rng.normal(0, 0.5 + r, (8, 512, 1024)).astype(np.float32)
+            ga_np = rng.normal(0, 1, (64, 512)).astype(np.float32)
+            sm_x.copy_(torch.from_numpy(sm_np))
+            dq_x.copy_(torch.from_numpy(dq_np))
+            ga.copy_(torch.from_numpy(ga_np))
+            for v in outs.values():
+                v.view(torch.uint8).fill_(0xA5)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            L.tensor_ops_hip_clear_error()
+            calls({k: et[k] for k in outs})
+            torch.cuda.synchronize()
+            assert not hip.last_error(), hip.last_error()
+            print(f"capture-first replay {r}", flush=True)
+            for k, v in outs.items():
+                if k == "gemm":
+                    continue
+                dt = dts.get(k, O.F32 if k.endswith("scale") else O.U8)
+                assert_bitexact(v.cpu().numpy(), eo[k].cpu().numpy(), dt, what=f"replay {r} {k}")
+            want = oracle_lib.gemm(ga_np, O.F32, gb.cpu().numpy(), O.F32, gc.cpu().numpy(), O.F32, O.F32,
+                                   1.0, 1.0, 0, 1)
+            assert_close(outs["gemm"].cpu().numpy(), want, O.F32, what=f"replay {r} gemm (unsplit) vs oracle")
+            assert_close(eo["gemm"].cpu().numpy(), want, O.F32, what=f"eager {r} gemm (split) vs oracle")
+        ry, rs, rz = oracle_lib.dql(dq_np, O.F32)
+        assert_bitexact(outs["dql"].cpu().numpy(), ry, O.U8, what="captured dql vs oracle")
+        assert_bitexact(outs["dql_noalloc_scale"].cpu().numpy(), rs, O.F32, what="captured noalloc scale vs oracle")
     finally:
         for p in keep:
             L.free_tensor(p)

@@ -416,38 +416,51 @@ def test_resnet_qdq_graph(hip, oracle_lib, exact):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("exact", [True, False], ids=["exact", "mfma"])
-def test_resnet_qdq_graph_batch64(hip, oracle_lib, exact):
+def test_resnet_qdq_graph_batch64(hip, oracle_lib):
     """Config-5 graph at its stated size (batch 64, the forward bench.py times),
-    images 0 and 63 against the graph oracle.  Static QDQ scales make images
-    independent, so the oracle runs the two images as a batch of 2 of the same
-    model (same seeded weights).  Exact mode: logits bit for bit, probabilities in
-    the Softmax tolerance class.  MFMA mode: fp32 accumulation flips a few uint8
-    activation codes at rounding ties; bounds below (measured error x ~7)."""
+    run in exact mode and in MFMA mode with every intermediate and output buffer
+    poisoned with NaN before its operator writes it (an unwritten element
+    propagates to the logits).  Exact mode: images 0 and 63 against the graph
+    oracle, logits bit for bit, probabilities in the Softmax tolerance class
+    (static QDQ scales make images independent, so the oracle runs the two
+    images as a batch of 2 of the same model, same seeded weights).  MFMA mode:
+    all 64 images against the exact-mode run; fp32 accumulation flips a few
+    uint8 activation codes at rounding ties, hence the bounds below (measured
+    error x ~7)."""
     from onnx_translator_amd.nn.graph import Graph
     from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
     m = resnet_qdq_model(batch=64)
     x = np.random.default_rng(4).normal(0, 1, (64, 3, 224, 224)).astype(np.float32)
     g = Graph(ONNXImport(m), ["input"], ["logits", "output"], initializers=initializers(m)).to_device().fuse()
-    hip.set_exact(exact)
-    try:
-        logits_t, probs_t = g.forward(x)
-        logits, probs = logits_t.numpy(), probs_t.numpy()
-    finally:
-        hip.set_exact(False)
-    assert logits.shape == (64, 1000) and probs.shape == (64, 1000)
-    np.testing.assert_allclose(probs.sum(axis=1), 1.0, rtol=1e-5)
+    out = {}
+    with hip.poisoned():
+        for exact in (True, False):
+            hip.set_exact(exact)
+            try:
+                logits_t, probs_t = g.forward(x)
+                out[exact] = (logits_t.numpy(), probs_t.numpy())
+            finally:
+                hip.set_exact(False)
+    for exact, (logits, probs) in out.items():
+        assert logits.shape == (64, 1000) and probs.shape == (64, 1000)
+        assert np.isfinite(logits).all() and np.isfinite(probs).all(), f"exact={exact}: unwritten (NaN) elements"
+        np.testing.assert_allclose(probs.sum(axis=1), 1.0, rtol=1e-5)
     sel = [0, 63]
     env = run_model(oracle_lib, resnet_qdq_model(batch=2), {"input": (np.ascontiguousarray(x[sel]), "float32")})
     ref_logits, ref_probs = env["logits"][0], env["output"][0]
-    if exact:
-        assert_bitexact(logits[sel], ref_logits, O.F32, what="batch-64 logits, exact mode")
-        assert_close(probs[sel], ref_probs, O.F32, what="batch-64 probabilities, exact mode")
-    else:
-        dl = np.abs(logits[sel].astype(np.float64) - ref_logits).max() / np.abs(ref_logits).max()
-        dp = np.abs(probs[sel].astype(np.float64) - ref_probs).max() / ref_probs.max()
-        assert dl < LOGIT_BOUND and dp < PROB_BOUND, (dl, dp)
-        assert (probs[sel].argmax(axis=1) == ref_probs.argmax(axis=1)).all()
+    el, ep = out[True]
+    assert_bitexact(el[sel], ref_logits, O.F32, what="batch-64 logits, exact mode")
+    assert_close(ep[sel], ref_probs, O.F32, what="batch-64 probabilities, exact mode")
+    ml, mp = out[False]
+    dl = np.abs(ml.astype(np.float64) - el).max() / np.abs(el).max()
+    dp = np.abs(mp.astype(np.float64) - ep).max() / ep.max()
+    print(f"batch-64 MFMA vs exact over all images: logits {dl:.2e}, probabilities {dp:.2e}", flush=True)
+    assert dl < LOGIT_BOUND and dp < PROB_BOUND, (dl, dp)
+    # a class may change only where the exact logits of the two classes are within the bound
+    am, ae = ml.argmax(axis=1), el.argmax(axis=1)
+    rows = np.nonzero(am != ae)[0]
+    gap = np.abs(el[rows, am[rows]].astype(np.float64) - el[rows, ae[rows]]) / np.abs(el).max()
+    assert (gap < 2 * LOGIT_BOUND).all(), list(zip(rows.tolist(), gap.tolist()))
 
 
 # MFMA-mode bounds of the batch-64 check, relative to the largest reference

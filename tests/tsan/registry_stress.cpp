@@ -9,6 +9,13 @@
 
 #include "../../include/tensor_ops.h"
 
+// runtime.hip's device initialisation calls the workspace hooks of the kernel
+// files, which this CPU-only build does not link; no device is initialised here.
+namespace tohip {
+void init_qdq_workspace() {}
+void init_reduce_workspace() {}
+}  // namespace tohip
+
 static float shared_buf[64];
 
 int main() {
