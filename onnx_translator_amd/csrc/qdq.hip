@@ -112,6 +112,9 @@ struct Params {
 
 // Per-axis parameters (MODE 1 and 3): element e uses Scale[(e / inner) % C]
 // and ZeroPoint[zs * ((e / inner) % C)], zs = 0 for a single zero point.
+// MODE 3 reads them through buffer resources of this extent (the indices stay
+// inside the tensors; the extent only has to cover them).
+constexpr uint32_t kParamReach = 0x7FFFFFF0u;
 struct AxisDesc {
     FastDiv inner, c;
     uint32_t zs;
@@ -120,21 +123,30 @@ struct AxisDesc {
 template <int ZDT, int MODE, int ND>
 __device__ __forceinline__ void load_params(Params<ZDT, MODE>& p, const float* S, const void* Z, const BDesc& d,
                                             const AxisDesc& ax, uint32_t v) {
-    if constexpr (MODE == 1 || MODE == 3) {
+    if constexpr (MODE == 3) {
+        // v is the wave's first unit (uniform), so the index math runs on the
+        // scalar unit.  The two loads are vector loads through buffer resources
+        // (every lane reads the same word): they complete in order with the
+        // tile's X loads, so the wait for the tile's data covers them, where
+        // scalar loads, which may complete out of order, made the tile wait for
+        // every scalar load in flight.  A 1-byte zero point is read as the
+        // aligned 32-bit word that holds it (the host selects this mode only
+        // when ZeroPoint's byte size and address are multiples of 4, so that
+        // word lies inside the tensor).
+        const uint32_t q = ax.inner.div(v * 4u);
+        const uint32_t ch = q - ax.c.div(q) * ax.c.d;
+        const uint32_t zi = ch * ax.zs;
+        p.s[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(S, kParamReach), ch * 4u, 0, 0));
+        const uint32_t zw = __builtin_amdgcn_raw_buffer_load_b32(
+            buffer_rsrc(Z, kParamReach), ZDT == kF32 ? zi * 4u : (zi >> 2) * 4u, 0, 0);
+        if constexpr (ZDT == kF32) p.z[0] = __builtin_bit_cast(float, zw);
+        else p.z[0] = (uint8_t)(zw >> (8 * (zi & 3)));
+    } else if constexpr (MODE == 1) {
         const uint32_t q = ax.inner.div(v * 4u);
         const uint32_t ch = q - ax.c.div(q) * ax.c.d;
         const uint32_t zi = ch * ax.zs;
         p.s[0] = S[ch];
-        if constexpr (MODE == 3 && ZDT != kF32) {
-            // v is the wave's first unit (uniform), so both loads are scalar.  A
-            // 1-byte zero point is read as the aligned 32-bit word that holds it
-            // (the host selects this mode only when ZeroPoint's byte size and
-            // address are multiples of 4, so that word lies inside the tensor).
-            const uint32_t w = reinterpret_cast<const uint32_t*>(Z)[zi >> 2];
-            p.z[0] = (uint8_t)(w >> (8 * (zi & 3)));
-        } else {
-            p.z[0] = reinterpret_cast<const zraw_t<ZDT>*>(Z)[zi];
-        }
+        p.z[0] = reinterpret_cast<const zraw_t<ZDT>*>(Z)[zi];
     } else if constexpr (MODE == 2) {
         int64_t off[3];
         bd_offsets32<3, ND>(d, v * 4u, off);
@@ -150,7 +162,11 @@ __device__ __forceinline__ void load_params(Params<ZDT, MODE>& p, const float* S
 }
 
 constexpr int kQU = 4;         // quantize: float4 units per thread and iteration
-constexpr int kQBlocksPerCU = 8;
+// Quantize grid: blocks per CU.  8 (two tiles per block at config 2, loads of
+// the second issued before the first is converted); per-axis MODE 3 takes 16
+// (one tile per block), which measured 15.0 -> 14.5 us at config 2 where the
+// per-tensor kernels measured slower with 16 (fp8: 14.8 -> 15.1 us).
+constexpr int kQBlocksPerCU = 8, kQBlocksPerCUAxis = 16;
 constexpr uint32_t kMaxUnitsPerLaunch = 1u << 27;   // 2 GiB of f32 per launch: buffer offsets stay below 2^32
 
 // Codes of the 4 elements of one float4 of X.
@@ -486,7 +502,7 @@ void qdq_entry(const char* name, const Tensor* X, const Tensor* S, const Tensor*
                 const uint32_t nv = nv_all - vbase < kMaxUnitsPerLaunch ? nv_all - vbase : kMaxUnitsPerLaunch;
                 const dim3 b(kBlock);
                 if (QUANT) {
-                    const dim3 g(grid_for(nv, kBlock * kQU, kQBlocksPerCU * num_cus()));
+                    const dim3 g(grid_for(nv, kBlock * kQU, (mode == 3 ? kQBlocksPerCUAxis : kQBlocksPerCU) * num_cus()));
                     const float* xc = (const float*)x + (size_t)vbase * 4;
                     uint8_t* yc = (uint8_t*)y + (size_t)vbase * 4;
 #define QK(M, NDV) \
