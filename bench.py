@@ -293,7 +293,8 @@ def bench_loop(torch, fn, iters, warm=3, warm_ms=100.0, graph=False):
 
 
 SUITE = ("add_f32_bcast", "mul_f32_bcast", "sub_f32_bcast", "div_f32_bcast", "relu_f32", "abs_f32", "cos_f32",
-         "chain7_f32_fused", "add_i32_f32_to_f64", "gemm_f32_4096", "gemm_f16_4096", "gemm_woq_int8_fused",
+         "chain7_f32_fused", "add_i32_f32_to_f64", "gemm_f32_4096", "gemm_f16_4096", "gemm_f16_4096_vendor",
+         "gemm_woq_int8_fused",
          "gemm_woq_int8_unfused", "conv_stem7x7s2", "conv_3x3", "conv_1x1", "maxpool_3x3s2", "softmax_64x32000",
          "global_avg_pool", "dynamic_quantize_linear", "graph_resnet_qdq_b64")
 
@@ -368,7 +369,7 @@ def run_suite(lib, torch, only=None, cpu=None):
     rng = np.random.default_rng(2)
     K = 4096
     flops = 2 * 4096 ** 3
-    if want("gemm_f32_4096", "gemm_f16_4096", "gemm_woq_int8_fused", "gemm_woq_int8_unfused"):
+    if want("gemm_f32_4096", "gemm_f16_4096", "gemm_f16_4096_vendor", "gemm_woq_int8_fused", "gemm_woq_int8_unfused"):
         a = rng.normal(0, 1 / 64, (4096, K)).astype(np.float32)
         b = rng.normal(0, 1 / 64, (4096, K)).astype(np.float32)
         c = rng.normal(0, 1 / 64, (4096,)).astype(np.float32)
@@ -386,6 +387,20 @@ def run_suite(lib, torch, only=None, cpu=None):
                  CpuLeg.gemm(aa, bb, c, dt))
             for t in (ta, tbb, ty):
                 L.free_tensor(t)
+        if want("gemm_f16_4096_vendor"):
+            # Context, not this library: the same f16 product through torch
+            # (F.linear -> the ROCm BLAS library, hipBLASLt on gfx950) on the same
+            # box, timed the same way; the bias is f16 there (torch requires it).
+            ah = torch.from_numpy(a.astype(np.float16)).cuda()
+            bh = torch.from_numpy(b.astype(np.float16)).cuda()
+            ch = torch.from_numpy(c.astype(np.float16)).cuda()
+            fl = torch.nn.functional.linear
+            ms = bench_loop(torch, lambda i: fl(ah, bh, ch), 20, 1)
+            line = op_line("gemm_f16_4096_vendor", "config3 4096^3 f16 through torch F.linear (vendor BLAS, "
+                           "for comparison only)", flops, ms, "mfma", MFMA_F16)
+            line["library"] = "torch " + torch.__version__ + " F.linear (ROCm BLAS)"
+            emit(line)
+            del ah, bh, ch
         lib.check("config3")
         # Config 3 weight-only-quant variant: B int8 [4096,4096] with per-row (axis 0)
         # scales, DequantizeLinear -> Gemm on A [256,4096]; fused (codes read in the
