@@ -11,6 +11,9 @@
 //     output encoder; integer outputs use the int64 path with saturation;
 //   * Cos replays the reference's 4097-entry table lookup in fp64 with
 //     contraction off, which reproduces its bits.
+#include <algorithm>
+#include <initializer_list>
+
 #include "runtime.h"
 
 namespace tohip {
@@ -143,6 +146,30 @@ __device__ __forceinline__ void cos_lds(float (&v)[W], const double* __restrict_
     }
 #pragma unroll
     for (int e = 0; e < W; e++) v[e] = (float)(t0[e] * (1.0 - w[e]) + t1[e] * w[e]);
+}
+
+// As load_table, for a block of any size (blockDim.x): groups of four 16-byte
+// loads per thread, each group's loads issued before its LDS stores (one
+// group at 512 threads and up).
+__device__ __forceinline__ void load_table_any(double* __restrict__ sT, const double* __restrict__ T) {
+    constexpr int kPairs = (kLutN - 1) / 2;
+    const double2* T2 = reinterpret_cast<const double2*>(T);
+    double2* S2 = reinterpret_cast<double2*>(sT);
+    const int bd = (int)blockDim.x;
+    for (int i0 = (int)threadIdx.x; i0 < kPairs; i0 += 4 * bd) {
+        double2 t0, t1, t2, t3;
+        const bool h1 = i0 + bd < kPairs, h2 = i0 + 2 * bd < kPairs, h3 = i0 + 3 * bd < kPairs;
+        t0 = T2[i0];
+        if (h1) t1 = T2[i0 + bd];
+        if (h2) t2 = T2[i0 + 2 * bd];
+        if (h3) t3 = T2[i0 + 3 * bd];
+        S2[i0] = t0;
+        if (h1) S2[i0 + bd] = t1;
+        if (h2) S2[i0 + 2 * bd] = t2;
+        if (h3) S2[i0 + 3 * bd] = t3;
+    }
+    if (threadIdx.x == 0) sT[kLutN - 1] = T[kLutN - 1];
+    __syncthreads();
 }
 
 // Copies the table into LDS (every thread of the block takes part): 16-byte
@@ -521,9 +548,12 @@ void unary_entry(const char* name, const Tensor* X, Tensor* Y) {
 // into two 64-bit words held in scalar registers, so the unrolled step loop
 // decodes it with shifts instead of indexing the kernel argument memory.
 constexpr int kChainMaxSteps = 16, kChainMaxOperands = kMaxOperands - 1;
-constexpr int kChainW = 8;          // elements per thread of the vectorised chain kernel
-constexpr int kChainLutBlock = 512; // threads per block of the chain kernel with a Cos step
-constexpr int kChainLutPerCU = 2;   // its blocks per CU (LDS: one 32 KB table each)
+// Chain launch shape: one block per CU when the program has a Cos step (each
+// block copies the 32 KB table into LDS once), two per CU otherwise; a
+// thread takes kChainU items of kChainW elements per chunk, and a block has as
+// many 64-thread waves (at most 16) as one chunk of its run needs.  At config
+// 1 (1,605,632 elements, 256 CUs): 784 items of 8 per block, 832 threads.
+constexpr int kChainW = 8, kChainU = 1, kChainMaxBlock = 1024;
 struct ChainProg {
     int n;
     uint64_t code[2];
@@ -599,112 +629,228 @@ __device__ __forceinline__ void operand_offsets(const BDesc& d, uint32_t i, uint
     for (int k = 0; k < NOP; k++) off[k] += i * (uint32_t)d.st[k + 1][0];
 }
 
-// The fused chain over Y->size elements, W consecutive elements per thread
-// (W = 4 or 8: X and Y 16-byte aligned, innermost dim a multiple of W; else 1).
-// X has Y's size and is read flat; operands go through the descriptor.  The
-// program is packed 8 bits per step (op | operand << 3 | reversed << 5) in
-// scalar registers; each step is one uniform dispatch (op, operand and order
-// select code paths, not per-element values).  LUT (the program has a Cos
-// step): blocks copy the cosine table into LDS first and the grid is capped
-// (see k_cos_f32), so the loop strides.
-template <int ND, int W, bool LUT, int BLOCK>
-__global__ __launch_bounds__(BLOCK) void k_chain_f32(const float* __restrict__ X, ChainOperands B,
-                                                     float* __restrict__ Y, BDesc d, ChainProg prog, uint32_t nitems,
-                                                     const double* __restrict__ Tg) {
-    constexpr int H = W >= 4 ? W / 4 : 1;      // float4 per thread
-    __shared__ __attribute__((aligned(16))) double sT[LUT ? kLutN : 2];
-    const uint32_t stride = gridDim.x * BLOCK;
-    uint32_t it = blockIdx.x * BLOCK + threadIdx.x;
-    // X of this thread's first item is requested before the table copy, so
-    // the two latencies overlap; later items load at the top of the loop
-    float4 xf[H];
+// One item of the fused chain: W consecutive elements of X and, per operand,
+// the W values they meet, loaded together so that every latency overlaps.
+template <int W> struct ChainItem {
+    float v[W];
+    float b[kChainMaxOperands][W];
+};
+
+// NOPI >= 0: exactly NOPI operands, each one value per item (kOpItem), known
+// at compile time; -1: B.n operands of the kinds in B.kind.
+template <int ND, int W, int NOPI = -1>
+__device__ __forceinline__ void chain_load(ChainItem<W>& c, const float* __restrict__ X, const ChainOperands& B,
+                                           const BDesc& d, uint32_t it, bool live) {
+    if (!live) it = 0;                          // a valid item: loaded, never stored
+    if constexpr (W >= 4) {
 #pragma unroll
-    for (int h = 0; h < H; h++) {
-        if constexpr (W >= 4) {
-            xf[h] = it < nitems ? ld_stream(reinterpret_cast<const float4*>(X) + H * it + h)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int h = 0; h < W / 4; h++) {
+            const float4 x = ld_stream(reinterpret_cast<const float4*>(X) + (W / 4) * it + h);
+            c.v[4 * h] = x.x; c.v[4 * h + 1] = x.y; c.v[4 * h + 2] = x.z; c.v[4 * h + 3] = x.w;
+        }
+    } else {
+        c.v[0] = X[it];
+    }
+    uint32_t off[kChainMaxOperands];
+    operand_offsets<kChainMaxOperands, ND>(d, it * W, off);
+#pragma unroll
+    for (int k = 0; k < kChainMaxOperands; k++) {
+        if (NOPI >= 0 ? k >= NOPI : k >= B.n) break;
+        const float* P = B.p[k];
+        if (W == 1 || NOPI >= 0 || B.kind[k] == kOpItem) {
+            const float t = P[off[k]];
+#pragma unroll
+            for (int e = 0; e < W; e++) c.b[k][e] = t;
+        } else if (B.kind[k] == kOpVec) {
+#pragma unroll
+            for (int h = 0; h < W / 4; h++) {
+                const float4 t = *reinterpret_cast<const float4*>(P + off[k] + 4 * h);
+                c.b[k][4 * h] = t.x; c.b[k][4 * h + 1] = t.y; c.b[k][4 * h + 2] = t.z; c.b[k][4 * h + 3] = t.w;
+            }
         } else {
-            xf[h].x = it < nitems ? X[it] : 0.f;
+            const uint32_t sb = (uint32_t)d.st[k + 1][d.nd - 1];
+#pragma unroll
+            for (int e = 0; e < W; e++) c.b[k][e] = P[off[k] + e * sb];
         }
     }
+}
+
+// The program's steps on the U items of a thread: each step is decoded once
+// (uniform dispatch: op, operand and order select code paths) and applied to
+// all U * W elements, so the decode is paid once per U * W elements.
+template <int W, int U, bool LUT>
+__device__ __forceinline__ void chain_apply(ChainItem<W> (&c)[U], const ChainOperands& B, const ChainProg& prog,
+                                            const double* __restrict__ T) {
+    for (int sidx = 0; sidx < prog.n; sidx++) {
+        const uint32_t code = (uint32_t)(prog.code[sidx >> 3] >> (8 * (sidx & 7))) & 0xFFu;
+        const int op = (int)(code & 7u), a = (int)((code >> 3) & 3u), rev = (int)((code >> 5) & 1u);
+        if (W > 1 && op == TENSOR_OPS_CHAIN_DIV && !rev && B.kind[a] == kOpItem) {
+            // v / b for one b per item: RN32((double)v * RN64(1 / b)).  The
+            // double product is within 2^-52 (relative) of v / b, and the
+            // quotient of two f32 values is never a rounding midpoint of f32
+            // nor within 2^-49 (relative) of one, so the product rounds to the
+            // same f32 as the correctly rounded division (zeros, infinities,
+            // NaN and subnormal results included).
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const double rb = 1.0 / (double)(a == 0 ? c[u].b[0][0] : (a == 1 ? c[u].b[1][0] : c[u].b[2][0]));
+#pragma unroll
+                for (int e = 0; e < W; e++) c[u].v[e] = (float)((double)c[u].v[e] * rb);
+            }
+        } else if (op <= TENSOR_OPS_CHAIN_DIV) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                if (a == 0) binary_step<W>(op, rev, c[u].v, c[u].b[0]);
+                else if (a == 1) binary_step<W>(op, rev, c[u].v, c[u].b[1]);
+                else binary_step<W>(op, rev, c[u].v, c[u].b[2]);
+            }
+        } else if (op == TENSOR_OPS_CHAIN_RELU) {
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int e = 0; e < W; e++) c[u].v[e] = unary_f32<U_RELU>(c[u].v[e], T);
+        } else if (op == TENSOR_OPS_CHAIN_ABS) {
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int e = 0; e < W; e++) c[u].v[e] = unary_f32<U_ABS>(c[u].v[e], T);
+        } else if constexpr (LUT) {
+#pragma unroll
+            for (int u = 0; u < U; u++) cos_lds<W>(c[u].v, T);
+        }
+    }
+}
+
+// Programs compiled in, so that their steps need no decoding at run time
+// (the per-step decode of chain_apply is uniform scalar work, about 40 scalar
+// instructions a step, which the CU's one scalar unit issues for every wave):
+// the packed step code (8 bits a step, as ChainProg) and the step count.
+// The config-1 chain: Add, Mul, Sub with operand 0, Div by operand 1, Relu,
+// Abs, Cos.
+constexpr uint64_t chain_code(std::initializer_list<TensorOpsChainStep> steps) {
+    uint64_t c = 0;
+    int i = 0;
+    for (const TensorOpsChainStep& st : steps) {
+        c |= ((uint64_t)st.op | ((uint64_t)st.operand << 3) | ((uint64_t)st.reversed << 5)) << (8 * i);
+        i++;
+    }
+    return c;
+}
+struct FixedProg {
+    uint64_t code;
+    int nsteps, noperands;
+};
+constexpr FixedProg kFixedProgs[] = {
+    {chain_code({{TENSOR_OPS_CHAIN_ADD, 0, 0}, {TENSOR_OPS_CHAIN_MUL, 0, 0}, {TENSOR_OPS_CHAIN_SUB, 0, 0},
+                 {TENSOR_OPS_CHAIN_DIV, 1, 0}, {TENSOR_OPS_CHAIN_RELU, 0, 0}, {TENSOR_OPS_CHAIN_ABS, 0, 0},
+                 {TENSOR_OPS_CHAIN_COS, 0, 0}}),
+     7, 2},
+};
+
+// Step S of fixed program FP (index + 1 into kFixedProgs) on the U items, then
+// the rest of the program; every operand is one value per item.  Same
+// arithmetic as chain_apply, step for step.
+template <int W, int U, bool LUT, int FP, int S = 0>
+__device__ __forceinline__ void chain_apply_fixed(ChainItem<W> (&c)[U], const double* __restrict__ T) {
+    constexpr FixedProg P = kFixedProgs[FP - 1];
+    if constexpr (S < P.nsteps) {
+        constexpr uint32_t code = (uint32_t)(P.code >> (8 * S)) & 0xFFu;
+        constexpr int op = (int)(code & 7u), a = (int)((code >> 3) & 3u), rev = (int)((code >> 5) & 1u);
+        if constexpr (op == TENSOR_OPS_CHAIN_DIV && !rev && W > 1) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const double rb = 1.0 / (double)c[u].b[a][0];
+#pragma unroll
+                for (int e = 0; e < W; e++) c[u].v[e] = (float)((double)c[u].v[e] * rb);
+            }
+        } else if constexpr (op <= TENSOR_OPS_CHAIN_DIV) {
+#pragma unroll
+            for (int u = 0; u < U; u++) binary_step<W>(op, rev, c[u].v, c[u].b[a]);
+        } else if constexpr (op == TENSOR_OPS_CHAIN_RELU) {
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int e = 0; e < W; e++) c[u].v[e] = unary_f32<U_RELU>(c[u].v[e], T);
+        } else if constexpr (op == TENSOR_OPS_CHAIN_ABS) {
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int e = 0; e < W; e++) c[u].v[e] = unary_f32<U_ABS>(c[u].v[e], T);
+        } else if constexpr (LUT) {
+#pragma unroll
+            for (int u = 0; u < U; u++) cos_lds<W>(c[u].v, T);
+        }
+        chain_apply_fixed<W, U, LUT, FP, S + 1>(c, T);
+    }
+}
+
+// Index + 1 of the compiled-in program equal to prog with every operand one
+// value per item, or 0.
+inline int fixed_prog_of(const ChainProg& prog, const ChainOperands& B) {
+    for (int k = 0; k < B.n; k++)
+        if (B.kind[k] != kOpItem) return 0;
+    for (int i = 0; i < (int)(sizeof kFixedProgs / sizeof kFixedProgs[0]); i++)
+        if (kFixedProgs[i].nsteps == prog.n && kFixedProgs[i].code == prog.code[0] && prog.code[1] == 0 &&
+            kFixedProgs[i].noperands == B.n)
+            return i + 1;
+    return 0;
+}
+
+template <int W>
+__device__ __forceinline__ void chain_store(float* __restrict__ Y, const ChainItem<W>& c, uint32_t it) {
+    if constexpr (W >= 4) {
+#pragma unroll
+        for (int h = 0; h < W / 4; h++)
+            st_stream(reinterpret_cast<float4*>(Y) + (W / 4) * it + h,
+                      make_float4(c.v[4 * h], c.v[4 * h + 1], c.v[4 * h + 2], c.v[4 * h + 3]));
+    } else {
+        Y[it] = c.v[0];
+    }
+}
+
+// The fused chain over Y->size elements in items of W consecutive elements
+// (W = 4: X and Y 16-byte aligned and the innermost dim a multiple of 4; else
+// 1).  X has Y's size and is read flat; operands go through the descriptor.
+// The program is packed 8 bits per step (op | operand << 3 | reversed << 5)
+// in scalar registers.
+// Block b owns the contiguous run of `per` items from b * per (the host sizes
+// the grid to the CUs, so every CU gets the same work) and walks it in chunks
+// of U items per thread (items base + threadIdx.x + u * blockDim.x): a chunk's
+// X and operand loads are all issued before any of them is waited for, and
+// the first chunk's before the cosine table is copied into LDS (LUT: the
+// program has a Cos step), so those latencies overlap.  At config 1 the run
+// is one chunk.  Items past the run load item 0 and store nothing.
+// FP > 0: the program is compiled-in program FP (chain_apply_fixed).
+template <int ND, int W, bool LUT, int U, int FP = 0>
+__global__ __launch_bounds__(kChainMaxBlock) void k_chain_f32(const float* __restrict__ X, ChainOperands B,
+                                                              float* __restrict__ Y, BDesc d, ChainProg prog,
+                                                              uint32_t nitems, uint32_t per,
+                                                              const double* __restrict__ Tg) {
+    __shared__ __attribute__((aligned(16))) double sT[LUT ? kLutN : 2];
+    const uint32_t b0 = blockIdx.x * per, b1 = min(b0 + per, nitems), bd = blockDim.x;
+    ChainItem<W> c[U];
+    uint32_t base = b0;
+    const auto load_chunk = [&]() {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t it = base + threadIdx.x + u * bd;
+            chain_load<ND, W, FP ? kFixedProgs[FP > 0 ? FP - 1 : 0].noperands : -1>(c[u], X, B, d, it, it < b1);
+        }
+    };
+    load_chunk();
     const double* T = Tg;
     if constexpr (LUT) {
-        load_table<BLOCK>(sT, Tg);
+        load_table_any(sT, Tg);
         T = sT;
     }
-    for (bool first = true; it < nitems; it += stride, first = false) {
-        float v[W], b[kChainMaxOperands][W];
-        if (!first) {
+    for (bool first = true; base < b1; base += bd * U, first = false) {
+        if (!first) load_chunk();
+        if constexpr (FP > 0) chain_apply_fixed<W, U, LUT, FP>(c, T);
+        else chain_apply<W, U, LUT>(c, B, prog, T);
 #pragma unroll
-            for (int h = 0; h < H; h++) {
-                if constexpr (W >= 4) xf[h] = ld_stream(reinterpret_cast<const float4*>(X) + H * it + h);
-                else xf[h].x = X[it];
-            }
-        }
-        if constexpr (W >= 4) {
-#pragma unroll
-            for (int h = 0; h < H; h++) {
-                v[4 * h] = xf[h].x; v[4 * h + 1] = xf[h].y; v[4 * h + 2] = xf[h].z; v[4 * h + 3] = xf[h].w;
-            }
-        } else {
-            v[0] = xf[0].x;
-        }
-        uint32_t off[kChainMaxOperands];
-        operand_offsets<kChainMaxOperands, ND>(d, it * W, off);
-#pragma unroll
-        for (int k = 0; k < kChainMaxOperands; k++) {
-            if (k >= B.n) break;
-            const float* P = B.p[k];
-            if (W == 1 || B.kind[k] == kOpItem) {
-                const float t = P[off[k]];
-#pragma unroll
-                for (int e = 0; e < W; e++) b[k][e] = t;
-            } else if (B.kind[k] == kOpVec) {
-#pragma unroll
-                for (int h = 0; h < H; h++) {
-                    const float4 t = *reinterpret_cast<const float4*>(P + off[k] + 4 * h);
-                    b[k][4 * h] = t.x; b[k][4 * h + 1] = t.y; b[k][4 * h + 2] = t.z; b[k][4 * h + 3] = t.w;
-                }
-            } else {
-                const uint32_t sb = (uint32_t)d.st[k + 1][d.nd - 1];
-#pragma unroll
-                for (int e = 0; e < W; e++) b[k][e] = P[off[k] + e * sb];
-            }
-        }
-        for (int sidx = 0; sidx < prog.n; sidx++) {
-            const uint32_t c = (uint32_t)(prog.code[sidx >> 3] >> (8 * (sidx & 7))) & 0xFFu;
-            const int op = (int)(c & 7u), a = (int)((c >> 3) & 3u), rev = (int)((c >> 5) & 1u);
-            if (W > 1 && op == TENSOR_OPS_CHAIN_DIV && !rev && B.kind[a] == kOpItem) {
-                // v / b for one b per item: RN32((double)v * RN64(1 / b)).  The
-                // double product is within 2^-52 (relative) of v / b, and the
-                // quotient of two f32 values is never a rounding midpoint of f32
-                // nor within 2^-49 (relative) of one, so the product rounds to the
-                // same f32 as the correctly rounded division (zeros, infinities,
-                // NaN and subnormal results included).
-                const double rb = 1.0 / (double)(a == 0 ? b[0][0] : (a == 1 ? b[1][0] : b[2][0]));
-#pragma unroll
-                for (int e = 0; e < W; e++) v[e] = (float)((double)v[e] * rb);
-            } else if (op <= TENSOR_OPS_CHAIN_DIV) {
-                if (a == 0) binary_step<W>(op, rev, v, b[0]);
-                else if (a == 1) binary_step<W>(op, rev, v, b[1]);
-                else binary_step<W>(op, rev, v, b[2]);
-            } else if (op == TENSOR_OPS_CHAIN_RELU) {
-#pragma unroll
-                for (int e = 0; e < W; e++) v[e] = unary_f32<U_RELU>(v[e], T);
-            } else if (op == TENSOR_OPS_CHAIN_ABS) {
-#pragma unroll
-                for (int e = 0; e < W; e++) v[e] = unary_f32<U_ABS>(v[e], T);
-            } else if constexpr (LUT) {
-                cos_lds<W>(v, T);
-            }
-        }
-        if constexpr (W >= 4) {
-#pragma unroll
-            for (int h = 0; h < H; h++)
-                st_stream(reinterpret_cast<float4*>(Y) + H * it + h,
-                          make_float4(v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]));
-        } else {
-            Y[it] = v[0];
+        for (int u = 0; u < U; u++) {
+            const uint32_t it = base + threadIdx.x + u * bd;
+            if (it < b1) chain_store<W>(Y, c[u], it);
         }
     }
 }
@@ -755,9 +901,8 @@ void chain_entry(const Tensor* X, const Tensor* const* operands, int noperands, 
     const size_t n = Y->size;
     if (n) {
         if (n >= ((size_t)1 << 31)) { set_error("%s: more than 2^31 elements", name); st.finish(); return; }
-        bool al = aligned16(x) && aligned16(y);
+        const bool al = aligned16(x) && aligned16(y);
         const uint32_t inner = d.dim[d.nd - 1];
-        // elements per thread: kChainW where the layout allows, else 4, else 1
         const int w = (al && inner % kChainW == 0) ? kChainW : ((al && inner % 4 == 0) ? 4 : 1);
         ChainOperands B{};
         B.n = noperands;
@@ -768,18 +913,24 @@ void chain_entry(const Tensor* X, const Tensor* const* operands, int noperands, 
         }
         const uint32_t items = (uint32_t)(n / w);
         hipStream_t s = stream();
-        const dim3 bl(cos ? kChainLutBlock : kBlock);
-        const dim3 gr(cos ? lut_grid((items + kChainLutBlock - 1) / kChainLutBlock, kChainLutPerCU)
-                          : grid_for(items, kBlock));
+        const uint32_t grid = std::max<uint32_t>(1u, std::min<uint32_t>((items + 64 * kChainU - 1) / (64 * kChainU),
+                                                                         (cos ? 1u : 2u) * (uint32_t)num_cus()));
+        const uint32_t per = (items + grid - 1) / grid;
+        const uint32_t block = std::max<uint32_t>(cos ? 128u : 64u,
+                                                  std::min<uint32_t>(kChainMaxBlock, (per + kChainU * 64 - 1) / (kChainU * 64) * 64));
 #define CHAIN_K(WV)                                                                                              \
     if (cos) {                                                                                                   \
-        ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, WV, true, kChainLutBlock>), gr, bl, 0, s, x, B, y, d,\
-                                           prog, items, T));                                                     \
+        ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, WV, true, kChainU>), dim3(grid), dim3(block), 0, s,  \
+                                           x, B, y, d, prog, items, per, T));                                    \
     } else {                                                                                                     \
-        ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, WV, false, kBlock>), gr, bl, 0, s, x, B, y, d, prog, \
-                                           items, T));                                                           \
+        ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, WV, false, kChainU>), dim3(grid), dim3(block), 0, s, \
+                                           x, B, y, d, prog, items, per, T));                                    \
     }
-        if (w == kChainW) { CHAIN_K(kChainW) }
+        const int fp = (w == kChainW && cos) ? fixed_prog_of(prog, B) : 0;
+        if (fp == 1) {
+            ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, kChainW, true, kChainU, 1>), dim3(grid), dim3(block),
+                                               0, s, x, B, y, d, prog, items, per, T));
+        } else if (w == kChainW) { CHAIN_K(kChainW) }
         else if (w == 4) { CHAIN_K(4) }
         else { CHAIN_K(1) }
 #undef CHAIN_K
