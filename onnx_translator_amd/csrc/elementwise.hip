@@ -233,8 +233,10 @@ __global__ __launch_bounds__(kBlock) void k_unary_f32(const float* __restrict__ 
 // Cos of f32 -> f32 with the table in LDS.  Blocks of kLutBlock threads, at
 // most kLutBlocksPerCU per CU (each block copies the 32 KB table once, so the
 // grid is capped and strides over the tensor); U float4 units per thread per
-// tile.  The first tile's loads are issued before the table copy, so the two
-// latencies overlap.
+// tile.  The table is copied before the first tile's loads are issued, so
+// each wave computes as soon as its own data lands (4.93 -> 4.83 us at
+// config 1; issued after the data, the table's loads, which complete in issue
+// order, held every wave until all of its data had arrived).
 constexpr int kLutBlock = 1024;
 constexpr int kLutBlocksPerCU = 1;
 constexpr int kCosUnits = 1;        // float4 units per thread of k_cos_f32
@@ -248,12 +250,12 @@ __global__ __launch_bounds__(kLutBlock) void k_cos_f32(const float* __restrict__
     const uint32_t tile = kLutBlock * U, stride = gridDim.x * tile;
     uint32_t base = blockIdx.x * tile;
     float4 x[U];
+    load_table<kLutBlock>(sT, T);
 #pragma unroll
     for (int u = 0; u < U; u++) {
         const uint32_t i = base + u * kLutBlock + threadIdx.x;
         x[u] = i < nv ? ld_stream(X4 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    load_table<kLutBlock>(sT, T);
     for (; base < nv; base += stride) {
         float v[4 * U];
 #pragma unroll
@@ -548,12 +550,14 @@ void unary_entry(const char* name, const Tensor* X, Tensor* Y) {
 // into two 64-bit words held in scalar registers, so the unrolled step loop
 // decodes it with shifts instead of indexing the kernel argument memory.
 constexpr int kChainMaxSteps = 16, kChainMaxOperands = kMaxOperands - 1;
-// Chain launch shape: one block per CU when the program has a Cos step (each
-// block copies the 32 KB table into LDS once), two per CU otherwise; a
-// thread takes kChainU items of kChainW elements per chunk, and a block has as
-// many 64-thread waves (at most 16) as one chunk of its run needs.  At config
-// 1 (1,605,632 elements, 256 CUs): 784 items of 8 per block, 832 threads.
-constexpr int kChainW = 8, kChainU = 1, kChainMaxBlock = 1024;
+// Chain launch shape: two blocks per CU (each block with a Cos step copies the
+// 32 KB table into LDS once); a thread takes kChainU items of kChainW elements
+// per chunk, and a block has as many 64-thread waves (at most 16) as one chunk
+// of its run needs.  At config 1 (1,605,632 elements, 256 CUs): 784 items of 4
+// per block, 832 threads.  Measured there (table first): 4 elements x 2
+// blocks per CU 5.1 us; 8 x 1 5.5, 8 x 2 5.7, 4 x 1 6.4, 4 x 3 6.1, 4 x 4
+// 6.5 us; two items of 4 per thread 5.2-5.4 us.
+constexpr int kChainW = 4, kChainU = 1, kChainMaxBlock = 1024;
 struct ChainProg {
     int n;
     uint64_t code[2];
@@ -817,9 +821,9 @@ __device__ __forceinline__ void chain_store(float* __restrict__ Y, const ChainIt
 // the grid to the CUs, so every CU gets the same work) and walks it in chunks
 // of U items per thread (items base + threadIdx.x + u * blockDim.x): a chunk's
 // X and operand loads are all issued before any of them is waited for, and
-// the first chunk's before the cosine table is copied into LDS (LUT: the
-// program has a Cos step), so those latencies overlap.  At config 1 the run
-// is one chunk.  Items past the run load item 0 and store nothing.
+// the cosine table is copied into LDS first (LUT: the program has a Cos
+// step).  At config 1 the run is one chunk.  Items past the run load item 0
+// and store nothing.
 // FP > 0: the program is compiled-in program FP (chain_apply_fixed).
 template <int ND, int W, bool LUT, int U, int FP = 0>
 __global__ __launch_bounds__(kChainMaxBlock) void k_chain_f32(const float* __restrict__ X, ChainOperands B,
@@ -837,12 +841,17 @@ __global__ __launch_bounds__(kChainMaxBlock) void k_chain_f32(const float* __res
             chain_load<ND, W, FP ? kFixedProgs[FP > 0 ? FP - 1 : 0].noperands : -1>(c[u], X, B, d, it, it < b1);
         }
     };
-    load_chunk();
+    // The table first: its copy (an L2 round trip) completes before the data
+    // loads are issued, so each wave then computes as soon as its own data
+    // lands and the arithmetic overlaps other waves' loads and stores (issued
+    // after the data, the table's loads, which complete in issue order, held
+    // every wave until all of its data had arrived: 5.7 -> 5.4 us at config 1)
     const double* T = Tg;
     if constexpr (LUT) {
         load_table_any(sT, Tg);
         T = sT;
     }
+    load_chunk();
     for (bool first = true; base < b1; base += bd * U, first = false) {
         if (!first) load_chunk();
         if constexpr (FP > 0) chain_apply_fixed<W, U, LUT, FP>(c, T);
@@ -903,7 +912,7 @@ void chain_entry(const Tensor* X, const Tensor* const* operands, int noperands, 
         if (n >= ((size_t)1 << 31)) { set_error("%s: more than 2^31 elements", name); st.finish(); return; }
         const bool al = aligned16(x) && aligned16(y);
         const uint32_t inner = d.dim[d.nd - 1];
-        const int w = (al && inner % kChainW == 0) ? kChainW : ((al && inner % 4 == 0) ? 4 : 1);
+        const int w = (al && inner % kChainW == 0) ? kChainW : 1;   // elements per item
         ChainOperands B{};
         B.n = noperands;
         for (int k = 0; k < noperands; k++) {
@@ -914,7 +923,7 @@ void chain_entry(const Tensor* X, const Tensor* const* operands, int noperands, 
         const uint32_t items = (uint32_t)(n / w);
         hipStream_t s = stream();
         const uint32_t grid = std::max<uint32_t>(1u, std::min<uint32_t>((items + 64 * kChainU - 1) / (64 * kChainU),
-                                                                         (cos ? 1u : 2u) * (uint32_t)num_cus()));
+                                                                         2u * (uint32_t)num_cus()));
         const uint32_t per = (items + grid - 1) / grid;
         const uint32_t block = std::max<uint32_t>(cos ? 128u : 64u,
                                                   std::min<uint32_t>(kChainMaxBlock, (per + kChainU * 64 - 1) / (kChainU * 64) * 64));
@@ -930,8 +939,7 @@ void chain_entry(const Tensor* X, const Tensor* const* operands, int noperands, 
         if (fp == 1) {
             ND_SWITCH(d.nd, hipLaunchKernelGGL((k_chain_f32<ND, kChainW, true, kChainU, 1>), dim3(grid), dim3(block),
                                                0, s, x, B, y, d, prog, items, per, T));
-        } else if (w == kChainW) { CHAIN_K(kChainW) }
-        else if (w == 4) { CHAIN_K(4) }
+        } else if (w == 4) { CHAIN_K(4) }
         else { CHAIN_K(1) }
 #undef CHAIN_K
         if (!check_launch(name)) { st.finish(); return; }
