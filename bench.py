@@ -332,13 +332,13 @@ def run_suite(lib, torch, only=None, cpu=None):
                 continue
             b = tbd if name == "div" else tb
             ms = bench_loop(torch, lambda i: fn(As[i % R], b, Os[i % R]), 200, graph=True)
-            emit(op_line(f"{name}_f32_bcast", "config1 [8,64,56,56] (+) [64,1,1]", nb, ms, "hbm"),
+            emit(op_line(f"{name}_f32_bcast", "config1 [8,64,56,56] (+) [64,1,1]", nb, ms, "hbm", rotated=R * nb),
                  CpuLeg.binary(name, A, Bd if name == "div" else B))
         for name, fn in (("relu", L.relu_forward), ("abs", L.abs_forward), ("cos", L.cos_forward)):
             if not want(f"{name}_f32"):
                 continue
             ms = bench_loop(torch, lambda i: fn(As[i % R], Os[i % R]), 200, graph=True)
-            emit(op_line(f"{name}_f32", "config1 [8,64,56,56]", nb, ms, "hbm"), CpuLeg.unary(name, A))
+            emit(op_line(f"{name}_f32", "config1 [8,64,56,56]", nb, ms, "hbm", rotated=R * nb), CpuLeg.unary(name, A))
         if want("chain7_f32_fused"):
             # The same chain fused into one kernel (bit-identical to the op-by-op chain):
             # 4 B in + 4 B out per element, plus the two [64,1,1] operands.  The CPU
@@ -348,17 +348,19 @@ def run_suite(lib, torch, only=None, cpu=None):
             opnds = (PT * 2)(tb, tbd)
             ms = bench_loop(torch, lambda i: L.elementwise_chain_forward(As[i % R], opnds, 2, steps, 7, Os[i % R]),
                             200, graph=True)
-            emit(op_line("chain7_f32_fused", "config1 Add>Mul>Sub>Div>Relu>Abs>Cos, one pass", nb, ms, "hbm"),
+            emit(op_line("chain7_f32_fused", "config1 Add>Mul>Sub>Div>Relu>Abs>Cos, one pass", nb, ms, "hbm",
+                         rotated=R * nb),
                  CpuLeg.chain(A, B, Bd))
         for t in As + Os:
             L.free_tensor(t)
         if want("add_i32_f32_to_f64"):
             I = rng.integers(-(2 ** 31), 2 ** 31 - 1, A.shape, dtype=np.int64).astype(np.int32)
-            Is = [lib.dev(I, I32) for _ in range(20)]
-            O64 = [lib.empty(list(A.shape), F64) for _ in range(20)]
-            ms = bench_loop(torch, lambda i: L.add_forward(Is[i % 20], tb, O64[i % 20]), 100, graph=True)
-            emit(op_line("add_i32_f32_to_f64", "config1 int32 [8,64,56,56] + f32 [64,1,1]", A.size * 12, ms, "hbm"),
-                 CpuLeg.binary("add", I, B, I32, F64))
+            RI = 30
+            Is = [lib.dev(I, I32) for _ in range(RI)]
+            O64 = [lib.empty(list(A.shape), F64) for _ in range(RI)]
+            ms = bench_loop(torch, lambda i: L.add_forward(Is[i % RI], tb, O64[i % RI]), 100, graph=True)
+            emit(op_line("add_i32_f32_to_f64", "config1 int32 [8,64,56,56] + f32 [64,1,1]", A.size * 12, ms, "hbm",
+                         rotated=RI * A.size * 12), CpuLeg.binary("add", I, B, I32, F64))
             for t in Is + O64:
                 L.free_tensor(t)
         lib.check("config1")
@@ -460,25 +462,29 @@ def run_suite(lib, torch, only=None, cpu=None):
             L.free_tensor(t)
     if want("maxpool_3x3s2"):
         x = rng.normal(0, 1, (32, 64, 112, 112)).astype(np.float32)
-        txs = [lib.dev(x, F32) for _ in range(4)]
-        tys = [lib.empty([32, 64, 56, 56], F32) for _ in range(4)]
+        RP = 10
+        txs = [lib.dev(x, F32) for _ in range(RP)]
+        tys = [lib.empty([32, 64, 56, 56], F32) for _ in range(RP)]
         keep = [ints([1, 1, 1, 1]), ints([2, 2]), ints([1, 1]), ints([3, 3])]
         pp = Params(*[ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep])
-        ms = bench_loop(torch, lambda i: L.max_pool_forward(txs[i % 4], tys[i % 4], ctypes.byref(pp)), 40, graph=True)
-        emit(op_line("maxpool_3x3s2", "config4 [32,64,112,112] -> [32,64,56,56]", x.size * 4 + x.size, ms, "hbm"),
-             CpuLeg.maxpool(x))
+        ms = bench_loop(torch, lambda i: L.max_pool_forward(txs[i % RP], tys[i % RP], ctypes.byref(pp)), 40,
+                        graph=True)
+        emit(op_line("maxpool_3x3s2", "config4 [32,64,112,112] -> [32,64,56,56]", x.size * 4 + x.size, ms, "hbm",
+                     rotated=RP * (x.size * 4 + x.size)), CpuLeg.maxpool(x))
         for t in txs + tys:
             L.free_tensor(t)
     lib.check("config4")
 
-    # Config 5: softmax [64,32000] axis 1 (rotating 20 sets > 320 MB).
+    # Config 5: softmax [64,32000] axis 1 (rotating 40 sets, 655 MB).
     if want("softmax_64x32000"):
         rng = np.random.default_rng(4)
         s = rng.normal(0, 3, (64, 32000)).astype(np.float32)
-        ts = [lib.dev(s, F32) for _ in range(20)]
-        to = [lib.empty([64, 32000], F32) for _ in range(20)]
-        ms = bench_loop(torch, lambda i: L.softmax_forward(ts[i % 20], to[i % 20], 1), 200)
-        emit(op_line("softmax_64x32000", "config5 [64,32000] axis=1", s.size * 8, ms, "hbm"), CpuLeg.softmax(s))
+        RS = 40
+        ts = [lib.dev(s, F32) for _ in range(RS)]
+        to = [lib.empty([64, 32000], F32) for _ in range(RS)]
+        ms = bench_loop(torch, lambda i: L.softmax_forward(ts[i % RS], to[i % RS], 1), 200)
+        emit(op_line("softmax_64x32000", "config5 [64,32000] axis=1", s.size * 8, ms, "hbm", rotated=RS * s.size * 8),
+             CpuLeg.softmax(s))
         for t in ts + to:
             L.free_tensor(t)
         lib.check("config5")
@@ -488,22 +494,25 @@ def run_suite(lib, torch, only=None, cpu=None):
     if want("global_avg_pool"):
         rng = np.random.default_rng(5)
         g = rng.normal(0, 1, (64, 512, 7, 7)).astype(np.float32)
-        tg = [lib.dev(g, F32) for _ in range(20)]
-        to = [lib.empty([64, 512, 1, 1], F32) for _ in range(20)]
-        ms = bench_loop(torch, lambda i: L.global_average_pool_forward(tg[i % 20], to[i % 20]), 200)
-        emit(op_line("global_avg_pool", "[64,512,7,7] -> [64,512,1,1]", g.size * 4 + 64 * 512 * 4, ms, "hbm"),
+        RG = 80
+        tg = [lib.dev(g, F32) for _ in range(RG)]
+        to = [lib.empty([64, 512, 1, 1], F32) for _ in range(RG)]
+        ms = bench_loop(torch, lambda i: L.global_average_pool_forward(tg[i % RG], to[i % RG]), 200)
+        gb = g.size * 4 + 64 * 512 * 4
+        emit(op_line("global_avg_pool", "[64,512,7,7] -> [64,512,1,1]", gb, ms, "hbm", rotated=RG * gb),
              CpuLeg.gap(g))
         for t in tg + to:
             L.free_tensor(t)
     if want("dynamic_quantize_linear"):
         x = config2_input(np.random.default_rng(1))
-        tx = [lib.dev(x, F32) for _ in range(4)]
-        ty = [lib.empty(list(x.shape), U8) for _ in range(4)]
+        RD = 7
+        tx = [lib.dev(x, F32) for _ in range(RD)]
+        ty = [lib.empty(list(x.shape), U8) for _ in range(RD)]
         ts, tz = lib.empty([1], F32), lib.empty([1], U8)
-        ms = bench_loop(torch, lambda i: L.dynamic_quantize_linear_forward(tx[i % 4], ty[i % 4], ts, tz), 50)
+        ms = bench_loop(torch, lambda i: L.dynamic_quantize_linear_forward(tx[i % RD], ty[i % RD], ts, tz), 50)
         # algorithmic bytes: x read once (4 B) and the codes written once (1 B)
-        emit(op_line("dynamic_quantize_linear", "x f32 [32,512,1024] -> u8", x.size * 5, ms, "hbm"),
-             CpuLeg.dql(x))
+        emit(op_line("dynamic_quantize_linear", "x f32 [32,512,1024] -> u8", x.size * 5, ms, "hbm",
+                     rotated=RD * x.size * 5), CpuLeg.dql(x))
         for t in tx + ty + [ts, tz]:
             L.free_tensor(t)
     lib.check("next rows")
@@ -546,11 +555,22 @@ def run_graph(torch, batch=64, iters=10):
             "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2), "fused_runs": len(g.fused_runs)}
 
 
-def op_line(name, shape, work, ms, bound, peak=HBM_PEAK):
+CACHE_BYTES = 256 << 20      # MI355X Infinity Cache
+
+
+def op_line(name, shape, work, ms, bound, peak=HBM_PEAK, rotated=None):
+    """rotated: bytes the timed calls cycle through (inputs and outputs); an HBM
+    line states whether that exceeds 2x the Infinity Cache, so its fraction is
+    of HBM traffic, or could have been served from the cache."""
     rate = work / (ms * 1e-3)
     if bound == "hbm":
-        return {"op": name, "shape": shape, "ms": round(ms, 5), "GB/s": round(rate / 1e9, 1),
+        line = {"op": name, "shape": shape, "ms": round(ms, 5), "GB/s": round(rate / 1e9, 1),
                 "frac_hbm": round(rate / peak, 4), "work": work}
+        if rotated is not None:
+            line["rotated_MB"] = round(rotated / 1e6, 1)
+            line["regime"] = ("hbm (rotation > 2x the 256 MB Infinity Cache)" if rotated >= 2 * CACHE_BYTES
+                              else "cache-resident possible (rotation below 2x the 256 MB Infinity Cache)")
+        return line
     return {"op": name, "shape": shape, "ms": round(ms, 4), "TFLOP/s": round(rate / 1e12, 2),
             "frac_mfma": round(rate / peak, 4), "work": work}
 
@@ -896,6 +916,8 @@ def main():
         "frac_hbm": round(value * 1e9 / HBM_PEAK, 4),
         "roofline": {"bound": "hbm", "kernel": h["dominant"], "achieved": round(achieved, 1), "peak": 8000.0,
                      "unit": "GB/s", "frac": round(achieved / 8000.0, 4), "traffic": traffic,
+                     "traffic_source": "profiles/traffic.json: calibrated rocprofv3 FETCH_SIZE / WRITE_SIZE runs of "
+                                       "this kernel (profiles/qdq_config2_hbm_traffic.md), not this run",
                      "avg_launch_ms": round(dom_ms, 5), "algorithmic_bytes": h["bytes_per_launch"]},
         "kernels_ms": {k: round(v, 5) for k, v in h["kernel_ms"].items()},
         "cpu_baseline": cpu,
