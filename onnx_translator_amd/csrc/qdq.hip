@@ -326,9 +326,23 @@ __device__ __forceinline__ void decode4(uint32_t w, float (&x)[4]) {
     }
 }
 
-// Dequantize 1-byte code -> f32: one 4-byte code word per thread and one
-// float4 nontemporal store, full grid (grid-stride beyond 2^20 blocks).
-// (x - zp) * s is evaluated in fp64 and rounded once.
+// Dequantize 1-byte code -> f32: each thread takes kDQU code words (4 codes
+// each) kBlock words apart, all loaded before any is converted, and writes
+// each as one nontemporal float4; grid-stride beyond 2^20 blocks.
+// (x - zp) * s is the reference's fp64 expression rounded once to f32
+// (tensor_ops.c:1018-1034).  It is evaluated in f32 where that gives the
+// same bits: for integer codes with an integer zero point x - zp is an exact
+// integer of at most 9 bits, so the f32 product is the correctly rounded
+// exact product, which is what rounding the (exact) fp64 product gives; for
+// fp8 codes with a zero zero point x * s is likewise one correctly rounded
+// product.  Otherwise (fp8 with a non-zero zero point, a float zero point
+// of integer codes) it stays in fp64.
+// kDQU = 4 measured against one word per thread (config 2, full grid either
+// way): each launch alone 12.8 -> 13.5-14.1 us, but the Q -> DQ round trip,
+// where the codes were just written, 119.5 -> 118.4 us per 8 launches (the
+// fp64 -> f32 change alone about 0.3 us of that).
+constexpr int kDQU = 4;
+
 template <int XDT, int ZDT, int MODE, int ND>
 __global__ __launch_bounds__(kBlock) void k_dequant_v(const uint8_t* __restrict__ X, const float* __restrict__ S,
                                                       const void* __restrict__ Z, float* __restrict__ Y, BDesc d,
@@ -340,25 +354,36 @@ __global__ __launch_bounds__(kBlock) void k_dequant_v(const uint8_t* __restrict_
         su = (double)S[0];
         zu = ld_d<ZDT>(Z, 0);
     }
+    constexpr bool kIntCodes = (XDT == kU8 || XDT == kI8) && (ZDT == kU8 || ZDT == kI8);
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wbase = __builtin_amdgcn_readfirstlane(threadIdx.x) & ~63u;
-    // vw: the wave's first unit (uniform); lanes past nv only skip their store
-    for (uint32_t vw = blockIdx.x * kBlock + wbase; vw < nv; vw += gridDim.x * kBlock) {
-        const uint32_t v = vw + lane;
-        if (v >= nv) continue;
-        const uint32_t w = X4[v];
-        Params<ZDT, MODE> p;
-        load_params<ZDT, MODE, ND>(p, S, Z, d, ax, vbase + (MODE == 3 ? vw : v));
-        float x[4], y[4];
-        decode4<XDT>(w, x);
+    // vw0: the wave's first word of this pass (uniform); lanes past nv load
+    // nothing and skip their store
+    for (uint32_t vw0 = blockIdx.x * kBlock * kDQU + wbase; vw0 < nv; vw0 += gridDim.x * kBlock * kDQU) {
+        uint32_t w[kDQU];
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const int k = MODE == 2 ? b : 0;
-            const double s = MODE == 0 ? su : (double)p.s[k];
-            const double z = MODE == 0 ? zu : ld_d<ZDT>(&p.z[k], 0);
-            y[b] = (float)(((double)x[b] - z) * s);
+        for (int u = 0; u < kDQU; u++) {
+            const uint32_t v = vw0 + u * kBlock + lane;
+            w[u] = v < nv ? X4[v] : 0u;
         }
-        st_stream(Y4 + v, make_float4(y[0], y[1], y[2], y[3]));
+#pragma unroll
+        for (int u = 0; u < kDQU; u++) {
+            const uint32_t vw = vw0 + u * kBlock, v = vw + lane;
+            if (v >= nv) continue;
+            Params<ZDT, MODE> p;
+            load_params<ZDT, MODE, ND>(p, S, Z, d, ax, vbase + (MODE == 3 ? vw : v));
+            float x[4], y[4];
+            decode4<XDT>(w[u], x);
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int k = MODE == 2 ? b : 0;
+                const double s = MODE == 0 ? su : (double)p.s[k];
+                const double z = MODE == 0 ? zu : ld_d<ZDT>(&p.z[k], 0);
+                if (kIntCodes || z == 0.0) y[b] = (x[b] - (float)z) * (float)s;
+                else y[b] = (float)(((double)x[b] - z) * s);
+            }
+            st_stream(Y4 + v, make_float4(y[0], y[1], y[2], y[3]));
+        }
     }
 }
 
@@ -510,7 +535,7 @@ void qdq_entry(const char* name, const Tensor* X, const Tensor* S, const Tensor*
                     CODE_SWITCH(dty, ZDT_SWITCH(dtz, QDQ_MODES(QK)))
 #undef QK
                 } else {
-                    const dim3 g(grid_for(nv, kBlock));
+                    const dim3 g(grid_for(nv, kBlock * kDQU));
                     const uint8_t* xc = (const uint8_t*)x + (size_t)vbase * 4;
                     float* yc = (float*)y + (size_t)vbase * 4;
 #define DQK(M, NDV) \
