@@ -417,6 +417,22 @@ def test_dequantize_all_codes(hip, oracle_lib, xdt):
                         what="DQ full-size")
 
 
+@pytest.mark.parametrize("words", [1, 255, 1023, 1025, 3 * 1024 + 517, 40 * 1024 + 1])
+def test_dequantize_ragged_lengths(hip, oracle_lib, words):
+    """Lengths (in 4-code words) that end inside a thread's group of code words and
+    inside a block's pass: with outputs pre-filled with NaN, every word must be
+    written (the fp8 cases with a zero point other than 0 take the fp64 branch)."""
+    rng = np.random.default_rng(words)
+    for xdt, zdt, z0 in ((O.U8, O.U8, 3), (O.E4M3, O.E4M3, 0), (O.E5M2, O.E5M2, 0x3D)):
+        codes = rng.integers(0, 256, 4 * words, dtype=np.uint8)
+        codes[(codes & 0x7F) >= (0x7C if xdt == O.E5M2 else 0x7F)] = 0x11     # finite codes only: NaN would mask a miss
+        sa, za = np.array([0.0371], np.float32), np.array([z0], O.STORAGE[zdt])
+        with hip.poisoned():
+            got = hip.qdq("dequantize", codes, xdt, sa, O.F32, za, zdt, O.F32)
+        assert_bitexact(got, oracle_lib.qdq("dequantize", codes, xdt, sa, O.F32, za, zdt, O.F32), O.F32,
+                        what=f"DQ {xdt} {words} words")
+
+
 # ---------------------------------------------------------------- next rows ---
 def test_dql_reciprocal_path_ties(hip, oracle_lib):
     """The quantize pass multiplies by 1/scale and falls back to the division
