@@ -40,8 +40,9 @@
 // Launch shapes (swept on MI355X; 64 MiB f32 <-> 16 MiB codes, not cache-resident):
 // quantize — software-pipelined grid-stride loop, kQU 16-byte nontemporal
 // loads per thread, plain 4-byte stores (nontemporal 4-byte stores cost ~1 us),
-// 256-thread blocks, 8 blocks per CU; dequantize — one 4-byte code load and
-// one 16-byte nontemporal store per thread, 256-thread blocks, full grid.
+// 256-thread blocks, 8 blocks per CU; dequantize — four 4-byte code loads per
+// thread issued together, one 16-byte nontemporal store per code word,
+// 256-thread blocks, full grid.
 #include <algorithm>
 #include <mutex>
 #include <cfloat>
