@@ -794,22 +794,34 @@ __device__ __forceinline__ void dql_chunk_minmax(const float* __restrict__ p, in
     __syncthreads();
 }
 
-// The code of v: rint(v / scale) + zp clamped to [0, 255].  With an f32
-// reciprocal (fast: 2^-120 < scale < 2^120, so 1 / scale is a normal float and
-// |v / scale| <= 255 + |zp| cannot overflow) p = RN(v * RN(1 / scale)) lies
-// within 2^-22.8 |p| of the exact quotient, and of its double rounding, which
-// is what the reference rounds; rint(p) is that quotient's rint unless p is
-// within 2^-21 |p| of a half-integer.  Those lanes (and NaN / inf, whose
-// compares fail) take dql_q, the double path.
-__device__ __forceinline__ uint32_t dql_code(float v, bool fast, float invf, float zpf, double scale, double inv,
-                                             double zpd) {
-    if (fast) {
-        const float p = v * invf;
+// The codes of the four values of v: rint(v / scale) + zp clamped to [0, 255].
+// With an f32 reciprocal (fast: 2^-120 < scale < 2^120, so 1 / scale is a
+// normal float and |v / scale| <= 255 + |zp| cannot overflow) p = RN(v * RN(1 /
+// scale)) lies within 2^-22.8 |p| of the exact quotient, and of its double
+// rounding, which is what the reference rounds; rint(p) is that quotient's
+// rint unless p is within 2^-21 |p| of a half-integer.  rint(p) + zp is then
+// an integer, which v_cvt_pk_u8_f32 clamps to [0, 255] and packs.  A word
+// with any lane out of that case (near a tie, NaN / inf, whose compares fail)
+// takes dql_q, the double path, for its four values: both paths give the
+// reference's code, so the word is the same either way.
+__device__ __forceinline__ uint32_t dql_code4(const float4& v, bool fast, float invf, float zpf, double scale,
+                                              double inv, double zpd) {
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    bool ok = fast;
+    uint32_t w = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const float p = e[b] * invf;
         const float r = __builtin_rintf(p);
-        if (__builtin_fabsf(__builtin_fabsf(p - r) - 0.5f) > 0x1p-21f * __builtin_fabsf(p))
-            return (uint32_t)__builtin_amdgcn_fmed3f(r + zpf, 0.0f, 255.0f);
+        ok = ok && __builtin_fabsf(__builtin_fabsf(p - r) - 0.5f) > 0x1p-21f * __builtin_fabsf(p);
+        w = __builtin_amdgcn_cvt_pk_u8_f32(r + zpf, b, w);
     }
-    return (uint32_t)dql_q((double)v, scale, inv, zpd);
+    if (!ok) {
+        w = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) w |= (uint32_t)dql_q((double)e[b], scale, inv, zpd) << (8 * b);
+    }
+    return w;
 }
 
 // (1024, 4): at most 128 registers per lane (4 waves per SIMD), so a block fits
@@ -912,10 +924,7 @@ __global__ __launch_bounds__(kDqlOneThreads, 4) void k_dql_one(const float* __re
     unsigned char* yb = Y + 4 * (int64_t)blockIdx.x * cv;
 #pragma unroll
     for (int k = 0; k < EPT4; k++) {
-        const uint32_t c = dql_code(x[k].x, fast, invf, zpf, scale, inv, zpd) |
-                           (dql_code(x[k].y, fast, invf, zpf, scale, inv, zpd) << 8) |
-                           (dql_code(x[k].z, fast, invf, zpf, scale, inv, zpd) << 16) |
-                           (dql_code(x[k].w, fast, invf, zpf, scale, inv, zpd) << 24);
+        const uint32_t c = dql_code4(x[k], fast, invf, zpf, scale, inv, zpd);
         __builtin_amdgcn_raw_buffer_store_b32(c, dql_rsrc(yb + 4 * k * kDqlOneThreads, n4 - k * kDqlOneThreads, 4),
                                               (uint32_t)(tid * 4), 0, 2 /* nt */);
     }
