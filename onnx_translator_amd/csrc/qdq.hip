@@ -698,6 +698,37 @@ __device__ __forceinline__ double dql_q(double v, double scale, double inv, doub
     return q;
 }
 
+// The codes of the four values of v: rint(v / scale) + zp clamped to [0, 255].
+// With an f32 reciprocal (fast: 2^-120 < scale < 2^120, so 1 / scale is a
+// normal float and |v / scale| <= 255 + |zp| cannot overflow) p = RN(v * RN(1 /
+// scale)) lies within 2^-22.8 |p| of the exact quotient, and of its double
+// rounding, which is what the reference rounds; rint(p) is that quotient's
+// rint unless p is within 2^-21 |p| of a half-integer.  rint(p) + zp is then
+// an integer, which v_cvt_pk_u8_f32 clamps to [0, 255] and packs.  A word
+// with any lane out of that case (near a tie, NaN / inf, whose compares fail)
+// takes dql_q, the double path, for its four values: both paths give the
+// reference's code, so the word is the same either way.
+__device__ __forceinline__ uint32_t dql_code4(const float4& v, bool fast, float invf, float zpf, double scale,
+                                              double inv, double zpd) {
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    bool ok = fast;
+    uint32_t w = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const float p = e[b] * invf;
+        const float r = __builtin_rintf(p);
+        ok = ok && __builtin_fabsf(__builtin_fabsf(p - r) - 0.5f) > 0x1p-21f * __builtin_fabsf(p);
+        w = __builtin_amdgcn_cvt_pk_u8_f32(r + zpf, b, w);
+    }
+    if (!ok) {
+        w = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) w |= (uint32_t)dql_q((double)e[b], scale, inv, zpd) << (8 * b);
+    }
+    return w;
+}
+
+
 template <int DIN, int DY>
 __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(const void* __restrict__ X, int dtx, int64_t n,
                                                            const double* __restrict__ params, void* __restrict__ Y,
@@ -706,13 +737,13 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(const void* __restric
     const int64_t stride = (int64_t)gridDim.x * kDqlThreads;
     int64_t tail = 0;
     if constexpr (DIN == kF32 && DY == kU8) {
+        // the one-launch kernel's codes (dql_code4), so the two forms agree bit for bit
+        const bool fast = scale > 0x1p-120 && scale < 0x1p120;
+        const float invf = (float)inv, zpf = (float)zpd;
         const int64_t nv = n / 4;
         for (int64_t v = (int64_t)blockIdx.x * kDqlThreads + threadIdx.x; v < nv; v += stride) {
             const float4 x = ld_stream(reinterpret_cast<const float4*>(X) + v);
-            const uint32_t c = (uint32_t)dql_q(x.x, scale, inv, zpd) | ((uint32_t)dql_q(x.y, scale, inv, zpd) << 8) |
-                               ((uint32_t)dql_q(x.z, scale, inv, zpd) << 16) |
-                               ((uint32_t)dql_q(x.w, scale, inv, zpd) << 24);
-            st_stream(reinterpret_cast<uint32_t*>(Y) + v, c);
+            st_stream(reinterpret_cast<uint32_t*>(Y) + v, dql_code4(x, fast, invf, zpf, scale, inv, zpd));
         }
         tail = nv * 4;
     }
@@ -792,36 +823,6 @@ __device__ __forceinline__ void dql_chunk_minmax(const float* __restrict__ p, in
         hi = lds[2 * i + 1] > hi ? lds[2 * i + 1] : hi;
     }
     __syncthreads();
-}
-
-// The codes of the four values of v: rint(v / scale) + zp clamped to [0, 255].
-// With an f32 reciprocal (fast: 2^-120 < scale < 2^120, so 1 / scale is a
-// normal float and |v / scale| <= 255 + |zp| cannot overflow) p = RN(v * RN(1 /
-// scale)) lies within 2^-22.8 |p| of the exact quotient, and of its double
-// rounding, which is what the reference rounds; rint(p) is that quotient's
-// rint unless p is within 2^-21 |p| of a half-integer.  rint(p) + zp is then
-// an integer, which v_cvt_pk_u8_f32 clamps to [0, 255] and packs.  A word
-// with any lane out of that case (near a tie, NaN / inf, whose compares fail)
-// takes dql_q, the double path, for its four values: both paths give the
-// reference's code, so the word is the same either way.
-__device__ __forceinline__ uint32_t dql_code4(const float4& v, bool fast, float invf, float zpf, double scale,
-                                              double inv, double zpd) {
-    const float e[4] = {v.x, v.y, v.z, v.w};
-    bool ok = fast;
-    uint32_t w = 0;
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-        const float p = e[b] * invf;
-        const float r = __builtin_rintf(p);
-        ok = ok && __builtin_fabsf(__builtin_fabsf(p - r) - 0.5f) > 0x1p-21f * __builtin_fabsf(p);
-        w = __builtin_amdgcn_cvt_pk_u8_f32(r + zpf, b, w);
-    }
-    if (!ok) {
-        w = 0;
-#pragma unroll
-        for (int b = 0; b < 4; b++) w |= (uint32_t)dql_q((double)e[b], scale, inv, zpd) << (8 * b);
-    }
-    return w;
 }
 
 // (1024, 4): at most 128 registers per lane (4 waves per SIMD), so a block fits
