@@ -348,7 +348,6 @@ template <int XDT, int ZDT, int MODE, int ND>
 __global__ __launch_bounds__(kBlock) void k_dequant_v(const uint8_t* __restrict__ X, const float* __restrict__ S,
                                                       const void* __restrict__ Z, float* __restrict__ Y, BDesc d,
                                                       AxisDesc ax, uint32_t vbase, uint32_t nv) {
-    const uint32_t* X4 = reinterpret_cast<const uint32_t*>(X);
     float4* Y4 = reinterpret_cast<float4*>(Y);
     double su = 0.0, zu = 0.0;
     if constexpr (MODE == 0) {
@@ -356,17 +355,18 @@ __global__ __launch_bounds__(kBlock) void k_dequant_v(const uint8_t* __restrict_
         zu = ld_d<ZDT>(Z, 0);
     }
     constexpr bool kIntCodes = (XDT == kU8 || XDT == kI8) && (ZDT == kU8 || ZDT == kI8);
+    // code words through a buffer resource: words at or past nv read as zero
+    // without a memory access (plain cached loads: measured against global
+    // loads, the same per launch and 0.4% faster in the Q -> DQ round trip)
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, nv * 4u);
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wbase = __builtin_amdgcn_readfirstlane(threadIdx.x) & ~63u;
-    // vw0: the wave's first word of this pass (uniform); lanes past nv load
-    // nothing and skip their store
+    // vw0: the wave's first word of this pass (uniform); lanes past nv skip
+    // their store
     for (uint32_t vw0 = blockIdx.x * kBlock * kDQU + wbase; vw0 < nv; vw0 += gridDim.x * kBlock * kDQU) {
         uint32_t w[kDQU];
 #pragma unroll
-        for (int u = 0; u < kDQU; u++) {
-            const uint32_t v = vw0 + u * kBlock + lane;
-            w[u] = v < nv ? X4[v] : 0u;
-        }
+        for (int u = 0; u < kDQU; u++) w[u] = __builtin_amdgcn_raw_buffer_load_b32(xr, (vw0 + u * kBlock + lane) * 4u, 0, 0);
 #pragma unroll
         for (int u = 0; u < kDQU; u++) {
             const uint32_t vw = vw0 + u * kBlock, v = vw + lane;
