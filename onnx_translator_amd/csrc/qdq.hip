@@ -401,6 +401,10 @@ __global__ __launch_bounds__(kBlock) void k_qdq_fused(const float* __restrict__ 
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, nv * 16u);
     const QParm pu = qparm<CDT>(SQ[0], ld_d<CDT>(ZQ, 0));
     const double sd = (double)SD[0], zd = ld_d<CDT>(ZD, 0);
+    // the dequantize step in f32 where k_dequant_v uses it (integer codes, or
+    // a zero zero point): the same bits as the fp64 expression rounded once
+    const bool f32dq = CDT == kU8 || CDT == kI8 || zd == 0.0;
+    const float sdf = SD[0], zdf = (float)zd;
     const Params<CDT, 0> none{};
     float4* Y4 = reinterpret_cast<float4*>(Y);
     for (uint32_t v0 = blockIdx.x * (kBlock * 2) + threadIdx.x; v0 < nv; v0 += gridDim.x * (kBlock * 2)) {
@@ -413,8 +417,13 @@ __global__ __launch_bounds__(kBlock) void k_qdq_fused(const float* __restrict__ 
             if (v >= nv) continue;
             float c[4], y[4];
             decode4<CDT>(quant_unit<CDT, CDT, 0>(xv[u], none, pu), c);
+            if (f32dq) {      // uniform
 #pragma unroll
-            for (int b = 0; b < 4; b++) y[b] = (float)(((double)c[b] - zd) * sd);
+                for (int b = 0; b < 4; b++) y[b] = (c[b] - zdf) * sdf;
+            } else {
+#pragma unroll
+                for (int b = 0; b < 4; b++) y[b] = (float)(((double)c[b] - zd) * sd);
+            }
             st_stream(Y4 + v, make_float4(y[0], y[1], y[2], y[3]));
         }
     }

@@ -53,8 +53,9 @@ __device__ __forceinline__ float qfast(float x, const QParm& p, bool& good) {
 // with one-element parameters and uint8 (kind 1) or int8 (kind 2) codes.  The
 // quantize step is the Q kernels' (fast path with the fp64 fallback per
 // element, the v_cvt_pk_u8_f32 encoder; int8 adds 128 first, so the code is
-// the unsigned byte minus 128), the dequantize step k_qdq_fused's ((c - zp) * s
-// in double, rounded once), so the value equals the operator pair bit for bit.
+// the unsigned byte minus 128), the dequantize step k_dequant_v's ((c - zp) * s
+// rounded once, here in f32, which gives those bits for integer codes), so the
+// value equals the operator pair bit for bit.
 struct FakeQuant {           // device pointers to one-element tensors; kind 0: none
     const float* qs;         // QuantizeLinear scale
     const void* qz;          // its zero point (code dtype), or null for 0
@@ -94,7 +95,9 @@ __device__ __forceinline__ float fq_apply(float v, const FQParm& f) {
         const double r = qval((double)v, (double)f.p.s, f.p.zd);
         c = f.kind == 2 ? (float)(int8_t)code8<kI8>(r) : (float)code8<kU8>(r);
     }
-    return (float)(((double)c - f.zd) * f.sd);
+    // c - zp is an exact integer of at most 9 bits, so the f32 product is the
+    // correctly rounded exact product: the double expression's value
+    return (c - (float)f.zd) * (float)f.sd;
 }
 
 }  // namespace tohip
