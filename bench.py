@@ -296,7 +296,7 @@ SUITE = ("add_f32_bcast", "mul_f32_bcast", "sub_f32_bcast", "div_f32_bcast", "re
          "chain7_f32_fused", "add_i32_f32_to_f64", "gemm_f32_4096", "gemm_f16_4096", "gemm_f16_4096_vendor",
          "gemm_woq_int8_fused",
          "gemm_woq_int8_unfused", "conv_stem7x7s2", "conv_3x3", "conv_1x1", "maxpool_3x3s2", "softmax_64x32000",
-         "global_avg_pool", "dynamic_quantize_linear", "graph_resnet_qdq_b64")
+         "global_avg_pool", "dynamic_quantize_linear", "graph_resnet_qdq_b64", "graph_resnet_qdq_b64_int8")
 
 
 def run_suite(lib, torch, only=None, cpu=None):
@@ -518,17 +518,22 @@ def run_suite(lib, torch, only=None, cpu=None):
     lib.check("next rows")
     if want("graph_resnet_qdq_b64"):
         emit(run_graph(torch), CpuLeg.graph())
+    if want("graph_resnet_qdq_b64_int8"):
+        emit(run_graph(torch, int8=True))
     return out
 
 
-def run_graph(torch, batch=64, iters=10):
+def run_graph(torch, batch=64, iters=10, int8=False):
     """Config 5: the QDQ ResNet-style ONNX graph (written by
     onnx_translator_amd.onnx.create_model, random-init weights, seed 4) through the
-    device-resident Graph executor, batch 64 of [3,224,224] inputs ~N(0,1)."""
+    device-resident Graph executor, batch 64 of [3,224,224] inputs ~N(0,1).
+    int8: with the QDQ blocks on the int8 MFMA kernels (Graph.fuse(int8_conv=True),
+    the convolution tolerance class instead of the default passes' bits)."""
     from onnx_translator_amd.nn import Tensor
     from onnx_translator_amd.nn.ONNXImport import load_graph
     from onnx_translator_amd.onnx.create_model import resnet_qdq_model
-    g = load_graph(resnet_qdq_model(batch=batch))
+    g = load_graph(resnet_qdq_model(batch=batch), fuse=False)
+    g.fuse(int8_conv=int8)
     x = np.random.default_rng(4).normal(0, 1, (batch, 3, 224, 224)).astype(np.float32)
     xd = Tensor(*x.shape, dtype="float32", data=x).to_device()
     t0, n = time.perf_counter(), 0
@@ -550,7 +555,9 @@ def run_graph(torch, batch=64, iters=10):
                          256 * 14 * 14 * 1152 + 256 * 14 * 14 * 128 + 512 * 7 * 7 * 2304 + 512 * 7 * 7 * 256 +
                          1000 * 512)
     del y
-    return {"op": "graph_resnet_qdq_b64", "shape": "config5 ONNX graph, batch 64 x [3,224,224], 37 nodes",
+    return {"op": "graph_resnet_qdq_b64" + ("_int8" if int8 else ""),
+            "shape": "config5 ONNX graph, batch 64 x [3,224,224], 37 nodes" +
+                     (", QDQ blocks on int8 MFMA (tolerance class)" if int8 else ""),
             "ms": round(ms, 4), "images/s": round(batch / (ms * 1e-3), 1), "host_ms": round(wall, 4),
             "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2), "fused_runs": len(g.fused_runs)}
 

@@ -294,6 +294,54 @@ void dequantize_conv2d_fused_forward(const Tensor* Xq, const Tensor* XScale, con
  * of dynamic_quantize_linear_forward): calls that overlap on one GPU race. */
 void dynamic_quantize_linear_forward_noalloc(const Tensor* x, Tensor* y, Tensor* y_scale, Tensor* y_zp);
 
+/* ---------------------------------------------------------------------------
+ * QDQ convolution blocks on int8 MFMA.  They replace, for a QDQ residual block,
+ * the sequence quantize_linear_forward -> dequantize_linear_forward (activation,
+ * tensor_ops/tensor_ops.h:149, 155) -> dequantize_linear_axis_forward (int8
+ * weights, per output channel, zero point 0) -> conv2d_forward (:161) ->
+ * relu_forward (:85) -> add_forward (:116) with the skip or a 1x1 projection
+ * conv2d_forward of the same activation, and the next block's
+ * quantize_linear_forward.  The convolution sums sum_k w (x - zx) exactly in
+ * int32 and scales it once (sx * sw[m], in double, rounded to float32): the
+ * tolerance class of the MFMA convolution, not the reference's bits, and no
+ * exact mode (qconv_block_forward fails while tensor_ops_hip_set_exact(1) is in
+ * effect).  Activations between blocks are channels-last int8 [N, H, W, C]
+ * holding code - 128 for uint8 codes (the code for int8): an internal layout
+ * that only these calls read.  Device tensors only; C a multiple of 32.
+ * ------------------------------------------------------------------------- */
+/* Y (int8 [N, H, W, C]) = QuantizeLinear(X, Scale, ZeroPoint) in that layout; X float32
+ * [N, C, H, W], Scale one float32, ZeroPoint one element of code_dtype (uint8 / int8)
+ * or NULL (0).  The codes are quantize_linear_forward's, bit for bit. */
+void quantize_linear_nhwc_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint,
+                                  int code_dtype, Tensor* Y);
+/* Weight codes int8 [M, C, KH, KW] -> Wk int8 [M, KH, KW, C] and WSum int32 [M, KH, KW],
+ * the sum of each tap's C codes (the zero-point correction). */
+void qconv_pack_weights(const Tensor* Wq, Tensor* Wk, Tensor* WSum);
+typedef struct {
+    const Tensor* x_scale;   /* one float32: DequantizeLinear scale of the input codes */
+    const Tensor* x_zero;    /* one element of x_codes' dtype, or NULL (0) */
+    int x_codes;             /* DataType of the input codes: DTYPE_UINT8 or DTYPE_INT8 */
+    const Tensor* w;         /* int8 [M, KH, KW, C] (qconv_pack_weights), zero points 0 */
+    const Tensor* w_sum;     /* int32 [M, KH, KW] (qconv_pack_weights) */
+    const Tensor* w_scale;   /* float32 [M]: per-output-channel weight scale */
+    const Tensor* bias;      /* float32 [M] or NULL */
+    int relu;                /* 1: Relu after the bias */
+    const Tensor* p;         /* 1x1 projection (pads 0, the conv's strides) added after the
+                                Relu: int8 [M, 1, 1, C], or NULL */
+    const Tensor* p_sum;     /* int32 [M, 1, 1] */
+    const Tensor* p_scale;   /* float32 [M] */
+    const Tensor* skip;      /* float32 [N, M, OH, OW] added after the Relu, or NULL */
+    const Tensor* q_scale;   /* one float32: quantize the output for the next block
+                                (Y int8 [N, OH, OW, M] in the layout above), or NULL:
+                                Y float32 [N, M, OH, OW] */
+    const Tensor* q_zero;    /* one element of y_codes' dtype, or NULL (0) */
+    int y_codes;             /* DataType of the output codes: DTYPE_UINT8 or DTYPE_INT8 */
+} QConvBlock;
+/* Y = [Q](Relu?(Conv(DQ(X), DQ(w)) + bias) [+ Conv1x1(DQ(X), DQ(p))] [+ skip]); params as
+ * conv2d_forward's (group 1; the output size follows from the pads, strides and
+ * dilations).  M a multiple of 64. */
+void qconv_block_forward(const Tensor* X, const QConvBlock* block, Tensor* Y, ConvParams* params);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,7 +23,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libtensor_ops_hip.so")
-SOURCES = ["runtime.hip", "elementwise.hip", "qdq.hip", "reduce.hip", "gemm.hip", "conv.hip"]
+SOURCES = ["runtime.hip", "elementwise.hip", "qdq.hip", "reduce.hip", "gemm.hip", "conv.hip", "qconv.hip"]
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -340,6 +340,98 @@ class DequantizeConv(FusedConv):
         return Conv.forward_(self, xq, w, b)
 
 
+class QuantizeNHWC(Ops):
+    """QuantizeLinear of a float32 NCHW tensor into the channels-last int8 codes
+    that :class:`QConvBlock` reads (``quantize_linear_nhwc_forward``): the codes
+    of QuantizeLinear (nn/Operators.py:427-450, tensor_ops.c:999-1016) bit for
+    bit, stored [N, H, W, C] as code - 128 for uint8 (the code for int8).
+    ``inputs`` = [x, scale, zero point or ""] with one-element parameters."""
+
+    def __init__(self, inputs, outputs, code_dtype, version="17"):
+        super().__init__(inputs, outputs)
+        self.code_dtype = code_dtype
+        self.version = version
+        self.lib.quantize_linear_nhwc_forward.argtypes = [PT, PT, PT, ctypes.c_int, PT]
+        self.lib.quantize_linear_nhwc_forward.restype = None
+
+    def forward(self, x: Tensor, scale: Tensor, zero_point: Tensor = None):
+        N, C, H, W = x.size
+        code = ctypes.c_int(DTYPE_MAP[self.code_dtype])
+
+        def arrange(ins, out):
+            return (ins[0], ins[1], ins[2], code, out)
+        t = self._run("quantize_linear_nhwc_forward", [x, scale, zero_point], (N, H, W, C), "int8", arrange=arrange)
+        return _values(self, t)
+
+    def forward_(self, x: Tensor_, *rest):
+        N, C, H, W = x.size
+        return _values(self, Tensor_(N, H, W, C, dtype="int8"))
+
+
+class CQConvBlock(ctypes.Structure):
+    """``QConvBlock`` (tensor_ops.h extension)."""
+    _fields_ = [("x_scale", PT), ("x_zero", PT), ("x_codes", ctypes.c_int), ("w", PT), ("w_sum", PT),
+                ("w_scale", PT), ("bias", PT), ("relu", ctypes.c_int), ("p", PT), ("p_sum", PT), ("p_scale", PT),
+                ("skip", PT), ("q_scale", PT), ("q_zero", PT), ("y_codes", ctypes.c_int)]
+
+
+class QConvBlock(Ops):
+    """A QDQ residual block on int8 MFMA (``qconv_block_forward``): y =
+    [Q](Relu?(Conv(DQ(x), DQ(w)) + b) [+ Conv1x1(DQ(x), DQ(p))] [+ skip]), the
+    sequence QuantizeLinear -> DequantizeLinear -> Conv -> Relu -> Add (and the
+    next block's QuantizeLinear) of nn/Operators.py:427-548, :32-79, :170-219
+    with the convolution's integer sum taken exactly: the tolerance class of
+    the MFMA convolution, not the sequence's bits.
+
+    ``inputs`` = [x codes (channels-last, from QuantizeNHWC or another block),
+    x scale, x zero point or "", packed weight codes [M, KH, KW, C], their
+    per-tap sums [M, KH, KW], weight scales [M], bias or "", projection codes
+    [M, 1, 1, C] or "", their sums, their scales, skip (f32 NCHW) or "",
+    output scale or "", output zero point or ""]; with an output scale the
+    block writes the next block's channels-last codes of ``y_codes``, else f32
+    NCHW."""
+
+    def __init__(self, inputs, outputs, pads, strides, dilations, relu, x_codes, y_codes=None, version="17"):
+        super().__init__(inputs, outputs)
+        self.pads, self.strides, self.dilations = pads, strides, dilations
+        self.relu = 1 if relu else 0
+        self.x_codes, self.y_codes = x_codes, y_codes
+        self.version = version
+        self.lib.qconv_block_forward.argtypes = [PT, ctypes.POINTER(CQConvBlock), PT, ctypes.POINTER(CConvParams)]
+        self.lib.qconv_block_forward.restype = None
+
+    def _shape(self, x, w):
+        N, H, W, _ = x.size
+        M, KH, KW, _ = w.size
+        OH, OW = _pool_out(H, W, self.pads, self.strides, self.dilations, KH, KW)
+        return ((N, OH, OW, M), "int8") if self.y_codes else ((N, M, OH, OW), "float32")
+
+    def forward(self, x, x_scale, x_zero, w, w_sum, w_scale, bias=None, p=None, p_sum=None, p_scale=None,
+                skip=None, q_scale=None, q_zero=None):
+        keep = [_int_arr(self.pads), _int_arr(self.strides), _int_arr(self.dilations)]
+        prm = CConvParams()
+        prm.pads, prm.strides, prm.dilations = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep]
+        prm.group = 1
+        blk = CQConvBlock()
+
+        def arrange(ins, out):
+            (blk.x_scale, blk.x_zero, blk.w, blk.w_sum, blk.w_scale, blk.bias, blk.p, blk.p_sum, blk.p_scale,
+             blk.skip, blk.q_scale, blk.q_zero) = ins[1:]
+            blk.x_codes = DTYPE_MAP[self.x_codes]
+            blk.relu = self.relu
+            blk.y_codes = DTYPE_MAP[self.y_codes] if self.y_codes else 0
+            return (ins[0], ctypes.byref(blk), out, ctypes.byref(prm))
+        shape, dt = self._shape(x, w)
+        t = self._run("qconv_block_forward", [x, x_scale, x_zero, w, w_sum, w_scale, bias, p, p_sum, p_scale, skip,
+                                              q_scale, q_zero], shape, dt, arrange=arrange)
+        del keep
+        return _values(self, t)
+
+    def forward_(self, x, x_scale=None, x_zero=None, w=None, *rest):
+        shape, dt = self._shape(x, w)
+        return _values(self, Tensor_(*shape, dtype=dt))
+
+
 class MaxPool(Ops):
     """2-D max pooling (nn/Operators.py:550-611 -> tensor_ops.c:1116-1165)."""
 

@@ -161,20 +161,25 @@ class Graph:
     # -- fusion --------------------------------------------------------------------
     def fuse(self, elementwise: bool = True, dequantize_gemm: bool = True, conv_epilogue: bool = True,
              fold_constants: bool = True, dequantize_conv: bool = False,
-             quantize_dequantize: bool = True, pool_quantize_dequantize: bool = False) -> "Graph":
+             quantize_dequantize: bool = True, pool_quantize_dequantize: bool = False,
+             int8_conv: bool = False) -> "Graph":
         """Request the graph passes; they are applied at the first ``forward`` (shapes needed).
         ``dequantize_conv`` folds activation DequantizeLinear nodes into their convolutions
         and so takes precedence over ``quantize_dequantize`` for those pairs.
         ``pool_quantize_dequantize`` lets a MaxPool write the fake-quantized copy of its
         output as well (MaxPoolQDQ); off by default, as on the config-5 graph the pooling
-        kernel with two outputs is slower than the two separate passes."""
+        kernel with two outputs is slower than the two separate passes.
+        ``int8_conv`` (device graphs) runs QDQ residual blocks on the int8 MFMA kernels
+        (QuantizeNHWC, QConvBlock): their convolutions sum the integer codes exactly and
+        scale once, the tolerance class of the MFMA convolution rather than the bits of the
+        operator sequence, and they have no exact mode, so it is off by default."""
         self._fuse_pending = (elementwise, dequantize_gemm, conv_epilogue, fold_constants, dequantize_conv,
-                              quantize_dequantize, pool_quantize_dequantize)
+                              quantize_dequantize, pool_quantize_dequantize, int8_conv)
         return self
 
     def fuse_elementwise(self) -> "Graph":
         """Request elementwise fusion only."""
-        return self.fuse(True, False, False, False, False, False, False)
+        return self.fuse(True, False, False, False, False, False, False, False)
 
     def _edge_shapes(self, inputs) -> Dict[str, tuple]:
         shapes: Dict[str, tuple] = {k: (tuple(v.size), v.dtype) for k, v in self.initializers.items()}
@@ -191,9 +196,11 @@ class Graph:
         return shapes
 
     def _fuse(self, inputs):
-        elementwise, dq_gemm, conv_epi, fold, dq_conv, qdq, pool_qdq = self._fuse_pending
+        elementwise, dq_gemm, conv_epi, fold, dq_conv, qdq, pool_qdq, int8_conv = self._fuse_pending
         self._fuse_pending = None
         shapes = self._edge_shapes(inputs)
+        if int8_conv and self.device and self._fuse_qconv_blocks(shapes, self._consumers()):
+            shapes = self._edge_shapes(inputs)
         if dq_gemm:
             self._fuse_dq_gemm(shapes, self._consumers())
         if fold:
@@ -211,6 +218,156 @@ class Graph:
         if elementwise:
             self._fuse_gap_flatten(shapes, self._consumers())
             self._fuse_runs(shapes, self._consumers())
+
+    def _fuse_qconv_blocks(self, shapes, consumers) -> bool:
+        """QDQ residual blocks onto the int8 MFMA kernels.  A block is
+        QuantizeLinear -> DequantizeLinear (one-element uint8 / int8 parameters) ->
+        Conv (group 1, dilation 1) whose weight is a DequantizeLinear of int8
+        codes along axis 0 with zero points 0, [-> Relu] [-> Add with a tensor of
+        the output's shape, or with a 1x1 / pads-0 Conv of the same activation and
+        strides, no bias, whose weight is such a DequantizeLinear], with C % 32 ==
+        0 and M % 64 == 0, and nothing else reading its intermediates.  It becomes
+        one QConvBlock at its last node; its input codes come from a QuantizeNHWC
+        at the QuantizeLinear's place, or straight from the previous block when
+        that block's output is read only by this block's QuantizeLinear.  The
+        weights are repacked once, channels-last with per-tap code sums, as new
+        device initializers.  Returns whether anything was replaced."""
+        ops = list(self.ops.values())
+        producer = {o: op for op in ops for o in op.outputs}
+        users: Dict[str, list] = {}
+        for op in ops:
+            for na in op.inputs:
+                if na:
+                    users.setdefault(na, []).append(op)
+        init = self.initializers
+
+        def only(edge):
+            u = users.get(edge, [])
+            return u[0] if len(u) == 1 and consumers.get(edge, 0) == 1 and edge not in self.output_name else None
+
+        def one(edge, dt):
+            return bool(edge) and edge in init and shapes[edge][1] == dt and int(np.prod(shapes[edge][0] or (1,))) == 1
+
+        def weight(edge, conv):
+            """(dq node, int8 codes, scales [M]) of a weight read only by conv, or None."""
+            dq = producer.get(edge)
+            if type(dq) is not Op.DequantizeLinear or only(edge) is not conv or dq.axis not in (0, -4):
+                return None
+            q, sc = dq.inputs[0], dq.inputs[1]
+            z = dq.inputs[2] if len(dq.inputs) > 2 else ""
+            if q not in init or sc not in init or (z and z not in init) or shapes[q][1] != "int8":
+                return None
+            if len(shapes[q][0]) != 4 or shapes[sc][1] != "float32":
+                return None
+            m = shapes[q][0][0]
+            sv = init[sc].numpy().reshape(-1)
+            if sv.size != m or (z and np.any(init[z].numpy() != 0)):
+                return None
+            return dq, init[q].numpy(), sv.astype(np.float32)
+
+        blocks = []
+        for c in ops:
+            if type(c) is not Op.Conv or c.group != 1 or c.dtype not in (None, "float32") or tuple(c.dilations) != (1, 1):
+                continue
+            xd = c.inputs[0]
+            dqx = producer.get(xd)
+            if type(dqx) is not Op.DequantizeLinear or len(dqx.inputs) < 2:
+                continue
+            xq = dqx.inputs[0]
+            qx = producer.get(xq)
+            if type(qx) is not Op.QuantizeLinear or only(xq) is not dqx or len(qx.inputs) < 2:
+                continue
+            cdt = shapes[xq][1]
+            qs, qz = qx.inputs[1], (qx.inputs[2] if len(qx.inputs) > 2 else "")
+            ds, dz = dqx.inputs[1], (dqx.inputs[2] if len(dqx.inputs) > 2 else "")
+            if cdt not in ("uint8", "int8") or not one(qs, "float32") or not one(ds, "float32"):
+                continue
+            if (qz and not one(qz, cdt)) or (dz and not one(dz, cdt)):
+                continue
+            xs = shapes[qx.inputs[0]]
+            if xs[1] != "float32" or len(xs[0]) != 4 or xs[0][1] % 32:
+                continue
+            wt = weight(c.inputs[1], c)
+            if wt is None or wt[1].shape[0] % 64 or wt[1].shape[1] != xs[0][1]:
+                continue
+            b = c.inputs[2] if len(c.inputs) > 2 else ""
+            if b and (b not in init or shapes[b][1] != "float32" or int(np.prod(shapes[b][0])) != wt[1].shape[0]):
+                continue
+            chain, cur, relu, skip, proj, pw = [c], c.outputs[0], False, "", None, None
+            nxt = only(cur)
+            if type(nxt) is Op.RELU and nxt.dtype in (None, "float32"):
+                chain.append(nxt)
+                cur, relu = nxt.outputs[0], True
+                nxt = only(cur)
+            if (type(nxt) is Op.ADD and nxt.dtype in (None, "float32") and len(nxt.inputs) == 2 and
+                    nxt.inputs.count(cur) == 1 and shapes[nxt.outputs[0]][0] == shapes[cur][0]):
+                other = nxt.inputs[1 - nxt.inputs.index(cur)]
+                po = producer.get(other)
+                if (type(po) is Op.Conv and po is not c and po.inputs[0] == xd and only(other) is nxt and
+                        po.group == 1 and tuple(po.dilations) == (1, 1) and tuple(po.pads) == (0, 0, 0, 0) and
+                        tuple(po.strides) == tuple(c.strides) and (len(po.inputs) < 3 or not po.inputs[2]) and
+                        shapes[other][0] == shapes[cur][0]):
+                    pw = weight(po.inputs[1], po)
+                    if pw is not None and pw[1].shape[2:] == (1, 1):
+                        proj = po
+                if proj is None and shapes[other][1] == "float32" and shapes[other][0] == shapes[cur][0]:
+                    skip = other
+                if proj is not None or skip:
+                    chain.append(nxt)
+                    cur = nxt.outputs[0]
+            # the activation must feed this block only
+            if set(o.name for o in users.get(xd, [])) != {c.name} | ({proj.name} if proj else set()):
+                continue
+            if proj is not None:
+                chain.insert(1, proj)
+            blocks.append(dict(c=c, qx=qx, dqx=dqx, xq=xq, cdt=cdt, qs=qs, qz=qz, ds=ds, dz=dz, w=wt, b=b,
+                               relu=relu, skip=skip, proj=proj, pw=pw, chain=chain, out=cur, src=None, nxt=None))
+        if not blocks:
+            return False
+        by_qx = {bl["qx"].name: bl for bl in blocks}
+        for bl in blocks:
+            u = only(bl["out"])
+            if type(u) is Op.QuantizeLinear and u.name in by_qx:
+                bl["nxt"] = by_qx[u.name]
+                by_qx[u.name]["src"] = bl
+
+        def put(name, arr, dt):
+            t = Tensor(*arr.shape, dtype=dt, data=np.ascontiguousarray(arr)).to_device()
+            self.initializers[name] = t
+            return name
+
+        def packed(prefix, codes, scales):
+            k = codes.transpose(0, 2, 3, 1)
+            return (put(prefix + ".qk", k, "int8"), put(prefix + ".qsum", k.sum(axis=3, dtype=np.int64).astype(np.int32),
+                                                        "int32"), put(prefix + ".qscale", scales, "float32"))
+
+        replace, drop = {}, set()
+        for bl in blocks:
+            c = bl["c"]
+            codes_in = bl["xq"] + ".nhwc"
+            if bl["src"] is None:
+                qn = Op.QuantizeNHWC([bl["qx"].inputs[0], bl["qs"], bl["qz"]], [codes_in], bl["cdt"])
+                qn.name = f"QuantizeNHWC.{bl['qx'].name}"
+                replace[bl["qx"].name] = qn
+            else:
+                drop.add(bl["qx"].name)
+            wk, wsum, wsc = packed(c.name, bl["w"][1], bl["w"][2])
+            pk = psum = psc = ""
+            if bl["proj"] is not None:
+                pk, psum, psc = packed(bl["proj"].name, bl["pw"][1], bl["pw"][2])
+            nb = bl["nxt"]
+            out = nb["xq"] + ".nhwc" if nb else bl["out"]
+            blk = Op.QConvBlock([codes_in, bl["ds"], bl["dz"], wk, wsum, wsc, bl["b"], pk, psum, psc, bl["skip"],
+                                 nb["qs"] if nb else "", nb["qz"] if nb else ""], [out], c.pads, c.strides,
+                                c.dilations, bl["relu"], bl["cdt"], nb["cdt"] if nb else None)
+            blk.name = "QConvBlock." + "+".join(o.name for o in bl["chain"])
+            replace[bl["chain"][-1].name] = blk
+            drop.update(o.name for o in bl["chain"][:-1])
+            drop.update({bl["dqx"].name, bl["w"][0].name} | ({bl["pw"][0].name} if bl["proj"] is not None else set()))
+            self.fused_runs.append([bl["qx"].name, bl["dqx"].name] + [o.name for o in bl["chain"]])
+        out = [replace.get(o.name, o) for o in ops if o.name not in drop]
+        self.ops = OrderedDict((o.name, o) for o in out)
+        return True
 
     def _fold_constants(self):
         """DequantizeLinear nodes over initializers only are evaluated once."""

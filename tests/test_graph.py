@@ -219,6 +219,48 @@ def test_conv_qdq_pass(monkeypatch):
         seen.update(o.outputs)
 
 
+def test_int8_conv_pass(monkeypatch):
+    """Placeholder-shape run of the int8 QDQ block pass on the config-5 graph:
+    each block (QuantizeLinear -> DequantizeLinear -> Conv with DequantizeLinear'd
+    int8 weights -> Relu -> Add of the pooled activation or of a 1x1 projection)
+    becomes one QConvBlock; block 1's codes come from a QuantizeNHWC of the
+    MaxPool output (which its residual also reads), blocks 2-4 read the codes the
+    previous block writes, and the last block writes f32 for the pooling."""
+    from onnx_translator_amd.nn import Graph, Tensor, Tensor_
+    from onnx_translator_amd.nn import Operators as Op
+    from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
+    monkeypatch.setattr(Tensor, "to_device", lambda self: self)
+    m = resnet_qdq_model(batch=1, image=64)
+    g = Graph(ONNXImport(m), ["input"], ["output"], initializers=initializers(m))
+    g.device = True
+    x = Tensor_(1, 3, 64, 64, dtype="float32")
+    shapes = g._edge_shapes([x])
+    assert g._fuse_qconv_blocks(shapes, g._consumers())
+    ops = list(g.ops.values())
+    names = [type(o).__name__ for o in ops]
+    assert names.count("QuantizeNHWC") == 1 and names.count("QConvBlock") == 4
+    assert "QuantizeLinear" not in names and "DequantizeLinear" not in names and names.count("Conv") == 1
+    blocks = [o for o in ops if type(o).__name__ == "QConvBlock"]
+    qn = next(o for o in ops if type(o).__name__ == "QuantizeNHWC")
+    assert qn.inputs == ["pool", "act.scale", "act.zp"] and qn.outputs == ["block1.xq.nhwc"]
+    assert [b.inputs[0] for b in blocks] == ["block1.xq.nhwc", "block2.xq.nhwc", "block3.xq.nhwc", "block4.xq.nhwc"]
+    assert [b.outputs[0] for b in blocks] == ["block2.xq.nhwc", "block3.xq.nhwc", "block4.xq.nhwc", "block4.out"]
+    assert blocks[0].inputs[10] == "pool" and not blocks[0].inputs[7]
+    assert all(b.inputs[7] and not b.inputs[10] for b in blocks[1:])
+    assert [b.y_codes for b in blocks] == ["uint8", "uint8", "uint8", None] and all(b.relu == 1 for b in blocks)
+    # repacked weights: channels-last codes and per-tap sums of the original int8 codes
+    wq = initializers(m)["block2.wq"].numpy()
+    k = g.initializers[blocks[1].inputs[3]].numpy()
+    assert k.dtype == np.int8 and np.array_equal(k, wq.transpose(0, 2, 3, 1))
+    assert np.array_equal(g.initializers[blocks[1].inputs[4]].numpy(), wq.transpose(0, 2, 3, 1).sum(axis=3))
+    seen = {"input"} | set(g.initializers)
+    for o in g.ops.values():
+        assert all((not na) or na in seen for na in o.inputs), o.name
+        seen.update(o.outputs)
+    shapes = g._edge_shapes([x])
+    assert shapes["block1.xq.nhwc"] == ((1, 16, 16, 64), "int8") and shapes["block4.out"] == ((1, 512, 2, 2), "float32")
+
+
 def test_conv_qdq_pass_needs_parameters_before_the_conv(monkeypatch):
     """A QuantizeLinear scale produced by a node after the Conv cannot be read at
     the Conv's position, so that Conv -> Q -> DQ is left unfused."""
@@ -461,6 +503,45 @@ def test_resnet_qdq_graph_batch64(hip, oracle_lib):
     rows = np.nonzero(am != ae)[0]
     gap = np.abs(el[rows, am[rows]].astype(np.float64) - el[rows, ae[rows]]) / np.abs(el).max()
     assert (gap < 2 * LOGIT_BOUND).all(), list(zip(rows.tolist(), gap.tolist()))
+
+
+@pytest.mark.gpu
+def test_resnet_qdq_graph_int8(hip, oracle_lib):
+    """Config-5 graph at batch 64 with its QDQ blocks on the int8 MFMA kernels
+    (fuse(int8_conv=True)), every output buffer poisoned with NaN, against the
+    exact-mode (fp64, the reference's bits) forward of the same graph without
+    the pass, with the MFMA-mode bounds below; images 0 and 63 also against the
+    graph oracle."""
+    from onnx_translator_amd.nn.graph import Graph
+    from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
+    m = resnet_qdq_model(batch=64)
+    x = np.random.default_rng(4).normal(0, 1, (64, 3, 224, 224)).astype(np.float32)
+    g8 = Graph(ONNXImport(m), ["input"], ["logits", "output"], initializers=initializers(m)).to_device()
+    g8.fuse(int8_conv=True)
+    ge = Graph(ONNXImport(m), ["input"], ["logits", "output"], initializers=initializers(m)).to_device().fuse()
+    with hip.poisoned():
+        l8, p8 = (t.numpy() for t in g8.forward(x))
+        hip.set_exact(True)
+        try:
+            el, ep = (t.numpy() for t in ge.forward(x))
+        finally:
+            hip.set_exact(False)
+    names = [type(o).__name__ for o in g8.ops.values()]
+    assert names.count("QConvBlock") == 4 and names.count("QuantizeNHWC") == 1, names
+    assert np.isfinite(l8).all() and np.isfinite(p8).all(), "unwritten (NaN) elements"
+    np.testing.assert_allclose(p8.sum(axis=1), 1.0, rtol=1e-5)
+    dl = np.abs(l8.astype(np.float64) - el).max() / np.abs(el).max()
+    dp = np.abs(p8.astype(np.float64) - ep).max() / ep.max()
+    print(f"batch-64 int8 blocks vs exact: logits {dl:.2e}, probabilities {dp:.2e}", flush=True)
+    assert dl < LOGIT_BOUND and dp < PROB_BOUND, (dl, dp)
+    am, ae = l8.argmax(axis=1), el.argmax(axis=1)
+    rows = np.nonzero(am != ae)[0]
+    gap = np.abs(el[rows, am[rows]].astype(np.float64) - el[rows, ae[rows]]) / np.abs(el).max()
+    assert (gap < 2 * LOGIT_BOUND).all(), list(zip(rows.tolist(), gap.tolist()))
+    sel = [0, 63]
+    env = run_model(oracle_lib, resnet_qdq_model(batch=2), {"input": (np.ascontiguousarray(x[sel]), "float32")})
+    ref = env["logits"][0]
+    assert np.abs(l8[sel].astype(np.float64) - ref).max() / np.abs(ref).max() < LOGIT_BOUND
 
 
 # MFMA-mode bounds of the batch-64 check, relative to the largest reference
