@@ -394,8 +394,8 @@ __global__ __launch_bounds__(256) void k_qconv(const int8_t* __restrict__ X, con
 
 // ---- the block kernel through an LDS ring -------------------------------------
 // C % 64 == 0.  Block tile 64 channels x 64 pixels, wave w computing the
-// 32x32 tile (w / 2, w % 2).  Per stage of two k steps, wave w fetches one 1 KB
-// group per step (w = 0, 1: weight rows 32 w..; w = 2, 3: pixels 32 (w - 2)..),
+// 32x32 tile (w / 2, w % 2).  Per stage of kQSteps k steps, wave w fetches one
+// 1 KB group per step (w = 0, 1: weight rows 32 w..; w = 2, 3: pixels 32 (w - 2)..),
 // lane l the 16 bytes (row l % 32, k half l / 32) that lane l of an MFMA reads
 // back, so every LDS access is one contiguous 1 KB.  Stages travel through
 // three register sets (loaded three iterations ahead of their LDS write) and
@@ -415,13 +415,15 @@ constexpr QPadTable make_qpad() {
         for (int i = 0; i < 4; i++) t.w[v][i] = (uint32_t)v * 0x01010101u;
     return t;
 }
-__device__ __attribute__((aligned(16))) QPadTable kQPad = make_qpad();    // global (not constant) memory: a load that picks it or X stays a global load
+// (global, not constant, memory: a load that picks it or X stays a global load)
+__device__ __attribute__((aligned(16))) QPadTable kQPad = make_qpad();
+constexpr int kQSteps = 2;     // k steps per LDS stage (4: slower, the prologue covers most of a short block)
 
 template <bool PROJ, int OUT>
-__global__ __launch_bounds__(256) void k_qconv_lds(const int8_t* __restrict__ X, const int8_t* __restrict__ Wk,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_qconv_lds(const int8_t* __restrict__ X, const int8_t* __restrict__ Wk,
                                                    const int8_t* __restrict__ Pk, void* __restrict__ Y, QGeom g,
                                                    QEpi e) {
-    __shared__ __attribute__((aligned(1024))) int8_t ring[3][2][4][1024];
+    __shared__ __attribute__((aligned(1024))) int8_t ring[3][kQSteps][4][1024];
     __shared__ double s_cm[64], s_cp[64];
     __shared__ int s_corr[64], s_corrp[64];
     __shared__ float s_bias[64];
@@ -479,8 +481,8 @@ __global__ __launch_bounds__(256) void k_qconv_lds(const int8_t* __restrict__ X,
     }
     const int8_t* const xrow = X + (size_t)rowb * g.W * g.C + half * 16;
     const int8_t* const pad = reinterpret_cast<const int8_t*>(&kQPad.w[zsh & 0xFF][0]);
-    const int total = g.steps + (PROJ ? g.psteps : 0);     // even: C % 64 == 0
-    const int nst = total >> 1;
+    const int total = g.steps + (PROJ ? g.psteps : 0);
+    const int nst = (total + kQSteps - 1) / kQSteps;
     // Next step to load: st, its channel step cs and tap (kh, kw); past the last
     // step the last is loaded again (its copy is never read).  One global load
     // on every path keeps the compiler's count of loads in flight exact, so its
@@ -505,9 +507,9 @@ __global__ __launch_bounds__(256) void k_qconv_lds(const int8_t* __restrict__ X,
         }
         return v;
     };
-    auto put = [&](int slot, const i32x4 (&v)[2]) {
+    auto put = [&](int slot, const i32x4 (&v)[kQSteps]) {
 #pragma unroll
-        for (int u = 0; u < 2; u++) *reinterpret_cast<i32x4*>(&ring[slot][u][wave][lane * 16]) = v[u];
+        for (int u = 0; u < kQSteps; u++) *reinterpret_cast<i32x4*>(&ring[slot][u][wave][lane * 16]) = v[u];
     };
 
     // skip values of this wave's tile, loaded before the k loop
@@ -531,39 +533,37 @@ __global__ __launch_bounds__(256) void k_qconv_lds(const int8_t* __restrict__ X,
         acc[r] = 0;
         accp[r] = 0;
     }
-    // Stage k (steps 2k, 2k + 1) is read from LDS slot k % 3 at iteration k;
+    // Stage k (steps kQSteps k ..) is read from LDS slot k % 3 at iteration k;
     // iteration k first writes stage k + 1 into slot (k + 1) % 3 (last read at
     // iteration k - 2, before the previous barrier) from register set
     // (k + 1) % 3, loaded three iterations earlier, and reloads that set with
     // stage k + 4.  The loop is unrolled by three so that every register set
     // and slot index is static (a rotated copy would wait for every load in
-    // flight), and runs whole rounds (loads on every path, for the same reason).
-    i32x4 R0[2], R1[2], R2[2];
-    R0[0] = gload();
-    R0[1] = gload();
+    // flight), and runs whole rounds (loads on every path, for the same reason);
+    // steps past the last are not multiplied.
+    i32x4 R0[kQSteps], R1[kQSteps], R2[kQSteps];
+#pragma unroll
+    for (int u = 0; u < kQSteps; u++) R0[u] = gload();
     put(0, R0);
-    R1[0] = gload();
-    R1[1] = gload();
-    R2[0] = gload();
-    R2[1] = gload();
-    R0[0] = gload();
-    R0[1] = gload();
-    auto body = [&](int k, int sr, int sw, i32x4 (&w)[2]) {
+#pragma unroll
+    for (int u = 0; u < kQSteps; u++) R1[u] = gload();
+#pragma unroll
+    for (int u = 0; u < kQSteps; u++) R2[u] = gload();
+#pragma unroll
+    for (int u = 0; u < kQSteps; u++) R0[u] = gload();
+    auto body = [&](int k, int sr, int sw, i32x4 (&w)[kQSteps]) {
         put(sw, w);
-        w[0] = gload();
-        w[1] = gload();
+#pragma unroll
+        for (int u = 0; u < kQSteps; u++) w[u] = gload();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        const i32x4 a0 = *reinterpret_cast<const i32x4*>(&ring[sr][0][wm][lane * 16]);
-        const i32x4 b0 = *reinterpret_cast<const i32x4*>(&ring[sr][0][2 + wp][lane * 16]);
-        const i32x4 a1 = *reinterpret_cast<const i32x4*>(&ring[sr][1][wm][lane * 16]);
-        const i32x4 b1 = *reinterpret_cast<const i32x4*>(&ring[sr][1][2 + wp][lane * 16]);
-        if (k >= nst) return;                      // a round-up iteration: no stage
-        if (!PROJ || 2 * k < g.steps) {
-            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc, 0, 0, 0);
-        } else {
-            accp = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, accp, 0, 0, 0);
-            accp = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, accp, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < kQSteps; u++) {
+            const int stp = kQSteps * k + u;
+            const i32x4 a = *reinterpret_cast<const i32x4*>(&ring[sr][u][wm][lane * 16]);
+            const i32x4 b = *reinterpret_cast<const i32x4*>(&ring[sr][u][2 + wp][lane * 16]);
+            if (stp >= total) break;
+            if (!PROJ || stp < g.steps) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc, 0, 0, 0);
+            else accp = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, accp, 0, 0, 0);
         }
     };
     for (int k = 0; k < nst; k += 3) {
