@@ -111,9 +111,12 @@ __device__ __forceinline__ QOut qout_parm(const float* qs, const void* qz, int k
 }
 
 // ---- QuantizeLinear into channels-last codes --------------------------------
-// Block: one image, 64 consecutive pixels x 32 channels.  Thread t reads pixel
-// t % 64 of channels t / 64 + 4 e (coalesced along the pixels), the bytes go
-// through LDS, and 128 threads write the 64 pixels' 32-byte channel runs.
+// Block: one image, 64 consecutive pixels x 32 channels.  VEC (H W % 4 == 0):
+// thread t reads 4 consecutive pixels (one float4) of channel t / 16 + 16 e, so
+// 16 lanes cover a channel's 256 contiguous bytes; otherwise one pixel of
+// channels t / 64 + 4 e.  The codes go through LDS ([pixel][channel] bytes) and
+// 128 threads write the 64 pixels' 32-byte channel runs as 16-byte stores.
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_quant_nhwc(const float* __restrict__ X, int8_t* __restrict__ Y,
                                                     const float* __restrict__ qs, const void* __restrict__ qz,
                                                     int kind, int C, int HW) {
@@ -121,15 +124,29 @@ __global__ __launch_bounds__(256) void k_quant_nhwc(const float* __restrict__ X,
     const int t = threadIdx.x;
     const int n = blockIdx.z, c0 = blockIdx.y * 32, px0 = blockIdx.x * 64;
     const QOut q = qout_parm(qs, qz, kind);
-    const int px = t & 63, cq = t >> 6;
-    const bool ok = px0 + px < HW;
-    const float* xp = X + ((size_t)n * C + c0) * HW + px0 + px;
-    uint8_t* tb = reinterpret_cast<uint8_t*>(&tile[px][0]);
+    const float* xb = X + ((size_t)n * C + c0) * HW + px0;
+    if constexpr (VEC) {
+        const int quad = t & 15, cq = t >> 4;
+        const bool ok = px0 + 4 * quad < HW;      // HW % 4 == 0: a quad is all in or all out
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const int c = cq + 4 * e;
-        const float v = ok ? xp[(size_t)c * HW] : 0.0f;
-        tb[c] = (uint8_t)qout_byte(v, q);
+        for (int e = 0; e < 2; e++) {
+            const int c = cq + 16 * e;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (ok) v = *reinterpret_cast<const float4*>(xb + (size_t)c * HW + 4 * quad);
+            const float f[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                reinterpret_cast<uint8_t*>(&tile[4 * quad + i][0])[c] = (uint8_t)qout_byte(f[i], q);
+        }
+    } else {
+        const int px = t & 63, cq = t >> 6;
+        const bool ok = px0 + px < HW;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int c = cq + 4 * e;
+            const float v = ok ? xb[(size_t)c * HW + px] : 0.0f;
+            reinterpret_cast<uint8_t*>(&tile[px][0])[c] = (uint8_t)qout_byte(v, q);
+        }
     }
     __syncthreads();
     if (t < 128) {
@@ -659,9 +676,13 @@ extern "C" void quantize_linear_nhwc_forward(const Tensor* X, const Tensor* Scal
     if (X->size == 0) return;
     const int HW = H * W;
     const dim3 grid((unsigned)((HW + 63) / 64), (unsigned)(C / 32), (unsigned)N);
-    hipLaunchKernelGGL(k_quant_nhwc, grid, dim3(256), 0, stream(), (const float*)X->data, (int8_t*)Y->data,
-                       (const float*)Scale->data, (ZeroPoint && ZeroPoint->data) ? ZeroPoint->data : nullptr, kind,
-                       C, HW);
+    const void* zp = (ZeroPoint && ZeroPoint->data) ? ZeroPoint->data : nullptr;
+    if (HW % 4 == 0 && ((uintptr_t)X->data & 15) == 0)
+        hipLaunchKernelGGL((k_quant_nhwc<true>), grid, dim3(256), 0, stream(), (const float*)X->data,
+                           (int8_t*)Y->data, (const float*)Scale->data, zp, kind, C, HW);
+    else
+        hipLaunchKernelGGL((k_quant_nhwc<false>), grid, dim3(256), 0, stream(), (const float*)X->data,
+                           (int8_t*)Y->data, (const float*)Scale->data, zp, kind, C, HW);
     check_launch(name);
 }
 
