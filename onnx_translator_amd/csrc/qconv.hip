@@ -556,8 +556,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     // (k + 1) % 3, loaded three iterations earlier, and reloads that set with
     // stage k + 4.  The loop is unrolled by three so that every register set
     // and slot index is static (a rotated copy would wait for every load in
-    // flight), and runs whole rounds (loads on every path, for the same reason);
-    // steps past the last are not multiplied.
+    // flight), with loads on every path inside it for the same reason; steps
+    // past the last are not multiplied.
     i32x4 R0[kQSteps], R1[kQSteps], R2[kQSteps];
 #pragma unroll
     for (int u = 0; u < kQSteps; u++) R0[u] = gload();
@@ -583,11 +583,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
             else accp = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, accp, 0, 0, 0);
         }
     };
-    for (int k = 0; k < nst; k += 3) {
+    int k = 0;
+    for (; k + 3 <= nst; k += 3) {
         body(k, 0, 1, R1);
         body(k + 1, 1, 2, R2);
         body(k + 2, 2, 0, R0);
     }
+    // the last one or two stages (their waits may be whole: no loop follows)
+    if (k < nst) body(k, 0, 1, R1);
+    if (k + 1 < nst) body(k + 1, 1, 2, R2);
 
     if (pme >= g.P) return;
     QOut qo;
