@@ -304,3 +304,92 @@ def test_qconv_block_config5_size(hip, case):
         assert_close(y, ref, O.F32, what=f"qconv {name}: every element against the exact sequence")
     finally:
         dev.free()
+
+
+def test_qconv_blocks_under_graph_capture(hip):
+    """The channels-last quantize and two chained blocks (skip + codes out, then
+    projection + f32 out) captured into a HIP graph on the library's stream and
+    replayed three times with the outputs overwritten before each replay and
+    eager library work between replays: every replay equals the eager results
+    bit for bit (the calls allocate nothing and record no memset)."""
+    import torch
+    _bind(hip.lib)
+    torch.cuda.init()
+    side = torch.cuda.Stream()
+    L = hip.lib
+    L.tensor_ops_hip_set_stream(ctypes.c_void_p(side.cuda_stream))
+    keep = []
+    dev = _Dev(hip)
+
+    def wrap(t, dt):
+        shape = list(t.shape)
+        p = L.tensor_wrap_device(ctypes.c_void_p(t.data_ptr()), (ctypes.c_int * len(shape))(*shape), len(shape), dt)
+        assert p
+        keep.append(p)
+        return p
+
+    try:
+        with torch.cuda.stream(side):
+            rng = np.random.default_rng(17)
+            N, C, H, M2 = 4, 64, 20, 128
+            x = torch.from_numpy(np.abs(rng.normal(0, 1.2, (N, C, H, H))).astype(np.float32)).cuda()
+            sx = np.float32(8.0 / 255)
+            w1, s1 = _weights(rng, C, C, 3, 3)
+            w2, s2 = _weights(rng, M2, C, 3, 3)
+            p2, sp2 = _weights(rng, M2, C, 1, 1)
+            b1 = rng.normal(0, 1 / 64, C).astype(np.float32)
+            b2 = rng.normal(0, 1 / 64, M2).astype(np.float32)
+            xs_t = torch.empty((N, H, H, C), dtype=torch.int8, device="cuda")
+            c1_t = torch.empty((N, H, H, C), dtype=torch.int8, device="cuda")
+            OH = (H - 1) // 2 + 1
+            y_t = torch.empty((N, M2, OH, OH), dtype=torch.float32, device="cuda")
+            tx, txs, tc1, ty = wrap(x, O.F32), wrap(xs_t, O.I8), wrap(c1_t, O.I8), wrap(y_t, O.F32)
+            tsx, tzx = dev.put(np.array([sx], np.float32), O.F32), dev.put(np.array([0]), O.U8)
+            tsy, tzy = dev.put(np.array([np.float32(0.04)], np.float32), O.F32), dev.put(np.array([0]), O.U8)
+            blk1, blk2 = QConvBlock(), QConvBlock()
+            blk1.x_scale, blk1.x_zero, blk1.x_codes = tsx, tzx, O.U8
+            blk1.w, blk1.w_sum = _pack(hip, dev, w1)
+            blk1.w_scale, blk1.bias, blk1.relu = dev.put(s1, O.F32), dev.put(b1, O.F32), 1
+            blk1.skip = tx
+            blk1.q_scale, blk1.q_zero, blk1.y_codes = tsy, tzy, O.U8
+            blk2.x_scale, blk2.x_zero, blk2.x_codes = tsy, tzy, O.U8
+            blk2.w, blk2.w_sum = _pack(hip, dev, w2)
+            blk2.w_scale, blk2.bias, blk2.relu = dev.put(s2, O.F32), dev.put(b2, O.F32), 1
+            blk2.p, blk2.p_sum = _pack(hip, dev, p2)
+            blk2.p_scale = dev.put(sp2, O.F32)
+            p1, k1 = _params((1, 1, 1, 1), (1, 1))
+            pp2, k2 = _params((1, 1, 1, 1), (2, 2))
+            torch.cuda.synchronize()
+
+            def step():
+                L.quantize_linear_nhwc_forward(tx, tsx, tzx, O.U8, txs)
+                L.qconv_block_forward(txs, ctypes.byref(blk1), tc1, ctypes.byref(p1))
+                L.qconv_block_forward(tc1, ctypes.byref(blk2), ty, ctypes.byref(pp2))
+
+            L.tensor_ops_hip_clear_error()
+            step()
+            torch.cuda.synchronize()
+            assert not hip.last_error(), hip.last_error()
+            outs = {"xs": xs_t, "c1": c1_t, "y": y_t}
+            eager = {k: v.cpu().numpy().copy() for k, v in outs.items()}
+            assert np.isfinite(eager["y"]).all()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                step()
+            assert not hip.last_error(), hip.last_error()
+            for r in range(3):
+                for v in outs.values():
+                    v.view(torch.uint8).fill_(0xA5)
+                torch.cuda.synchronize()
+                g.replay()
+                torch.cuda.synchronize()
+                for k, v in outs.items():
+                    assert np.array_equal(v.cpu().numpy().view(np.uint8), eager[k].view(np.uint8)), f"replay {r} {k}"
+                L.quantize_linear_nhwc_forward(tx, tsy, tzy, O.U8, txs)      # eager work between replays
+                torch.cuda.synchronize()
+            del k1, k2
+    finally:
+        for p in keep:
+            L.free_tensor(p)
+        dev.free()
+        L.tensor_ops_hip_set_stream(None)

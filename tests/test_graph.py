@@ -261,6 +261,36 @@ def test_int8_conv_pass(monkeypatch):
     assert shapes["block1.xq.nhwc"] == ((1, 16, 16, 64), "int8") and shapes["block4.out"] == ((1, 512, 2, 2), "float32")
 
 
+def test_int8_conv_pass_only_where_it_applies(monkeypatch):
+    """Blocks whose input has a channel count that is not a multiple of 32 stay
+    as they are (blocks 1 and 2 of a 48-channel stem); block 3 then takes its
+    codes from a QuantizeNHWC of block 2's f32 output, and block 4 from block
+    3.  Without a device (Graph.device False) the pass does nothing."""
+    from onnx_translator_amd.nn import Graph, Tensor, Tensor_
+    from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
+    monkeypatch.setattr(Tensor, "to_device", lambda self: self)
+    m = resnet_qdq_model(batch=1, image=64, widths=(48, 128, 256, 512))
+    x = Tensor_(1, 3, 64, 64, dtype="float32")
+    g0 = Graph(ONNXImport(m), ["input"], ["output"], initializers=initializers(m))
+    g0.fuse(False, False, False, False, False, False, False, int8_conv=True)._fuse([x])
+    assert not any(type(o).__name__ == "QConvBlock" for o in g0.ops.values())
+    g = Graph(ONNXImport(m), ["input"], ["output"], initializers=initializers(m))
+    g.device = True
+    assert g._fuse_qconv_blocks(g._edge_shapes([x]), g._consumers())
+    ops = list(g.ops.values())
+    blocks = [o for o in ops if type(o).__name__ == "QConvBlock"]
+    qn = [o for o in ops if type(o).__name__ == "QuantizeNHWC"]
+    assert len(blocks) == 2 and len(qn) == 1
+    assert qn[0].inputs[0] == "block2.out" and qn[0].outputs == ["block3.xq.nhwc"]
+    assert blocks[0].outputs == ["block4.xq.nhwc"] and blocks[1].outputs == ["block4.out"]
+    names = [type(o).__name__ for o in ops]
+    assert names.count("QuantizeLinear") == 2 and names.count("Conv") == 1 + 2 + 1   # stem, block 1, block 2 (+ proj)
+    seen = {"input"} | set(g.initializers)
+    for o in ops:
+        assert all((not na) or na in seen for na in o.inputs), o.name
+        seen.update(o.outputs)
+
+
 def test_conv_qdq_pass_needs_parameters_before_the_conv(monkeypatch):
     """A QuantizeLinear scale produced by a node after the Conv cannot be read at
     the Conv's position, so that Conv -> Q -> DQ is left unfused."""
