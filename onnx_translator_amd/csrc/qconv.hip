@@ -159,6 +159,43 @@ __global__ __launch_bounds__(256) void k_quant_nhwc(const float* __restrict__ X,
     }
 }
 
+// C % 64 == 0 and H W % 4 == 0: a block covers 64 pixels x 64 channels; thread t
+// loads 4 consecutive pixels (one float4) of channels 4 (t / 16) .. + 3 (16 lanes
+// per 256-byte channel row), packs each pixel's 4 codes into one word for LDS,
+// and every thread then stores 16 of the 64 pixels' 64-byte channel runs.
+__global__ __launch_bounds__(256) void k_quant_nhwc64(const float* __restrict__ X, int8_t* __restrict__ Y,
+                                                      const float* __restrict__ qs, const void* __restrict__ qz,
+                                                      int kind, int C, int HW) {
+    __shared__ uint32_t tile[64][17];         // 64 pixels x 64 bytes (+4: distinct banks per pixel)
+    const int t = threadIdx.x;
+    const int n = blockIdx.z, c0 = blockIdx.y * 64, px0 = blockIdx.x * 64;
+    const QOut q = qout_parm(qs, qz, kind);
+    const int quad = t & 15, cg = t >> 4;
+    const bool ok = px0 + 4 * quad < HW;          // HW % 4 == 0: a quad is all in or all out
+    const float* xb = X + ((size_t)n * C + c0 + 4 * cg) * HW + px0 + 4 * quad;
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        v[j] = ok ? *reinterpret_cast<const float4*>(xb + (size_t)j * HW) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float f = i == 0 ? v[j].x : i == 1 ? v[j].y : i == 2 ? v[j].z : v[j].w;
+            w |= qout_byte(f, q) << (8 * j);
+        }
+        tile[4 * quad + i][cg] = w;
+    }
+    __syncthreads();
+    const int p = t >> 2, part = t & 3;
+    if (px0 + p < HW) {
+        const uint32_t* s = &tile[p][4 * part];
+        *reinterpret_cast<uint4*>(Y + ((size_t)n * HW + px0 + p) * C + c0 + 16 * part) =
+            make_uint4(s[0], s[1], s[2], s[3]);
+    }
+}
+
 // ---- weight packing ------------------------------------------------------------
 // One block per output channel: [C, KH, KW] codes -> [KH, KW, C], and the sum
 // of each tap's C codes (wave w sums taps w, w + 4, ...).
@@ -681,7 +718,11 @@ extern "C" void quantize_linear_nhwc_forward(const Tensor* X, const Tensor* Scal
     const int HW = H * W;
     const dim3 grid((unsigned)((HW + 63) / 64), (unsigned)(C / 32), (unsigned)N);
     const void* zp = (ZeroPoint && ZeroPoint->data) ? ZeroPoint->data : nullptr;
-    if (HW % 4 == 0 && ((uintptr_t)X->data & 15) == 0)
+    if (HW % 4 == 0 && C % 64 == 0 && ((uintptr_t)X->data & 15) == 0)
+        hipLaunchKernelGGL(k_quant_nhwc64, dim3((unsigned)((HW + 63) / 64), (unsigned)(C / 64), (unsigned)N),
+                           dim3(256), 0, stream(), (const float*)X->data, (int8_t*)Y->data,
+                           (const float*)Scale->data, zp, kind, C, HW);
+    else if (HW % 4 == 0 && ((uintptr_t)X->data & 15) == 0)
         hipLaunchKernelGGL((k_quant_nhwc<true>), grid, dim3(256), 0, stream(), (const float*)X->data,
                            (int8_t*)Y->data, (const float*)Scale->data, zp, kind, C, HW);
     else

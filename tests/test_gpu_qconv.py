@@ -165,7 +165,7 @@ def test_quantize_nhwc_matches_quantize_linear(hip, oracle_lib):
     try:
         for shape, dt, s, z in (((2, 64, 9, 13), O.U8, 8 / 255, 0), ((1, 96, 8, 8), O.U8, 0.05, 37),
                                 ((3, 32, 5, 7), O.I8, 0.04, -3), ((1, 64, 64, 3), O.U8, 0.02, 128),
-                                ((2, 32, 10, 10), O.U8, 0.03, 5)):
+                                ((2, 32, 10, 10), O.U8, 0.03, 5), ((2, 128, 10, 10), O.I8, 0.05, -7)):
             x = rng.normal(0.5, 2.0, shape).astype(np.float32)
             x.flat[::97] = np.float32(s) * (np.rint(x.flat[::97] / s) + 0.5)      # ties
             ref = oracle_lib.qdq("quantize", x, O.F32, np.float32(s), O.F32, np.array(z), dt, dt)
