@@ -448,10 +448,12 @@ __global__ __launch_bounds__(256) void k_qconv(const int8_t* __restrict__ X, con
 
 // ---- the block kernel through an LDS ring -------------------------------------
 // C % 64 == 0.  Block tile 64 channels x 64 pixels, wave w computing the
-// 32x32 tile (w / 2, w % 2).  Per stage of kQSteps k steps, wave w fetches one
-// 1 KB group per step (w = 0, 1: weight rows 32 w..; w = 2, 3: pixels 32 (w - 2)..),
-// lane l the 16 bytes (row l % 32, k half l / 32) that lane l of an MFMA reads
-// back, so every LDS access is one contiguous 1 KB.  Stages travel through
+// 32x32 tile (w / 2, w % 2).  A stage is two k steps of one tap: 64 contiguous
+// bytes per weight row and per pixel.  Wave w fetches its group's 32 rows of a
+// stage (w = 0, 1: weight rows 32 w..; w = 2, 3: pixels 32 (w - 2)..) with two
+// loads in which four lanes read one row's 64 bytes, and writes each 16 bytes
+// to where lane (row, k half) of an MFMA reads them back (one contiguous
+// 512 bytes per half-wave).  Stages travel through
 // three register sets (loaded three iterations ahead of their LDS write) and
 // three LDS slots.  A padded tap loads 16 bytes of zx - shift from a table,
 // the stored form of the code whose dequantized value is 0.  The k step of
@@ -472,12 +474,16 @@ constexpr QPadTable make_qpad() {
 // (global, not constant, memory: a load that picks it or X stays a global load)
 __device__ __attribute__((aligned(16))) QPadTable kQPad = make_qpad();
 constexpr int kQSteps = 2;     // k steps per LDS stage (4: slower, the prologue covers most of a short block)
+// LDS stage layout [step u][group][half h][32 rows][16 B] with pitches that put
+// the 16 lanes of one 16-byte write pass (4 rows x 4 chunks) on distinct banks:
+// half 512 + 64, group 2 halves, step 4 groups + 128 (128 mod 256)
+constexpr int kQHalf = 576, kQGroup = 2 * kQHalf, kQStep = 4 * kQGroup + 128, kQSlot = kQSteps * kQStep;
 
 template <bool PROJ, int OUT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_qconv_lds(const int8_t* __restrict__ X, const int8_t* __restrict__ Wk,
                                                    const int8_t* __restrict__ Pk, void* __restrict__ Y, QGeom g,
                                                    QEpi e) {
-    __shared__ __attribute__((aligned(1024))) int8_t ring[3][kQSteps][4][1024];
+    __shared__ __attribute__((aligned(1024))) int8_t ring[3 * kQSlot];
     __shared__ double s_cm[64], s_cp[64];
     __shared__ int s_corr[64], s_corrp[64];
     __shared__ float s_bias[64];
@@ -517,41 +523,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
         }
     }
 
-    // the load this lane issues per step: weight row (waves 0, 1) or pixel (2, 3)
+    // The loads this lane issues per stage: rows (weight rows for waves 0, 1,
+    // pixels for waves 2, 3) rr[j] = 16 j + lane / 4 of the wave's 32, the 16
+    // bytes at chunk lane % 4 of the stage's 64 contiguous bytes (step u =
+    // chunk / 2, half h = chunk % 2): four lanes read one 64-byte run.
     const bool is_a = wave < 2;
     const int K = khw * g.C;
-    const int8_t* const arow = Wk + (size_t)(m0 + 32 * wave + col) * K + half * 16;
-    const int8_t* const prow = PROJ ? Pk + (size_t)(m0 + 32 * wave + col) * g.C + half * 16 : arow;
-    int ih0 = -(1 << 29), iw0 = 0, rowb = 0;
-    {
-        const int p = p0 + 32 * (wave - 2) + col;
+    const int chunk = lane & 3;
+    // row rr[1] = rr[0] + 16: weight rows 16 K bytes on, LDS rows 256 bytes on
+    const int8_t* const arow = Wk + (size_t)(m0 + 32 * wave + (lane >> 2)) * K + chunk * 16;
+    const int8_t* const prow = PROJ ? Pk + (size_t)(m0 + 32 * wave + (lane >> 2)) * g.C + chunk * 16 : arow;
+    const uint32_t loff =                     // LDS byte offset of row rr[0] in a slot
+        (uint32_t)((chunk >> 1) * kQStep + wave * kQGroup + (chunk & 1) * kQHalf + (lane >> 2) * 16);
+    const int8_t* xrow[2];
+    int ih0[2], iw0[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int rr = 16 * j + (lane >> 2);
+        ih0[j] = -(1 << 29);
+        iw0[j] = 0;
+        int rowb = 0;
+        const int p = p0 + 32 * (wave - 2) + rr;
         if (!is_a && p < g.P) {
             const int n = (int)g.fd_ohw.div((uint32_t)p), r = p - n * g.OHW;
             const int oh = (int)g.fd_ow.div((uint32_t)r), ow = r - oh * g.OW;
-            ih0 = oh * g.sh - g.pt;
-            iw0 = ow * g.sw - g.pl;
+            ih0[j] = oh * g.sh - g.pt;
+            iw0[j] = ow * g.sw - g.pl;
             rowb = n * g.H;
         }
+        xrow[j] = X + (size_t)rowb * g.W * g.C + chunk * 16;
     }
-    const int8_t* const xrow = X + (size_t)rowb * g.W * g.C + half * 16;
     const int8_t* const pad = reinterpret_cast<const int8_t*>(&kQPad.w[zsh & 0xFF][0]);
     const int total = g.steps + (PROJ ? g.psteps : 0);
     const int nst = (total + kQSteps - 1) / kQSteps;
-    // Next step to load: st, its channel step cs and tap (kh, kw); past the last
-    // step the last is loaded again (its copy is never read).  One global load
-    // on every path keeps the compiler's count of loads in flight exact, so its
-    // waits stay partial.
-    int st = 0, cs = 0, kh = 0, kw = 0;
-    auto gload = [&]() -> i32x4 {
-        const bool main = !PROJ || st < g.steps;
-        const int ih = ih0 + (main ? kh * g.dh : g.pt), iw = iw0 + (main ? kw * g.dw : g.pl);
-        const bool ok = (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
-        const int8_t* pb = ok ? xrow + ((size_t)ih * g.W + iw) * g.C + cs * 32 : pad;
-        const int8_t* pa = main ? arow + (size_t)st * 32 : prow + cs * 32;
-        const i32x4 v = *reinterpret_cast<const i32x4*>(is_a ? pa : pb);
-        if (st + 1 < total) {
-            st++;
-            if (++cs == g.csteps) {
+    // Next stage to load: sst, its first channel step cs (even: a stage is two
+    // steps of one tap) and tap (kh, kw); past the last stage the last is
+    // loaded again (its copy is never read).  One global load per row on every
+    // path keeps the compiler's count of loads in flight exact, so its waits
+    // stay partial.
+    int sst = 0, cs = 0, kh = 0, kw = 0;
+    auto gload = [&](i32x4 (&v)[2]) {
+        const bool main = !PROJ || 2 * sst < g.steps;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int ih = ih0[j] + (main ? kh * g.dh : g.pt), iw = iw0[j] + (main ? kw * g.dw : g.pl);
+            const bool ok = (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+            const int8_t* pb = ok ? xrow[j] + ((size_t)ih * g.W + iw) * g.C + cs * 32 : pad;
+            const int8_t* pa = main ? arow + ((size_t)j * 16 * K + (size_t)sst * 64)
+                                    : prow + ((size_t)j * 16 * g.C + cs * 32);
+            v[j] = *reinterpret_cast<const i32x4*>(is_a ? pa : pb);
+        }
+        if (sst + 1 < nst) {
+            sst++;
+            cs += 2;
+            if (cs == g.csteps) {
                 cs = 0;
                 if (++kw == g.KW) {
                     kw = 0;
@@ -559,11 +584,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
                 }
             }
         }
-        return v;
     };
-    auto put = [&](int slot, const i32x4 (&v)[kQSteps]) {
+    auto put = [&](int slot, const i32x4 (&v)[2]) {
 #pragma unroll
-        for (int u = 0; u < kQSteps; u++) *reinterpret_cast<i32x4*>(&ring[slot][u][wave][lane * 16]) = v[u];
+        for (int j = 0; j < 2; j++) *reinterpret_cast<i32x4*>(&ring[slot * kQSlot + loff + 256 * j]) = v[j];
     };
 
     // skip values of this wave's tile, loaded before the k loop
@@ -595,26 +619,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     // and slot index is static (a rotated copy would wait for every load in
     // flight), with loads on every path inside it for the same reason; steps
     // past the last are not multiplied.
-    i32x4 R0[kQSteps], R1[kQSteps], R2[kQSteps];
-#pragma unroll
-    for (int u = 0; u < kQSteps; u++) R0[u] = gload();
+    i32x4 R0[2], R1[2], R2[2];
+    gload(R0);
     put(0, R0);
-#pragma unroll
-    for (int u = 0; u < kQSteps; u++) R1[u] = gload();
-#pragma unroll
-    for (int u = 0; u < kQSteps; u++) R2[u] = gload();
-#pragma unroll
-    for (int u = 0; u < kQSteps; u++) R0[u] = gload();
-    auto body = [&](int k, int sr, int sw, i32x4 (&w)[kQSteps]) {
+    gload(R1);
+    gload(R2);
+    gload(R0);
+    // MFMA operand of lane l in a group: row l % 32, k half l / 32
+    const uint32_t rdo = (uint32_t)((lane >> 5) * kQHalf + (lane & 31) * 16);
+    auto body = [&](int k, int sr, int sw, i32x4 (&w)[2]) {
         put(sw, w);
-#pragma unroll
-        for (int u = 0; u < kQSteps; u++) w[u] = gload();
+        gload(w);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
         for (int u = 0; u < kQSteps; u++) {
             const int stp = kQSteps * k + u;
-            const i32x4 a = *reinterpret_cast<const i32x4*>(&ring[sr][u][wm][lane * 16]);
-            const i32x4 b = *reinterpret_cast<const i32x4*>(&ring[sr][u][2 + wp][lane * 16]);
+            const int8_t* base = &ring[sr * kQSlot + u * kQStep + rdo];
+            const i32x4 a = *reinterpret_cast<const i32x4*>(base + wm * kQGroup);
+            const i32x4 b = *reinterpret_cast<const i32x4*>(base + (2 + wp) * kQGroup);
             if (stp >= total) break;
             if (!PROJ || stp < g.steps) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc, 0, 0, 0);
             else accp = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, accp, 0, 0, 0);
