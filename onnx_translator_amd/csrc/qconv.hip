@@ -480,7 +480,7 @@ constexpr int kQSteps = 2;     // k steps per LDS stage (4: slower, the prologue
 constexpr int kQHalf = 576, kQGroup = 2 * kQHalf, kQStep = 4 * kQGroup + 128, kQSlot = kQSteps * kQStep;
 
 template <bool PROJ, int OUT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_qconv_lds(const int8_t* __restrict__ X, const int8_t* __restrict__ Wk,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PROJ && OUT == 0 ? 3 : 4))) void k_qconv_lds(const int8_t* __restrict__ X, const int8_t* __restrict__ Wk,
                                                    const int8_t* __restrict__ Pk, void* __restrict__ Y, QGeom g,
                                                    QEpi e) {
     __shared__ __attribute__((aligned(1024))) int8_t ring[3 * kQSlot];
