@@ -811,7 +811,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
 // non-finite, input).  Output register r of lane l: block r / 16, channel
 // 8*((r%16)/4) + r%4 + 4*(l/32), pixel l%32 of that block's group.
 constexpr int kStemRows = 13, kStemCols = 232;   // LDS patch per input channel: rows x columns
-template <int C, int KH, int KW, int S>
+template <int C, int KH, int KW, int S, bool ONE_M>
 __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ X, const float* __restrict__ Wt,
                                                    const float* __restrict__ Bv, float* __restrict__ Y, ConvTiled g,
                                                    int tiles_per_img, int ntm, int tiles, uint32_t xbytes,
@@ -853,7 +853,7 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
     constexpr int NW = 8, WROWS = BM / NW, WCOLJ = (K + 63) / 64;
     constexpr int PROWS = C * PRM, PRW = (PROWS + NW - 1) / NW, PCOLJ = (PCM + 63) / 64;
     float wv[WROWS][WCOLJ], pv[PRW][PCOLJ], bv = 0.0f;
-    auto load = [&](const Tile& T) {
+    auto load_w = [&](const Tile& T) {
         if (t < BM) bv = (Bv && T.m0 + t < g.Mg) ? Bv[T.m0 + t] : 0.0f;
 #pragma unroll
         for (int i = 0; i < WROWS; i++) {
@@ -866,6 +866,8 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
                 wv[i][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0));
             }
         }
+    };
+    auto load_p = [&](const Tile& T) {
 #pragma unroll
         for (int i = 0; i < PRW; i++) {
             const int row = wave + i * NW;
@@ -880,7 +882,7 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
             }
         }
     };
-    auto store = [&]() {
+    auto store_w = [&]() {
         if (t < BM) Bs[t] = bv;
 #pragma unroll
         for (int i = 0; i < WROWS; i++)
@@ -889,6 +891,8 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
                 const int k = lane + 64 * j;
                 if (k < K) As[(wave + i * NW) * KA + k] = wv[i][j];
             }
+    };
+    auto store_p = [&]() {
 #pragma unroll
         for (int i = 0; i < PRW; i++)
 #pragma unroll
@@ -901,17 +905,26 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
     int slot = blockIdx.x;
     if (slot >= tiles) return;
     Tile T = tile_of(slot);
-    load(T);
-    store();
+    load_w(T);
+    load_p(T);
+    store_w();
+    store_p();
     __syncthreads();
     const float* pa = &As[(wm * 32 + lr) * KA];
+    float bias_r[16];
+    if constexpr (ONE_M) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) bias_r[r] = Bs[wm * 32 + 8 * (r >> 2) + (r & 3) + 4 * lk];
+    }
     while (true) {
         // the next tile's operands go to registers while this one is multiplied
+        // (with one channel tile, ONE_M, the weights stay in LDS from the start)
         const int next = slot + (int)gridDim.x;
         Tile Tn = T;
         if (next < tiles) {
             Tn = tile_of(next);
-            load(Tn);
+            if (!ONE_M) load_w(Tn);
+            load_p(Tn);
         }
         const int q = min(T.q0 + pw + lk * 32 + lr, g.OHW - 1);
         const int oh = (int)g.fd_ow.div((uint32_t)q), ow = q - oh * g.OW;
@@ -919,22 +932,84 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
         floatx32 acc;
 #pragma unroll
         for (int r = 0; r < 32; r++) acc[r] = 0.0f;
-        // k = (c, kh, kw): one rolled trip per input channel (bounded read-ahead,
-        // so the next tile's operands fit beside it), its KH x KW taps unrolled
+        // k = (c, kh, kw).  Without the next tile's weights in registers (ONE_M),
+        // unrolled: each row of KW taps' operands is read from LDS while the row
+        // before it is multiplied.  Otherwise one rolled trip per input channel
+        // (bounded read-ahead, so the next tile's operands fit beside it).
+        if constexpr (!ONE_M) {
 #pragma nounroll
-        for (int c = 0; c < C; c++) {
-            const float* ac = pa + c * KH * KW;
-            const float* bc = pb + c * PRM * PCM;
+            for (int c = 0; c < C; c++) {
+                const float* ac = pa + c * KH * KW;
+                const float* bc = pb + c * PRM * PCM;
 #pragma unroll
-            for (int kh = 0; kh < KH; kh++)
+                for (int kh = 0; kh < KH; kh++)
 #pragma unroll
-                for (int kw = 0; kw < KW; kw++)
-                    acc = __builtin_amdgcn_mfma_f32_32x32x1f32(ac[kh * KW + kw], bc[kh * PCM + kw], acc, 0, 0, 0);
+                    for (int kw = 0; kw < KW; kw++)
+                        acc = __builtin_amdgcn_mfma_f32_32x32x1f32(ac[kh * KW + kw], bc[kh * PCM + kw], acc, 0, 0, 0);
+            }
+        } else {
+        float ra[2][KW], rb[2][KW];
+#pragma unroll
+        for (int kw = 0; kw < KW; kw++) {
+            ra[0][kw] = pa[kw];
+            rb[0][kw] = pb[kw];
+        }
+#pragma unroll
+        for (int row = 0; row < C * KH; row++) {
+            const int cur = row & 1;
+            if (row + 1 < C * KH) {
+                const int c1 = (row + 1) / KH, kh1 = (row + 1) % KH;
+#pragma unroll
+                for (int kw = 0; kw < KW; kw++) {
+                    ra[cur ^ 1][kw] = pa[c1 * KH * KW + kh1 * KW + kw];
+                    rb[cur ^ 1][kw] = pb[c1 * PRM * PCM + kh1 * PCM + kw];
+                }
+            }
+            // keep the scheduler from sinking those reads next to their MFMAs
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kw = 0; kw < KW; kw++)
+                acc = __builtin_amdgcn_mfma_f32_32x32x1f32(ra[cur][kw], rb[cur][kw], acc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         }
 
         // epilogue (f32 output): bias, Relu, residual; pixels past the image and
         // channels past Mg take the out-of-range offset (loads zero, stores
-        // dropped); residual values loaded four at a time ahead of their stores
+        // dropped); residual values loaded four at a time ahead of their stores.
+        // With one channel tile the bias values sit in registers, and a lane's 16
+        // channels of a pixel differ by a wave-uniform offset (the scalar offset
+        // operand), so each output costs the bias add, the Relu and its store.
+        if constexpr (ONE_M) {
+            const int chan = wm * 32 + 4 * lk, mlim = g.Mg - chan;
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const int qq = T.q0 + pw + b * 32 + lr;
+                const uint32_t base = qq < g.OHW ? (uint32_t)(((T.n * g.M + chan) * g.OHW + qq) * 4) : kOOB;
+#pragma unroll
+                for (int r0 = 0; r0 < 16; r0 += 4) {
+                    float sk[4];
+                    if (epi.skip) {
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            const int cr = 8 * ((r0 + u) >> 2) + ((r0 + u) & 3);
+                            sk[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                  zr, cr < mlim ? base : kOOB, cr * g.OHW * 4, 0));
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int cr = 8 * ((r0 + u) >> 2) + ((r0 + u) & 3);
+                        // + 0.0f without a bias, as the reference adds bias_val = 0.0 (-0 -> +0)
+                        float v = acc[b * 16 + r0 + u] + bias_r[r0 + u];
+                        if (epi.relu) v = relu_f(v);
+                        if (epi.skip) v += sk[u];
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr,
+                                                              cr < mlim ? base : kOOB, cr * g.OHW * 4, 0);
+                    }
+                }
+            }
+        } else {
 #pragma unroll
         for (int b = 0; b < 2; b++) {
             const int qq = T.q0 + pw + b * 32 + lr;
@@ -963,9 +1038,11 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
                 }
             }
         }
+        }
         if (next >= tiles) break;
         __syncthreads();   // every wave is done reading this tile's operands
-        store();
+        if (!ONE_M) store_w();
+        store_p();
         __syncthreads();
         slot = next;
         T = Tn;
@@ -989,8 +1066,12 @@ void launch_conv_stem(const float* x, const float* w, const float* b, float* y, 
     const int tiles = N * tiles_per_img * ntm;
     // persistent grid: two blocks per CU (the LDS footprint allows two), a multiple of 8
     const int grid = std::min(2 * num_cus(), (tiles + 7) / 8 * 8);
-    hipLaunchKernelGGL((k_conv_stem<C, KH, KW, S>), dim3((unsigned)grid), dim3(512), 0, s, x, w, b, y, g,
-                       tiles_per_img, ntm, tiles, xbytes, wbytes, ybytes, epi);
+    if (ntm == 1)
+        hipLaunchKernelGGL((k_conv_stem<C, KH, KW, S, true>), dim3((unsigned)grid), dim3(512), 0, s, x, w, b, y, g,
+                           tiles_per_img, ntm, tiles, xbytes, wbytes, ybytes, epi);
+    else
+        hipLaunchKernelGGL((k_conv_stem<C, KH, KW, S, false>), dim3((unsigned)grid), dim3(512), 0, s, x, w, b, y, g,
+                           tiles_per_img, ntm, tiles, xbytes, wbytes, ybytes, epi);
 }
 
 // XQ != 0 (quantized input) runs with an f32 output and an f32 or no bias only.
