@@ -314,6 +314,12 @@ void dynamic_quantize_linear_forward_noalloc(const Tensor* x, Tensor* y, Tensor*
  * or NULL (0).  The codes are quantize_linear_forward's, bit for bit. */
 void quantize_linear_nhwc_forward(const Tensor* X, const Tensor* Scale, const Tensor* ZeroPoint,
                                   int code_dtype, Tensor* Y);
+/* Y = max_pool_forward(X, params) (tensor_ops/tensor_ops.h:166) and Yc (int8 [N, OH, OW, C]
+ * in the layout above) = quantize_linear_nhwc_forward(Y, Scale, ZeroPoint, code_dtype), bit
+ * for bit, in one pass that reads X once (f32, 3x3 window, stride 2, top / left padding 1,
+ * W == 2 * OW <= 128, C a multiple of 16; other pools run as those two calls). */
+void max_pool_quantize_nhwc_forward(const Tensor* X, Tensor* Y, PoolParams* params, const Tensor* Scale,
+                                    const Tensor* ZeroPoint, int code_dtype, Tensor* Yc);
 /* Weight codes int8 [M, C, KH, KW] -> Wk int8 [M, KH, KW, C] and WSum int32 [M, KH, KW],
  * the sum of each tap's C codes (the zero-point correction). */
 void qconv_pack_weights(const Tensor* Wq, Tensor* Wk, Tensor* WSum);

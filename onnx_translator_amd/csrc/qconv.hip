@@ -196,6 +196,102 @@ __global__ __launch_bounds__(256) void k_quant_nhwc64(const float* __restrict__ 
     }
 }
 
+// ---- MaxPool with the channels-last codes of its output -----------------------
+// max_pool_forward (f32, 3x3, stride 2, top / left padding 1, W == 2 OW, OW <=
+// 64) and quantize_linear_nhwc_forward of its output in one pass.  Block: a
+// strip of kMPRows output rows of 16 channels of one image; wave w pools the
+// group's channels 2w and 2w + 1, the input rows of both loaded up front (one
+// wait for memory per wave).  Output row oh reads input rows 2oh-1, 2oh,
+// 2oh+1, each tap in the reference's order with a strict > (a NaN never wins,
+// the padding is -inf), as the plain MaxPool kernel; lane l holds input
+// columns (2l, 2l+1) and takes column 2l-1 from lane l-1.  The f32 result goes
+// to Y (NCHW, cached stores: the next layer reads it as its residual); its
+// two codes per lane, as one halfword, to LDS [pixel][channel], and the
+// strip's codes leave as one 16-byte store per pixel.
+constexpr int kMPRows = 4;
+__global__ __launch_bounds__(512) void k_maxpool_q16(const float* __restrict__ X, float* __restrict__ Y,
+                                                     int8_t* __restrict__ Yc, const float* __restrict__ qs,
+                                                     const void* __restrict__ qz, int kind, int C, int H, int W,
+                                                     int OH, int OW, int strips) {
+    __shared__ uint32_t tile[kMPRows * 64][5];    // [pixel][16 channel bytes] (+1 word: distinct banks per pixel)
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = threadIdx.x & 63;
+    // work index: each XCD (block index mod 8) takes a contiguous run of
+    // (image, strip, channel group), channel group fastest: the four blocks
+    // that fill one pixel's 64 bytes of codes write through one L2, and
+    // neighbouring strips share their edge input row through it
+    int strip, c0, n;
+    {
+        const int groups = C / 16, total = strips * groups * (int)gridDim.y;
+        const int L = (int)blockIdx.x + (int)blockIdx.y * (int)gridDim.x;
+        const int cls = L & 7, q = total >> 3, rem = total & 7;
+        const int w = cls * q + min(cls, rem) + (L >> 3);
+        c0 = (w % groups) * 16;
+        const int rest = w / groups;
+        strip = rest % strips;
+        n = rest / strips;
+    }
+    const int oh0 = strip * kMPRows, nrow = min(kMPRows, OH - oh0);
+    const uint32_t plane = (uint32_t)H * W;
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X + ((size_t)n * C + c0) * plane, 16u * plane * 4u);
+    const QOut q = qout_parm(qs, qz, kind);
+    const float ninf = -__builtin_inff();
+    const uint32_t lo = (uint32_t)lane * 8u;
+    // (HIP's float2 struct: hipcc folds a bit_cast of an ext_vector element to element 0)
+    auto ldrows = [&](int cl, float2 (&rows)[2 * kMPRows + 1]) {
+#pragma unroll
+        for (int j = 0; j < 2 * kMPRows + 1; j++) {
+            const int ih = 2 * oh0 - 1 + j;
+            float2 v = make_float2(ninf, ninf);
+            if ((unsigned)ih < (unsigned)H && j <= 2 * nrow) {   // uniform
+                const uint64_t u = __builtin_bit_cast(
+                    uint64_t, __builtin_amdgcn_raw_buffer_load_b64(xr, lo, ((uint32_t)cl * plane + (uint32_t)ih * W) * 4u,
+                                                                   2 /* nt */));
+                v = make_float2(__builtin_bit_cast(float, (uint32_t)u), __builtin_bit_cast(float, (uint32_t)(u >> 32)));
+            }
+            rows[j] = v;
+        }
+    };
+    auto row_max = [&](float best, float2 v) {
+        const float left = __builtin_bit_cast(
+            float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, ninf), __builtin_bit_cast(int, v.y),
+                                               0x138 /* wave_shr:1 */, 0xF, 0xF, false));
+        best = left > best ? left : best;
+        best = v.x > best ? v.x : best;
+        best = v.y > best ? v.y : best;
+        return best;
+    };
+    const bool live = lane < OW;
+    float2 ra[2 * kMPRows + 1], rb[2 * kMPRows + 1];
+    uint32_t cw[kMPRows];
+    // one channel (j = 0, 1 of the wave's pair): pool, store f32, code into cw
+    auto pool = [&](const float2 (&rows)[2 * kMPRows + 1], int j) {
+        float* yp = Y + (((size_t)n * C + c0 + 2 * wave + j) * OH + oh0) * OW;
+#pragma unroll
+        for (int o = 0; o < kMPRows; o++) {
+            if (o >= nrow) break;
+            const float best = row_max(row_max(row_max(ninf, rows[2 * o]), rows[2 * o + 1]), rows[2 * o + 2]);
+            if (live) yp[o * OW + lane] = best;
+            const uint32_t b = qout_byte(best, q) << (8 * j);
+            cw[o] = j == 0 ? b : (cw[o] | b);
+        }
+    };
+    ldrows(2 * wave, ra);
+    ldrows(2 * wave + 1, rb);
+    pool(ra, 0);
+    pool(rb, 1);
+    if (live) {
+        uint16_t* t16 = reinterpret_cast<uint16_t*>(&tile[0][0]);
+#pragma unroll
+        for (int o = 0; o < kMPRows; o++)
+            if (o < nrow) t16[(o * OW + lane) * 10 + wave] = (uint16_t)cw[o];
+    }
+    __syncthreads();
+    const int npx = nrow * OW;
+    int8_t* yc = Yc + (((size_t)n * OH + oh0) * OW) * C + c0;
+    for (int p = threadIdx.x; p < npx; p += 512)
+        *reinterpret_cast<uint4*>(yc + (size_t)p * C) = make_uint4(tile[p][0], tile[p][1], tile[p][2], tile[p][3]);
+}
+
 // ---- weight packing ------------------------------------------------------------
 // One block per output channel: [C, KH, KW] codes -> [KH, KW, C], and the sum
 // of each tap's C codes (wave w sums taps w, w + 4, ...).
@@ -750,6 +846,54 @@ extern "C" void quantize_linear_nhwc_forward(const Tensor* X, const Tensor* Scal
     else
         hipLaunchKernelGGL((k_quant_nhwc<false>), grid, dim3(256), 0, stream(), (const float*)X->data,
                            (int8_t*)Y->data, (const float*)Scale->data, zp, kind, C, HW);
+    check_launch(name);
+}
+
+extern "C" void max_pool_quantize_nhwc_forward(const Tensor* X, Tensor* Y, PoolParams* params, const Tensor* Scale,
+                                               const Tensor* ZeroPoint, int code_dtype, Tensor* Yc) {
+    const char* name = "max_pool_quantize_nhwc_forward";
+    tensor_ops_hip_clear_error();
+    if (!ensure_device()) return;
+    if (!dev_tensor(X, name, "X") || !dev_tensor(Y, name, "Y") || !dev_tensor(Scale, name, "Scale") ||
+        !dev_tensor(Yc, name, "Yc"))
+        return;
+    if (!params || !params->pads || !params->strides || !params->dilations || !params->kernel_shape) {
+        set_error("%s: NULL params", name);
+        return;
+    }
+    const int kind = code_dtype == kU8 ? 1 : (code_dtype == kI8 ? 2 : 0);
+    if (!kind) { set_error("%s: code_dtype must be uint8 or int8", name); return; }
+    if (!one_code(ZeroPoint, kind, name, "ZeroPoint")) return;
+    if ((int)X->dtype != kF32 || X->ndim != 4 || (int)Y->dtype != kF32 || Y->ndim != 4 || (int)Scale->dtype != kF32 ||
+        Scale->size != 1) {
+        set_error("%s: X and Y must be 4-D float32 and Scale one float32", name);
+        return;
+    }
+    const int N = X->shape[0], C = X->shape[1], H = X->shape[2], W = X->shape[3], OH = Y->shape[2], OW = Y->shape[3];
+    if (Y->shape[0] != N || Y->shape[1] != C) { set_error("%s: Y batch/channels differ from X", name); return; }
+    if ((int)Yc->dtype != kI8 || Yc->ndim != 4 || Yc->shape[0] != N || Yc->shape[1] != OH || Yc->shape[2] != OW ||
+        Yc->shape[3] != C) {
+        set_error("%s: Yc must be int8 [N, OH, OW, C]", name);
+        return;
+    }
+    const int* k = params->kernel_shape;
+    const bool fits = k[0] == 3 && k[1] == 3 && params->strides[0] == 2 && params->strides[1] == 2 &&
+                      params->dilations[0] == 1 && params->dilations[1] == 1 && params->pads[0] == 1 &&
+                      params->pads[1] == 1 && W == 2 * OW && OW <= 64 && OH >= 1 && 2 * OH <= H + 2 && C % 16 == 0 &&
+                      ((uintptr_t)X->data & 7) == 0 && (size_t)16 * H * W * 4 < ((size_t)1 << 31);
+    if (!fits) {
+        // the two calls it stands for
+        max_pool_forward(X, Y, params);
+        if (tensor_ops_hip_last_error()[0]) return;
+        quantize_linear_nhwc_forward(Y, Scale, ZeroPoint, code_dtype, Yc);
+        return;
+    }
+    if (X->size == 0) return;
+    const int strips = (OH + kMPRows - 1) / kMPRows, blocks = strips * (C / 16);
+    const void* zp = (ZeroPoint && ZeroPoint->data) ? ZeroPoint->data : nullptr;
+    hipLaunchKernelGGL(k_maxpool_q16, dim3((unsigned)blocks, (unsigned)N), dim3(512), 0, stream(),
+                       (const float*)X->data, (float*)Y->data, (int8_t*)Yc->data, (const float*)Scale->data, zp, kind,
+                       C, H, W, OH, OW, strips);
     check_launch(name);
 }
 

@@ -509,6 +509,55 @@ class MaxPoolQDQ(MaxPool):
         return _values(self, [y, Tensor_(*y.size, dtype=self.dtype)])
 
 
+class MaxPoolQuantizeNHWC(MaxPool):
+    """MaxPool whose output is also quantized into the channels-last int8 codes
+    :class:`QConvBlock` reads, in one call to ``max_pool_quantize_nhwc_forward``:
+    outputs [y, codes] with y = MaxPool(x) (nn/Operators.py:550-611) and codes =
+    :class:`QuantizeNHWC` of y, both bit for bit, x read once.  ``inputs`` = [x,
+    scale, zero point or ""] (one-element parameters of the codes' dtype)."""
+
+    def __init__(self, inputs, outputs, kernel_shape, pads, strides, dtype, code_dtype, dilations=[1, 1],
+                 version="17"):
+        super().__init__(inputs, outputs, kernel_shape, pads, strides, dtype, dilations, version)
+        self.code_dtype = code_dtype
+        self.lib.max_pool_quantize_nhwc_forward.argtypes = [PT, PT, ctypes.POINTER(CPoolParams), PT, PT,
+                                                            ctypes.c_int, PT]
+        self.lib.max_pool_quantize_nhwc_forward.restype = None
+
+    def forward(self, x: Tensor, scale: Tensor, zero_point: Tensor = None):
+        N, C, H, W = x.size
+        KH, KW = self.kernel_shape
+        OH, OW = _pool_out(H, W, self.pads, self.strides, self.dilations, KH, KW)
+        arrs = [_int_arr(self.pads), _int_arr(self.strides), _int_arr(self.dilations), _int_arr(self.kernel_shape)]
+        p = CPoolParams()
+        p.pads, p.strides, p.dilations, p.kernel_shape = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in arrs]
+        keep: list = []
+        dev = any(isinstance(t.data, DeviceArray) for t in (x, scale, zero_point) if t is not None)
+        outs = []
+        try:
+            cins = [self._in_ctensor(t, keep) if t is not None else PT() for t in (x, scale, zero_point)]
+            for shape, dt in (((N, C, OH, OW), self.dtype), ((N, OH, OW, C), "int8")):
+                outs.append((shape, dt) + self._out_ctensor(shape, dt, dev))
+            self._call("max_pool_quantize_nhwc_forward", cins[0], outs[0][3], ctypes.byref(p), cins[1], cins[2],
+                       ctypes.c_int(DTYPE_MAP[self.code_dtype]), outs[1][3])
+        except Exception:
+            for shape, dt, d, c in outs:
+                if d is None:
+                    self.lib.free_tensor(c)
+            for c in keep:
+                self.lib.free_tensor(c)
+            raise
+        tensors = [self._finish(shape, dt, d, c, []) for shape, dt, d, c in outs]
+        for c in keep:
+            self.lib.free_tensor(c)
+        return _values(self, tensors)
+
+    def forward_(self, x: Tensor_, *params):
+        y = super().forward_(x)["tensor"]
+        N, C, OH, OW = y.size
+        return _values(self, [y, Tensor_(N, OH, OW, C, dtype="int8")])
+
+
 class Gemm(Ops):
     """Y = alpha * A' B' + beta * C (nn/Operators.py:613-669 -> tensor_ops.c:1167-1228)."""
 

@@ -346,9 +346,21 @@ class Graph:
             c = bl["c"]
             codes_in = bl["xq"] + ".nhwc"
             if bl["src"] is None:
-                qn = Op.QuantizeNHWC([bl["qx"].inputs[0], bl["qs"], bl["qz"]], [codes_in], bl["cdt"])
-                qn.name = f"QuantizeNHWC.{bl['qx'].name}"
-                replace[bl["qx"].name] = qn
+                x = bl["qx"].inputs[0]
+                mp = producer.get(x)
+                if (type(mp) is Op.MaxPool and mp.dtype == "float32" and shapes[x][1] == "float32" and
+                        list(mp.kernel_shape) == [3, 3] and list(mp.strides) == [2, 2] and
+                        list(mp.pads)[:2] == [1, 1] and list(mp.dilations) == [1, 1] and mp.name not in replace):
+                    # the MaxPool writes the codes as well: its output is read once
+                    qn = Op.MaxPoolQuantizeNHWC([mp.inputs[0], bl["qs"], bl["qz"]], [x, codes_in], mp.kernel_shape,
+                                                mp.pads, mp.strides, mp.dtype, bl["cdt"], mp.dilations)
+                    qn.name = f"MaxPoolQuantizeNHWC.{mp.name}+{bl['qx'].name}"
+                    replace[mp.name] = qn
+                    drop.add(bl["qx"].name)
+                else:
+                    qn = Op.QuantizeNHWC([x, bl["qs"], bl["qz"]], [codes_in], bl["cdt"])
+                    qn.name = f"QuantizeNHWC.{bl['qx'].name}"
+                    replace[bl["qx"].name] = qn
             else:
                 drop.add(bl["qx"].name)
             wk, wsum, wsc = packed(c.name, bl["w"][1], bl["w"][2])

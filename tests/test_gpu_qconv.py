@@ -183,6 +183,61 @@ def test_quantize_nhwc_matches_quantize_linear(hip, oracle_lib):
         dev.free()
 
 
+def _pool_params(pads, strides):
+    keep = [(ctypes.c_int * 4)(*pads), (ctypes.c_int * 2)(*strides), (ctypes.c_int * 2)(1, 1),
+            (ctypes.c_int * 2)(3, 3)]
+    p = O.CPoolParams()
+    p.pads, p.strides, p.dilations, p.kernel_shape = [ctypes.cast(k, ctypes.POINTER(ctypes.c_int)) for k in keep]
+    return p, keep
+
+
+# (shape, pads, code dtype, scale, zero point): the config-5 pool (strips of 4 output
+# rows, 16 channels per block), a partial last strip with an int8 zero point, an odd
+# input height with W % 4 == 2, 128 and 32 channels, and a shape the fused kernel does
+# not take (W != 2 OW): max_pool_forward then quantize_linear_nhwc_forward.
+MAXPOOL_Q = [((2, 64, 112, 112), (1, 1, 1, 1), O.U8, 8 / 255, 0),
+             ((3, 64, 20, 22), (1, 1, 1, 1), O.I8, 0.05, -3),
+             ((2, 128, 15, 18), (1, 1, 1, 1), O.U8, 0.03, 17),
+             ((1, 32, 16, 16), (1, 1, 1, 1), O.U8, 0.02, 0),
+             ((2, 64, 16, 17), (1, 1, 0, 0), O.I8, 0.04, 5)]
+
+
+@pytest.mark.parametrize("case", MAXPOOL_Q, ids=[f"{c[0]}-{c[2]}" for c in MAXPOOL_Q])
+def test_maxpool_quantize_nhwc(hip, oracle_lib, case):
+    """max_pool_quantize_nhwc_forward = max_pool_forward -> quantize_linear_nhwc_forward
+    bit for bit (both outputs against the oracle's MaxPool and QuantizeLinear), with
+    NaN, +-inf and rounding ties among the inputs."""
+    shape, pads, dt, s, z = case
+    L = hip.lib
+    _bind(L)
+    L.max_pool_quantize_nhwc_forward.argtypes = [O.PT, O.PT, ctypes.POINTER(O.CPoolParams), O.PT, O.PT,
+                                                 ctypes.c_int, O.PT]
+    rng = np.random.default_rng(shape[1] + shape[2])
+    x = rng.normal(0.5, 2.0, shape).astype(np.float32)
+    x.flat[::89] = np.float32(s) * (np.rint(x.flat[::89] / s) + 0.5)     # ties after pooling, some of them
+    x.flat[5::1013] = np.nan
+    x.flat[7::2039] = np.inf
+    x.flat[11::3001] = -np.inf
+    x[0, 0, :3, :3] = np.nan                                             # a window of NaN only: -inf out
+    ref_y = oracle_lib.maxpool(x, O.F32, O.F32, (3, 3), pads, (2, 2))
+    ref_c = oracle_lib.qdq("quantize", ref_y, O.F32, np.float32(s), O.F32, np.array(z), dt, dt)
+    n, c, oh, ow = ref_y.shape
+    dev = _Dev(hip)
+    try:
+        tx, ts, tz = dev.put(x, O.F32), dev.put(np.array([s], np.float32), O.F32), dev.put(np.array([z]), dt)
+        p, keep = _pool_params(pads, (2, 2))
+        with hip.poisoned():
+            ty, tc = dev.output((n, c, oh, ow), O.F32), dev.output((n, oh, ow, c), O.I8)
+            L.tensor_ops_hip_clear_error()
+            L.max_pool_quantize_nhwc_forward(tx, ty, ctypes.byref(p), ts, tz, dt, tc)
+        assert not hip.last_error(), hip.last_error()
+        assert_bitexact(hip.dev_read(ty, O.F32), ref_y, O.F32, what=f"pooled {shape}")
+        assert_bitexact(_codes_from_stored(hip.dev_read(tc, O.I8), dt), ref_c, dt, what=f"codes {shape}")
+        del keep
+    finally:
+        dev.free()
+
+
 def test_pack_weights(hip):
     _bind(hip.lib)
     rng = np.random.default_rng(12)

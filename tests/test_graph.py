@@ -223,9 +223,10 @@ def test_int8_conv_pass(monkeypatch):
     """Placeholder-shape run of the int8 QDQ block pass on the config-5 graph:
     each block (QuantizeLinear -> DequantizeLinear -> Conv with DequantizeLinear'd
     int8 weights -> Relu -> Add of the pooled activation or of a 1x1 projection)
-    becomes one QConvBlock; block 1's codes come from a QuantizeNHWC of the
-    MaxPool output (which its residual also reads), blocks 2-4 read the codes the
-    previous block writes, and the last block writes f32 for the pooling."""
+    becomes one QConvBlock; block 1's codes come from the MaxPool, which writes
+    them beside its f32 output (which block 1's residual reads) as one
+    MaxPoolQuantizeNHWC, blocks 2-4 read the codes the previous block writes, and
+    the last block writes f32 for the pooling."""
     from onnx_translator_amd.nn import Graph, Tensor, Tensor_
     from onnx_translator_amd.nn import Operators as Op
     from onnx_translator_amd.nn.ONNXImport import ONNXImport, initializers
@@ -238,11 +239,13 @@ def test_int8_conv_pass(monkeypatch):
     assert g._fuse_qconv_blocks(shapes, g._consumers())
     ops = list(g.ops.values())
     names = [type(o).__name__ for o in ops]
-    assert names.count("QuantizeNHWC") == 1 and names.count("QConvBlock") == 4
+    assert names.count("MaxPoolQuantizeNHWC") == 1 and names.count("QConvBlock") == 4
+    assert "QuantizeNHWC" not in names and "MaxPool" not in names
     assert "QuantizeLinear" not in names and "DequantizeLinear" not in names and names.count("Conv") == 1
     blocks = [o for o in ops if type(o).__name__ == "QConvBlock"]
-    qn = next(o for o in ops if type(o).__name__ == "QuantizeNHWC")
-    assert qn.inputs == ["pool", "act.scale", "act.zp"] and qn.outputs == ["block1.xq.nhwc"]
+    qn = next(o for o in ops if type(o).__name__ == "MaxPoolQuantizeNHWC")
+    assert qn.inputs == ["stem.relu", "act.scale", "act.zp"] and qn.outputs == ["pool", "block1.xq.nhwc"]
+    assert list(qn.kernel_shape) == [3, 3] and list(qn.strides) == [2, 2] and qn.code_dtype == "uint8"
     assert [b.inputs[0] for b in blocks] == ["block1.xq.nhwc", "block2.xq.nhwc", "block3.xq.nhwc", "block4.xq.nhwc"]
     assert [b.outputs[0] for b in blocks] == ["block2.xq.nhwc", "block3.xq.nhwc", "block4.xq.nhwc", "block4.out"]
     assert blocks[0].inputs[10] == "pool" and not blocks[0].inputs[7]
@@ -557,7 +560,7 @@ def test_resnet_qdq_graph_int8(hip, oracle_lib):
         finally:
             hip.set_exact(False)
     names = [type(o).__name__ for o in g8.ops.values()]
-    assert names.count("QConvBlock") == 4 and names.count("QuantizeNHWC") == 1, names
+    assert names.count("QConvBlock") == 4 and names.count("MaxPoolQuantizeNHWC") == 1, names
     assert np.isfinite(l8).all() and np.isfinite(p8).all(), "unwritten (NaN) elements"
     np.testing.assert_allclose(p8.sum(axis=1), 1.0, rtol=1e-5)
     dl = np.abs(l8.astype(np.float64) - el).max() / np.abs(el).max()
