@@ -811,7 +811,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
 // non-finite, input).  Output register r of lane l: block r / 16, channel
 // 8*((r%16)/4) + r%4 + 4*(l/32), pixel l%32 of that block's group.
 constexpr int kStemRows = 13, kStemCols = 232;   // LDS patch per input channel: rows x columns
-template <int C, int KH, int KW, int S, bool ONE_M>
+template <int C, int KH, int KW, int S, bool ONE_M, bool DEFER>
 __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ X, const float* __restrict__ Wt,
                                                    const float* __restrict__ Bv, float* __restrict__ Y, ConvTiled g,
                                                    int tiles_per_img, int ntm, int tiles, uint32_t xbytes,
@@ -911,8 +911,23 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
     store_p();
     __syncthreads();
     const float* pa = &As[(wm * 32 + lr) * KA];
+    // DEFER (one channel tile, no residual): a tile's 32 outputs per lane stay in
+    // registers and are stored during the next tile's first kh rows, so the
+    // stores (64 KB per tile, issued by every block at once otherwise) overlap
+    // the MFMAs; the next tile's patch loads are issued half way through the
+    // multiply, after those registers are free.
+    static_assert(!DEFER || ONE_M, "DEFER needs the one-channel-tile form");
+    float outv[32];
+    uint32_t obase[2] = {kOOB, kOOB};
+    int omlim = 0;
+    bool have_out = false;
+    auto store_out = [&](int idx) {
+        const int b = idx >> 4, r = idx & 15, cr = 8 * (r >> 2) + (r & 3);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, outv[idx]), yr,
+                                              cr < omlim ? obase[b] : kOOB, cr * g.OHW * 4, 0);
+    };
     float bias_r[16];
-    if constexpr (ONE_M) {
+    if constexpr (ONE_M && !DEFER) {
 #pragma unroll
         for (int r = 0; r < 16; r++) bias_r[r] = Bs[wm * 32 + 8 * (r >> 2) + (r & 3) + 4 * lk];
     }
@@ -924,7 +939,7 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
         if (next < tiles) {
             Tn = tile_of(next);
             if (!ONE_M) load_w(Tn);
-            load_p(Tn);
+            if (!DEFER) load_p(Tn);
         }
         const int q = min(T.q0 + pw + lk * 32 + lr, g.OHW - 1);
         const int oh = (int)g.fd_ow.div((uint32_t)q), ow = q - oh * g.OW;
@@ -957,6 +972,13 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
 #pragma unroll
         for (int row = 0; row < C * KH; row++) {
             const int cur = row & 1;
+            if constexpr (DEFER) {
+                if (row == (C * KH) / 2 && next < tiles) load_p(Tn);
+                if (row < 8 && have_out) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++) store_out(4 * row + u);
+                }
+            }
             if (row + 1 < C * KH) {
                 const int c1 = (row + 1) / KH, kh1 = (row + 1) % KH;
 #pragma unroll
@@ -980,7 +1002,24 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
         // With one channel tile the bias values sit in registers, and a lane's 16
         // channels of a pixel differ by a wave-uniform offset (the scalar offset
         // operand), so each output costs the bias add, the Relu and its store.
-        if constexpr (ONE_M) {
+        if constexpr (DEFER) {
+            const int chan = wm * 32 + 4 * lk;
+            omlim = g.Mg - chan;
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const int qq = T.q0 + pw + b * 32 + lr;
+                obase[b] = qq < g.OHW ? (uint32_t)(((T.n * g.M + chan) * g.OHW + qq) * 4) : kOOB;
+            }
+#pragma unroll
+            for (int i = 0; i < 32; i++) {
+                const int r = i & 15;
+                // + 0.0f without a bias, as the reference adds bias_val = 0.0 (-0 -> +0)
+                float v = acc[i] + Bs[wm * 32 + 8 * (r >> 2) + (r & 3) + 4 * lk];
+                if (epi.relu) v = relu_f(v);
+                outv[i] = v;
+            }
+            have_out = true;
+        } else if constexpr (ONE_M) {
             const int chan = wm * 32 + 4 * lk, mlim = g.Mg - chan;
 #pragma unroll
             for (int b = 0; b < 2; b++) {
@@ -1047,6 +1086,10 @@ __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ 
         slot = next;
         T = Tn;
     }
+    if constexpr (DEFER) {
+#pragma unroll
+        for (int i = 0; i < 32; i++) store_out(i);
+    }
 }
 
 // The few-channel plan: 3 input channels, 7x7, stride 2, no dilation, one
@@ -1066,12 +1109,15 @@ void launch_conv_stem(const float* x, const float* w, const float* b, float* y, 
     const int tiles = N * tiles_per_img * ntm;
     // persistent grid: two blocks per CU (the LDS footprint allows two), a multiple of 8
     const int grid = std::min(2 * num_cus(), (tiles + 7) / 8 * 8);
-    if (ntm == 1)
-        hipLaunchKernelGGL((k_conv_stem<C, KH, KW, S, true>), dim3((unsigned)grid), dim3(512), 0, s, x, w, b, y, g,
-                           tiles_per_img, ntm, tiles, xbytes, wbytes, ybytes, epi);
+    if (ntm == 1 && !epi.skip)
+        hipLaunchKernelGGL((k_conv_stem<C, KH, KW, S, true, true>), dim3((unsigned)grid), dim3(512), 0, s, x, w, b, y,
+                           g, tiles_per_img, ntm, tiles, xbytes, wbytes, ybytes, epi);
+    else if (ntm == 1)
+        hipLaunchKernelGGL((k_conv_stem<C, KH, KW, S, true, false>), dim3((unsigned)grid), dim3(512), 0, s, x, w, b,
+                           y, g, tiles_per_img, ntm, tiles, xbytes, wbytes, ybytes, epi);
     else
-        hipLaunchKernelGGL((k_conv_stem<C, KH, KW, S, false>), dim3((unsigned)grid), dim3(512), 0, s, x, w, b, y, g,
-                           tiles_per_img, ntm, tiles, xbytes, wbytes, ybytes, epi);
+        hipLaunchKernelGGL((k_conv_stem<C, KH, KW, S, false, false>), dim3((unsigned)grid), dim3(512), 0, s, x, w, b,
+                           y, g, tiles_per_img, ntm, tiles, xbytes, wbytes, ybytes, epi);
 }
 
 // XQ != 0 (quantized input) runs with an f32 output and an f32 or no bias only.
