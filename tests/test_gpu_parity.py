@@ -280,6 +280,8 @@ CONV_TILED = [
     ("stem_plan_m80", (2, 3, 20, 180), (80, 3, 7, 7), [3, 3, 3, 3], [2, 2], [1, 1], 1, True, "float32"),
     # one partial channel tile (the weights-resident-in-LDS form with channels past M)
     ("stem_plan_m40", (2, 3, 20, 180), (40, 3, 7, 7), [3, 3, 3, 3], [2, 2], [1, 1], 1, True, "float32"),
+    # a single tile (one busy block in the persistent grid)
+    ("stem_plan_one_tile", (1, 3, 3, 224), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2], [1, 1], 1, True, "float32"),
     ("stem_plan_asym_nobias", (1, 3, 17, 224), (64, 3, 7, 7), [2, 3, 4, 1], [2, 2], [1, 1], 1, False, "float32"),
     # direct 1x1 layers of the config-4 shape class (64 input channels, 256 and 512
     # output channels)
@@ -319,6 +321,7 @@ CONV_FUSED = [
     ("tap_small_img_relu_skip", (2, 64, 14, 14), (192, 64, 3, 3), [1, 1, 1, 1], [2, 2], 1, True, True, "full", "float32"),
     ("stem_plan_relu_skip", (2, 3, 20, 180), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2], 1, True, True, "full", "float32"),
     ("stem_plan_m40_skip", (2, 3, 20, 180), (40, 3, 7, 7), [3, 3, 3, 3], [2, 2], 1, True, False, "full", "float32"),
+    ("stem_plan_one_tile_relu", (1, 3, 3, 224), (64, 3, 7, 7), [3, 3, 3, 3], [2, 2], 1, True, True, None, "float32"),
     ("stem_plan_m80_relu_skip", (2, 3, 20, 180), (80, 3, 7, 7), [3, 3, 3, 3], [2, 2], 1, True, True, "full", "float32"),
     ("direct_m256_relu_skip", (2, 64, 16, 16), (256, 64, 1, 1), [0, 0, 0, 0], [1, 1], 1, True, True, "full", "float32"),
     ("direct_m512_skip_nobias", (1, 64, 8, 32), (512, 64, 1, 1), [0, 0, 0, 0], [1, 1], 1, False, False, "full", "float32"),
