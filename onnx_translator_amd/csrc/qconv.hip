@@ -200,20 +200,20 @@ __global__ __launch_bounds__(256) void k_quant_nhwc64(const float* __restrict__ 
 // max_pool_forward (f32, 3x3, stride 2, top / left padding 1, W == 2 OW, OW <=
 // 64) and quantize_linear_nhwc_forward of its output in one pass.  Block: a
 // strip of kMPRows output rows of 16 channels of one image; wave w pools the
-// group's channels 2w and 2w + 1, the input rows of both loaded up front (one
-// wait for memory per wave).  Output row oh reads input rows 2oh-1, 2oh,
-// 2oh+1, each tap in the reference's order with a strict > (a NaN never wins,
-// the padding is -inf), as the plain MaxPool kernel; lane l holds input
-// columns (2l, 2l+1) and takes column 2l-1 from lane l-1.  The f32 result goes
-// to Y (NCHW, cached stores: the next layer reads it as its residual); its
-// two codes per lane, as one halfword, to LDS [pixel][channel], and the
-// strip's codes leave as one 16-byte store per pixel.
-constexpr int kMPRows = 4;
-__global__ __launch_bounds__(512) void k_maxpool_q16(const float* __restrict__ X, float* __restrict__ Y,
+// group's channel w, its input rows loaded up front (one wait for memory per
+// wave).  Output row oh reads input rows 2oh-1, 2oh, 2oh+1, each tap in the
+// reference's order with a strict > (a NaN never wins, the padding is -inf),
+// as the plain MaxPool kernel; lane l holds input columns (2l, 2l+1) and takes
+// column 2l-1 from lane l-1.  The f32 result goes to Y (NCHW, cached stores:
+// the next layer reads it as its residual), its code to LDS [pixel][channel],
+// and the strip's codes leave as one 16-byte store per pixel.
+constexpr int kMPRows = 7;
+__global__ __launch_bounds__(1024) void k_maxpool_q16(const float* __restrict__ X, float* __restrict__ Y,
                                                      int8_t* __restrict__ Yc, const float* __restrict__ qs,
                                                      const void* __restrict__ qz, int kind, int C, int H, int W,
                                                      int OH, int OW, int strips) {
     __shared__ uint32_t tile[kMPRows * 64][5];    // [pixel][16 channel bytes] (+1 word: distinct banks per pixel)
+    uint8_t* t8 = reinterpret_cast<uint8_t*>(&tile[0][0]);
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = threadIdx.x & 63;
     // work index: each XCD (block index mod 8) takes a contiguous run of
     // (image, strip, channel group), channel group fastest: the four blocks
@@ -261,34 +261,22 @@ __global__ __launch_bounds__(512) void k_maxpool_q16(const float* __restrict__ X
         return best;
     };
     const bool live = lane < OW;
-    float2 ra[2 * kMPRows + 1], rb[2 * kMPRows + 1];
-    uint32_t cw[kMPRows];
-    // one channel (j = 0, 1 of the wave's pair): pool, store f32, code into cw
-    auto pool = [&](const float2 (&rows)[2 * kMPRows + 1], int j) {
-        float* yp = Y + (((size_t)n * C + c0 + 2 * wave + j) * OH + oh0) * OW;
+    float2 rows[2 * kMPRows + 1];
+    ldrows(wave, rows);
+    float* yp = Y + (((size_t)n * C + c0 + wave) * OH + oh0) * OW;
 #pragma unroll
-        for (int o = 0; o < kMPRows; o++) {
-            if (o >= nrow) break;
-            const float best = row_max(row_max(row_max(ninf, rows[2 * o]), rows[2 * o + 1]), rows[2 * o + 2]);
-            if (live) yp[o * OW + lane] = best;
-            const uint32_t b = qout_byte(best, q) << (8 * j);
-            cw[o] = j == 0 ? b : (cw[o] | b);
+    for (int o = 0; o < kMPRows; o++) {
+        if (o >= nrow) break;
+        const float best = row_max(row_max(row_max(ninf, rows[2 * o]), rows[2 * o + 1]), rows[2 * o + 2]);
+        if (live) {
+            yp[o * OW + lane] = best;
+            t8[(o * OW + lane) * 20 + wave] = (uint8_t)qout_byte(best, q);
         }
-    };
-    ldrows(2 * wave, ra);
-    ldrows(2 * wave + 1, rb);
-    pool(ra, 0);
-    pool(rb, 1);
-    if (live) {
-        uint16_t* t16 = reinterpret_cast<uint16_t*>(&tile[0][0]);
-#pragma unroll
-        for (int o = 0; o < kMPRows; o++)
-            if (o < nrow) t16[(o * OW + lane) * 10 + wave] = (uint16_t)cw[o];
     }
     __syncthreads();
     const int npx = nrow * OW;
     int8_t* yc = Yc + (((size_t)n * OH + oh0) * OW) * C + c0;
-    for (int p = threadIdx.x; p < npx; p += 512)
+    for (int p = threadIdx.x; p < npx; p += 1024)
         *reinterpret_cast<uint4*>(yc + (size_t)p * C) = make_uint4(tile[p][0], tile[p][1], tile[p][2], tile[p][3]);
 }
 
@@ -891,7 +879,7 @@ extern "C" void max_pool_quantize_nhwc_forward(const Tensor* X, Tensor* Y, PoolP
     if (X->size == 0) return;
     const int strips = (OH + kMPRows - 1) / kMPRows, blocks = strips * (C / 16);
     const void* zp = (ZeroPoint && ZeroPoint->data) ? ZeroPoint->data : nullptr;
-    hipLaunchKernelGGL(k_maxpool_q16, dim3((unsigned)blocks, (unsigned)N), dim3(512), 0, stream(),
+    hipLaunchKernelGGL(k_maxpool_q16, dim3((unsigned)blocks, (unsigned)N), dim3(1024), 0, stream(),
                        (const float*)X->data, (float*)Y->data, (int8_t*)Yc->data, (const float*)Scale->data, zp, kind,
                        C, H, W, OH, OW, strips);
     check_launch(name);
