@@ -868,7 +868,7 @@ extern "C" void max_pool_quantize_nhwc_forward(const Tensor* X, Tensor* Y, PoolP
     const bool fits = k[0] == 3 && k[1] == 3 && params->strides[0] == 2 && params->strides[1] == 2 &&
                       params->dilations[0] == 1 && params->dilations[1] == 1 && params->pads[0] == 1 &&
                       params->pads[1] == 1 && W == 2 * OW && OW <= 64 && OH >= 1 && 2 * OH <= H + 2 && C % 16 == 0 &&
-                      ((uintptr_t)X->data & 7) == 0 && (size_t)16 * H * W * 4 < ((size_t)1 << 31);
+                      ((uintptr_t)X->data & 7) == 0 && (size_t)16 * H * W * 4 < ((size_t)1 << 31) && N <= 65535;
     if (!fits) {
         // the two calls it stands for
         max_pool_forward(X, Y, params);
