@@ -563,16 +563,23 @@ constexpr int kQSteps = 2;     // k steps per LDS stage (4: slower, the prologue
 // half 512 + 64, group 2 halves, step 4 groups + 128 (128 mod 256)
 constexpr int kQHalf = 576, kQGroup = 2 * kQHalf, kQStep = 4 * kQGroup + 128, kQSlot = kQSteps * kQStep;
 
-template <bool PROJ, int OUT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PROJ && OUT == 0 ? 3 : 4))) void k_qconv_lds(const int8_t* __restrict__ X, const int8_t* __restrict__ Wk,
+// KG = 2 (grids of at most two blocks per CU): 8 waves per block, waves 4-7 a
+// second k group that runs the second half of the stages through a ring of its
+// own; its integer partial sums are added to the first group's through LDS
+// (exact), and the first group writes the output.  The two groups meet at the
+// same barriers (the shorter runs its last stage again without multiplying).
+template <bool PROJ, int OUT, int KG>
+__global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(PROJ && OUT == 0 ? 3 : 4))) void k_qconv_lds(const int8_t* __restrict__ X, const int8_t* __restrict__ Wk,
                                                    const int8_t* __restrict__ Pk, void* __restrict__ Y, QGeom g,
                                                    QEpi e) {
-    __shared__ __attribute__((aligned(1024))) int8_t ring[3 * kQSlot];
+    __shared__ __attribute__((aligned(1024))) int8_t rings[KG * 3 * kQSlot];
     __shared__ double s_cm[64], s_cp[64];
     __shared__ int s_corr[64], s_corrp[64];
     __shared__ float s_bias[64];
     const int lane = threadIdx.x & 63, col = lane & 31, half = lane >> 5;
-    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) & 3;
+    const int grp = KG == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8);
+    int8_t* const ring = rings + grp * (3 * kQSlot);
     // Tile order: the dispatcher deals consecutive blocks to the 8 XCDs in
     // turn, each with its own L2.  Block L works on tile w, which gives XCD
     // L % 8 a contiguous run of the tiles, ordered (pixel tile, channel tile)
@@ -639,13 +646,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PROJ && OUT
     }
     const int8_t* const pad = reinterpret_cast<const int8_t*>(&kQPad.w[zsh & 0xFF][0]);
     const int total = g.steps + (PROJ ? g.psteps : 0);
-    const int nst = (total + kQSteps - 1) / kQSteps;
+    const int nst_all = (total + kQSteps - 1) / kQSteps;
+    // this group's stages [s_beg, s_end) and the loop's trip count nst (the
+    // same for both groups)
+    const int s_half = (nst_all + KG - 1) / KG;
+    const int s_beg = grp * s_half, s_end = min(nst_all, s_beg + s_half), nst = s_half;
+    const int step_end = min(total, kQSteps * s_end);
     // Next stage to load: sst, its first channel step cs (even: a stage is two
-    // steps of one tap) and tap (kh, kw); past the last stage the last is
-    // loaded again (its copy is never read).  One global load per row on every
-    // path keeps the compiler's count of loads in flight exact, so its waits
-    // stay partial.
-    int sst = 0, cs = 0, kh = 0, kw = 0;
+    // steps of one tap) and tap (kh, kw); past the group's last stage the last
+    // is loaded again (its copy is never read).  One global load per row on
+    // every path keeps the compiler's count of loads in flight exact, so its
+    // waits stay partial.
+    int sst = s_beg, cs = 0, kh = 0, kw = 0;
+    if (KG > 1 && s_beg > 0) {
+        const int st0 = kQSteps * s_beg;
+        if (st0 < g.steps) {
+            const int tap = st0 / g.csteps;
+            cs = st0 - tap * g.csteps;
+            kh = tap / g.KW;
+            kw = tap - kh * g.KW;
+        } else {
+            cs = st0 - g.steps;
+            kh = g.KH;
+        }
+    }
     auto gload = [&](i32x4 (&v)[2]) {
         const bool main = !PROJ || 2 * sst < g.steps;
 #pragma unroll
@@ -657,7 +681,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PROJ && OUT
                                     : prow + ((size_t)j * 16 * g.C + cs * 32);
             v[j] = *reinterpret_cast<const i32x4*>(is_a ? pa : pb);
         }
-        if (sst + 1 < nst) {
+        if (sst + 1 < s_end) {
             sst++;
             cs += 2;
             if (cs == g.csteps) {
@@ -686,7 +710,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PROJ && OUT
 #pragma unroll
     for (int k = 0; k < 16; k++) {
         const int ml = 8 * (k >> 2) + 4 * half + (k & 3);
-        sk[k] = (has_skip && pme < g.P) ? e.skip[yb + (size_t)ml * g.OHW] : 0.0f;
+        sk[k] = (has_skip && pme < g.P && grp == 0) ? e.skip[yb + (size_t)ml * g.OHW] : 0.0f;
     }
 
     i32x16 acc, accp;
@@ -717,11 +741,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PROJ && OUT
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
         for (int u = 0; u < kQSteps; u++) {
-            const int stp = kQSteps * k + u;
+            const int stp = kQSteps * (s_beg + k) + u;
             const int8_t* base = &ring[sr * kQSlot + u * kQStep + rdo];
             const i32x4 a = *reinterpret_cast<const i32x4*>(base + wm * kQGroup);
             const i32x4 b = *reinterpret_cast<const i32x4*>(base + (2 + wp) * kQGroup);
-            if (stp >= total) break;
+            if (stp >= step_end) break;
             if (!PROJ || stp < g.steps) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc, 0, 0, 0);
             else accp = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, accp, 0, 0, 0);
         }
@@ -736,6 +760,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PROJ && OUT
     if (k < nst) body(k, 0, 1, R1);
     if (k + 1 < nst) body(k + 1, 1, 2, R2);
 
+    if constexpr (KG == 2) {
+        // the second group's partial sums through the rings' memory
+        int* xch = reinterpret_cast<int*>(rings);
+        __syncthreads();
+        if (grp == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                xch[(wave * 16 + r) * 64 + lane] = acc[r];
+                if constexpr (PROJ) xch[((4 + wave) * 16 + r) * 64 + lane] = accp[r];
+            }
+        }
+        __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            acc[r] += xch[(wave * 16 + r) * 64 + lane];
+            if constexpr (PROJ) accp[r] += xch[((4 + wave) * 16 + r) * 64 + lane];
+        }
+    }
     if (pme >= g.P) return;
     QOut qo;
     if constexpr (OUT == 1) qo = qout_parm(e.qs, e.qz, e.qkind);
@@ -761,9 +804,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PROJ && OUT
 template <bool PROJ>
 void launch_qconv_lds(int out, const int8_t* x, const int8_t* wk, const int8_t* pk, void* y, const QGeom& g,
                       const QEpi& e, hipStream_t s) {
-    const dim3 grid((unsigned)(((g.P + 63) / 64) * (g.M / 64)));
-    if (out == 0) hipLaunchKernelGGL((k_qconv_lds<PROJ, 0>), grid, dim3(256), 0, s, x, wk, pk, y, g, e);
-    else hipLaunchKernelGGL((k_qconv_lds<PROJ, 1>), grid, dim3(256), 0, s, x, wk, pk, y, g, e);
+    const int tiles = ((g.P + 63) / 64) * (g.M / 64);
+    const dim3 grid((unsigned)tiles);
+    // a grid of at most two blocks per CU: two k groups per block (each tile's
+    // chain of stages halves; its blocks still fit on the CUs at once)
+    if (tiles <= 2 * num_cus()) {
+        if (out == 0) hipLaunchKernelGGL((k_qconv_lds<PROJ, 0, 2>), grid, dim3(512), 0, s, x, wk, pk, y, g, e);
+        else hipLaunchKernelGGL((k_qconv_lds<PROJ, 1, 2>), grid, dim3(512), 0, s, x, wk, pk, y, g, e);
+        return;
+    }
+    if (out == 0) hipLaunchKernelGGL((k_qconv_lds<PROJ, 0, 1>), grid, dim3(256), 0, s, x, wk, pk, y, g, e);
+    else hipLaunchKernelGGL((k_qconv_lds<PROJ, 1, 1>), grid, dim3(256), 0, s, x, wk, pk, y, g, e);
 }
 
 template <int KS, bool PROJ>
