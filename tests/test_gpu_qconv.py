@@ -254,30 +254,37 @@ def test_pack_weights(hip):
         dev.free()
 
 
-# name, N, C, H, W, M, stride, projection, skip, x code dtype, x zero point
+# name, N, C, H, W, M, stride, projection, skip, x code dtype, x zero point[, kernel size (3)].
+# Grids this small run two k groups per block; the 1x1 cases put the second group's
+# stages wholly in the projection, or leave it none.
 SMALL = [
     ("s1_skip_u8", 2, 64, 12, 12, 64, 1, False, True, O.U8, 0),
     ("s1_skip_u8_zp", 2, 64, 11, 9, 64, 1, False, True, O.U8, 41),
     ("s2_proj_u8", 2, 64, 13, 13, 128, 2, True, False, O.U8, 0),
     ("s2_proj_i8_zp", 1, 96, 10, 7, 64, 2, True, False, O.I8, -5),
     ("s1_plain_c32", 3, 32, 6, 6, 64, 1, False, False, O.U8, 200),
+    ("k1_s2_proj_u8", 2, 64, 9, 9, 64, 2, True, False, O.U8, 0, 1),
+    ("k1_skip_c128_i8", 1, 128, 8, 8, 128, 1, False, True, O.I8, 7, 1),
+    ("k1_one_stage_c64", 2, 64, 6, 6, 64, 1, False, True, O.U8, 3, 1),
 ]
 
 
 @pytest.mark.parametrize("case", SMALL, ids=[c[0] for c in SMALL])
 def test_qconv_block_against_sequence(hip, oracle_lib, case):
     _bind(hip.lib)
-    name, N, C, H, W, M, stride, proj, has_skip, xdt, zx = case
+    name, N, C, H, W, M, stride, proj, has_skip, xdt, zx = case[:11]
+    ks = case[11] if len(case) > 11 else 3
     rng = np.random.default_rng(sum(map(ord, name)))
     lo, hi = (0, 256) if xdt == O.U8 else (-128, 128)
     xq = rng.integers(lo, hi, (N, C, H, W)).astype(np.uint8 if xdt == O.U8 else np.int8)
     sx = np.float32(8.0 / 255)
-    wq, sw = _weights(rng, M, C, 3, 3)
+    wq, sw = _weights(rng, M, C, ks, ks)
     pq, sp = _weights(rng, M, C, 1, 1) if proj else (None, None)
     bias = rng.normal(0, 1 / 64, M).astype(np.float32)
-    OH, OW = (H - 1) // stride + 1, (W - 1) // stride + 1
+    pd = ks // 2
+    OH, OW = (H + 2 * pd - ks) // stride + 1, (W + 2 * pd - ks) // stride + 1
     skip = rng.normal(0, 1, (N, M, OH, OW)).astype(np.float32) if has_skip else None
-    pads, strides = (1, 1, 1, 1), (stride, stride)
+    pads, strides = (pd, pd, pd, pd), (stride, stride)
     ref = _oracle_block(oracle_lib, xq, xdt, sx, zx, wq, sw, bias, True, pq, sp, skip, pads, strides)
     dev = _Dev(hip)
     try:
