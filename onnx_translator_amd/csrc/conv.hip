@@ -809,7 +809,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_conv_tiled(const float* __re
 // channels over two 32-pixel groups: a 32x64 wave tile per instruction, and no
 // padded k slots (a padded slot would multiply a zero weight by a real, possibly
 // non-finite, input).  Output register r of lane l: block r / 16, channel
-// 8*((r%16)/4) + r%4 + 4*(l/32), pixel l%32 of that block's group.
+// 8*((r%16)/4) + r%4 + 4*(l/32), pixel l%32 of that block's group.  ONE_M (one
+// channel tile): the weights go to LDS once per block and each kh row's
+// operands are read while the row before it is multiplied; DEFER (ONE_M
+// without a residual): a tile's outputs are stored during the next tile's
+// multiply.
 constexpr int kStemRows = 13, kStemCols = 232;   // LDS patch per input channel: rows x columns
 template <int C, int KH, int KW, int S, bool ONE_M, bool DEFER>
 __global__ __launch_bounds__(512, 4) void k_conv_stem(const float* __restrict__ X, const float* __restrict__ Wt,
