@@ -248,6 +248,12 @@ void quantize_dequantize_linear_forward(const Tensor* X, const Tensor* QScale, c
 void dequantize_gemm_forward(const Tensor* A, const Tensor* Bq, const Tensor* Scale, const Tensor* ZeroPoint,
                              int axis, const Tensor* C, Tensor* Y, float alpha, float beta, int transA,
                              int transB);
+/* Gemm followed by Softmax over the last axis: Y = gemm_forward(A, B, C, alpha, beta, transA,
+ * transB) and P = softmax_forward(Y, axis = last) (tensor_ops/tensor_ops.h:173-174, 179), bit
+ * for bit.  With f32 device Y and P and a Gemm that runs as a k-split product, the split
+ * reduction also takes the softmax (one launch fewer); otherwise the two calls run. */
+void gemm_softmax_forward(const Tensor* A, const Tensor* B, const Tensor* C, Tensor* Y, Tensor* P, float alpha,
+                          float beta, int transA, int transB);
 /* Convolution with the residual block's epilogue: Y = [Skip +] [Relu](Conv(X, W, B)), the
  * conv2d_forward -> relu_forward -> add_forward(., Skip) sequence (tensor_ops/tensor_ops.h:161,
  * 85, 116) in one pass over Y.  Each step rounds to the output dtype as the standalone

@@ -1022,8 +1022,10 @@ void launch_nt_kernel(const GemmArgs& g, const WoqB& q, int kchunk, int nsplit, 
         hipLaunchKernelGGL((k_gemm_f32_nt<BM, BN, BK, WGM, WGN, -1, BQ, -1, SPLIT>), grid, block, 0, s, g, q, kchunk);
 }
 
+// probs (f32 [M, N], or null): with a k split, the reduction also takes the
+// rows' softmax into probs (returns 2); otherwise the caller runs the softmax.
 template <int BQ>
-int launch_f32_nt(const GemmArgs& g, const WoqB& q, hipStream_t s) {
+int launch_f32_nt(const GemmArgs& g, const WoqB& q, hipStream_t s, float* probs = nullptr) {
     const int64_t reach = (int64_t)1 << 31;
     const int eb = BQ ? 1 : 4;
     if ((int64_t)(g.M + 256) * g.lda * 4 >= reach || (int64_t)(g.N + 256) * g.ldb * eb >= reach) return 0;
@@ -1049,6 +1051,12 @@ int launch_f32_nt(const GemmArgs& g, const WoqB& q, hipStream_t s) {
     GemmArgs gp = g;
     gp.Y = part;
     launch_nt_kernel<128, 64, 16, 2, 2, BQ, true>(gp, q, kchunk, nsplit, kF32, s);
+    if (probs && ydt == kF32 &&
+        launch_splitk_softmax(part, nsplit, g.M, g.N, g.alpha, g.beta, (const float*)g.c.p, g.c.mode, (float*)g.Y,
+                              probs, s)) {
+        pool_free(part);
+        return 2;
+    }
     const dim3 rgrid((unsigned)((mn + 255) / 256));
     const FastDiv fd_n = make_fastdiv((uint32_t)g.N);
     if (ydt == kF32)
@@ -1081,9 +1089,11 @@ bool launch_f32_mfma(const GemmArgs& g, int dta, int dtb, int ta, int tb, hipStr
 
 using namespace tohip;
 
-extern "C" void gemm_forward(const Tensor* A, const Tensor* B, const Tensor* C, Tensor* Y, float alpha, float beta,
-                             int transA, int transB) {
-    const char* name = "gemm_forward";
+namespace {
+// gemm_forward; with probs (a device f32 [M, N] buffer) the rows' softmax of Y is
+// written there as well when the split reduction can take it (*softmax_done).
+void gemm_impl(const char* name, const Tensor* A, const Tensor* B, const Tensor* C, Tensor* Y, float alpha,
+               float beta, int transA, int transB, float* probs, bool* softmax_done) {
     if (!tensor_sane(A, name) || !tensor_sane(B, name) || !tensor_sane(Y, name)) return;
     if (A->ndim < 2 || B->ndim < 2) { set_error("%s: A and B must be 2-D", name); return; }
     const int M = transA ? A->shape[1] : A->shape[0];
@@ -1140,9 +1150,10 @@ extern "C" void gemm_forward(const Tensor* A, const Tensor* B, const Tensor* C, 
             } else if (f32_exact_dtype(dta) && f32_exact_dtype(dtb)) {
                 const bool nt = dta == kF32 && dtb == kF32 && !transA && transB && (g.lda % 4) == 0 &&
                                 (g.ldb % 4) == 0 && ((uintptr_t)g.A & 15) == 0 && ((uintptr_t)g.B & 15) == 0;
-                const int r = nt ? launch_f32_nt<0>(g, WoqB{nullptr, nullptr, 0, 0}, s) : 0;
+                const int r = nt ? launch_f32_nt<0>(g, WoqB{nullptr, nullptr, 0, 0}, s, probs) : 0;
                 if (r < 0) { st.finish(); return; }
-                done = r == 1 || launch_f32_mfma(g, dta, dtb, transA, transB, s);
+                if (r == 2 && softmax_done) *softmax_done = true;
+                done = r >= 1 || launch_f32_mfma(g, dta, dtb, transA, transB, s);
             }
         }
         if (!done) {
@@ -1152,6 +1163,25 @@ extern "C" void gemm_forward(const Tensor* A, const Tensor* B, const Tensor* C, 
         if (!check_launch(name)) { st.finish(); return; }
     }
     st.finish();
+}
+}  // namespace
+
+extern "C" void gemm_forward(const Tensor* A, const Tensor* B, const Tensor* C, Tensor* Y, float alpha, float beta,
+                             int transA, int transB) {
+    gemm_impl("gemm_forward", A, B, C, Y, alpha, beta, transA, transB, nullptr, nullptr);
+}
+
+extern "C" void gemm_softmax_forward(const Tensor* A, const Tensor* B, const Tensor* C, Tensor* Y, Tensor* P,
+                                     float alpha, float beta, int transA, int transB) {
+    const char* name = "gemm_softmax_forward";
+    if (!tensor_sane(Y, name) || !tensor_sane(P, name)) return;
+    if (P->size != Y->size || Y->ndim < 2) { set_error("%s: P must have Y's size and Y two dimensions", name); return; }
+    const bool fuse = (int)Y->dtype == kF32 && (int)P->dtype == kF32 && is_dev(classify(Y->data)) &&
+                      is_dev(classify(P->data));
+    bool done = false;
+    gemm_impl(name, A, B, C, Y, alpha, beta, transA, transB, fuse ? (float*)P->data : nullptr, &done);
+    if (tensor_ops_hip_last_error()[0] || done) return;
+    softmax_forward(Y, P, Y->ndim - 1);
 }
 
 namespace {

@@ -733,7 +733,48 @@ __global__ __launch_bounds__(kGapSmallThreads) void k_gap_small_f32(const float*
     }
 }
 
+// Gemm -> Softmax (last axis) with the Gemm's k split: one block per row adds
+// the row's slice sums and the bias as k_splitk_reduce does (double sum in
+// slice order, alpha * acc + beta * c, rounded to f32), writes the logits, and
+// takes the row's softmax as k_softmax_row<1> does (max from -DBL_MAX with a
+// strict >, sm_exp, the block sums, one reciprocal): both outputs equal the
+// two launches they replace bit for bit.  cmode: 0 no bias, 1 one value, 2 per
+// column, 3 per row.  N <= kRowThreads.
+__global__ __launch_bounds__(kRowThreads) void k_splitk_softmax(const float* __restrict__ part, int nsplit, int M,
+                                                                int N, double alpha, double beta,
+                                                                const float* __restrict__ c, int cmode,
+                                                                float* __restrict__ Y, float* __restrict__ P) {
+    __shared__ double lds[kWaves];
+    const int m = blockIdx.x, j = threadIdx.x;
+    const int64_t mn = (int64_t)M * N, i = (int64_t)m * N + j;
+    double v = -DBL_MAX;
+    if (j < N) {
+        double acc = 0.0;
+        for (int sp = 0; sp < nsplit; sp++) acc += (double)part[(int64_t)sp * mn + i];
+        double r = alpha * acc;
+        if (cmode) r += beta * (double)c[cmode == 1 ? 0 : (cmode == 2 ? j : m)];
+        const float y = (float)r;
+        Y[i] = y;
+        v = (double)y;
+    }
+    double mx = -DBL_MAX;
+    mx = v > mx ? v : mx;
+    mx = block_reduce<true, kWaves>(mx, lds);
+    const double e = j < N ? sm_exp(v - mx) : 0.0;
+    const double sum = block_reduce<false, kWaves>(e, lds);
+    const double rs = 1.0 / sum;
+    if (j < N) P[i] = (float)(e * rs);
+}
+
 }  // namespace
+
+bool launch_splitk_softmax(const float* part, int nsplit, int M, int N, double alpha, double beta, const float* c,
+                           int cmode, float* Y, float* P, hipStream_t s) {
+    if (N < 1 || N > kRowThreads || M < 1 || cmode < 0 || cmode > 3) return false;
+    hipLaunchKernelGGL(k_splitk_softmax, dim3((unsigned)M), dim3(kRowThreads), 0, s, part, nsplit, M, N, alpha, beta, c,
+                       cmode, Y, P);
+    return true;
+}
 
 // Resolves sm_capture_ws on the library's device (current during initialisation).
 void init_reduce_workspace() {

@@ -59,6 +59,14 @@ bool stream_capturing(hipStream_t s);
 void init_qdq_workspace();
 void init_reduce_workspace();
 
+// Gemm -> Softmax over the last axis after a k-split Gemm (reduce.hip): adds the
+// nsplit slices of M x N partial sums at part with the bias (cmode 0 none, 1
+// one value, 2 per column, 3 per row of f32 c) into Y (f32 logits) and writes
+// their row softmax to P (f32), bit for bit as the split reduction followed by
+// softmax_forward.  false (nothing launched) unless 1 <= N <= 1024.
+bool launch_splitk_softmax(const float* part, int nsplit, int M, int N, double alpha, double beta, const float* c,
+                           int cmode, float* Y, float* P, hipStream_t s);
+
 // ---- memory -----------------------------------------------------------------
 enum class Mem { kHostPinned, kHostMalloc, kDevOwned, kDevBorrowed, kHostForeign, kDevForeign };
 Mem classify(const void* p);     // registry first, then hipPointerGetAttributes

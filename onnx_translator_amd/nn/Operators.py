@@ -589,6 +589,55 @@ class Gemm(Ops):
         return _values(self, Tensor_(M, N, dtype=self.dtype))
 
 
+class GemmSoftmax(Gemm):
+    """Gemm followed by Softmax over the last axis of its output in one call to
+    ``gemm_softmax_forward``: outputs [y, p] with y = Gemm(A, B, C) and p =
+    Softmax(y) (nn/Operators.py:613-669, :671-704), both bit for bit; on device
+    tensors the Gemm's k-split reduction also takes the softmax."""
+
+    def __init__(self, inputs, outputs, alpha, beta, transA, transB, dtype, version="17"):
+        super().__init__(inputs, outputs, alpha, beta, transA, transB, dtype, version)
+        self.lib.gemm_softmax_forward.argtypes = [PT] * 5 + [ctypes.c_float, ctypes.c_float, ctypes.c_int,
+                                                             ctypes.c_int]
+        self.lib.gemm_softmax_forward.restype = None
+
+    def forward(self, A: Tensor, B: Tensor, C: Tensor = None):
+        M = A.size[0] if self.transA == 0 else A.size[1]
+        N = B.size[1] if self.transB == 0 else B.size[0]
+        if C is not None and not isinstance(C.data, DeviceArray) and np.asarray(C.data).ndim == 1:
+            c = np.asarray(C.data)
+            if c.shape[0] == N:
+                c = c.reshape(1, -1)
+            elif c.shape[0] == M:
+                c = c.reshape(-1, 1)
+            C = Tensor(*c.shape, dtype=C.dtype, data=np.ascontiguousarray(c))
+        keep: list = []
+        dev = any(isinstance(t.data, DeviceArray) for t in (A, B, C) if t is not None)
+        outs = []
+        try:
+            cins = [self._in_ctensor(t, keep) if t is not None else PT() for t in (A, B, C)]
+            for _ in range(2):
+                outs.append(((M, N), self.dtype) + self._out_ctensor((M, N), self.dtype, dev))
+            self._call("gemm_softmax_forward", cins[0], cins[1], cins[2], outs[0][3], outs[1][3],
+                       ctypes.c_float(self.alpha), ctypes.c_float(self.beta), ctypes.c_int(self.transA),
+                       ctypes.c_int(self.transB))
+        except Exception:
+            for shape, dt, d, c in outs:
+                if d is None:
+                    self.lib.free_tensor(c)
+            for c in keep:
+                self.lib.free_tensor(c)
+            raise
+        tensors = [self._finish(shape, dt, d, c, []) for shape, dt, d, c in outs]
+        for c in keep:
+            self.lib.free_tensor(c)
+        return _values(self, tensors)
+
+    def forward_(self, A: Tensor_, B: Tensor_, C: Tensor_ = None):
+        y = super().forward_(A, B, C)["tensor"]
+        return _values(self, [y, Tensor_(*y.size, dtype=self.dtype)])
+
+
 class QuantizeDequantize(Ops):
     """DequantizeLinear(QuantizeLinear(x, q_scale, q_zero_point), d_scale,
     d_zero_point) in one call to ``quantize_dequantize_linear_forward``: the

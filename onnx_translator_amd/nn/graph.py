@@ -162,7 +162,7 @@ class Graph:
     def fuse(self, elementwise: bool = True, dequantize_gemm: bool = True, conv_epilogue: bool = True,
              fold_constants: bool = True, dequantize_conv: bool = False,
              quantize_dequantize: bool = True, pool_quantize_dequantize: bool = False,
-             int8_conv: bool = False) -> "Graph":
+             int8_conv: bool = False, gemm_softmax: bool = True) -> "Graph":
         """Request the graph passes; they are applied at the first ``forward`` (shapes needed).
         ``dequantize_conv`` folds activation DequantizeLinear nodes into their convolutions
         and so takes precedence over ``quantize_dequantize`` for those pairs.
@@ -172,14 +172,17 @@ class Graph:
         ``int8_conv`` (device graphs) runs QDQ residual blocks on the int8 MFMA kernels
         (QuantizeNHWC, QConvBlock): their convolutions sum the integer codes exactly and
         scale once, the tolerance class of the MFMA convolution rather than the bits of the
-        operator sequence, and they have no exact mode, so it is off by default."""
+        operator sequence, and they have no exact mode, so it is off by default.
+        ``gemm_softmax`` (device graphs) runs a Gemm whose f32 output only a Softmax over
+        its last axis reads as one GemmSoftmax (bit for bit; the Gemm's split reduction
+        takes the softmax)."""
         self._fuse_pending = (elementwise, dequantize_gemm, conv_epilogue, fold_constants, dequantize_conv,
-                              quantize_dequantize, pool_quantize_dequantize, int8_conv)
+                              quantize_dequantize, pool_quantize_dequantize, int8_conv, gemm_softmax)
         return self
 
     def fuse_elementwise(self) -> "Graph":
         """Request elementwise fusion only."""
-        return self.fuse(True, False, False, False, False, False, False, False)
+        return self.fuse(True, False, False, False, False, False, False, False, False)
 
     def _edge_shapes(self, inputs) -> Dict[str, tuple]:
         shapes: Dict[str, tuple] = {k: (tuple(v.size), v.dtype) for k, v in self.initializers.items()}
@@ -196,7 +199,7 @@ class Graph:
         return shapes
 
     def _fuse(self, inputs):
-        elementwise, dq_gemm, conv_epi, fold, dq_conv, qdq, pool_qdq, int8_conv = self._fuse_pending
+        elementwise, dq_gemm, conv_epi, fold, dq_conv, qdq, pool_qdq, int8_conv, gemm_sm = self._fuse_pending
         self._fuse_pending = None
         shapes = self._edge_shapes(inputs)
         if int8_conv and self.device and self._fuse_qconv_blocks(shapes, self._consumers()):
@@ -215,9 +218,41 @@ class Graph:
                 self._fuse_conv_qdq(shapes, self._consumers())
             if pool_qdq:
                 self._fuse_pool_qdq(shapes)
+        if gemm_sm and self.device:
+            self._fuse_gemm_softmax(shapes)
         if elementwise:
             self._fuse_gap_flatten(shapes, self._consumers())
             self._fuse_runs(shapes, self._consumers())
+
+    def _fuse_gemm_softmax(self, shapes):
+        """A float32 Gemm whose output is read only by a Softmax over its last axis
+        becomes one GemmSoftmax with both outputs (the Gemm's output stays an edge)."""
+        ops = list(self.ops.values())
+        users: Dict[str, list] = {}
+        for op in ops:
+            for na in op.inputs:
+                if na:
+                    users.setdefault(na, []).append(op)
+        replace, drop = {}, set()
+        for op in ops:
+            if type(op) is not Op.Gemm or op.dtype != "float32":
+                continue
+            y = op.outputs[0]
+            u = users.get(y, [])
+            if len(u) != 1 or type(u[0]) is not Op.Softmax or y not in shapes or shapes[y][1] != "float32":
+                continue
+            sm = u[0]
+            nd = len(shapes[y][0])
+            if sm.dtype not in (None, "float32") or sm.axis not in (nd - 1, -1):
+                continue
+            fused = Op.GemmSoftmax(list(op.inputs), [y, sm.outputs[0]], op.alpha, op.beta, op.transA, op.transB,
+                                   op.dtype)
+            fused.name = f"GemmSoftmax.{op.name}+{sm.name}"
+            replace[op.name] = fused
+            drop.add(sm.name)
+            self.fused_runs.append([op.name, sm.name])
+        if replace:
+            self.ops = OrderedDict((o.name, o) for o in [replace.get(o.name, o) for o in ops if o.name not in drop])
 
     def _fuse_qconv_blocks(self, shapes, consumers) -> bool:
         """QDQ residual blocks onto the int8 MFMA kernels.  A block is
